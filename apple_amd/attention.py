@@ -1,0 +1,83 @@
+"""Blockwise exact attention entry points on MI355X -- the counterpart of the
+reference's ``attention.py`` (attention.py:16-171).
+
+``_blockwise_exact_attention`` runs the HIP split-K kernel over fp16 K/V; the
+``block_size`` argument is accepted for drop-in compatibility and, as in the
+reference, only changes fp32 rounding (the kernel's tile is fixed).  Keys and
+values may have fewer heads than the query (GQA): query head ``h`` reads KV
+head ``h // (Hq // Hkv)`` (llama32_adapter.py:384-386).
+``RFSNHybridAttentionMLX`` decodes both compressed stores with the decode
+kernel and attends, as attention.py:159-171 does; the fused
+dequant-attention kernel is driven by the cache (``cache.py``), which owns the
+tiled code layout that kernel streams.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import kernels as K
+from .quantization import HybridQuantizerMLX, _decode_compressed_tensor
+from .storage import MASK_FILL_VALUE, CompressedTensorMLX, RFSNConfig
+
+logger = logging.getLogger("RFSN_ATTENTION")
+
+Positions = Optional[Union[Sequence[int], torch.Tensor]]
+
+
+def _normalize_query_positions(query_positions: Positions, batch_size: int, num_heads: int,
+                               default_position: int, device=None) -> torch.Tensor:
+    """int32 [B, H] positions (attention.py:16-36)."""
+    if query_positions is None:
+        return torch.full((batch_size, num_heads), default_position, dtype=torch.int32, device=device)
+    if isinstance(query_positions, torch.Tensor):
+        positions = query_positions.to(device=device)
+    else:
+        positions = torch.tensor(query_positions, dtype=torch.int32, device=device)
+    if positions.dim() == 1:
+        if int(positions.shape[0]) != batch_size:
+            raise ValueError("query_positions length must equal batch size")
+        return positions.reshape(batch_size, 1).to(torch.int32).expand(batch_size, num_heads).contiguous()
+    if tuple(int(d) for d in positions.shape) == (batch_size, num_heads):
+        return positions.to(torch.int32).contiguous()
+    raise ValueError("query_positions must have shape [B] or [B, H]")
+
+
+def _blockwise_exact_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, scale: float,
+                               block_size: int, causal: bool = False,
+                               query_positions: Positions = None) -> torch.Tensor:
+    """attention.py:39-105 on the GPU.  q [B, Hq, D]; keys/values [T, Hkv, D]."""
+    batch_size, num_heads, head_dim = q.shape
+    seq_len = int(keys.shape[0])
+    if seq_len == 0:
+        return torch.zeros((batch_size, num_heads, head_dim), dtype=q.dtype, device=q.device)
+    if int(block_size) <= 0:
+        raise ValueError("block_size must be positive")
+    pos = _normalize_query_positions(query_positions, batch_size, num_heads, seq_len - 1, q.device)
+    qh = q.to(torch.float16)
+    out = K.blockwise_attention(qh, keys.to(torch.float16), values.to(torch.float16), scale, causal,
+                                pos if causal else None)
+    return out.to(q.dtype)
+
+
+class RFSNHybridAttentionMLX:
+    """Attention over compressed key/value stores (attention.py:141-171)."""
+
+    def __init__(self, config: RFSNConfig):
+        self.config = config
+        self.scale = config.head_dim ** -0.5
+        self.block_size = config.block_size_seq
+
+    def __call__(self, q: torch.Tensor, key_store: CompressedTensorMLX, value_store: CompressedTensorMLX,
+                 quantizer: HybridQuantizerMLX, causal: bool = False,
+                 query_positions: Positions = None) -> torch.Tensor:
+        if key_store.num_tokens != value_store.num_tokens:
+            raise ValueError("Key/value stores must have the same token count")
+        decoded_keys = _decode_compressed_tensor(key_store, quantizer)
+        decoded_values = _decode_compressed_tensor(value_store, quantizer)
+        return _blockwise_exact_attention(q=q, keys=decoded_keys, values=decoded_values, scale=self.scale,
+                                          block_size=self.block_size, causal=causal,
+                                          query_positions=query_positions)

@@ -1,0 +1,186 @@
+"""Batched warm-tier KV cache: B independent sequences decoded by one fused
+launch.
+
+The reference keeps one ``RFSNv10KVCacheMLX`` per sequence
+(cache.py:33-57) and its ``attention_forward`` serves queries over that one
+cache.  Here the HBM image of B sequences lives in shared device buffers:
+
+* hot tier: ``hot_k / hot_v`` fp16 ``[B, Hkv, hot_cap, D]`` (newest tokens);
+* warm tier: PQ / RVQ codes in the tiled layout ``[B, Hkv, cap*M]`` and the
+  sparse residual ``[B, Hkv, cap, k]`` (u8 index, fp16 value);
+* codebooks per sequence, K and V separately: ``[B, M, C, d]``.
+
+Window order per sequence is warm (positions 0..W-1) then hot, the recency
+tier policy.  ``sequence_window(b)`` materializes one sequence's window with
+the decode kernel for parity checks (cache.py:344-393 semantics).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import kernels as K
+from .quantization import HybridQuantizerMLX
+from .storage import RFSNConfig
+
+
+class RFSNBatchedKVCache:
+    def __init__(self, config: RFSNConfig, batch: int, device=None):
+        self.config = config
+        self.batch = batch
+        self.H = config.kv_heads
+        self.D = config.head_dim
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.hot_cap = config.hot_capacity
+        self.warm_cap = K.round_up(config.warm_capacity, K.TILE)
+        self.fmt: Optional[K.WarmFormat] = None
+        self.num_hot = [0] * batch
+        self.num_warm = [0] * batch
+        self._table = None
+        self._ws = None
+        self.quantizers: List[Optional[Tuple[HybridQuantizerMLX, HybridQuantizerMLX]]] = [None] * batch
+
+    def _alloc(self, fmt: K.WarmFormat) -> None:
+        B, H, D, dev = self.batch, self.H, self.D, self.device
+        self.fmt = fmt
+        self.hot_k = torch.zeros((B, H, self.hot_cap, D), dtype=torch.float16, device=dev)
+        self.hot_v = torch.zeros_like(self.hot_k)
+        cap = self.warm_cap
+        self.codes = {}
+        for kv in ("k", "v"):
+            c = {"pq": torch.zeros((B, H, cap * fmt.pq_subspaces), dtype=torch.uint8, device=dev)}
+            c["rvq"] = (torch.zeros((B, H, cap * fmt.rvq_subspaces), dtype=torch.uint8, device=dev)
+                        if fmt.rvq_subspaces else None)
+            c["sparse_idx"] = (torch.zeros((B, H, cap, fmt.sparse_k), dtype=torch.uint8, device=dev)
+                               if fmt.sparse_k else None)
+            c["sparse_val"] = (torch.zeros((B, H, cap, fmt.sparse_k), dtype=torch.float16, device=dev)
+                               if fmt.sparse_k else None)
+            self.codes[kv] = c
+        M, Cn, d = fmt.pq_subspaces, fmt.pq_centroids, D // fmt.pq_subspaces
+        self.cb = {"k_pq": torch.zeros((B, M, Cn, d), dtype=torch.float16, device=dev)}
+        self.cb["v_pq"] = torch.zeros_like(self.cb["k_pq"])
+        if fmt.rvq_subspaces:
+            Mr, Cr = fmt.rvq_subspaces, fmt.rvq_centroids
+            self.cb["k_rvq"] = torch.zeros((B, Mr, Cr, D // Mr), dtype=torch.float16, device=dev)
+            self.cb["v_rvq"] = torch.zeros_like(self.cb["k_rvq"])
+
+    def prefill(self, b: int, keys: torch.Tensor, values: torch.Tensor, key_quantizer: HybridQuantizerMLX,
+                value_quantizer: HybridQuantizerMLX) -> None:
+        """Load sequence b: the newest ``hot_capacity`` tokens stay exact, the
+        older ones are encoded into the warm tier."""
+        if keys.shape != values.shape or keys.dim() != 3 or keys.shape[1:] != (self.H, self.D):
+            raise ValueError(f"keys/values must be [T, {self.H}, {self.D}]")
+        fmt = key_quantizer.warm_format()
+        if value_quantizer.warm_format() != fmt:
+            raise ValueError("key and value quantizers must share one format")
+        if self.fmt is None:
+            self._alloc(fmt)
+        elif fmt != self.fmt:
+            raise ValueError("every sequence must use the same warm format")
+        T = int(keys.shape[0])
+        nh = min(T, self.hot_cap)
+        nw = T - nh
+        if nw > self.warm_cap:
+            raise ValueError(f"{nw} warm tokens exceed the warm capacity {self.warm_cap}")
+        keys = keys.to(self.device, torch.float16)
+        values = values.to(self.device, torch.float16)
+        self.hot_k[b, :, :nh] = keys[nw:].permute(1, 0, 2)
+        self.hot_v[b, :, :nh] = values[nw:].permute(1, 0, 2)
+        for kv, x, qz in (("k", keys, key_quantizer), ("v", values, value_quantizer)):
+            self.cb[f"{kv}_pq"][b] = qz.pq.codebooks
+            if fmt.rvq_subspaces:
+                self.cb[f"{kv}_rvq"][b] = qz.rvq.codebooks
+            if nw == 0:
+                continue
+            flat = x[:nw].permute(1, 0, 2).reshape(self.H * nw, self.D).contiguous()
+            out = K.warm_encode(flat, fmt, qz.pq.codebooks, qz.rvq.codebooks if fmt.rvq_subspaces else None)
+            c = self.codes[kv]
+            K.pack_codes(out["pq"].view(self.H, nw, -1), c["pq"][b], 0)
+            if fmt.rvq_subspaces:
+                K.pack_codes(out["rvq"].view(self.H, nw, -1), c["rvq"][b], 0)
+            if fmt.sparse_k:
+                c["sparse_idx"][b, :, :nw] = out["sparse_idx"].view(self.H, nw, -1)
+                c["sparse_val"][b, :, :nw] = out["sparse_val"].view(self.H, nw, -1)
+        self.num_hot[b] = nh
+        self.num_warm[b] = nw
+        self.quantizers[b] = (key_quantizer, value_quantizer)
+        self._table = None
+
+    def _segment_table(self):
+        if self._table is None:
+            t = K.SegmentTable(self.batch)
+            for b in range(self.batch):
+                if self.num_warm[b]:
+                    kc = {k: (None if v is None else v[b]) for k, v in self.codes["k"].items()}
+                    vc = {k: (None if v is None else v[b]) for k, v in self.codes["v"].items()}
+                    t.add(b, kc, vc, self.warm_cap, self.num_warm[b], 0)
+            self._table = (t, t.to_device(self.device))
+        return self._table
+
+    def attention_forward(self, q: torch.Tensor, causal: bool = False, query_positions=None, splits: int = 0,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """q [B, Hq, D] (one decode query per sequence) -> [B, Hq, D] fp16."""
+        if q.shape[0] != self.batch or q.shape[2] != self.D or q.shape[1] % self.H:
+            raise ValueError("q must be [B, Hq, D] with Hq a multiple of the KV heads")
+        if len(set(self.num_hot)) != 1 or (causal and len(set(self.num_warm)) != 1):
+            raise ValueError("every sequence must hold the same hot length (and warm length when causal)")
+        table, dev_table = self._segment_table()
+        f = self.fmt
+        qpos = None
+        if causal:
+            total = self.num_hot[0] + self.num_warm[0]
+            if query_positions is None:
+                qpos = torch.full((self.batch, q.shape[1]), total - 1, dtype=torch.int32, device=self.device)
+            else:
+                qpos = torch.as_tensor(query_positions, device=self.device).to(torch.int32)
+                if qpos.dim() == 1:
+                    qpos = qpos[:, None].expand(self.batch, q.shape[1]).contiguous()
+        if self._ws is None:
+            self._ws = torch.empty(4 << 20, dtype=torch.uint8, device=self.device)
+        return K.fused_attention(
+            q, f, kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos, hot_k=self.hot_k,
+            hot_v=self.hot_v, hot_len=self.num_hot[0], hot_pos0=self.num_warm[0],
+            hot_seq_stride=self.H * self.hot_cap * self.D, segments=table, table=dev_table,
+            k_pq_cb=self.cb["k_pq"], v_pq_cb=self.cb["v_pq"], k_rvq_cb=self.cb.get("k_rvq"),
+            v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True,
+            max_tokens=max(h + w for h, w in zip(self.num_hot, self.num_warm)), splits=splits,
+            workspace=self._ws, out=out, hot_cap=self.hot_cap)
+
+    def sequence_window(self, b: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Materialized (keys, values) [W, Hkv, D] of sequence b, warm then hot."""
+        kq, vq = self.quantizers[b]
+        nw, nh = self.num_warm[b], self.num_hot[b]
+        outs = []
+        for kv, qz, hot in (("k", kq, self.hot_k), ("v", vq, self.hot_v)):
+            parts = []
+            if nw:
+                parts.append(self._decode_warm(kv, b, qz).view(self.H, nw, self.D).permute(1, 0, 2))
+            parts.append(hot[b, :, :nh].permute(1, 0, 2))
+            outs.append(torch.cat(parts, 0).contiguous())
+        return outs[0], outs[1]
+
+    def _decode_warm(self, kv: str, b: int, qz: HybridQuantizerMLX) -> torch.Tensor:
+        """Unpack the tiled codes of sequence b and decode them (head-major rows)."""
+        f = self.fmt
+        nw = self.num_warm[b]
+        c = self.codes[kv]
+        pq = untile(c["pq"][b], f.pq_subspaces, nw)
+        rvq = untile(c["rvq"][b], f.rvq_subspaces, nw) if f.rvq_subspaces else None
+        sidx = c["sparse_idx"][b, :, :nw].reshape(self.H * nw, -1) if f.sparse_k else None
+        sval = c["sparse_val"][b, :, :nw].reshape(self.H * nw, -1) if f.sparse_k else None
+        return K.decode(f, pq.reshape(self.H * nw, -1), qz.pq.codebooks,
+                        None if rvq is None else rvq.reshape(self.H * nw, -1),
+                        qz.rvq.codebooks if f.rvq_subspaces else None, sidx, sval)
+
+
+def untile(tiled: torch.Tensor, M: int, T: int) -> torch.Tensor:
+    """Inverse of the tiled code layout: [H, cap*M] -> plain [H, T, M]."""
+    H = tiled.shape[0]
+    tpi = 64 // M
+    ipt = 32 // tpi
+    t = torch.arange(T, device=tiled.device)
+    m = torch.arange(M, device=tiled.device)
+    off = ((t // 32) * 32 * M)[:, None] + ((t % tpi)[:, None] * M + m[None, :]) * ipt + ((t % 32) // tpi)[:, None]
+    return tiled[:, off.reshape(-1)].reshape(H, T, M)

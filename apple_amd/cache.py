@@ -1,0 +1,765 @@
+"""Tiered KV cache on MI355X -- the counterpart of the reference's ``cache.py``
+(``RFSNv10KVCacheMLX``, cache.py:33-440).
+
+Reference behaviour kept: tier fill by arrival (hot, then warm, then cold;
+cache.py:89-120), cold chunking by ``block_size_seq`` with merge-on-append
+(cache.py:134-191), window bounds and adjusted positions (cache.py:199-241),
+materialization order and access counters (cache.py:250-393),
+``attention_forward`` semantics (cache.py:395-428) and ``memory_usage_bytes``
+(cache.py:430-440).  ``append`` is an alias of ``update``.
+
+MI355X design:
+* the hot tier is a head-major device buffer ``[Hkv, cap, D]`` fp16;
+* warm codes stay in the reference layout (``CompressedTensorMLX``) and, for
+  the subspace format, are also packed into the tiled layout streamed by the
+  fused dequant-attention kernel (one pass over hot + warm + attended cold
+  chunks, no window written to HBM);
+* cold chunks go either to NPZ files (reference schema, storage.py:113-151)
+  or to pinned host memory; attended pinned chunks are copied into device
+  slots with hipMemcpyAsync on a side stream, ordered by events.
+
+Extensions: ``num_kv_heads`` (GQA: the cache stores Hkv heads and attention
+accepts Hq query heads), separate K/V quantizers (``update(..., (kq, vq))``),
+``tier_policy="recency"`` (hot = newest tokens, window order cold|warm|hot),
+explicit cold chunk sets (``attention_forward(..., cold_chunks=[...])``).
+"""
+
+from __future__ import annotations
+
+import logging
+from collections import OrderedDict
+from pathlib import Path
+from typing import Any, Dict, List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import kernels as K
+from .attention import _blockwise_exact_attention, _normalize_query_positions
+from .quantization import (
+    HybridQuantizerMLX,
+    _append_compressed_tensor,
+    _compress_tensor_sequence,
+    _decode_compressed_tensor,
+    _slice_compressed_tensor,
+)
+from .storage import (
+    AsyncHierarchicalRouterMLX,
+    CompressedTensorMLX,
+    RFSNConfig,
+    chunk_file_path,
+    compressed_tensor_from_loaded,
+    load_compressed_chunk,
+    save_compressed_chunk,
+)
+
+logger = logging.getLogger("RFSN_CACHE")
+
+QuantizerArg = Union[HybridQuantizerMLX, Tuple[HybridQuantizerMLX, HybridQuantizerMLX]]
+
+
+def _pair(q: QuantizerArg) -> Tuple[HybridQuantizerMLX, HybridQuantizerMLX]:
+    if isinstance(q, (tuple, list)):
+        if len(q) != 2:
+            raise ValueError("quantizer pair must be (key_quantizer, value_quantizer)")
+        return q[0], q[1]
+    return q, q
+
+
+class TiledCodes:
+    """Device codes of the subspace format in the fused kernel's tiled layout."""
+
+    def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0):
+        self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
+        self.cap = 0
+        self.len = 0
+        self.t: Dict[str, Optional[torch.Tensor]] = {}
+        self._alloc(cap)
+
+    def _new(self, shape, dtype):
+        if self.pinned:
+            return torch.zeros(shape, dtype=dtype, pin_memory=True)
+        return torch.zeros(shape, dtype=dtype, device=self.device)
+
+    def _alloc(self, cap: int) -> None:
+        cap = K.round_up(max(cap, 0), K.TILE)
+        if cap <= self.cap and self.t:
+            return
+        f, H = self.fmt, self.heads
+        new = {"pq": self._new((H, cap * f.pq_subspaces), torch.uint8),
+               "rvq": self._new((H, cap * f.rvq_subspaces), torch.uint8) if f.rvq_subspaces else None,
+               "sparse_idx": self._new((H, cap, f.sparse_k), torch.uint8) if f.sparse_k else None,
+               "sparse_val": self._new((H, cap, f.sparse_k), torch.float16) if f.sparse_k else None}
+        if self.t and self.cap:
+            for key, old in self.t.items():
+                if old is None:
+                    continue
+                if key in ("pq", "rvq"):
+                    new[key][:, : old.shape[1]] = old
+                else:
+                    new[key][:, : self.cap] = old
+        self.t, self.cap = new, cap
+
+    def append(self, pq: torch.Tensor, rvq: Optional[torch.Tensor], sidx: Optional[torch.Tensor],
+               sval: Optional[torch.Tensor]) -> None:
+        """Append plain codes [H, T, *] (device) at token ``len``."""
+        H, T, _ = pq.shape
+        need = self.len + T
+        if need > self.cap:
+            self._alloc(max(need, 2 * self.cap))
+        K.pack_codes(pq, self.t["pq"], self.len)
+        if self.fmt.rvq_subspaces:
+            K.pack_codes(rvq, self.t["rvq"], self.len)
+        if self.fmt.sparse_k:
+            self.t["sparse_idx"][:, self.len:need] = sidx
+            self.t["sparse_val"][:, self.len:need] = sval
+        self.len = need
+
+    def codes(self, tile_skip: int = 0) -> Dict[str, Optional[torch.Tensor]]:
+        """Per-array views starting at tile ``tile_skip`` (head stride unchanged)."""
+        f = self.fmt
+        o = tile_skip * K.TILE
+        out = {"pq": self.t["pq"][:, o * f.pq_subspaces:]}
+        out["rvq"] = self.t["rvq"][:, o * f.rvq_subspaces:] if f.rvq_subspaces else None
+        out["sparse_idx"] = self.t["sparse_idx"][:, o:] if f.sparse_k else None
+        out["sparse_val"] = self.t["sparse_val"][:, o:] if f.sparse_k else None
+        return out
+
+
+def _plain_head_major(store: CompressedTensorMLX):
+    """Reference-layout subspace codes [T, H, *] -> head-major [H, T, *]."""
+    pm = lambda t: None if t is None else t.permute(1, 0, 2).contiguous()
+    return pm(store.pq_codes), pm(store.rvq_codes), pm(store.sparse_idx), pm(store.sparse_val)
+
+
+class RFSNv10KVCacheMLX:
+    """Tiered KV cache with exact hot storage and compressed warm/cold storage."""
+
+    def __init__(self, config: RFSNConfig, layer_idx: int = 0, device=None, cold_slots: int = 32):
+        self.config = config
+        self.layer_idx = layer_idx
+        self.hot_capacity = config.hot_capacity
+        self.warm_capacity = config.warm_capacity
+        if device is None:
+            if not torch.cuda.is_available():
+                raise RuntimeError("the RFSN MI355X cache needs a ROCm GPU; none is visible")
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.device = torch.device(device)
+        self.H = config.kv_heads
+        self.D = config.head_dim
+        self._hot_k = torch.zeros((self.H, 0, self.D), dtype=torch.float16, device=self.device)
+        self._hot_v = torch.zeros_like(self._hot_k)
+
+        self.warm_keys = CompressedTensorMLX.empty(config, self.H, self.device)
+        self.warm_values = CompressedTensorMLX.empty(config, self.H, self.device)
+        self._warm_tiled: Optional[Tuple[TiledCodes, TiledCodes]] = None
+
+        self.cold_chunk_paths: List[Path] = []
+        self.cold_chunk_paths_by_id: Dict[int, Path] = {}
+        self.cold_chunk_metadata: List[dict] = []
+        self._cold_pinned: Dict[int, dict] = {}
+        self._cold_slots: "OrderedDict[int, dict]" = OrderedDict()
+        self._cold_slot_limit = cold_slots
+        self._side: Optional[K.SideStream] = None
+
+        self.num_hot = 0
+        self.num_warm = 0
+        self.num_cold = 0
+        self.total_tokens = 0
+        self.quantizer: Optional[QuantizerArg] = None
+        self._kq: Optional[HybridQuantizerMLX] = None
+        self._vq: Optional[HybridQuantizerMLX] = None
+        self.last_access_stats = self._empty_access_stats()
+
+    # ------------------------------------------------------------------ stats
+    def _empty_access_stats(self) -> Dict[str, int]:
+        """cache.py:59-76."""
+        return {
+            "window_start": 0, "window_end": 0, "window_tokens": 0, "context_window": -1, "query_tokens": 0,
+            "used_router": 0, "hot_tokens_materialized": 0, "warm_tokens_materialized": 0,
+            "cold_tokens_materialized": 0, "reconstructed_tokens": 0, "warm_chunk_decodes": 0,
+            "cold_chunk_decodes": 0, "cold_chunks_touched": 0, "cold_chunk_cache_hits": 0,
+            "cold_chunk_cache_misses": 0,
+        }
+
+    def get_last_access_stats(self) -> Dict[str, int]:
+        return dict(self.last_access_stats)
+
+    @property
+    def current_tier(self) -> str:
+        if self.total_tokens < self.hot_capacity:
+            return "hot"
+        if self.total_tokens < self.hot_capacity + self.warm_capacity:
+            return "warm"
+        return "cold"
+
+    @property
+    def hot_keys(self) -> torch.Tensor:
+        """[T_hot, H, D] view of the hot tier (oldest first)."""
+        return self._hot_k[:, : self.num_hot].permute(1, 0, 2)
+
+    @property
+    def hot_values(self) -> torch.Tensor:
+        return self._hot_v[:, : self.num_hot].permute(1, 0, 2)
+
+    # ------------------------------------------------------------------ helpers
+    @property
+    def _recency(self) -> bool:
+        return self.config.tier_policy == "recency"
+
+    @property
+    def _subspace(self) -> bool:
+        return self.config.ext_format
+
+    def _fmt(self) -> K.WarmFormat:
+        return self._kq.warm_format()
+
+    def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append [T, H, D] tokens to the hot tier."""
+        T = int(k.shape[0])
+        need = self.num_hot + T
+        if need > self._hot_k.shape[1]:
+            cap = max(need, min(self.hot_capacity, 2 * self._hot_k.shape[1]))
+            nk = torch.zeros((self.H, cap, self.D), dtype=torch.float16, device=self.device)
+            nv = torch.zeros_like(nk)
+            nk[:, : self.num_hot] = self._hot_k[:, : self.num_hot]
+            nv[:, : self.num_hot] = self._hot_v[:, : self.num_hot]
+            self._hot_k, self._hot_v = nk, nv
+        self._hot_k[:, self.num_hot:need] = k.permute(1, 0, 2).to(self.device, torch.float16)
+        self._hot_v[:, self.num_hot:need] = v.permute(1, 0, 2).to(self.device, torch.float16)
+        self.num_hot = need
+
+    def _hot_pop_oldest(self, n: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Remove and return the n oldest hot tokens as [n, H, D]."""
+        k = self._hot_k[:, :n].permute(1, 0, 2).clone()
+        v = self._hot_v[:, :n].permute(1, 0, 2).clone()
+        rest = self.num_hot - n
+        self._hot_k[:, :rest] = self._hot_k[:, n:self.num_hot].clone()
+        self._hot_v[:, :rest] = self._hot_v[:, n:self.num_hot].clone()
+        self.num_hot = rest
+        return k, v
+
+    def _warm_tiled_append(self, ck: CompressedTensorMLX, cv: CompressedTensorMLX) -> None:
+        """Mirror appended warm codes into the tiled layout of the fused kernel
+        (for the reference format only the PQ codes, used while no RVQ row is
+        active)."""
+        fmt = self._fmt()
+        if not fmt.fused_ok:
+            return
+        if self._warm_tiled is None:
+            self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
+        for tiled, store in zip(self._warm_tiled, (ck, cv)):
+            if self._subspace:
+                tiled.append(*_plain_head_major(store))
+            else:
+                tiled.append(store.pq_codes.permute(1, 0, 2).contiguous(), None, None, None)
+
+    # ------------------------------------------------------------------ update
+    def update(self, new_keys: torch.Tensor, new_values: torch.Tensor, quantizer: QuantizerArg,
+               disk_dir: Optional[Path] = None) -> None:
+        """cache.py:89-120 (arrival policy) / newest-in-hot (recency policy)."""
+        if tuple(new_keys.shape) != tuple(new_values.shape):
+            raise ValueError("new_keys and new_values must have identical shapes")
+        if new_keys.dim() != 3 or new_keys.shape[1] != self.H or new_keys.shape[2] != self.D:
+            raise ValueError(f"new_keys must be [T, {self.H}, {self.D}]")
+        self.quantizer = quantizer
+        self._kq, self._vq = _pair(quantizer)
+        keys = new_keys.to(self.device, torch.float16)
+        values = new_values.to(self.device, torch.float16)
+        num_tokens = int(keys.shape[0])
+        if self._recency:
+            self._update_recency(keys, values, disk_dir)
+        else:
+            offset = 0
+            hot_space = max(self.hot_capacity - self.num_hot, 0)
+            if hot_space > 0 and offset < num_tokens:
+                take = min(hot_space, num_tokens - offset)
+                self._hot_append(keys[offset:offset + take], values[offset:offset + take])
+                offset += take
+            warm_space = max(self.warm_capacity - self.num_warm, 0)
+            if warm_space > 0 and offset < num_tokens:
+                take = min(warm_space, num_tokens - offset)
+                self._add_to_warm(keys[offset:offset + take], values[offset:offset + take])
+                offset += take
+            if offset < num_tokens:
+                self._add_to_cold(keys[offset:], values[offset:], disk_dir)
+        self.total_tokens += num_tokens
+
+    append = update
+
+    def _update_recency(self, keys, values, disk_dir) -> None:
+        """Hot keeps the newest ``hot_capacity`` tokens; demoted tokens go to
+        warm; warm overflow moves the oldest warm tokens to cold."""
+        T = int(keys.shape[0])
+        # tokens that never stay hot go straight to warm/cold, in order
+        keep_new = min(T, self.hot_capacity)
+        direct = T - keep_new
+        overflow_hot = max(self.num_hot + keep_new - self.hot_capacity, 0)
+        demoted_k, demoted_v = [], []
+        if overflow_hot:
+            k_old, v_old = self._hot_pop_oldest(min(overflow_hot, self.num_hot))
+            demoted_k.append(k_old)
+            demoted_v.append(v_old)
+        if direct:
+            demoted_k.append(keys[:direct])
+            demoted_v.append(values[:direct])
+        if demoted_k:
+            dk = torch.cat(demoted_k, 0)
+            dv = torch.cat(demoted_v, 0)
+            n = int(dk.shape[0])
+            # oldest demoted tokens beyond the warm capacity go to cold first
+            warm_room = self.warm_capacity - self.num_warm
+            if n > warm_room:
+                # move old warm tokens out to make room, then cold-store what still does not fit
+                spill_warm = min(self.num_warm, n - warm_room)
+                if spill_warm:
+                    self._warm_to_cold(spill_warm, disk_dir)
+                warm_room = self.warm_capacity - self.num_warm
+                to_cold = max(n - warm_room, 0)
+                if to_cold:
+                    self._add_to_cold(dk[:to_cold], dv[:to_cold], disk_dir)
+                    dk, dv = dk[to_cold:], dv[to_cold:]
+            if dk.shape[0]:
+                self._add_to_warm(dk, dv)
+        self._hot_append(keys[direct:], values[direct:])
+
+    def _add_to_warm(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """cache.py:122-132."""
+        ck = _compress_tensor_sequence(keys, self._kq)
+        cv = _compress_tensor_sequence(values, self._vq)
+        self.warm_keys = _append_compressed_tensor(self.warm_keys, ck)
+        self.warm_values = _append_compressed_tensor(self.warm_values, cv)
+        self._warm_tiled_append(ck, cv)
+        self.num_warm += int(keys.shape[0])
+
+    def _warm_to_cold(self, n: int, disk_dir) -> None:
+        """Move the n oldest warm tokens (already encoded) to the cold tier."""
+        ck = _slice_compressed_tensor(self.warm_keys, 0, n)
+        cv = _slice_compressed_tensor(self.warm_values, 0, n)
+        rest_k = _slice_compressed_tensor(self.warm_keys, n, self.num_warm)
+        rest_v = _slice_compressed_tensor(self.warm_values, n, self.num_warm)
+        self._store_cold(ck, cv, disk_dir)
+        self.warm_keys, self.warm_values = rest_k, rest_v
+        self.num_warm -= n
+        if self._warm_tiled is not None:
+            fmt = self._fmt()
+            self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
+            if self.num_warm:
+                self._warm_tiled_append(rest_k, rest_v)
+
+    # ------------------------------------------------------------------ cold tier
+    def _cold_start_token(self) -> int:
+        if self._recency:
+            return self.num_cold
+        return self.num_hot + self.num_warm + self.num_cold
+
+    def _add_to_cold(self, keys, values, disk_dir) -> None:
+        """cache.py:134-191: encode per chunk and store."""
+        chunk = self.config.chunk_tokens
+        start_token = self._cold_start_token()
+        for offset in range(0, int(keys.shape[0]), chunk):
+            end = min(offset + chunk, int(keys.shape[0]))
+            # align pieces to chunk boundaries of the absolute position
+            ck = _compress_tensor_sequence(keys[offset:end], self._kq)
+            cv = _compress_tensor_sequence(values[offset:end], self._vq)
+            self._store_cold(ck, cv, disk_dir, start=start_token + offset)
+
+    def _store_cold(self, ck: CompressedTensorMLX, cv: CompressedTensorMLX, disk_dir, start: Optional[int] = None
+                    ) -> None:
+        """Store encoded tokens starting at absolute token ``start`` as cold chunks."""
+        chunk = self.config.chunk_tokens
+        s0 = self._cold_start_token() if start is None else start
+        n = ck.num_tokens
+        o = 0
+        while o < n:
+            cstart = s0 + o
+            cid = cstart // chunk
+            take = min(n - o, (cid + 1) * chunk - cstart) if self._recency else min(n - o, chunk)
+            k_part = _slice_compressed_tensor(ck, o, o + take)
+            v_part = _slice_compressed_tensor(cv, o, o + take)
+            self._store_cold_piece(cid, cstart, k_part, v_part, disk_dir)
+            self.num_cold += take
+            o += take
+
+    def _store_cold_piece(self, cid, cstart, ck, cv, disk_dir) -> None:
+        n = ck.num_tokens
+        meta = next((m for m in self.cold_chunk_metadata if m["chunk_id"] == cid), None)
+        if self.config.cold_medium == "npz":
+            disk_root = Path(self.config.disk_cache_dir) if disk_dir is None else Path(disk_dir)
+            disk_root.mkdir(parents=True, exist_ok=True)
+            path = chunk_file_path(disk_root, self.layer_idx, cid)
+            if meta is not None and cid in self.cold_chunk_paths_by_id:
+                if cstart != meta["end_token"]:
+                    raise ValueError(
+                        "Cold chunk append must be contiguous with existing metadata: "
+                        f"chunk_id={cid} start={cstart} expected={meta['end_token']}")
+                loaded = load_compressed_chunk(self.cold_chunk_paths_by_id[cid], self.device)
+                ck = _append_compressed_tensor(compressed_tensor_from_loaded(loaded, "key"), ck)
+                cv = _append_compressed_tensor(compressed_tensor_from_loaded(loaded, "value"), cv)
+                save_compressed_chunk(path, ck, cv)
+                meta["end_token"] += n
+                meta["num_tokens"] += n
+                meta["path"] = str(path)
+            else:
+                save_compressed_chunk(path, ck, cv)
+                self.cold_chunk_paths.append(path)
+                self.cold_chunk_paths_by_id[cid] = path
+                self.cold_chunk_metadata.append({"chunk_id": cid, "start_token": cstart, "end_token": cstart + n,
+                                                 "num_tokens": n, "path": str(path)})
+            return
+        # pinned host memory
+        if meta is not None:
+            if cstart != meta["end_token"]:
+                raise ValueError(
+                    "Cold chunk append must be contiguous with existing metadata: "
+                    f"chunk_id={cid} start={cstart} expected={meta['end_token']}")
+            old = self._cold_pinned[cid]
+            ck = _append_compressed_tensor(_to_device_store(old["key"], self.device), ck)
+            cv = _append_compressed_tensor(_to_device_store(old["value"], self.device), cv)
+            meta["end_token"] += n
+            meta["num_tokens"] += n
+            self._cold_slots.pop(cid, None)
+        else:
+            meta = {"chunk_id": cid, "start_token": cstart, "end_token": cstart + n, "num_tokens": n,
+                    "path": f"pinned:{cid}"}
+            self.cold_chunk_metadata.append(meta)
+            self.cold_chunk_metadata.sort(key=lambda m: m["start_token"])
+        self._cold_pinned[cid] = self._pin_chunk(ck, cv)
+
+    def _pin_chunk(self, ck: CompressedTensorMLX, cv: CompressedTensorMLX) -> dict:
+        """Keep a chunk in pinned host memory: the reference layout (for decode
+        and NPZ export) and, for the subspace format, the tiled layout that
+        prefetch copies into device slots."""
+        entry = {"key": _to_host_store(ck), "value": _to_host_store(cv)}
+        if self._subspace:
+            fmt = self._fmt()
+            chunk = K.round_up(self.config.chunk_tokens, K.TILE)
+            for name, store in (("key", ck), ("value", cv)):
+                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk)
+                dev_t.append(*_plain_head_major(store))
+                host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk)
+                for key, t in dev_t.t.items():
+                    if t is not None:
+                        host_t.t[key].copy_(t)
+                host_t.len = dev_t.len
+                entry[f"{name}_tiled"] = host_t
+        return entry
+
+    def has_cold_chunk(self, chunk_id: int) -> bool:
+        if self.config.cold_medium == "pinned":
+            return chunk_id in self._cold_pinned
+        return chunk_id in self.cold_chunk_paths_by_id
+
+    def load_cold_chunk(self, chunk_id: int) -> Dict[str, torch.Tensor]:
+        """cache.py:193-194 (NPZ) / the pinned chunk's arrays (pinned)."""
+        if self.config.cold_medium == "pinned":
+            e = self._cold_pinned[chunk_id]
+            return {"key": e["key"], "value": e["value"]}
+        return load_compressed_chunk(self.cold_chunk_paths_by_id[chunk_id], self.device)
+
+    def _chunk_store(self, loaded, prefix: str) -> CompressedTensorMLX:
+        if self.config.cold_medium == "pinned":
+            return _to_device_store(loaded[prefix], self.device)
+        return compressed_tensor_from_loaded(loaded, prefix)
+
+    def prefetch_cold_chunks(self, chunk_ids: Sequence[int]) -> Dict[int, dict]:
+        """Make pinned chunks resident in device slots; copies are issued with
+        hipMemcpyAsync on a side stream and the current stream waits on its event."""
+        if self.config.cold_medium != "pinned":
+            raise RuntimeError("prefetch_cold_chunks needs cold_medium='pinned'")
+        if self._side is None:
+            self._side = K.SideStream()
+        copies = []
+        out: Dict[int, dict] = {}
+        self._side.wait_for_current(self.device)
+        for cid in chunk_ids:
+            if cid in self._cold_slots:
+                self._cold_slots.move_to_end(cid)
+                out[cid] = self._cold_slots[cid]
+                continue
+            e = self._cold_pinned[cid]
+            slot = None
+            if len(self._cold_slots) >= self._cold_slot_limit:
+                _, slot = self._cold_slots.popitem(last=False)
+            dev = {}
+            for name in ("key", "value"):
+                host_t: TiledCodes = e[f"{name}_tiled"]
+                if slot is not None and slot[name].cap == host_t.cap:
+                    dt = slot[name]
+                else:
+                    dt = TiledCodes(host_t.fmt, self.H, self.device, cap=host_t.cap)
+                dt.len = host_t.len
+                for key, t in host_t.t.items():
+                    if t is not None:
+                        copies.append((dt.t[key].data_ptr(), t.data_ptr(), t.numel() * t.element_size()))
+                dev[name] = dt
+            self._cold_slots[cid] = dev
+            out[cid] = dev
+        if copies:
+            self._side.prefetch(copies)
+        self._side.make_current_wait(self.device)
+        return out
+
+    # ------------------------------------------------------------------ windows
+    def _max_query_position(self, query_positions, current_position) -> int:
+        if query_positions is not None:
+            if isinstance(query_positions, torch.Tensor):
+                return int(query_positions.max().item())
+            return int(np.max(np.asarray(query_positions, dtype=np.int64)))
+        if current_position is not None:
+            return current_position
+        return max(self.total_tokens - 1, 0)
+
+    def _window_bounds(self, query_positions, context_window, current_position):
+        """cache.py:210-241."""
+        def to_query_array(value):
+            if value is None:
+                return None
+            if isinstance(value, torch.Tensor):
+                return value.to(device=self.device, dtype=torch.int32)
+            return torch.tensor(np.asarray(value), dtype=torch.int32, device=self.device)
+
+        if self.total_tokens == 0:
+            return 0, 0, to_query_array(query_positions)
+        max_query = self._max_query_position(query_positions, current_position)
+        window_end = min(max_query + 1, self.total_tokens)
+        window_start = 0 if context_window is None else max(0, window_end - context_window)
+        if query_positions is None:
+            return window_start, window_end, None
+        adjusted = to_query_array(query_positions) - window_start
+        adjusted = torch.clamp(adjusted, min=-1).to(torch.int32)
+        return window_start, window_end, adjusted
+
+    @staticmethod
+    def _overlap(start, end, span_start, span_end):
+        a, b = max(start, span_start), min(end, span_end)
+        return None if a >= b else (a, b)
+
+    def _tier_spans(self) -> Dict[str, Tuple[int, int]]:
+        """Absolute position span of the hot and warm tiers."""
+        if self._recency:
+            return {"warm": (self.num_cold, self.num_cold + self.num_warm),
+                    "hot": (self.num_cold + self.num_warm, self.total_tokens)}
+        return {"hot": (0, self.num_hot), "warm": (self.num_hot, self.num_hot + self.num_warm)}
+
+    def _warm_chunks(self, ov) -> int:
+        chunk = max(1, self.config.block_size_seq)
+        return (ov[1] - ov[0] + chunk - 1) // chunk
+
+    def _plan(self, start, end, stats, router, current_position, context_window, cold_chunks):
+        """Which tier spans the window touches, in position order, with the
+        reference's access counters (cache.py:250-342)."""
+        spans = self._tier_spans()
+        parts = []
+        hov = self._overlap(start, end, *spans["hot"])
+        wov = self._overlap(start, end, *spans["warm"])
+        if hov is not None:
+            stats["hot_tokens_materialized"] += hov[1] - hov[0]
+        if wov is not None and self.quantizer is not None:
+            n = wov[1] - wov[0]
+            stats["warm_tokens_materialized"] += n
+            stats["reconstructed_tokens"] += n
+            stats["warm_chunk_decodes"] += self._warm_chunks(wov)
+        cold = []
+        if self.quantizer is not None and self.cold_chunk_metadata:
+            loaded_by_router = {}
+            if cold_chunks is not None:
+                wanted = set(int(c) for c in cold_chunks)
+                metas = [m for m in self.cold_chunk_metadata if m["chunk_id"] in wanted]
+            else:
+                if router is not None and current_position is not None and context_window is not None:
+                    ct = self.config.chunk_tokens
+                    top_k = max(1, (context_window + ct - 1) // ct)
+                    router.prefetch_sync(current_position=current_position, context_window=context_window,
+                                         top_k=top_k)
+                metas = [m for m in self.cold_chunk_metadata
+                         if self._overlap(start, end, m["start_token"], m["end_token"]) is not None]
+            for m in metas:
+                cid = m["chunk_id"]
+                got = router.get_chunk(cid) if router is not None else None
+                if got is None:
+                    if router is not None:
+                        stats["cold_chunk_cache_misses"] += 1
+                else:
+                    stats["cold_chunk_cache_hits"] += 1
+                if cold_chunks is not None:
+                    ov = (m["start_token"], m["end_token"])
+                else:
+                    ov = self._overlap(start, end, m["start_token"], m["end_token"])
+                n = ov[1] - ov[0]
+                stats["cold_tokens_materialized"] += n
+                stats["reconstructed_tokens"] += n
+                stats["cold_chunk_decodes"] += 1
+                stats["cold_chunks_touched"] += 1
+                cold.append((m, ov, got))
+        if self._recency:
+            order = [("cold", c) for c in cold] + [("warm", wov), ("hot", hov)]
+        else:
+            order = [("hot", hov), ("warm", wov)] + [("cold", c) for c in cold]
+        return [(kind, x) for kind, x in order if x is not None]
+
+    # ------------------------------------------------------------------ materialize
+    def materialize_window(self, query_positions=None, context_window: Optional[int] = None,
+                           router: Optional[AsyncHierarchicalRouterMLX] = None,
+                           current_position: Optional[int] = None, cold_chunks: Optional[Sequence[int]] = None):
+        """(keys [W, H, D], values [W, H, D], adjusted positions) (cache.py:344-393)."""
+        if self.quantizer is None:
+            raise RuntimeError("Cache cannot materialize values before update() provides a quantizer")
+        start, end, adjusted = self._window_bounds(query_positions, context_window, current_position)
+        stats = self._empty_access_stats()
+        stats["window_start"], stats["window_end"] = start, end
+        stats["window_tokens"] = max(0, end - start)
+        stats["context_window"] = -1 if context_window is None else context_window
+        stats["used_router"] = int(router is not None)
+        plan = self._plan(start, end, stats, router, current_position, context_window, cold_chunks)
+        spans = self._tier_spans()
+        ks, vs = [], []
+        for kind, x in plan:
+            if kind == "hot":
+                a, b = x[0] - spans["hot"][0], x[1] - spans["hot"][0]
+                ks.append(self._hot_k[:, a:b].permute(1, 0, 2))
+                vs.append(self._hot_v[:, a:b].permute(1, 0, 2))
+            elif kind == "warm":
+                a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
+                ks.append(_decode_compressed_tensor(_slice_compressed_tensor(self.warm_keys, a, b), self._kq))
+                vs.append(_decode_compressed_tensor(_slice_compressed_tensor(self.warm_values, a, b), self._vq))
+            else:
+                meta, ov, got = x
+                if got is None or self.config.cold_medium == "pinned":
+                    loaded = self.load_cold_chunk(meta["chunk_id"])
+                else:
+                    loaded = got
+                a, b = ov[0] - meta["start_token"], ov[1] - meta["start_token"]
+                kst = _slice_compressed_tensor(self._chunk_store(loaded, "key"), a, b)
+                vst = _slice_compressed_tensor(self._chunk_store(loaded, "value"), a, b)
+                ks.append(_decode_compressed_tensor(kst, self._kq))
+                vs.append(_decode_compressed_tensor(vst, self._vq))
+        self.last_access_stats = dict(stats)
+        if not ks:
+            empty = torch.zeros((0, self.H, self.D), dtype=torch.float16, device=self.device)
+            return empty, empty, adjusted
+        keys = ks[0] if len(ks) == 1 else torch.cat(ks, 0)
+        values = vs[0] if len(vs) == 1 else torch.cat(vs, 0)
+        return keys.contiguous(), values.contiguous(), adjusted
+
+    # ------------------------------------------------------------------ attention
+    def _fused_ok(self) -> bool:
+        """The fused kernel serves the long-context warm format, and the
+        reference format while no warm vector carries an RVQ correction (the
+        reference's pq_only mode, threshold = inf)."""
+        if self._kq is None or not self._fmt().fused_ok or self._kq.warm_format() != self._vq.warm_format():
+            return False
+        if self.num_warm and self._warm_tiled is None:
+            return False
+        if self._subspace:
+            return self.num_cold == 0 or self.config.cold_medium == "pinned"
+        no_rvq = int(self.warm_keys.rvq_codes.shape[0]) == 0 and int(self.warm_values.rvq_codes.shape[0]) == 0
+        return no_rvq and self.num_cold == 0
+
+    def attention_forward(self, q: torch.Tensor, pq_codebook=None, rvq_codebook=None, causal: bool = True,
+                          query_positions=None, router: Optional[AsyncHierarchicalRouterMLX] = None,
+                          current_position: Optional[int] = None, context_window: Optional[int] = None,
+                          cold_chunks: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """cache.py:395-428.  Subspace-format caches run the fused kernel."""
+        del pq_codebook, rvq_codebook
+        if self.quantizer is None:
+            raise RuntimeError("Cache cannot run attention before update() provides a quantizer")
+        if q.shape[-1] != self.D or q.dim() != 3 or q.shape[1] % self.H:
+            raise ValueError("q must be [B, Hq, D] with Hq a multiple of the cache's KV heads")
+        if not self._fused_ok():
+            keys, values, adjusted = self.materialize_window(query_positions, context_window, router,
+                                                             current_position, cold_chunks)
+            self.last_access_stats["query_tokens"] = int(q.shape[0])
+            if int(keys.shape[0]) == 0:
+                return torch.zeros_like(q)
+            return _blockwise_exact_attention(q=q, keys=keys, values=values, scale=self.D ** -0.5,
+                                              block_size=self.config.block_size_seq, causal=causal,
+                                              query_positions=adjusted)
+        return self._fused_forward(q, causal, query_positions, router, current_position, context_window, cold_chunks)
+
+    def _fused_forward(self, q, causal, query_positions, router, current_position, context_window, cold_chunks):
+        start, end, adjusted = self._window_bounds(query_positions, context_window, current_position)
+        stats = self._empty_access_stats()
+        stats["window_start"], stats["window_end"] = start, end
+        stats["window_tokens"] = max(0, end - start)
+        stats["context_window"] = -1 if context_window is None else context_window
+        stats["used_router"] = int(router is not None)
+        plan = self._plan(start, end, stats, router, current_position, context_window, cold_chunks)
+        stats["query_tokens"] = int(q.shape[0])
+        self.last_access_stats = dict(stats)
+        B, Hq, D = q.shape
+        if not plan:
+            return torch.zeros_like(q)
+        qh = q.to(self.device, torch.float16)
+        spans = self._tier_spans()
+        fmt = self._fmt()
+        table = K.SegmentTable(B)
+        hot_len, hot_pos0, hot_off = 0, 0, 0
+        max_tokens = 0
+        cold_ids = [x[0]["chunk_id"] for kind, x in plan if kind == "cold"]
+        if len(cold_ids) > self._cold_slot_limit:
+            raise ValueError(f"window touches {len(cold_ids)} cold chunks; the device slot pool holds "
+                             f"{self._cold_slot_limit} (raise cold_slots)")
+        slots = self.prefetch_cold_chunks(cold_ids) if cold_ids else {}
+        for kind, x in plan:
+            if kind == "hot":
+                hot_off = x[0] - spans["hot"][0]
+                hot_len = x[1] - x[0]
+                hot_pos0 = x[0] - start
+                max_tokens += hot_len
+            elif kind == "warm":
+                a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
+                skip = a // K.TILE
+                kt, vt = self._warm_tiled
+                for bi in range(B):
+                    table.add(bi, kt.codes(skip), vt.codes(skip), kt.cap, b - skip * K.TILE,
+                              spans["warm"][0] + skip * K.TILE - start)
+                max_tokens += b - skip * K.TILE
+            else:
+                meta, ov, _ = x
+                dev = slots[meta["chunk_id"]]
+                a, b = ov[0] - meta["start_token"], ov[1] - meta["start_token"]
+                skip = a // K.TILE
+                for bi in range(B):
+                    table.add(bi, dev["key"].codes(skip), dev["value"].codes(skip), dev["key"].cap,
+                              b - skip * K.TILE, meta["start_token"] + skip * K.TILE - start)
+                max_tokens += b - skip * K.TILE
+        qpos = adjusted
+        if causal:
+            qpos = _normalize_query_positions(adjusted, B, Hq, stats["window_tokens"] - 1, self.device)
+        hk = self._hot_k[:, hot_off:] if hot_len else None
+        hv = self._hot_v[:, hot_off:] if hot_len else None
+        return K.fused_attention(
+            qh, fmt, kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos if causal else None,
+            hot_k=hk, hot_v=hv, hot_len=hot_len, hot_pos0=hot_pos0, hot_seq_stride=0, segments=table,
+            k_pq_cb=self._kq.pq.codebooks, v_pq_cb=self._vq.pq.codebooks,
+            k_rvq_cb=self._kq.rvq.codebooks if fmt.rvq_subspaces else None,
+            v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
+            cb_batch_stride=False, max_tokens=max(max_tokens, 1), hot_cap=int(self._hot_k.shape[1]),
+        ).to(q.dtype)
+
+    def memory_usage_bytes(self) -> Dict[str, int]:
+        """cache.py:430-440.  Subspace format: warm_rvq_bytes counts the RVQ
+        and sparse bytes actually stored (every vector carries them)."""
+        hot_bytes = self.num_hot * self.H * self.D * 2 * 2
+        warm_pq_bytes = self.num_warm * self.H * self.config.num_subspaces * 2
+        if self._subspace:
+            k = self.config.sparse_topk
+            warm_rvq_bytes = self.num_warm * self.H * (self.config.rvq_subspaces + 3 * k) * 2
+        else:
+            rows = int(self.warm_keys.rvq_codes.shape[0] + self.warm_values.rvq_codes.shape[0])
+            warm_rvq_bytes = rows * self.config.num_rvq_layers * 2
+        return {"hot_bytes": hot_bytes, "warm_pq_bytes": warm_pq_bytes, "warm_rvq_bytes": warm_rvq_bytes,
+                "cold_chunks": len(self.cold_chunk_metadata), "cold_tokens": self.num_cold}
+
+
+def _to_host_store(s: CompressedTensorMLX) -> CompressedTensorMLX:
+    h = lambda t: None if t is None else t.detach().to("cpu")
+    return CompressedTensorMLX(h(s.pq_codes), h(s.rvq_codes), h(s.rvq_mask), h(s.rvq_offsets), s.num_heads,
+                               h(s.sparse_idx), h(s.sparse_val))
+
+
+def _to_device_store(s: CompressedTensorMLX, device) -> CompressedTensorMLX:
+    d = lambda t: None if t is None else t.to(device)
+    return CompressedTensorMLX(d(s.pq_codes), d(s.rvq_codes), d(s.rvq_mask), d(s.rvq_offsets), s.num_heads,
+                               d(s.sparse_idx), d(s.sparse_val))

@@ -1,0 +1,175 @@
+// Standalone decode kernels (materialize_window compatibility path) and the
+// k-means centroid update, for gfx950.
+//
+// Warm format (quantization.py:146-157 and the subspace-RVQ / sparse
+// extension): base = C_pq[code]; with an RVQ stage K = fp16(base + C_rvq[code_r]);
+// then K[idx] = fp16(K[idx] + val) for each sparse coordinate.
+// Reference format (quantization.py:254-275, 310-319): corr = fp16(sum_l
+// fl32(C_l[code_l])) in stage order from +0.0 on active rows, 0 elsewhere;
+// out = fp16(base + corr).
+#include "rfsn_common.h"
+
+namespace rfsn {
+namespace {
+
+// One thread per (vector, group of 4 coordinates).
+__global__ void __launch_bounds__(256)
+decode_ext_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C, const uint16_t* __restrict__ pq_cb,
+                  const uint8_t* __restrict__ rvq, int Mr, int Cr, const uint16_t* __restrict__ rvq_cb,
+                  const uint8_t* __restrict__ sidx, const uint16_t* __restrict__ sval, int k, int add_zero,
+                  uint16_t* __restrict__ out, int64_t ldo) {
+  const int groups = D / 4;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * groups) return;
+  const int64_t v = gid / groups;
+  const int i0 = (int)(gid - v * groups) * 4;
+  const int d = D / M;
+  const int dr = Mr > 0 ? D / Mr : 1;
+  uint16_t r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = i0 + e;
+    const int m = i / d;
+    uint16_t val = pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)];
+    if (Mr > 0) {
+      const int mr = i / dr;
+      val = hadd_bits(val, rvq_cb[((size_t)mr * Cr + min((int)rvq[v * Mr + mr], Cr - 1)) * dr + (i - mr * dr)]);
+    } else if (add_zero) {
+      val = hadd_bits(val, 0);
+    }
+    for (int j = 0; j < k; ++j) {
+      if ((int)sidx[v * k + j] == i) val = hadd_bits(val, sval[v * k + j]);
+    }
+    r[e] = val;
+  }
+  uint16_t* o = out + v * ldo + i0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = r[e];
+}
+
+__global__ void __launch_bounds__(256)
+decode_ref_base_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C,
+                       const uint16_t* __restrict__ pq_cb, uint16_t* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * D) return;
+  const int64_t v = gid / D;
+  const int i = (int)(gid - v * D);
+  const int d = D / M;
+  const int m = i / d;
+  out[gid] = hadd_bits(pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)], 0);
+}
+
+__global__ void __launch_bounds__(256)
+decode_ref_corr_kernel(int64_t n, int64_t active, int D, const uint8_t* __restrict__ pq, int M, int C,
+                       const uint16_t* __restrict__ pq_cb, const uint16_t* __restrict__ codes,
+                       const int32_t* __restrict__ offsets, int L, int Cr, const uint16_t* __restrict__ rvq_cb,
+                       uint16_t* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= active * D) return;
+  const int64_t a = gid / D;
+  const int i = (int)(gid - a * D);
+  const int64_t v = offsets[a];
+  if (v < 0 || v >= n) return;  // offsets outside the decoded rows are ignored
+  float total = 0.0f;
+  for (int l = 0; l < L; ++l) {
+    const int c = min((int)codes[a * L + l], Cr - 1);
+    total = __fadd_rn(total, h2f(rvq_cb[((size_t)l * Cr + c) * D + i]));
+  }
+  const uint16_t corr = f2h(total);
+  const int d = D / M;
+  const int m = i / d;
+  out[v * D + i] = hadd_bits(pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)], corr);
+}
+
+// k-means: per-(subspace, centroid) sums in float64 via atomics, then mean.
+__global__ void kmeans_accum_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx,
+                                    const uint8_t* __restrict__ codes, int M, int C, double* __restrict__ sums,
+                                    unsigned int* __restrict__ counts) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * M) return;
+  const int64_t v = gid / M;
+  const int m = (int)(gid - v * M);
+  const int d = D / M;
+  const int c = codes[v * M + m];
+  double* s = sums + ((size_t)m * C + c) * d;
+  for (int u = 0; u < d; ++u) atomicAdd(s + u, (double)h2f(x[v * ldx + m * d + u]));
+  atomicAdd(counts + (size_t)m * C + c, 1u);
+}
+
+__global__ void kmeans_finish_kernel(int M, int C, int d, const double* __restrict__ sums,
+                                     const unsigned int* __restrict__ counts, uint16_t* __restrict__ cb) {
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= M * C * d) return;
+  const int mc = gid / d;
+  const unsigned int cnt = counts[mc];
+  if (cnt == 0) return;
+  cb[gid] = f2h((float)(sums[gid] / (double)cnt));
+}
+
+__global__ void zero_kernel(uint32_t* __restrict__ p, int64_t words) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+}  // namespace
+}  // namespace rfsn
+
+using namespace rfsn;
+
+extern "C" int rfsn_decode(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
+                           const void* rvq_cb, void* out, int64_t ldo, int32_t add_zero, void* stream) {
+  RFSN_REQUIRE(f && codes && codes->pq && pq_cb && out, "decode: null pointer");
+  RFSN_REQUIRE(f->head_dim % 4 == 0 && f->head_dim % f->pq_subspaces == 0, "decode: head_dim must be a multiple of 4");
+  RFSN_REQUIRE(f->rvq_subspaces == 0 || (codes->rvq && rvq_cb && f->head_dim % f->rvq_subspaces == 0),
+               "decode: RVQ stage needs codes and codebooks");
+  RFSN_REQUIRE(f->sparse_k == 0 || (codes->sparse_idx && codes->sparse_val), "decode: sparse stage needs codes");
+  RFSN_REQUIRE(ldo >= f->head_dim, "decode: bad leading dimension");
+  if (n == 0) return RFSN_OK;
+  const int64_t total = n * (f->head_dim / 4);
+  hipLaunchKernelGGL(decode_ext_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     f->head_dim, codes->pq, f->pq_subspaces, f->pq_centroids, (const uint16_t*)pq_cb, codes->rvq,
+                     f->rvq_subspaces, f->rvq_centroids, (const uint16_t*)rvq_cb, codes->sparse_idx,
+                     (const uint16_t*)codes->sparse_val, f->sparse_k, add_zero, (uint16_t*)out, ldo);
+  return check_launch("decode");
+}
+
+extern "C" int rfsn_decode_ref(const uint8_t* pq, int64_t n, int32_t D, int32_t M, int32_t C, const void* pq_cb,
+                               const uint16_t* rvq_codes, const int32_t* offsets, int64_t active, int32_t L,
+                               int32_t Cr, const void* rvq_cb, void* out, void* stream) {
+  RFSN_REQUIRE(pq && pq_cb && out && D > 0 && M > 0 && D % M == 0, "decode_ref: bad arguments");
+  RFSN_REQUIRE(active == 0 || (rvq_codes && offsets && rvq_cb && L >= 1), "decode_ref: RVQ arguments missing");
+  hipStream_t s = (hipStream_t)stream;
+  if (n > 0) {
+    hipLaunchKernelGGL(decode_ref_base_kernel, dim3((unsigned)ceil_div(n * D, 256)), dim3(256), 0, s, n, D, pq, M, C,
+                       (const uint16_t*)pq_cb, (uint16_t*)out);
+  }
+  if (active > 0) {
+    hipLaunchKernelGGL(decode_ref_corr_kernel, dim3((unsigned)ceil_div(active * D, 256)), dim3(256), 0, s, n, active, D,
+                       pq, M, C, (const uint16_t*)pq_cb, rvq_codes, offsets, L, Cr, (const uint16_t*)rvq_cb,
+                       (uint16_t*)out);
+  }
+  return check_launch("decode_ref");
+}
+
+extern "C" size_t rfsn_kmeans_workspace_bytes(int32_t M, int32_t C, int32_t d) {
+  return (size_t)M * C * d * sizeof(double) + (size_t)M * C * sizeof(unsigned int) + 256;
+}
+
+extern "C" int rfsn_kmeans_update(const void* x, int64_t n, int32_t D, int64_t ldx, const uint8_t* codes, int32_t M,
+                                  int32_t C, void* cb, void* ws, size_t ws_bytes, void* stream) {
+  RFSN_REQUIRE(x && codes && cb && ws && M > 0 && D % M == 0 && C >= 1 && C <= 256, "kmeans_update: bad arguments");
+  const int d = D / M;
+  RFSN_REQUIRE(ws_bytes >= rfsn_kmeans_workspace_bytes(M, C, d), "kmeans_update: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  double* sums = (double*)ws;
+  unsigned int* counts = (unsigned int*)(sums + (size_t)M * C * d);
+  const int64_t words = ((int64_t)M * C * d * 2 + (int64_t)M * C);
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, s, (uint32_t*)ws, words);
+  if (n > 0) {
+    hipLaunchKernelGGL(kmeans_accum_kernel, dim3((unsigned)ceil_div(n * M, 256)), dim3(256), 0, s,
+                       (const uint16_t*)x, n, D, ldx, codes, M, C, sums, counts);
+  }
+  hipLaunchKernelGGL(kmeans_finish_kernel, dim3((unsigned)ceil_div((int64_t)M * C * d, 256)), dim3(256), 0, s, M, C, d,
+                     sums, counts, (uint16_t*)cb);
+  return check_launch("kmeans_update");
+}

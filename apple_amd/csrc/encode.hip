@@ -1,0 +1,433 @@
+// Nearest-centroid encode kernels (PQ, subspace RVQ, reference-mode gated
+// full-dimension RVQ) and the top-k sparse residual, for gfx950.
+//
+// Distances follow the canonical chain of quantization.py:92-96:
+//   L = fl32(S x*x), X_j = fl32(S x*c_j), R_j = fl32(S c_j*c_j),
+//   dist_j = fl32(fl32(L - 2 X_j) + R_j),
+// where S is a float64 sum in coordinate order from +0.0.  Products of fp16
+// (or fp32) values with fp16 values are exact in float64, so v_fma_f64 in
+// coordinate order reproduces S exactly.  Ties go to the lowest index
+// (mx.argmin, quantization.py:139; strict-< chunk merge, quantization.py:244).
+#include "rfsn_common.h"
+
+namespace rfsn {
+
+namespace {
+
+constexpr int kEncodeThreads = 256;
+
+// One block: 256 vectors x one subspace m of one group.  The subspace
+// codebook is staged in LDS as float64 (exact), together with R_j.
+template <int DSUB>
+__global__ void __launch_bounds__(kEncodeThreads)
+pq_encode_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, int64_t x_gstride,
+                 const uint16_t* __restrict__ cb, int M, int C, int dsub_rt, int64_t cb_gstride,
+                 uint8_t* __restrict__ codes, int64_t ldc, int64_t codes_gstride,
+                 uint16_t* __restrict__ resid, int64_t ldr, int64_t resid_gstride) {
+  extern __shared__ double smem[];
+  const int d = DSUB > 0 ? DSUB : dsub_rt;
+  const int m = blockIdx.y;
+  const int g = blockIdx.z;
+  double* c64 = smem;                                  // [C][d]
+  float* R = reinterpret_cast<float*>(smem + (size_t)C * d);  // [C]
+  const uint16_t* cbm = cb + (size_t)g * cb_gstride + (size_t)m * C * d;
+  for (int i = threadIdx.x; i < C * d; i += blockDim.x) c64[i] = (double)h2f(cbm[i]);
+  __syncthreads();
+  for (int j = threadIdx.x; j < C; j += blockDim.x) {
+    double acc = 0.0;
+    for (int u = 0; u < d; ++u) acc = __builtin_fma(c64[j * d + u], c64[j * d + u], acc);
+    R[j] = (float)acc;
+  }
+  __syncthreads();
+
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= n) return;
+  const uint16_t* xv = x + (size_t)g * x_gstride + v * ldx + (size_t)m * d;
+  double xs[DSUB > 0 ? DSUB : 32];
+  double lacc = 0.0;
+#pragma unroll
+  for (int u = 0; u < (DSUB > 0 ? DSUB : 32); ++u) {
+    if (DSUB == 0 && u >= d) break;
+    xs[u] = (double)h2f(xv[u]);
+    lacc = __builtin_fma(xs[u], xs[u], lacc);
+  }
+  const float L = (float)lacc;
+  float best = __builtin_inff();
+  int bi = 0;
+  for (int j = 0; j < C; ++j) {
+    const double* cj = c64 + j * d;
+    double acc = 0.0;
+#pragma unroll
+    for (int u = 0; u < (DSUB > 0 ? DSUB : 32); ++u) {
+      if (DSUB == 0 && u >= d) break;
+      acc = __builtin_fma(xs[u], cj[u], acc);
+    }
+    const float X = (float)acc;
+    const float t = __fsub_rn(L, 2.0f * X);
+    const float dist = __fadd_rn(t, R[j]);
+    if (dist < best) {
+      best = dist;
+      bi = j;
+    }
+  }
+  codes[(size_t)g * codes_gstride + v * ldc + m] = (uint8_t)bi;
+  if (resid != nullptr) {
+    uint16_t* rv = resid + (size_t)g * resid_gstride + v * ldr + (size_t)m * d;
+    for (int u = 0; u < d; ++u) {
+      const float diff = __fsub_rn((float)xs[u], (float)c64[bi * d + u]);
+      rv[u] = f2h(diff);
+    }
+  }
+}
+
+// Reference-mode RVQ gate: fl32(sqrt(fl32(S r^2))) > thr.
+__global__ void rvq_gate_kernel(const uint16_t* __restrict__ r, int64_t n, int D, int64_t ld, float thr,
+                                uint8_t* __restrict__ mask) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint16_t* row = r + i * ld;
+  double acc = 0.0;
+  for (int u = 0; u < D; ++u) {
+    const double v = (double)h2f(row[u]);
+    acc = __builtin_fma(v, v, acc);
+  }
+  const float s = (float)acc;
+  // correctly rounded float sqrt: the f64 square root of an f32 input rounded
+  // to f32 is the correctly rounded f32 square root (53 >= 2*24+2).
+  const float norm = (float)__builtin_sqrt((double)s);
+  mask[i] = norm > thr ? 1 : 0;
+}
+
+// Stream compaction of a 0/1 mask into ascending offsets (single pass per
+// 1024-element tile: tile counts, then tile prefix, then scatter).
+constexpr int kScanTile = 1024;
+
+__global__ void mask_count_kernel(const uint8_t* __restrict__ mask, int64_t n, int32_t* __restrict__ tile_counts) {
+  __shared__ int32_t wsum[kScanTile / 64];
+  const int64_t i = (int64_t)blockIdx.x * kScanTile + threadIdx.x;
+  int v = (i < n && mask[i]) ? 1 : 0;
+  int s = v;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+    for (int w = 0; w < kScanTile / 64; ++w) t += wsum[w];
+    tile_counts[blockIdx.x] = t;
+  }
+}
+
+__global__ void tile_prefix_kernel(int32_t* __restrict__ tile_counts, int64_t tiles, int32_t* __restrict__ count) {
+  // single thread: tiles is small (n / 1024)
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t acc = 0;
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int32_t c = tile_counts[t];
+    tile_counts[t] = acc;
+    acc += c;
+  }
+  count[0] = acc;
+}
+
+__global__ void mask_scatter_kernel(const uint8_t* __restrict__ mask, int64_t n, const int32_t* __restrict__ tile_base,
+                                    int32_t* __restrict__ offsets) {
+  __shared__ int32_t wpre[kScanTile / 64];
+  const int64_t i = (int64_t)blockIdx.x * kScanTile + threadIdx.x;
+  const int v = (i < n && mask[i]) ? 1 : 0;
+  const int lane = threadIdx.x & 63;
+  const uint64_t ballot = __ballot(v);
+  const int before = __popcll(ballot & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+  if (lane == 0) wpre[threadIdx.x >> 6] = __popcll(ballot);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int w = 0; w < kScanTile / 64; ++w) {
+      const int c = wpre[w];
+      wpre[w] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  if (v) offsets[tile_base[blockIdx.x] + wpre[threadIdx.x >> 6] + before] = (int32_t)i;
+}
+
+// Reference-mode full-dimension RVQ: one wave per active row; lanes split the
+// centroids, argmin merged across the wave with lowest index on ties.
+__global__ void __launch_bounds__(256)
+rvq_full_kernel(const uint16_t* __restrict__ resid, int64_t ld, int D, const int32_t* __restrict__ offsets,
+                int64_t active, const uint16_t* __restrict__ cb, int L, int C, uint16_t* __restrict__ codes) {
+  extern __shared__ double run_all[];  // [waves][D] running residual as f64 (values are fp32)
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t a = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+  double* run = run_all + (size_t)wave * D;
+  const bool live = a < active;
+  if (live) {
+    const uint16_t* row = resid + (int64_t)offsets[a] * ld;
+    for (int u = lane; u < D; u += 64) run[u] = (double)h2f(row[u]);
+  }
+  __syncthreads();
+  for (int layer = 0; layer < L; ++layer) {
+    float best = __builtin_inff();
+    int bi = 0x7fffffff;
+    if (live) {
+      double lacc = 0.0;
+      for (int u = 0; u < D; ++u) lacc = __builtin_fma(run[u], run[u], lacc);
+      const float Lf = (float)lacc;
+      const uint16_t* cbl = cb + (size_t)layer * C * D;
+      for (int j = lane; j < C; j += 64) {
+        const uint16_t* cj = cbl + (size_t)j * D;
+        double xacc = 0.0, racc = 0.0;
+        for (int u = 0; u < D; ++u) {
+          const double c = (double)h2f(cj[u]);
+          xacc = __builtin_fma(run[u], c, xacc);
+          racc = __builtin_fma(c, c, racc);
+        }
+        const float t = __fsub_rn(Lf, 2.0f * (float)xacc);
+        const float dist = __fadd_rn(t, (float)racc);
+        if (dist < best) {  // ascending j per lane: first min kept
+          best = dist;
+          bi = j;
+        }
+      }
+      // wave argmin, ties -> lowest index
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ob < best || (ob == best && oi < bi)) {
+          best = ob;
+          bi = oi;
+        }
+      }
+      if (bi == 0x7fffffff) bi = 0;  // all-NaN row: mx.argmin would return 0
+      if (lane == 0) codes[a * L + layer] = (uint16_t)bi;
+    }
+    __syncthreads();
+    if (live) {
+      const uint16_t* cj = cb + (size_t)layer * C * D + (size_t)bi * D;
+      for (int u = lane; u < D; u += 64) run[u] = (double)__fsub_rn((float)run[u], h2f(cj[u]));
+    }
+    __syncthreads();
+  }
+}
+
+// Top-k |r2| of r2 = fl32(x - fp16(base + rvq)) per vector; descending |r2|,
+// ties to the lower coordinate.  One thread per vector; codebooks are read
+// through the cache (they are a few KB and shared by all vectors).
+template <int K>
+__global__ void __launch_bounds__(256)
+sparse_topk_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx,
+                   const uint8_t* __restrict__ pq, int M, int C, const uint16_t* __restrict__ pq_cb,
+                   const uint8_t* __restrict__ rvq, int Mr, int Cr, const uint16_t* __restrict__ rvq_cb,
+                   uint8_t* __restrict__ idx_out, uint16_t* __restrict__ val_out) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= n) return;
+  const int d = D / M;
+  const int dr = Mr > 0 ? D / Mr : 1;
+  float bmag[K];
+  float bval[K];
+  int bidx[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    bmag[j] = -1.0f;
+    bval[j] = 0.0f;
+    bidx[j] = 0;
+  }
+  const uint16_t* xv = x + v * ldx;
+  for (int i = 0; i < D; ++i) {
+    const int m = i / d;
+    uint16_t rec = pq_cb[((size_t)m * C + pq[v * M + m]) * d + (i - m * d)];
+    if (Mr > 0) {
+      const int mr = i / dr;
+      rec = hadd_bits(rec, rvq_cb[((size_t)mr * Cr + rvq[v * Mr + mr]) * dr + (i - mr * dr)]);
+    }
+    const float r2 = __fsub_rn(h2f(xv[i]), h2f(rec));
+    const float mag = fabsf(r2);
+    if (mag > bmag[K - 1]) {
+      // insert keeping earlier (lower-index) entries ahead of equal magnitudes
+      int pos = K - 1;
+#pragma unroll
+      for (int j = K - 1; j > 0; --j) {
+        if (j <= pos && mag > bmag[j - 1]) {
+          bmag[j] = bmag[j - 1];
+          bval[j] = bval[j - 1];
+          bidx[j] = bidx[j - 1];
+          pos = j - 1;
+        }
+      }
+      bmag[pos] = mag;
+      bval[pos] = r2;
+      bidx[pos] = i;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    idx_out[v * K + j] = (uint8_t)bidx[j];
+    val_out[v * K + j] = f2h(bval[j]);
+  }
+}
+
+template <int DSUB>
+int launch_pq(const void* x, int64_t n, int64_t ldx, int64_t xg, const void* cb, int M, int C, int d, int64_t cbg,
+              uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg, int groups,
+              hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(n, kEncodeThreads), (unsigned)M, (unsigned)groups);
+  const size_t lds = (size_t)C * d * sizeof(double) + (size_t)C * sizeof(float);
+  if (lds > 64 * 1024) {
+    hipFuncSetAttribute((const void*)pq_encode_kernel<DSUB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  }
+  hipLaunchKernelGGL(pq_encode_kernel<DSUB>, grid, dim3(kEncodeThreads), lds, s,
+                     (const uint16_t*)x, n, ldx, xg, (const uint16_t*)cb, M, C, d, cbg, codes, ldc, cg,
+                     (uint16_t*)resid, ldr, rg);
+  return check_launch("pq_encode");
+}
+
+}  // namespace
+
+int pq_encode_impl(const void* x, int64_t n, int D, int64_t ldx, int64_t xg, const void* cb, int M, int C,
+                   int64_t cbg, uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg,
+                   int groups, hipStream_t s) {
+  RFSN_REQUIRE(x && cb && codes, "pq_encode: null pointer");
+  RFSN_REQUIRE(M > 0 && D > 0 && D % M == 0, "pq_encode: head_dim must equal num_subspaces * subspace_dim");
+  RFSN_REQUIRE(C > 0 && C <= 256, "pq_encode: codebook size must be in [1, 256] (uint8 codes)");
+  RFSN_REQUIRE(n >= 0 && groups >= 1, "pq_encode: bad n / groups");
+  RFSN_REQUIRE(ldx >= D && ldc >= M && (resid == nullptr || ldr >= D), "pq_encode: bad leading dimension");
+  const int d = D / M;
+  RFSN_REQUIRE(d <= 32, "pq_encode: subspace_dim > 32 unsupported");
+  if (n == 0) return RFSN_OK;
+  switch (d) {
+    case 4: return launch_pq<4>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    case 8: return launch_pq<8>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    case 16: return launch_pq<16>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    default: return launch_pq<0>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+  }
+}
+
+int sparse_topk_impl(const void* x, int64_t n, int D, int64_t ldx, const uint8_t* pq, int M, int C,
+                     const void* pq_cb, const uint8_t* rvq, int Mr, int Cr, const void* rvq_cb, int k,
+                     uint8_t* idx, void* val, hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(n, 256));
+#define RFSN_TOPK(KK)                                                                                  \
+  hipLaunchKernelGGL(sparse_topk_kernel<KK>, grid, dim3(256), 0, s, (const uint16_t*)x, n, D, ldx, pq, M, C, \
+                     (const uint16_t*)pq_cb, rvq, Mr, Cr, (const uint16_t*)rvq_cb, idx, (uint16_t*)val)
+  switch (k) {
+    case 1: RFSN_TOPK(1); break;
+    case 2: RFSN_TOPK(2); break;
+    case 3: RFSN_TOPK(3); break;
+    case 4: RFSN_TOPK(4); break;
+    case 5: RFSN_TOPK(5); break;
+    case 6: RFSN_TOPK(6); break;
+    case 7: RFSN_TOPK(7); break;
+    case 8: RFSN_TOPK(8); break;
+    default: return fail(RFSN_ERR_UNSUPPORTED, "sparse_k must be in [0, 8]");
+  }
+#undef RFSN_TOPK
+  return check_launch("sparse_topk");
+}
+
+}  // namespace rfsn
+
+using namespace rfsn;
+
+extern "C" int rfsn_pq_encode(const void* x, int64_t n, int32_t D, int64_t ldx, int64_t x_gstride,
+                              const void* cb, int32_t M, int32_t C, int64_t cb_gstride, uint8_t* codes, int64_t ldc,
+                              int64_t codes_gstride, void* resid, int64_t ldr, int64_t resid_gstride, int32_t groups,
+                              void* stream) {
+  return pq_encode_impl(x, n, D, ldx, x_gstride, cb, M, C, cb_gstride, codes, ldc, codes_gstride, resid, ldr,
+                        resid_gstride, groups, (hipStream_t)stream);
+}
+
+static int validate_format(const rfsn_format* f) {
+  RFSN_REQUIRE(f != nullptr, "null format");
+  RFSN_REQUIRE(f->head_dim > 0 && f->pq_subspaces > 0 && f->head_dim % f->pq_subspaces == 0,
+               "head_dim must equal num_subspaces * subspace_dim");
+  RFSN_REQUIRE(f->pq_centroids >= 1 && f->pq_centroids <= 256, "PQ codebook size must be in [1, 256]");
+  RFSN_REQUIRE(f->rvq_subspaces >= 0, "rvq_subspaces must be >= 0");
+  if (f->rvq_subspaces > 0) {
+    RFSN_REQUIRE(f->head_dim % f->rvq_subspaces == 0, "head_dim must be a multiple of rvq_subspaces");
+    RFSN_REQUIRE(f->rvq_centroids >= 1 && f->rvq_centroids <= 256, "RVQ codebook size must be in [1, 256]");
+  }
+  RFSN_REQUIRE(f->sparse_k >= 0 && f->sparse_k <= 8 && f->sparse_k <= f->head_dim, "sparse_k must be in [0, 8]");
+  RFSN_REQUIRE(f->head_dim <= 256, "head_dim must be <= 256 (uint8 sparse indices)");
+  return RFSN_OK;
+}
+
+extern "C" size_t rfsn_warm_encode_workspace_bytes(const rfsn_format* f, int64_t n) {
+  if (f == nullptr || n <= 0) return 0;
+  return (size_t)n * f->head_dim * 2 + 256;
+}
+
+extern "C" int rfsn_warm_encode(const rfsn_format* f, const void* x, int64_t n, int64_t ldx, const void* pq_cb,
+                                const void* rvq_cb, rfsn_codes out, void* ws, size_t ws_bytes, void* stream) {
+  int st = validate_format(f);
+  if (st) return st;
+  RFSN_REQUIRE(x && pq_cb && out.pq, "warm_encode: null pointer");
+  RFSN_REQUIRE(ldx >= f->head_dim, "warm_encode: bad leading dimension");
+  if (n == 0) return RFSN_OK;
+  const size_t need = rfsn_warm_encode_workspace_bytes(f, n);
+  RFSN_REQUIRE(ws != nullptr && ws_bytes >= need, "warm_encode: workspace too small");
+  const int D = f->head_dim;
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* r1 = (uint16_t*)ws;  // [n][D] PQ residual
+  st = pq_encode_impl(x, n, D, ldx, 0, pq_cb, f->pq_subspaces, f->pq_centroids, 0, out.pq, f->pq_subspaces, 0, r1,
+                      D, 0, 1, s);
+  if (st) return st;
+  if (f->rvq_subspaces > 0) {
+    RFSN_REQUIRE(rvq_cb && out.rvq, "warm_encode: RVQ stage needs codebooks and an output");
+    st = pq_encode_impl(r1, n, D, D, 0, rvq_cb, f->rvq_subspaces, f->rvq_centroids, 0, out.rvq, f->rvq_subspaces, 0,
+                        nullptr, D, 0, 1, s);
+    if (st) return st;
+  }
+  if (f->sparse_k > 0) {
+    RFSN_REQUIRE(out.sparse_idx && out.sparse_val, "warm_encode: sparse stage needs outputs");
+    st = sparse_topk_impl(x, n, D, ldx, out.pq, f->pq_subspaces, f->pq_centroids, pq_cb, out.rvq, f->rvq_subspaces,
+                          f->rvq_centroids, rvq_cb, f->sparse_k, out.sparse_idx, out.sparse_val, s);
+    if (st) return st;
+  }
+  return RFSN_OK;
+}
+
+extern "C" int rfsn_rvq_gate(const void* r, int64_t n, int32_t D, int64_t ld, float thr, uint8_t* mask, void* stream) {
+  RFSN_REQUIRE(r && mask && D > 0 && ld >= D, "rvq_gate: bad arguments");
+  if (n == 0) return RFSN_OK;
+  hipLaunchKernelGGL(rvq_gate_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)r, n, D, ld, thr, mask);
+  return check_launch("rvq_gate");
+}
+
+extern "C" size_t rfsn_mask_compact_workspace_bytes(int64_t n) {
+  return (size_t)(ceil_div(n > 0 ? n : 1, kScanTile)) * sizeof(int32_t) + 256;
+}
+
+extern "C" int rfsn_mask_compact(const uint8_t* mask, int64_t n, int32_t* offsets, int32_t* count, void* ws,
+                                 size_t ws_bytes, void* stream) {
+  RFSN_REQUIRE(mask && offsets && count && ws, "mask_compact: null pointer");
+  RFSN_REQUIRE(ws_bytes >= rfsn_mask_compact_workspace_bytes(n), "mask_compact: workspace too small");
+  RFSN_REQUIRE(n >= 0 && n < (int64_t)0x7fffffff, "mask_compact: n out of range");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t tiles = ceil_div(n > 0 ? n : 1, kScanTile);
+  int32_t* tile = (int32_t*)ws;
+  if (n == 0) {
+    hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, tile, (int64_t)0, count);
+    return check_launch("mask_compact");
+  }
+  hipLaunchKernelGGL(mask_count_kernel, dim3((unsigned)tiles), dim3(kScanTile), 0, s, mask, n, tile);
+  hipLaunchKernelGGL(tile_prefix_kernel, dim3(1), dim3(64), 0, s, tile, tiles, count);
+  hipLaunchKernelGGL(mask_scatter_kernel, dim3((unsigned)tiles), dim3(kScanTile), 0, s, mask, n, tile, offsets);
+  return check_launch("mask_compact");
+}
+
+extern "C" int rfsn_rvq_encode_full(const void* resid, int64_t ld, int32_t D, const int32_t* offsets, int64_t active,
+                                    const void* cb, int32_t L, int32_t C, uint16_t* codes, void* stream) {
+  RFSN_REQUIRE(resid && offsets && cb && codes, "rvq_encode_full: null pointer");
+  RFSN_REQUIRE(D > 0 && D <= 1024 && ld >= D && L >= 1 && C >= 1 && C <= 65535, "rvq_encode_full: bad shape");
+  if (active == 0) return RFSN_OK;
+  const int waves = 4;
+  const size_t lds = (size_t)waves * D * sizeof(double);
+  hipLaunchKernelGGL(rvq_full_kernel, dim3((unsigned)ceil_div(active, waves)), dim3(64 * waves), lds,
+                     (hipStream_t)stream, (const uint16_t*)resid, ld, D, offsets, active, (const uint16_t*)cb, L, C,
+                     codes);
+  return check_launch("rvq_encode_full");
+}

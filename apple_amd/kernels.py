@@ -1,0 +1,374 @@
+"""Torch-facing wrappers over the C ABI of ``librfsn_hip.so``.
+
+Every function takes and returns device tensors, launches on the current
+torch stream, takes its scratch space from torch's caching allocator (the
+library itself never allocates device memory) and raises on failure.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib as L
+
+TILE = 32  # tokens per tile of the tiled code layout
+
+
+def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
+    L.require_device(t, what)
+    return t
+
+
+def _contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return L.stream_handle(t.device)
+
+
+# --------------------------------------------------------------------------
+# warm format description
+# --------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class WarmFormat:
+    head_dim: int
+    pq_subspaces: int
+    pq_centroids: int
+    rvq_subspaces: int = 0
+    rvq_centroids: int = 0
+    sparse_k: int = 0
+
+    def c(self) -> L.Format:
+        return L.Format(self.head_dim, self.pq_subspaces, self.pq_centroids, self.rvq_subspaces,
+                        self.rvq_centroids, self.sparse_k)
+
+    @property
+    def bytes_per_vector(self) -> int:
+        return self.pq_subspaces + self.rvq_subspaces + 3 * self.sparse_k
+
+    @property
+    def fused_ok(self) -> bool:
+        return (self.head_dim == 64 and self.pq_subspaces in (8, 16)
+                and self.rvq_subspaces in (0, self.pq_subspaces) and self.sparse_k in (0, 4))
+
+
+def round_up(n: int, m: int) -> int:
+    return (n + m - 1) // m * m
+
+
+# --------------------------------------------------------------------------
+# encode
+# --------------------------------------------------------------------------
+
+def pq_encode(x: torch.Tensor, codebooks: torch.Tensor, want_residual: bool = True
+              ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Canonical nearest-centroid PQ encode (quantization.py:124-144).
+
+    x [N, D] fp16 (row stride >= D), codebooks [M, C, d] fp16.
+    """
+    _dev(x, "pq_encode")
+    if x.dtype != torch.float16 or codebooks.dtype != torch.float16:
+        raise ValueError("pq_encode expects fp16 vectors and codebooks")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("pq_encode expects [N, D] rows with unit column stride")
+    n, D = x.shape
+    M, Cn, d = codebooks.shape
+    if D != M * d:
+        raise ValueError(f"Expected vectors with dim {M * d}, got {D}")
+    cb = _contig(codebooks)
+    codes = torch.empty((n, M), dtype=torch.uint8, device=x.device)
+    resid = torch.empty((n, D), dtype=torch.float16, device=x.device) if want_residual else None
+    L.call("rfsn_pq_encode", x.data_ptr(), n, D, x.stride(0), 0, cb.data_ptr(), M, Cn, 0,
+           codes.data_ptr(), M, 0, L.ptr(resid), D, 0, 1, _stream(x))
+    return codes, resid
+
+
+def pq_encode_grouped(x: torch.Tensor, codebooks: torch.Tensor) -> torch.Tensor:
+    """Encode ``groups`` independent sets: x [G, N, D], codebooks [G, M, C, d] -> [G, N, M]."""
+    _dev(x, "pq_encode_grouped")
+    x = _contig(x)
+    cb = _contig(codebooks)
+    G, n, D = x.shape
+    _, M, Cn, d = cb.shape
+    codes = torch.empty((G, n, M), dtype=torch.uint8, device=x.device)
+    L.call("rfsn_pq_encode", x.data_ptr(), n, D, D, n * D, cb.data_ptr(), M, Cn, M * Cn * d,
+           codes.data_ptr(), M, n * M, None, D, 0, G, _stream(x))
+    return codes
+
+
+def warm_encode(x: torch.Tensor, fmt: WarmFormat, pq_cb: torch.Tensor,
+                rvq_cb: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
+    """PQ + optional subspace RVQ + optional top-k sparse residual of x [N, D]."""
+    _dev(x, "warm_encode")
+    if x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.float16:
+        raise ValueError("warm_encode expects fp16 [N, D] rows")
+    n = x.shape[0]
+    dev = x.device
+    out = {"pq": torch.empty((n, fmt.pq_subspaces), dtype=torch.uint8, device=dev)}
+    if fmt.rvq_subspaces:
+        out["rvq"] = torch.empty((n, fmt.rvq_subspaces), dtype=torch.uint8, device=dev)
+    if fmt.sparse_k:
+        out["sparse_idx"] = torch.empty((n, fmt.sparse_k), dtype=torch.uint8, device=dev)
+        out["sparse_val"] = torch.empty((n, fmt.sparse_k), dtype=torch.float16, device=dev)
+    f = fmt.c()
+    ws_bytes = L.load().rfsn_warm_encode_workspace_bytes(C.byref(f), n)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    codes = L.Codes(out["pq"].data_ptr(), L.ptr(out.get("rvq")), L.ptr(out.get("sparse_idx")),
+                    L.ptr(out.get("sparse_val")))
+    L.call("rfsn_warm_encode", C.byref(f), x.data_ptr(), n, x.stride(0), _contig(pq_cb).data_ptr(),
+           L.ptr(None if rvq_cb is None else _contig(rvq_cb)), codes, ws.data_ptr(), ws_bytes, _stream(x))
+    return out
+
+
+def rvq_encode_full(resid: torch.Tensor, codebooks: torch.Tensor, threshold: float
+                    ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gated full-dimension RVQ (quantization.py:206-252) -> (codes u16 [A, L], mask [N], offsets [A])."""
+    _dev(resid, "rvq_encode_full")
+    resid = _contig(resid)
+    n, D = resid.shape
+    Ls, Cn, Dc = codebooks.shape
+    if D != Dc:
+        raise ValueError(f"Expected residual dim {Dc}, got {D}")
+    dev = resid.device
+    s = _stream(resid)
+    mask8 = torch.empty(n, dtype=torch.uint8, device=dev)
+    L.call("rfsn_rvq_gate", resid.data_ptr(), n, D, D, float(threshold), mask8.data_ptr(), s)
+    offsets_all = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    wsb = L.load().rfsn_mask_compact_workspace_bytes(n)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    L.call("rfsn_mask_compact", mask8.data_ptr(), n, offsets_all.data_ptr(), count.data_ptr(), ws.data_ptr(), wsb, s)
+    a = int(count.item())  # host sync, as the reference's np.asarray(mask) (quantization.py:217)
+    offsets = offsets_all[:a].clone()
+    codes = torch.empty((a, Ls), dtype=torch.uint16, device=dev)
+    if a:
+        L.call("rfsn_rvq_encode_full", resid.data_ptr(), D, D, offsets.data_ptr(), a, _contig(codebooks).data_ptr(),
+               Ls, Cn, codes.data_ptr(), s)
+    return codes, mask8.bool(), offsets
+
+
+# --------------------------------------------------------------------------
+# decode
+# --------------------------------------------------------------------------
+
+def decode(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional[torch.Tensor] = None,
+           rvq_cb: Optional[torch.Tensor] = None, sparse_idx: Optional[torch.Tensor] = None,
+           sparse_val: Optional[torch.Tensor] = None, add_zero: bool = False) -> torch.Tensor:
+    """Warm-format decode of pq [N, M] (+ rvq [N, M_r], sparse [N, k]) -> fp16 [N, D]."""
+    _dev(pq, "decode")
+    pq = _contig(pq)
+    n = pq.shape[0]
+    out = torch.empty((n, fmt.head_dim), dtype=torch.float16, device=pq.device)
+    if n == 0:
+        return out
+    rvq = None if rvq is None else _contig(rvq)
+    sparse_idx = None if sparse_idx is None else _contig(sparse_idx)
+    sparse_val = None if sparse_val is None else _contig(sparse_val)
+    codes = L.Codes(pq.data_ptr(), L.ptr(rvq), L.ptr(sparse_idx), L.ptr(sparse_val))
+    f = fmt.c()
+    L.call("rfsn_decode", C.byref(f), C.byref(codes), n, _contig(pq_cb).data_ptr(),
+           L.ptr(None if rvq_cb is None else _contig(rvq_cb)), out.data_ptr(), fmt.head_dim, int(add_zero),
+           _stream(pq))
+    return out
+
+
+def decode_ref(pq: torch.Tensor, pq_cb: torch.Tensor, rvq_codes: torch.Tensor, offsets: torch.Tensor,
+               rvq_cb: torch.Tensor) -> torch.Tensor:
+    """Reference-format hybrid decode (quantization.py:310-319) -> fp16 [N, D]."""
+    _dev(pq, "decode_ref")
+    pq = _contig(pq)
+    n, M = pq.shape
+    Mc, Cn, d = pq_cb.shape
+    D = M * d
+    Ls, Cr, _ = rvq_cb.shape
+    out = torch.empty((n, D), dtype=torch.float16, device=pq.device)
+    a = int(rvq_codes.shape[0])
+    L.call("rfsn_decode_ref", pq.data_ptr(), n, D, M, Cn, _contig(pq_cb).data_ptr(),
+           _contig(rvq_codes).data_ptr() if a else None, _contig(offsets).data_ptr() if a else None, a, Ls, Cr,
+           _contig(rvq_cb).data_ptr(), out.data_ptr(), _stream(pq))
+    return out
+
+
+# --------------------------------------------------------------------------
+# attention
+# --------------------------------------------------------------------------
+
+def blockwise_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, scale: float,
+                        causal: bool, qpos: Optional[torch.Tensor]) -> torch.Tensor:
+    """Exact attention of q [B, Hq, D] over keys/values [T, Hkv, D] (strided rows)."""
+    _dev(q, "blockwise_attention")
+    q = _contig(q)
+    B, Hq, D = q.shape
+    T, Hkv, Dk = keys.shape
+    if Dk != D or values.shape != keys.shape:
+        raise ValueError("keys/values must be [T, H, D] with the query's head_dim")
+    aligned = all(t.data_ptr() % 16 == 0 for t in (keys, values)) and keys.stride(0) % 8 == 0 \
+        and keys.stride(1) % 8 == 0
+    if keys.stride() != values.stride() or keys.stride(2) != 1 or not aligned:
+        keys, values = keys.contiguous(), values.contiguous()
+    out = torch.empty_like(q)
+    qp = None if qpos is None else _contig(qpos.to(device=q.device, dtype=torch.int32))
+    lib = L.load()
+    splits_max = 1024
+    wsb = lib.rfsn_attention_workspace_bytes(B, Hq, D, splits_max)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    L.call("rfsn_blockwise_attention", q.data_ptr(), B, Hq, D, keys.data_ptr() if T else None,
+           values.data_ptr() if T else None, T, Hkv, keys.stride(0), keys.stride(1), float(scale), int(causal),
+           L.ptr(qp), out.data_ptr(), ws.data_ptr(), wsb, _stream(q))
+    return out
+
+
+def pack_codes(src: torch.Tensor, dst: torch.Tensor, t_base: int) -> None:
+    """Plain codes src [H, T, M] into the tiled layout dst [H, cap*M] at tokens t_base.."""
+    _dev(src, "pack_codes")
+    H, T, M = src.shape
+    src = _contig(src)
+    L.call("rfsn_pack_codes", src.data_ptr(), T * M, T, M, H, dst.data_ptr(), dst.stride(0), t_base, _stream(src))
+
+
+class SegmentTable:
+    """Host builder of the device ``rfsn_segment`` table of the fused kernel."""
+
+    def __init__(self, batch: int):
+        self.rows: List[List[L.Segment]] = [[] for _ in range(batch)]
+        self.keep: List[torch.Tensor] = []
+
+    def add(self, b: int, k: Dict[str, Optional[torch.Tensor]], v: Dict[str, Optional[torch.Tensor]],
+            head_stride: int, length: int, pos0: int) -> None:
+        def codes(c):
+            for t in c.values():
+                if t is not None:
+                    self.keep.append(t)
+            return L.Codes(L.ptr(c.get("pq")), L.ptr(c.get("rvq")), L.ptr(c.get("sparse_idx")),
+                           L.ptr(c.get("sparse_val")))
+        self.rows[b].append(L.Segment(codes(k), codes(v), head_stride, length, pos0))
+
+    def to_device(self, device) -> Tuple[torch.Tensor, torch.Tensor, int]:
+        maxs = max(1, max(len(r) for r in self.rows))
+        size = C.sizeof(L.Segment)
+        host = (L.Segment * (len(self.rows) * maxs))()
+        for b, r in enumerate(self.rows):
+            for s, seg in enumerate(r):
+                host[b * maxs + s] = seg
+        raw = torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8).clone()
+        table = raw.to(device, non_blocking=False)
+        nseg = torch.tensor([len(r) for r in self.rows], dtype=torch.int32).to(device)
+        assert table.numel() == size * len(self.rows) * maxs
+        return table, nseg, maxs
+
+
+def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: float, causal: bool,
+                    qpos: Optional[torch.Tensor], hot_k: Optional[torch.Tensor], hot_v: Optional[torch.Tensor],
+                    hot_len: int, hot_pos0: int, hot_seq_stride: int, segments: SegmentTable,
+                    k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor, k_rvq_cb: Optional[torch.Tensor],
+                    v_rvq_cb: Optional[torch.Tensor], cb_batch_stride: bool, max_tokens: int,
+                    splits: int = 0, table: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
+                    workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                    hot_cap: Optional[int] = None) -> torch.Tensor:
+    """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
+
+    hot_k/hot_v: [.., Hkv, hot_cap, D] fp16 (sequence stride ``hot_seq_stride``
+    elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
+    else [M, C, d] shared.
+    """
+    _dev(q, "fused_attention")
+    q = _contig(q)
+    B, Hq, D = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if table is None:
+        table = segments.to_device(q.device)
+    seg_t, nseg_t, maxs = table
+    qp = None if qpos is None else _contig(qpos.to(device=q.device, dtype=torch.int32))
+    pq_stride = k_pq_cb[0].numel() if cb_batch_stride else 0
+    rvq_stride = (k_rvq_cb[0].numel() if (cb_batch_stride and k_rvq_cb is not None) else 0)
+    if hot_cap is None:
+        hot_cap = hot_k.shape[-2] if hot_k is not None else 0
+    p = L.FusedParams()
+    p.fmt = fmt.c()
+    p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
+    p.q, p.out = q.data_ptr(), out.data_ptr()
+    p.scale, p.causal, p.qpos = float(scale), int(causal), L.ptr(qp)
+    p.hot_k, p.hot_v = L.ptr(hot_k), L.ptr(hot_v)
+    p.hot_cap, p.hot_seq_stride, p.hot_len, p.hot_pos0 = hot_cap, hot_seq_stride, hot_len, hot_pos0
+    p.segments, p.num_segments, p.max_segments = seg_t.data_ptr(), nseg_t.data_ptr(), maxs
+    p.k_pq_cb, p.v_pq_cb = _contig(k_pq_cb).data_ptr(), _contig(v_pq_cb).data_ptr()
+    p.k_rvq_cb = L.ptr(None if k_rvq_cb is None else _contig(k_rvq_cb))
+    p.v_rvq_cb = L.ptr(None if v_rvq_cb is None else _contig(v_rvq_cb))
+    p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
+    p.max_tokens, p.splits = max_tokens, splits
+    lib = L.load()
+    wsb = lib.rfsn_fused_workspace_bytes(C.byref(p))
+    if workspace is None or workspace.numel() < wsb:
+        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
+    p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    L.call("rfsn_fused_decode_attention", C.byref(p), _stream(q))
+    return out
+
+
+# --------------------------------------------------------------------------
+# k-means (rfsn_v10_mlx_ane_complete.py:197-207)
+# --------------------------------------------------------------------------
+
+def kmeans_update(x: torch.Tensor, codes: torch.Tensor, codebooks: torch.Tensor) -> None:
+    """In-place Lloyd update of codebooks [M, C, d] from x [N, D] and codes [N, M]."""
+    _dev(x, "kmeans_update")
+    x = _contig(x)
+    n, D = x.shape
+    M, Cn, d = codebooks.shape
+    if not codebooks.is_contiguous():
+        raise ValueError("kmeans_update needs contiguous codebooks")
+    wsb = L.load().rfsn_kmeans_workspace_bytes(M, Cn, d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=x.device)
+    L.call("rfsn_kmeans_update", x.data_ptr(), n, D, D, _contig(codes).data_ptr(), M, Cn, codebooks.data_ptr(),
+           ws.data_ptr(), wsb, _stream(x))
+
+
+# --------------------------------------------------------------------------
+# cold tier host API
+# --------------------------------------------------------------------------
+
+class SideStream:
+    """A default-priority non-blocking HIP stream plus an event, for prefetch."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        L.call("rfsn_stream_create", C.byref(h))
+        self.stream = h.value
+        e = C.c_void_p()
+        L.call("rfsn_event_create", C.byref(e))
+        self.event = e.value
+        e2 = C.c_void_p()
+        L.call("rfsn_event_create", C.byref(e2))
+        self.main_event = e2.value
+
+    def wait_for_current(self, device=None) -> None:
+        """Order the side stream after all work already queued on the current stream."""
+        L.call("rfsn_event_record", self.main_event, L.stream_handle(device))
+        L.call("rfsn_stream_wait_event", self.stream, self.main_event)
+
+    def prefetch(self, copies: Sequence[Tuple[int, int, int]]) -> None:
+        arr = (L.Copy * max(1, len(copies)))()
+        for i, (dst, src, nbytes) in enumerate(copies):
+            arr[i] = L.Copy(dst, src, nbytes)
+        L.call("rfsn_prefetch_h2d", arr, len(copies), self.stream)
+        L.call("rfsn_event_record", self.event, self.stream)
+
+    def make_current_wait(self, device=None) -> None:
+        L.call("rfsn_stream_wait_event", L.stream_handle(device), self.event)
+
+    def close(self) -> None:
+        for name in ("event", "main_event"):
+            ev = getattr(self, name)
+            if ev:
+                L.call("rfsn_event_destroy", ev)
+                setattr(self, name, None)
+        if self.stream:
+            L.call("rfsn_stream_destroy", self.stream)
+            self.stream = None

@@ -1,0 +1,238 @@
+/*
+ * rfsn_abi.h -- C ABI of the MI355X (gfx950) warm-tier quantized-KV decode
+ * library (librfsn_hip.so).
+ *
+ * Conventions
+ *  - Every entry point returns int: RFSN_OK (0) or a negative RFSN_ERR_*;
+ *    rfsn_last_error() returns the message of the last failure on the
+ *    calling thread.  No C++ exception crosses this boundary.
+ *  - Every pointer is caller-owned.  Pointers named *_dev are device
+ *    (HBM) pointers; nothing here allocates device memory: scratch space is
+ *    passed in as a workspace sized by the matching *_workspace_bytes().
+ *  - Every kernel is asynchronous on the caller's hipStream_t (passed as
+ *    void*; NULL = the legacy default stream).  No global mutable state.
+ *  - fp16 tensors are passed as void* and hold IEEE binary16 bit patterns.
+ *  - Shapes use the reference's names: N vectors, D = head_dim,
+ *    M PQ subspaces of d = D/M dims with C centroids, M_r RVQ subspaces of
+ *    d_r = D/M_r dims with C_r centroids, k sparse residual coordinates.
+ *
+ * Reference interfaces replaced (files of dawsonblock/apple):
+ *  see the comment above each entry point.
+ */
+#ifndef RFSN_ABI_H
+#define RFSN_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RFSN_ABI_VERSION 1
+
+#define RFSN_OK 0
+#define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
+#define RFSN_ERR_STATE (-2)       /* use before set-up          -> RuntimeError */
+#define RFSN_ERR_HIP (-3)         /* HIP runtime failure        -> RuntimeError */
+#define RFSN_ERR_UNSUPPORTED (-4) /* shape outside the compiled kernels          */
+
+int rfsn_abi_version(void);
+const char* rfsn_last_error(void);
+
+/* Warm-tier format: PQ base, optional subspace RVQ stage, optional top-k
+ * sparse residual.  The reference's PQ (quantization.py:99-157) is the case
+ * rvq_subspaces = 0, sparse_k = 0. */
+typedef struct rfsn_format {
+  int32_t head_dim;      /* D                                   */
+  int32_t pq_subspaces;  /* M  (D % M == 0)                     */
+  int32_t pq_centroids;  /* C  (<= 256, uint8 codes)            */
+  int32_t rvq_subspaces; /* M_r, 0 = no RVQ stage               */
+  int32_t rvq_centroids; /* C_r (<= 256)                        */
+  int32_t sparse_k;      /* k, 0 = no sparse residual (<= 8)    */
+} rfsn_format;
+
+/* Codes of N vectors in the warm format, row-major, contiguous rows:
+ * pq [N][M] u8, rvq [N][M_r] u8, sparse_idx [N][k] u8, sparse_val [N][k] fp16. */
+typedef struct rfsn_codes {
+  uint8_t* pq;
+  uint8_t* rvq;
+  uint8_t* sparse_idx;
+  void* sparse_val;
+} rfsn_codes;
+
+/* ---------------------------------------------------------------- encode
+ * Nearest-centroid PQ encode with the canonical distance
+ * fl32(fl32(L - 2X) + R) and first-min argmin; residual fp16(x - c).
+ * Replaces ProductQuantizerMLX.quantize (quantization.py:124-144) and
+ * _squared_l2_distance (quantization.py:92-96).
+ * x_dev [groups][N][ldx] fp16 (group stride x_gstride elements);
+ * codebooks_dev [groups][M][C][d] fp16 (stride cb_gstride elements);
+ * codes_dev [groups][N][ldc] u8 (stride codes_gstride); resid_dev may be NULL,
+ * else [groups][N][ldr] fp16 (stride resid_gstride). */
+int rfsn_pq_encode(const void* x_dev, int64_t n, int32_t D, int64_t ldx, int64_t x_gstride,
+                   const void* codebooks_dev, int32_t M, int32_t C, int64_t cb_gstride,
+                   uint8_t* codes_dev, int64_t ldc, int64_t codes_gstride,
+                   void* resid_dev, int64_t ldr, int64_t resid_gstride,
+                   int32_t groups, void* stream);
+
+/* Fused warm-format encode: PQ, then (if fmt->rvq_subspaces) PQ of the fp16
+ * residual with the RVQ codebooks, then (if fmt->sparse_k) the top-k |r2|
+ * coordinates of r2 = fl32(x - fp16(base + rvq)).  No reference symbol: the
+ * RVQ stage generalises ResidualVQMLX.encode (quantization.py:206-252) to
+ * subspaces; the sparse stage is new.  Output rows go to out.* (rows of the
+ * same vector order as x).  workspace_dev: rfsn_warm_encode_workspace_bytes. */
+size_t rfsn_warm_encode_workspace_bytes(const rfsn_format* fmt, int64_t n);
+int rfsn_warm_encode(const rfsn_format* fmt, const void* x_dev, int64_t n, int64_t ldx,
+                     const void* pq_cb_dev, const void* rvq_cb_dev, rfsn_codes out,
+                     void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* Reference-mode RVQ (quantization.py:206-252), three steps:
+ * (1) gate: mask[i] = fl32(sqrt(fl32(sum r^2))) > threshold (u8 0/1);
+ * (2) compaction: offsets[0..A) = ascending indices with mask set,
+ *     count_dev[0] = A  (np.flatnonzero, quantization.py:218);
+ * (3) L-stage full-dimension encode of the active rows (running residual in
+ *     fp32, first-min argmin over C <= 65535 centroids), codes [A][L] u16. */
+int rfsn_rvq_gate(const void* resid_dev, int64_t n, int32_t D, int64_t ld, float threshold,
+                  uint8_t* mask_dev, void* stream);
+size_t rfsn_mask_compact_workspace_bytes(int64_t n);
+int rfsn_mask_compact(const uint8_t* mask_dev, int64_t n, int32_t* offsets_dev, int32_t* count_dev,
+                      void* workspace_dev, size_t workspace_bytes, void* stream);
+int rfsn_rvq_encode_full(const void* resid_dev, int64_t ld, int32_t D, const int32_t* offsets_dev,
+                         int64_t active, const void* codebooks_dev, int32_t L, int32_t C,
+                         uint16_t* codes_dev, void* stream);
+
+/* ---------------------------------------------------------------- decode
+ * Warm-format decode to fp16 [N][ldo]: fp16(base + rvq) then sparse
+ * K[idx] = fp16(K[idx] + val).  Replaces ProductQuantizerMLX.decode
+ * (quantization.py:146-157) for the PQ-only format and
+ * _decode_compressed_tensor (quantization.py:394-403) for the warm format. */
+int rfsn_decode(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
+                const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, int64_t ldo,
+                int32_t add_zero_correction, void* stream);
+
+/* Reference-format hybrid decode (quantization.py:310-319): base =
+ * C_pq[pq_codes]; corr = fp16(sum_l C_l[rvq_codes[a][l]]) scattered to rows
+ * offsets[a]; out = fp16(base + corr) (corr = +0 for inactive rows). */
+int rfsn_decode_ref(const uint8_t* pq_codes_dev, int64_t n, int32_t D, int32_t M, int32_t C,
+                    const void* pq_cb_dev, const uint16_t* rvq_codes_dev, const int32_t* offsets_dev,
+                    int64_t active, int32_t L, int32_t C_r, const void* rvq_cb_dev,
+                    void* out_dev, void* stream);
+
+/* ---------------------------------------------------------------- attention
+ * Exact blockwise decode attention over fp16 K/V (attention.py:39-105,
+ * _blockwise_exact_attention), split over the token axis with an LSE merge.
+ * q [B][Hq][D] fp16, K/V element (t, h, i) at base + t*stride_t + h*stride_h + i,
+ * Hq % Hkv == 0 (query head h reads KV head h / (Hq/Hkv)),
+ * qpos_dev [B][Hq] int32 or NULL (= every query at T-1), causal masks
+ * positions > qpos; out [B][Hq][D] fp16 = q.dtype.  Any block size gives the
+ * same result up to fp32 rounding. */
+size_t rfsn_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t splits);
+int rfsn_blockwise_attention(const void* q_dev, int32_t B, int32_t Hq, int32_t D,
+                             const void* k_dev, const void* v_dev, int64_t T, int32_t Hkv,
+                             int64_t stride_t, int64_t stride_h, float scale, int32_t causal,
+                             const int32_t* qpos_dev, void* out_dev,
+                             void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* Code layout the fused kernel streams ("tiled"): codes of one KV head live
+ * in a block of cap*M bytes (cap a multiple of 32); inside 32-token tile
+ * tau, the code of (token t, subspace m) sits at byte
+ *   tau*32*M + ((t % TPI)*M + m)*IPT + (t % 32)/TPI,  TPI = 64/M, IPT = 32/TPI,
+ * so that one 64-lane gather instruction reads TPI tokens x M subspaces.
+ * rfsn_pack_codes converts plain rows [heads][T][M] (head stride
+ * src_head_stride bytes) into tokens t_base .. t_base+T-1 of the tiled
+ * layout (head stride dst_head_stride bytes).  M must be 8 or 16. */
+int rfsn_pack_codes(const uint8_t* src_dev, int64_t src_head_stride, int64_t T, int32_t M, int32_t heads,
+                    uint8_t* dst_dev, int64_t dst_head_stride, int64_t t_base, void* stream);
+
+/* Fused warm-tier dequant + exact decode attention over [hot | segments] (or
+ * [segments | hot]).  Replaces RFSNv10KVCacheMLX.attention_forward
+ * (cache.py:395-428) = materialize_window (cache.py:344-393) +
+ * _blockwise_exact_attention, without writing the window to HBM.
+ *
+ * A segment is a run of encoded tokens of one sequence for all KV heads.
+ * PQ and RVQ codes are in the tiled layout (head h at byte h*head_stride*M
+ * resp. h*head_stride*M_r); sparse arrays are plain rows, (head h, token t)
+ * at row h*head_stride + t.  head_stride is a multiple of 32.
+ * Segment window positions are pos0 .. pos0+len-1 (used by causal masking). */
+typedef struct rfsn_segment {
+  rfsn_codes k;
+  rfsn_codes v;
+  int64_t head_stride; /* token rows between KV heads (multiple of 32) */
+  int32_t len;         /* tokens                  */
+  int32_t pos0;        /* window position of token 0 */
+} rfsn_segment;
+
+typedef struct rfsn_fused_params {
+  rfsn_format fmt;
+  int32_t batch;       /* B sequences                                   */
+  int32_t q_heads;     /* Hq                                            */
+  int32_t kv_heads;    /* Hkv                                           */
+  const void* q;       /* [B][Hq][D] fp16                               */
+  void* out;           /* [B][Hq][D] fp16                               */
+  float scale;
+  int32_t causal;
+  const int32_t* qpos; /* [B][Hq] int32 window positions, or NULL       */
+  /* exact (hot) tier: sequence b, KV head h, token t at
+   * hot_k + b*hot_seq_stride + (h*hot_cap + t)*D  (fp16 elements);
+   * hot_seq_stride = 0 lets B queries share one cache. */
+  const void* hot_k;
+  const void* hot_v;
+  int64_t hot_cap;
+  int64_t hot_seq_stride;
+  int32_t hot_len;     /* tokens, same for every sequence               */
+  int32_t hot_pos0;    /* window position of hot token 0                */
+  /* encoded tiers: segments[b*max_segments + s], s < num_segments[b] */
+  const rfsn_segment* segments;   /* device array                       */
+  const int32_t* num_segments;    /* device [B]                         */
+  int32_t max_segments;
+  /* codebooks per sequence: pq [B][M][C][d], rvq [B][M_r][C_r][d_r], for K and V */
+  const void* k_pq_cb;
+  const void* k_rvq_cb;
+  const void* v_pq_cb;
+  const void* v_rvq_cb;
+  int64_t pq_cb_stride;   /* elements between sequences (0 = shared)  */
+  int64_t rvq_cb_stride;
+  int32_t max_tokens;     /* upper bound on hot_len + sum of segment lengths */
+  int32_t splits;         /* token splits per (sequence, KV head); 0 = auto  */
+  void* workspace;
+  size_t workspace_bytes;
+} rfsn_fused_params;
+
+size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);
+int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
+
+/* ---------------------------------------------------------------- k-means
+ * One Lloyd update of PQ codebooks (rfsn_v10_mlx_ane_complete.py:197-207):
+ * every centroid with members becomes fp16(fp32 mean of its members); empty
+ * clusters keep their row.  workspace: rfsn_kmeans_workspace_bytes. */
+size_t rfsn_kmeans_workspace_bytes(int32_t M, int32_t C, int32_t d);
+int rfsn_kmeans_update(const void* x_dev, int64_t n, int32_t D, int64_t ldx, const uint8_t* codes_dev,
+                       int32_t M, int32_t C, void* codebooks_dev, void* workspace_dev,
+                       size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- cold tier
+ * Pinned host pool + asynchronous host-to-device chunk prefetch on a side
+ * stream.  Replaces the NPZ chunk files and the router's executor-thread
+ * loads (cache.py:134-197, storage.py:113-151, storage.py:203-234). */
+int rfsn_host_alloc(size_t bytes, void** ptr_out);
+int rfsn_host_free(void* ptr);
+typedef struct rfsn_copy {
+  void* dst_dev;
+  const void* src_host;
+  size_t bytes;
+} rfsn_copy;
+int rfsn_prefetch_h2d(const rfsn_copy* copies, int32_t count, void* stream);
+int rfsn_stream_create(void** stream_out);   /* default priority, non-blocking */
+int rfsn_stream_destroy(void* stream);
+int rfsn_event_create(void** event_out);
+int rfsn_event_destroy(void* event);
+int rfsn_event_record(void* event, void* stream);
+int rfsn_stream_wait_event(void* stream, void* event);
+int rfsn_event_synchronize(void* event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RFSN_ABI_H */

@@ -1,0 +1,143 @@
+"""GPU parity of the fused warm-tier dequant + decode attention against the
+oracle (decode the window, then blockwise attention), within 2e-3 max-abs."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nx
+from tests.conftest import rand_codebooks, randn16, rng
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def T(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def H(t):
+    return t.detach().cpu().numpy()
+
+
+def _kv(g, n, Hkv, D):
+    s = (g.random((Hkv, D), dtype=np.float32) * 1.5 + 0.5).astype(np.float32)
+    k = (g.standard_normal((n, Hkv, D), dtype=np.float32) * s).astype(np.float16)
+    v = (g.standard_normal((n, Hkv, D), dtype=np.float32) * s).astype(np.float16)
+    return k, v
+
+
+def _setup(seed, Hq, Hkv, M, Mr, k, nw, nh, D=64):
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    g = rng(seed)
+    keys, values = _kv(g, nw + nh, Hkv, D)
+    cbs = {n: rand_codebooks(g, M, 256, D // M) for n in ("kp", "vp")}
+    if Mr:
+        cbs.update({n: rand_codebooks(g, Mr, 256, D // Mr) * np.float16(0.35) for n in ("kr", "vr")})
+    # Mr = k = 0 is the reference format in its pq_only mode (threshold = inf)
+    cfg = RFSNConfig(num_heads=Hq, head_dim=D, num_subspaces=M, subspace_dim=D // M, num_rvq_layers=1,
+                     rvq_codebook_size=256, rvq_sparsity_threshold=float("inf") if not (Mr or k) else 0.005,
+                     hot_capacity=nh, warm_capacity=nw + 4096, block_size_seq=128,
+                     num_kv_heads=Hkv, rvq_subspaces=Mr, sparse_topk=k, tier_policy="recency", cold_medium="pinned")
+    kq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["kp"]),
+                            rvq_codebooks=torch.from_numpy(cbs["kr"]) if Mr else None)
+    vq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["vp"]),
+                            rvq_codebooks=torch.from_numpy(cbs["vr"]) if Mr else None)
+    return g, cfg, keys, values, cbs, kq, vq
+
+
+def _oracle_window(keys, values, cbs, Mr, k, nw):
+    Hkv, D = keys.shape[1], keys.shape[2]
+    outs = []
+    for x, p, r in ((keys, cbs["kp"], cbs.get("kr")), (values, cbs["vp"], cbs.get("vr"))):
+        flat = x[:nw].reshape(-1, D)
+        enc = nx.ext_encode(flat, p, r if Mr else None, k)
+        dec = nx.ext_decode(enc["pq_codes"], p, enc.get("rvq_codes"), r, enc.get("sparse_idx"),
+                            enc.get("sparse_val"))
+        if not (Mr or k):  # reference pq_only mode: fp16(base + 0) (quantization.py:319)
+            dec = nx.hybrid_add(dec, np.zeros_like(dec))
+        dec = dec.reshape(nw, Hkv, D)
+        outs.append(np.concatenate([dec, x[nw:]], 0))
+    return outs
+
+
+CASES = [
+    # seed, Hq, Hkv, M, Mr, k, nw, nh
+    (1, 8, 8, 8, 0, 0, 896, 128),       # 1,024-token smoke shape, PQ-only
+    (2, 32, 8, 16, 16, 4, 7680, 512),   # Llama-3.2-1B layer shape, PQ+RVQ+top-4
+    (3, 32, 4, 16, 16, 4, 1000, 100),   # GQA 8:1, ragged tiles
+    (4, 16, 8, 8, 8, 4, 333, 33),       # M=8 with RVQ and sparse, ragged
+    (5, 8, 8, 16, 0, 4, 64, 0),         # no hot tier
+    (6, 8, 4, 16, 16, 0, 0, 77),        # hot tier only
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_fused_cache_attention(device, case):
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    seed, Hq, Hkv, M, Mr, k, nw, nh = case
+    g, cfg, keys, values, cbs, kq, vq = _setup(seed, Hq, Hkv, M, Mr, k, nw, nh)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._fused_ok()
+    wk, wv = _oracle_window(keys, values, cbs, Mr, k, nw)
+    # the cache materializes exactly the oracle's window
+    mk, mv, _ = cache.materialize_window()
+    assert np.array_equal(H(mk).view(np.uint16), wk.view(np.uint16))
+    assert np.array_equal(H(mv).view(np.uint16), wv.view(np.uint16))
+    B = 3
+    q = randn16(g, B, Hq, 64)
+    Ttot = nw + nh
+    for causal, qp in ((True, None), (False, None), (True, g.integers(-1, Ttot, (B,)).astype(np.int32))):
+        out = cache.attention_forward(T(q, device), causal=causal, query_positions=None if qp is None else T(qp, device))
+        ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, causal, qp)
+        err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
+        assert err <= TOL, (causal, qp, err)
+
+
+@pytest.mark.parametrize("cw", [1, 31, 100, 1500])
+def test_fused_context_window(device, cw):
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    g, cfg, keys, values, cbs, kq, vq = _setup(40 + cw, 32, 8, 16, 16, 4, 1200, 96)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    wk, wv = _oracle_window(keys, values, cbs, 16, 4, 1200)
+    q = randn16(g, 1, 32, 64)
+    qpos = np.array([1250], np.int32)
+    out = cache.attention_forward(T(q, device), causal=True, query_positions=T(qpos, device), context_window=cw)
+    st = cache.get_last_access_stats()
+    start = max(0, 1251 - cw)
+    ref = nx.blockwise_attention(q, wk[start:1251], wv[start:1251], 0.125, 256, True, qpos - start)
+    err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
+    assert err <= TOL
+    assert st["window_start"] == start and st["window_tokens"] == 1251 - start
+    mk, _, adj = cache.materialize_window(query_positions=T(qpos, device), context_window=cw)
+    assert np.array_equal(H(mk).view(np.uint16), wk[start:1251].view(np.uint16))
+    assert int(H(adj)[0]) == 1250 - start
+
+
+def test_batched_matches_per_sequence(device):
+    from apple_amd.batched import RFSNBatchedKVCache
+    from apple_amd.quantization import HybridQuantizerMLX
+
+    B, Hq, Hkv, nw, nh = 4, 32, 8, 2048, 256
+    seqs = [_setup(70 + b, Hq, Hkv, 16, 16, 4, nw, nh) for b in range(B)]
+    cfg = seqs[0][1]
+    bc = RFSNBatchedKVCache(cfg, B, device=device)
+    refs = []
+    for b, (g, _, keys, values, cbs, kq, vq) in enumerate(seqs):
+        bc.prefill(b, T(keys, device), T(values, device), kq, vq)
+        refs.append(_oracle_window(keys, values, cbs, 16, 4, nw))
+    q = randn16(rng(99), B, Hq, 64)
+    out = H(bc.attention_forward(T(q, device)))
+    for b in range(B):
+        mk, mv = bc.sequence_window(b)
+        assert np.array_equal(H(mk).view(np.uint16), refs[b][0].view(np.uint16))
+        assert np.array_equal(H(mv).view(np.uint16), refs[b][1].view(np.uint16))
+        ref = nx.blockwise_attention(q[b:b + 1], refs[b][0], refs[b][1], 0.125, 256, False, None)
+        assert np.abs(out[b:b + 1].astype(np.float32) - ref.astype(np.float32)).max() <= TOL

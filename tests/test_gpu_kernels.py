@@ -1,0 +1,146 @@
+"""GPU parity of every HIP kernel against the CPU oracle (bit-exact codes and
+reconstructions; attention within 2e-3 max-abs on fp16 outputs)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nx
+from tests.conftest import rand_codebooks, randn16, rng
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def T(a, dev):
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.uint16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def H(t):
+    t = t.detach().cpu()
+    if t.dtype == torch.uint16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+@pytest.mark.parametrize("M,d,C,n", [(8, 8, 256, 1000), (16, 4, 256, 777), (8, 16, 256, 300), (4, 16, 100, 129)])
+def test_pq_encode_bit_exact(device, M, d, C, n):
+    from apple_amd import kernels as K
+
+    g = rng(11 + M + d)
+    x = randn16(g, n, M * d)
+    cb = rand_codebooks(g, M, C, d)
+    codes, resid = K.pq_encode(T(x, device), T(cb, device))
+    rc, rr = nx.pq_encode(x, cb)
+    assert np.array_equal(H(codes), rc)
+    assert np.array_equal(H(resid).view(np.uint16), rr.view(np.uint16))
+
+
+def test_pq_encode_known_answers(device):
+    """Rows equal to centroids return those centroids; duplicated rows return
+    the lowest index; a zero vector against a zero row 0 returns 0."""
+    from apple_amd import kernels as K
+
+    g = rng(5)
+    cb = rand_codebooks(g, 4, 64, 4)
+    cb[:, 10] = cb[:, 3]  # duplicate centroid 3 at index 10
+    pick = np.array([3, 10, 0, 63, 17, 10])
+    x = np.concatenate([cb[m][pick] for m in range(4)], axis=1)
+    codes, resid = K.pq_encode(T(x, device), T(cb, device))
+    want = np.where(pick == 10, 3, pick)
+    assert np.array_equal(H(codes), np.repeat(want[:, None], 4, axis=1))
+    assert not H(resid).any()
+    cb0 = cb.copy()
+    cb0[:, 0] = 0
+    zc, _ = K.pq_encode(T(np.zeros((5, 16), np.float16), device), T(cb0, device))
+    assert not H(zc).any()
+
+
+@pytest.mark.parametrize("M,Mr,k", [(16, 16, 4), (8, 8, 4), (8, 0, 0), (16, 16, 0), (16, 0, 4)])
+def test_warm_encode_bit_exact(device, M, Mr, k):
+    from apple_amd import kernels as K
+
+    g = rng(100 + M + Mr + k)
+    n, D = 901, 64
+    x = (randn16(g, n, D).astype(np.float32) * np.linspace(0.5, 2.0, D, dtype=np.float32)).astype(np.float16)
+    pq_cb = rand_codebooks(g, M, 256, D // M)
+    rvq_cb = rand_codebooks(g, Mr, 256, D // Mr) * np.float16(0.3) if Mr else None
+    fmt = K.WarmFormat(D, M, 256, Mr, 256 if Mr else 0, k)
+    out = K.warm_encode(T(x, device), fmt, T(pq_cb, device), None if rvq_cb is None else T(rvq_cb, device))
+    ref = nx.ext_encode(x, pq_cb, rvq_cb, k)
+    assert np.array_equal(H(out["pq"]), ref["pq_codes"])
+    if Mr:
+        assert np.array_equal(H(out["rvq"]), ref["rvq_codes"])
+    if k:
+        assert np.array_equal(H(out["sparse_idx"]), ref["sparse_idx"])
+        assert np.array_equal(H(out["sparse_val"]).view(np.uint16), ref["sparse_val"].view(np.uint16))
+    # decode round trip, bit-exact
+    dec = K.decode(fmt, out["pq"], T(pq_cb, device), out.get("rvq"), None if rvq_cb is None else T(rvq_cb, device),
+                   out.get("sparse_idx"), out.get("sparse_val"))
+    rdec = nx.ext_decode(ref["pq_codes"], pq_cb, ref.get("rvq_codes"), rvq_cb, ref.get("sparse_idx"),
+                         ref.get("sparse_val"))
+    assert np.array_equal(H(dec).view(np.uint16), rdec.view(np.uint16))
+
+
+@pytest.mark.parametrize("thr", [0.25, 5.0, float("inf"), 0.0])
+def test_rvq_full_bit_exact(device, thr):
+    from apple_amd import kernels as K
+
+    g = rng(7)
+    n, D, L, C = 300, 128, 3, 256
+    resid = np.concatenate([randn16(g, n // 2, D, scale=0.01), randn16(g, n - n // 2, D)], 0)
+    cb = rand_codebooks(g, L, C, D)
+    cb[:, 0] = 0
+    codes, mask, offs = K.rvq_encode_full(T(resid, device), T(cb, device), thr)
+    rc, rm, ro = nx.rvq_encode_full(resid, cb, thr)
+    assert np.array_equal(H(mask), rm)
+    assert np.array_equal(H(offs), ro)
+    assert np.array_equal(H(codes), rc)
+    # reference hybrid decode
+    pq_cb = rand_codebooks(g, 8, 256, 16)
+    pq = g.integers(0, 256, (n, 8)).astype(np.uint8)
+    dec = K.decode_ref(T(pq, device), T(pq_cb, device), T(rc, device), T(ro, device), T(cb, device))
+    rdec = nx.hybrid_decode(pq, rc, rm, ro, pq_cb, cb)
+    assert np.array_equal(H(dec).view(np.uint16), rdec.view(np.uint16))
+
+
+def _qpos_cases(B, Hq, T_):
+    g = rng(3)
+    return [None, g.integers(-1, T_, (B, Hq)).astype(np.int32)]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,T_", [(8, 8, 64, 1024), (32, 8, 64, 3000), (4, 4, 128, 60), (32, 4, 64, 777),
+                                         (16, 8, 128, 1)])
+def test_blockwise_attention(device, Hq, Hkv, D, T_):
+    from apple_amd import kernels as K
+
+    g = rng(Hq + Hkv + D + T_)
+    B = 2
+    q = randn16(g, B, Hq, D)
+    k = randn16(g, T_, Hkv, D)
+    v = randn16(g, T_, Hkv, D)
+    for causal in (False, True):
+        for qp in _qpos_cases(B, Hq, T_):
+            out = K.blockwise_attention(T(q, device), T(k, device), T(v, device), D ** -0.5, causal,
+                                        None if qp is None else T(qp, device))
+            ref = nx.blockwise_attention(q, k, v, D ** -0.5, 128, causal, qp)
+            err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
+            assert err <= TOL, (causal, qp is None, err)
+
+
+def test_pack_untile_roundtrip(device):
+    from apple_amd import kernels as K
+    from apple_amd.batched import untile
+
+    g = rng(9)
+    for M in (8, 16):
+        Hh, Tt = 3, 133
+        src = g.integers(0, 256, (Hh, Tt, M)).astype(np.uint8)
+        cap = K.round_up(Tt + 40, 32)
+        dst = torch.zeros((Hh, cap * M), dtype=torch.uint8, device=device)
+        K.pack_codes(T(src[:, :50], device), dst, 0)
+        K.pack_codes(T(src[:, 50:], device), dst, 50)
+        assert np.array_equal(H(untile(dst, M, Tt)), src)
