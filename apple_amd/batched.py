@@ -119,8 +119,14 @@ class RFSNBatchedKVCache:
             self._table = (t, t.to_device(self.device))
         return self._table
 
+    def prepare(self, q: torch.Tensor, causal: bool = False, query_positions=None, splits: int = 0,
+                out: Optional[torch.Tensor] = None) -> "K.FusedLaunch":
+        """A reusable launch of ``attention_forward`` on these buffers (q is
+        read at launch time, so a decode loop refills q in place)."""
+        return self.attention_forward(q, causal, query_positions, splits, out, launch=False)
+
     def attention_forward(self, q: torch.Tensor, causal: bool = False, query_positions=None, splits: int = 0,
-                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          out: Optional[torch.Tensor] = None, launch: bool = True):
         """q [B, Hq, D] (one decode query per sequence) -> [B, Hq, D] fp16."""
         if q.shape[0] != self.batch or q.shape[2] != self.D or q.shape[1] % self.H:
             raise ValueError("q must be [B, Hq, D] with Hq a multiple of the KV heads")
@@ -146,7 +152,7 @@ class RFSNBatchedKVCache:
             k_pq_cb=self.cb["k_pq"], v_pq_cb=self.cb["v_pq"], k_rvq_cb=self.cb.get("k_rvq"),
             v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True,
             max_tokens=max(h + w for h, w in zip(self.num_hot, self.num_warm)), splits=splits,
-            workspace=self._ws, out=out, hot_cap=self.hot_cap)
+            workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=launch)
 
     def sequence_window(self, b: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Materialized (keys, values) [W, Hkv, D] of sequence b, warm then hot."""

@@ -29,7 +29,7 @@ exact_attn_kernel(const uint16_t* __restrict__ q, int Hq, const uint16_t* __rest
   __shared__ float red_m[kWaves][G], red_l[kWaves][G];
   __shared__ float red_acc[kWaves][G][D];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
     const int g = i / D, c = i % D;
     qs[g][c] = h2f(q[((int64_t)b * Hq + h * G + g) * D + c]) * scale_log2;

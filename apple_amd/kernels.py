@@ -270,12 +270,13 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
                     v_rvq_cb: Optional[torch.Tensor], cb_batch_stride: bool, max_tokens: int,
                     splits: int = 0, table: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
                     workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                    hot_cap: Optional[int] = None) -> torch.Tensor:
+                    hot_cap: Optional[int] = None, launch: bool = True):
     """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
 
     hot_k/hot_v: [.., Hkv, hot_cap, D] fp16 (sequence stride ``hot_seq_stride``
     elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
-    else [M, C, d] shared.
+    else [M, C, d] shared.  With ``launch=False`` returns a ``FusedLaunch``
+    that re-issues the same launch (same buffers) without rebuilding it.
     """
     _dev(q, "fused_attention")
     q = _contig(q)
@@ -308,8 +309,31 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     if workspace is None or workspace.numel() < wsb:
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
-    L.call("rfsn_fused_decode_attention", C.byref(p), _stream(q))
+    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments], out, _stream(q))
+    if not launch:
+        return fl
+    fl()
     return out
+
+
+class FusedLaunch:
+    """A prepared fused launch: the parameter block and the tensors it points
+    to, re-issued on the same stream by ``__call__`` (a decode loop's inner
+    step, no host-side rebuilding)."""
+
+    def __init__(self, params: L.FusedParams, keep: list, out: torch.Tensor, stream: int):
+        self.params = params
+        self._keep = keep
+        self.out = out
+        self.stream = stream
+        self._fn = L.load().rfsn_fused_decode_attention
+        self._ref = C.byref(self.params)
+
+    def __call__(self) -> torch.Tensor:
+        st = self._fn(self._ref, self.stream)
+        if st:
+            L.check(st, "rfsn_fused_decode_attention")
+        return self.out
 
 
 # --------------------------------------------------------------------------

@@ -1,0 +1,89 @@
+"""Timed CPU baseline of the warm-tier decode path (test infrastructure only;
+``bench.py`` times it beside the GPU kernel, it is never the thing measured
+on the GPU).
+
+Restates the reference's PyTorch form (rfsn_v10_unified_mac_launcher.py:
+217-273): per-subspace ``F.embedding`` decode of the PQ codes, the same for
+the RVQ stage, ``fp16(base + rvq)`` (quantization.py:317-319), the sparse
+residual ``K[idx] = fp16(K[idx] + val)``, then the blockwise online-softmax
+recurrence of attention.py:53-105 in fp32 with ``block`` tokens per step.
+GQA: query head h reads KV head h // (Hq // Hkv).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+MASK_FILL_VALUE = -1e30
+
+
+def decode_codes(codes: torch.Tensor, codebooks: torch.Tensor) -> torch.Tensor:
+    """codes [N, M] -> fp16 [N, M*d] (launcher:217-224, in fp16 storage)."""
+    M, C, d = codebooks.shape
+    out = torch.empty((codes.shape[0], M * d), dtype=torch.float16)
+    for m in range(M):
+        out[:, m * d:(m + 1) * d] = F.embedding(codes[:, m].long(), codebooks[m])
+    return out
+
+
+def warm_decode(pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional[torch.Tensor] = None,
+                rvq_cb: Optional[torch.Tensor] = None, sidx: Optional[torch.Tensor] = None,
+                sval: Optional[torch.Tensor] = None) -> torch.Tensor:
+    x = decode_codes(pq, pq_cb)
+    if rvq is not None:
+        x = (x.float() + decode_codes(rvq, rvq_cb).float()).half()
+    if sidx is not None and sidx.shape[1]:
+        idx = sidx.long()
+        cur = torch.gather(x, 1, idx).float()
+        x.scatter_(1, idx, (cur + sval.float()).half())
+    return x
+
+
+def blockwise_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, scale: float,
+                        block: int) -> torch.Tensor:
+    """q [B, Hq, D]; keys/values [T, Hkv, D]; non-causal decode (the query is
+    the newest position, so every window token is allowed)."""
+    B, Hq, D = q.shape
+    T, Hkv, _ = keys.shape
+    rep = Hq // Hkv
+    qf = q.float()
+    run_max = torch.full((B, Hq), MASK_FILL_VALUE)
+    run_sum = torch.zeros((B, Hq))
+    acc = torch.zeros((B, Hq, D))
+    for s in range(0, T, block):
+        kb = keys[s:s + block].float().repeat_interleave(rep, dim=1).permute(1, 0, 2)  # [Hq, n, D]
+        vb = values[s:s + block].float().repeat_interleave(rep, dim=1).permute(1, 0, 2)
+        scores = torch.einsum("bhd,hnd->bhn", qf, kb) * scale
+        new_max = torch.maximum(run_max, scores.max(dim=-1).values)
+        rescale = torch.exp(run_max - new_max)
+        run_sum = run_sum * rescale
+        acc = acc * rescale[..., None]
+        e = torch.exp(scores - new_max[..., None])
+        run_sum = run_sum + e.sum(dim=-1)
+        acc = acc + torch.einsum("bhn,hnd->bhd", e, vb)
+        run_max = new_max
+    safe = torch.where(run_sum > 0, run_sum, torch.ones_like(run_sum))
+    return (acc / safe[..., None]).half()
+
+
+def decode_step(q: torch.Tensor, hot_k: torch.Tensor, hot_v: torch.Tensor, warm_k: dict, warm_v: dict,
+                cbs: dict, scale: float, block: int) -> torch.Tensor:
+    """One decode step of one sequence: decode the warm tier, concatenate
+    [warm | hot] and attend.  warm_* hold plain codes [Hkv, T, *]."""
+    Hkv, T, _ = warm_k["pq"].shape
+    D = hot_k.shape[-1]
+    parts_k, parts_v = [], []
+    for codes, p, r, parts in ((warm_k, cbs["k_pq"], cbs.get("k_rvq"), parts_k),
+                               (warm_v, cbs["v_pq"], cbs.get("v_rvq"), parts_v)):
+        n = Hkv * T
+        x = warm_decode(codes["pq"].reshape(n, -1), p,
+                        None if codes.get("rvq") is None else codes["rvq"].reshape(n, -1), r,
+                        None if codes.get("sparse_idx") is None else codes["sparse_idx"].reshape(n, -1),
+                        None if codes.get("sparse_val") is None else codes["sparse_val"].reshape(n, -1))
+        parts.append(x.reshape(Hkv, T, D).permute(1, 0, 2))
+    keys = torch.cat([parts_k[0], hot_k.permute(1, 0, 2)], 0)
+    values = torch.cat([parts_v[0], hot_v.permute(1, 0, 2)], 0)
+    return blockwise_attention(q, keys, values, scale, block)
