@@ -41,7 +41,26 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-sample", type=int, default=4, help="sequences timed on the CPU baseline")
     ap.add_argument("--cpu-repeats", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     return ap.parse_args(argv)
+
+
+def copy_calibration(mib: int, reps: int = 5) -> dict:
+    """A device-to-device copy of exactly ``mib`` MiB, ``reps`` times: its
+    per-dispatch FETCH_SIZE and WRITE_SIZE should each read ``mib * 1024`` KiB."""
+    import torch
+
+    n = mib << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(src, dst))
+    return {"copy_calibration_bytes": n, "expected_kib_per_dispatch": n / 1024, "reps": reps, "ok": ok}
 
 
 def fit_quantizer(cfg, x, g, w, dev):
@@ -144,6 +163,9 @@ def main(argv=None) -> int:
         return 2
     import torch
 
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(args.copy_calibration)), flush=True)
+        return 0
     sys.path.insert(0, str(ROOT))
     from apple_amd.workloads import WORKLOADS
 

@@ -1,0 +1,101 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+include/rfsn_abi.h declares, its structs have the layout the ctypes mirror
+assumes, and host-side argument validation reports errors through the
+status codes and rfsn_last_error (no kernel is launched)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "rfsn_abi.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(rfsn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from apple_amd import _lib
+
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for must in ("rfsn_pq_encode", "rfsn_warm_encode", "rfsn_rvq_encode_full", "rfsn_decode",
+                 "rfsn_blockwise_attention", "rfsn_fused_decode_attention", "rfsn_prefetch_h2d",
+                 "rfsn_host_alloc", "rfsn_stream_wait_event", "rfsn_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ROOT / "apple_amd" / "librfsn_hip.so")],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (rfsn_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(declared_functions()) <= exported
+
+
+def test_ctypes_signatures_cover_the_header():
+    from apple_amd import _lib
+
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_struct_layout_matches_c(tmp_path):
+    """sizeof / offsetof from gcc on the real header against the ctypes mirror."""
+    from apple_amd import _lib
+
+    src = tmp_path / "layout.c"
+    fields = {
+        "rfsn_format": ["head_dim", "pq_subspaces", "pq_centroids", "rvq_subspaces", "rvq_centroids", "sparse_k"],
+        "rfsn_codes": ["pq", "rvq", "sparse_idx", "sparse_val"],
+        "rfsn_segment": ["k", "v", "head_stride", "len", "pos0"],
+        "rfsn_fused_params": [f for f, _ in _lib.FusedParams._fields_],
+        "rfsn_copy": ["dst_dev", "src_host", "bytes"],
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "rfsn_abi.h"', "int main(void) {"]
+    for s, fs in fields.items():
+        lines.append(f'printf("{s} %zu\\n", sizeof({s}));')
+        for f in fs:
+            lines.append(f'printf("{s}.{f} %zu\\n", offsetof({s}, {f}));')
+    lines.append("return 0; }")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                  check=True).stdout.splitlines())
+    py = {"rfsn_format": _lib.Format, "rfsn_codes": _lib.Codes, "rfsn_segment": _lib.Segment,
+          "rfsn_fused_params": _lib.FusedParams, "rfsn_copy": _lib.Copy}
+    for s, cls in py.items():
+        assert int(got[s]) == ctypes.sizeof(cls), s
+        for f in fields[s]:
+            assert int(got[f"{s}.{f}"]) == getattr(cls, f).offset, (s, f)
+
+
+def test_version_and_validation_errors(lib):
+    from apple_amd import _lib
+
+    assert lib.rfsn_abi_version() >= 1
+    # null parameter block: rejected on the host, no kernel launched
+    assert lib.rfsn_fused_decode_attention(None, None) == -1
+    assert b"null" in lib.rfsn_last_error()
+    p = _lib.FusedParams()
+    p.fmt.head_dim = 128
+    assert lib.rfsn_fused_decode_attention(ctypes.byref(p), None) == -1
+    assert b"head_dim" in lib.rfsn_last_error()
+    p.fmt.head_dim = 64
+    p.fmt.pq_subspaces = 12
+    assert lib.rfsn_fused_decode_attention(ctypes.byref(p), None) == -1
+    assert lib.rfsn_fused_workspace_bytes(None) == 0
+    with pytest.raises(ValueError):
+        _lib.check(-1, "probe")

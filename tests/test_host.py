@@ -1,0 +1,145 @@
+"""Host-side logic that needs no GPU: configuration checks, the NPZ chunk
+schema (storage.py:113-151), the router's ranking over chunk files
+(storage.py:166-201), query-position normalization (attention.py:16-36),
+the tiled code layout, workload byte accounting and the bench contract."""
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from apple_amd.storage import (AsyncHierarchicalRouterMLX, CompressedTensorMLX, RFSNConfig, _concat0, _index0,
+                               chunk_file_path, compressed_tensor_from_loaded, load_compressed_chunk,
+                               save_compressed_chunk)
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_config_validation():
+    with pytest.raises(ValueError):
+        RFSNConfig(head_dim=64, num_subspaces=8, subspace_dim=4)
+    c = RFSNConfig(num_heads=32, head_dim=64, num_subspaces=16, subspace_dim=4, num_kv_heads=8,
+                   rvq_subspaces=16, sparse_topk=4)
+    assert c.kv_heads == 8 and c.ext_format and c.subspace_rvq
+    r = RFSNConfig(num_heads=4, head_dim=128, num_subspaces=8, subspace_dim=16)
+    assert r.kv_heads == 4 and not r.ext_format
+    assert r.chunk_tokens == r.block_size_seq
+    with pytest.raises(ValueError):
+        RFSNConfig(head_dim=64, num_subspaces=16, subspace_dim=4, cold_medium="tape")
+
+
+def test_compressed_empty_and_uint16_helpers():
+    cfg = RFSNConfig(num_heads=4, head_dim=128, num_subspaces=8, subspace_dim=16, num_rvq_layers=3)
+    e = CompressedTensorMLX.empty(cfg)
+    assert e.num_tokens == 0 and e.rvq_codes.dtype == torch.uint16 and e.rvq_codes.shape == (0, 3)
+    a = torch.tensor([1, 65535, 7], dtype=torch.int32).to(torch.uint16)
+    b = torch.tensor([40000], dtype=torch.int32).to(torch.uint16)
+    ab = _concat0(a, b)
+    assert ab.dtype == torch.uint16 and ab.to(torch.int32).tolist() == [1, 65535, 7, 40000]
+    assert _concat0(a[:0], b) is b
+    assert _index0(ab, torch.tensor([3, 1])).to(torch.int32).tolist() == [40000, 65535]
+
+
+def test_npz_chunk_schema_roundtrip(tmp_path):
+    g = torch.Generator().manual_seed(0)
+    T, H, M, L = 5, 3, 8, 2
+
+    def store():
+        mask = torch.rand((T, H), generator=g) > 0.5
+        A = int(mask.sum())
+        return CompressedTensorMLX(
+            pq_codes=torch.randint(0, 256, (T, H, M), generator=g, dtype=torch.uint8),
+            rvq_codes=torch.randint(0, 65536, (A, L), generator=g, dtype=torch.int32).to(torch.uint16),
+            rvq_mask=mask, rvq_offsets=torch.nonzero(mask.reshape(-1)).reshape(-1).to(torch.int32), num_heads=H)
+
+    k, v = store(), store()
+    p = chunk_file_path(tmp_path, 2, 7)
+    assert p.name == "layer2_chunk7.npz"
+    save_compressed_chunk(p, k, v)
+    with np.load(p, allow_pickle=False) as z:
+        assert sorted(z.files) == sorted(["num_tokens", "num_heads"] + [
+            f"{s}_{f}" for s in ("key", "value") for f in ("pq_codes", "rvq_codes", "rvq_mask", "rvq_offsets")])
+        assert z["key_rvq_codes"].dtype == np.uint16 and z["num_tokens"].tolist() == [T]
+    loaded = load_compressed_chunk(p)
+    for prefix, ref in (("key", k), ("value", v)):
+        t = compressed_tensor_from_loaded(loaded, prefix)
+        assert t.num_heads == H and t.num_tokens == T
+        assert torch.equal(t.pq_codes, ref.pq_codes) and torch.equal(t.rvq_mask, ref.rvq_mask)
+        assert torch.equal(t.rvq_codes.view(torch.int16), ref.rvq_codes.view(torch.int16))
+        assert torch.equal(t.rvq_offsets, ref.rvq_offsets)
+
+
+def test_router_ranking_over_chunk_files(tmp_path):
+    cfg = RFSNConfig(num_heads=4, head_dim=128, num_subspaces=8, subspace_dim=16, block_size_seq=16,
+                     disk_cache_dir=str(tmp_path), prefetch_throttle_s=0.0)
+    cfg_e = RFSNConfig(num_heads=4, head_dim=128, num_subspaces=8, subspace_dim=16, num_rvq_layers=3)
+    e = CompressedTensorMLX.empty(cfg_e)
+    for cid in (2, 3, 4, 5, 9):
+        save_compressed_chunk(chunk_file_path(tmp_path, 0, cid), e, e)
+    r = AsyncHierarchicalRouterMLX(cfg, 0)
+    # candidates in [(70-40)//16, (70+40)//16] = [1, 6] that exist, by |cid*16 - 70|
+    assert r.rank(70, 40) == [4, 5, 3, 2]
+    assert r.prefetch_sync(70, 40, top_k=3) == [4, 5, 3]
+    assert r.get_chunk(4) is not None and r.get_chunk(2) is None
+    assert r.prefetch_sync(0, 1024, top_k=1) == [2]
+
+
+def test_normalize_query_positions_host():
+    from apple_amd.attention import _normalize_query_positions as nqp
+
+    assert nqp(None, 2, 3, 9).tolist() == [[9] * 3] * 2
+    assert nqp([4, 5], 2, 3, 9).tolist() == [[4] * 3, [5] * 3]
+    assert nqp(torch.arange(6).reshape(2, 3), 2, 3, 9).tolist() == [[0, 1, 2], [3, 4, 5]]
+    for bad in ([1, 2, 3], torch.zeros(3, 2)):
+        with pytest.raises(ValueError):
+            nqp(bad, 2, 3, 9)
+
+
+@pytest.mark.parametrize("M", [8, 16])
+def test_tiled_layout_is_a_bijection(M):
+    """untile() inverts the tiled code layout: every (token, subspace) of a
+    tile owns one byte, and a tile's bytes are contiguous."""
+    from apple_amd.batched import untile
+
+    T = 96
+    tiled = torch.arange(T * M, dtype=torch.int64).reshape(1, -1)
+    plain = untile(tiled, M, T)[0]
+    assert sorted(plain.reshape(-1).tolist()) == list(range(T * M))
+    for t in range(0, T, 32):
+        assert plain[t:t + 32].min() == t * M and plain[t:t + 32].max() == (t + 32) * M - 1
+    # one lane's IPT bytes hold one subspace m for TPI-strided tokens of its tile
+    tpi, ipt = 64 // M, 32 // (64 // M)
+    lane = 5
+    j, m = lane // M, lane % M
+    for i in range(ipt):
+        assert plain[tpi * i + j, m] == lane * ipt + i
+
+
+def test_workload_bytes_known_answers():
+    from apple_amd.workloads import WORKLOADS
+
+    want = {"smoke_1k": 444_416, "llama1b_8k": 6_594_560, "batched_32x32k": 786_694_144,
+            "longctx_128k": 9_478_144}
+    for name, b in want.items():
+        assert WORKLOADS[name].bytes_per_step() == b, name
+    w = WORKLOADS["batched_32x32k"]
+    assert (w.batch, w.context, w.q_heads, w.kv_heads, w.hot, w.warm) == (32, 32768, 32, 8, 1024, 31744)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_product_path_refuses_cpu_tensors():
+    from apple_amd import kernels as K
+
+    x = torch.zeros((4, 64), dtype=torch.float16)
+    cb = torch.zeros((16, 256, 4), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        K.pq_encode(x, cb)
