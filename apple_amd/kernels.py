@@ -199,6 +199,17 @@ def decode_ref(pq: torch.Tensor, pq_cb: torch.Tensor, rvq_codes: torch.Tensor, o
 # attention
 # --------------------------------------------------------------------------
 
+def _qpos(qpos: torch.Tensor, B: int, Hq: int, device) -> torch.Tensor:
+    """Query positions as the int32 [B, Hq] array the kernels index; [B] is
+    broadcast over heads (attention.py:28-33), any other shape is rejected."""
+    qp = qpos.to(device=device, dtype=torch.int32)
+    if qp.dim() == 1 and qp.shape[0] == B:
+        qp = qp[:, None].expand(B, Hq)
+    if tuple(qp.shape) != (B, Hq):
+        raise ValueError(f"query positions must be [B] or [B, Hq] = [{B}, {Hq}], got {tuple(qpos.shape)}")
+    return qp.contiguous()
+
+
 def blockwise_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, scale: float,
                         causal: bool, qpos: Optional[torch.Tensor]) -> torch.Tensor:
     """Exact attention of q [B, Hq, D] over keys/values [T, Hkv, D] (strided rows)."""
@@ -213,7 +224,7 @@ def blockwise_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tenso
     if keys.stride() != values.stride() or keys.stride(2) != 1 or not aligned:
         keys, values = keys.contiguous(), values.contiguous()
     out = torch.empty_like(q)
-    qp = None if qpos is None else _contig(qpos.to(device=q.device, dtype=torch.int32))
+    qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)
     lib = L.load()
     splits_max = 1024
     wsb = lib.rfsn_attention_workspace_bytes(B, Hq, D, splits_max)
@@ -286,7 +297,10 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     if table is None:
         table = segments.to_device(q.device)
     seg_t, nseg_t, maxs = table
-    qp = None if qpos is None else _contig(qpos.to(device=q.device, dtype=torch.int32))
+    qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)
+    if out.shape != q.shape or out.dtype != torch.float16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp16 tensor shaped like q")
+    cbs = [None if t is None else _contig(t) for t in (k_pq_cb, v_pq_cb, k_rvq_cb, v_rvq_cb)]
     pq_stride = k_pq_cb[0].numel() if cb_batch_stride else 0
     rvq_stride = (k_rvq_cb[0].numel() if (cb_batch_stride and k_rvq_cb is not None) else 0)
     if hot_cap is None:
@@ -299,9 +313,7 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     p.hot_k, p.hot_v = L.ptr(hot_k), L.ptr(hot_v)
     p.hot_cap, p.hot_seq_stride, p.hot_len, p.hot_pos0 = hot_cap, hot_seq_stride, hot_len, hot_pos0
     p.segments, p.num_segments, p.max_segments = seg_t.data_ptr(), nseg_t.data_ptr(), maxs
-    p.k_pq_cb, p.v_pq_cb = _contig(k_pq_cb).data_ptr(), _contig(v_pq_cb).data_ptr()
-    p.k_rvq_cb = L.ptr(None if k_rvq_cb is None else _contig(k_rvq_cb))
-    p.v_rvq_cb = L.ptr(None if v_rvq_cb is None else _contig(v_rvq_cb))
+    p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
     p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
     p.max_tokens, p.splits = max_tokens, splits
     lib = L.load()
@@ -309,7 +321,7 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     if workspace is None or workspace.numel() < wsb:
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
-    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments], out, _stream(q))
+    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments, *cbs], out, _stream(q))
     if not launch:
         return fl
     fl()

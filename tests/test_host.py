@@ -136,6 +136,18 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
 
 
+def test_kernel_query_positions_shape():
+    """The kernels index query positions as int32 [B, Hq]; [B] is broadcast
+    and any other shape is rejected before a launch."""
+    from apple_amd.kernels import _qpos
+
+    assert _qpos(torch.tensor([3, 4]), 2, 3, "cpu").tolist() == [[3] * 3, [4] * 3]
+    assert _qpos(torch.arange(6).reshape(2, 3), 2, 3, "cpu").dtype == torch.int32
+    for bad in (torch.arange(3), torch.zeros(2, 2), torch.zeros(2, 3, 1)):
+        with pytest.raises(ValueError):
+            _qpos(bad, 2, 3, "cpu")
+
+
 def test_product_path_refuses_cpu_tensors():
     from apple_amd import kernels as K
 
