@@ -5,23 +5,32 @@
 // _blockwise_exact_attention (attention.py:39-105), without ever writing the
 // reconstructed window to HBM.
 //
-// Work decomposition: one block = (sequence b, KV head h, token split);
-// 4 waves; each wave streams 32-token tiles of the split.  Per tile:
-//   1. K^ tile: PQ and RVQ codebook entries are gathered from LDS with one
-//      lane per (token, subspace) -- the codebooks are stored entry-major,
-//      [entry][subspace][d], so the 16 (or 8) lanes that one LDS pass serves
-//      read 16 distinct bank pairs -- summed as fp16(base + rvq)
-//      (quantization.py:317-319) and written to a per-wave LDS tile
-//      (8-byte chunks XOR-swizzled by row); the sparse residual is applied in
-//      place, K[idx] = fp16(K[idx] + val).
-//   2. Scores on MFMA 4x4x4 f16 (16 blocks): B = K^ rows (lane = token),
-//      A = the 4 query heads of this KV head; fp32 accumulation.
-//   3. Online softmax in base 2 (lane = token, one register per head).
+// Work decomposition: one block = (sequence b, KV head h, token split) with
+// 8 waves, two per SIMD; each wave streams 32-token tiles of the split.
+// LDS holds the sequence's codebooks as two 64 KB tables (K, V), entry-major
+// with 256-byte entries [PQ entries of the M subspaces | RVQ entries], then
+// one 4 KB tile per wave (160 KB in total).  Per tile:
+//   1. K^ rows: one lane per (token, subspace) and gather; the LDS address of
+//      a codebook entry is built from the code byte with one v_perm_b32
+//      (code * 256 + subspace slot), and the 16 lanes of an LDS pass read 16
+//      distinct bank pairs.  fp16(base + rvq) on v_pk_add_f16
+//      (quantization.py:317-319) goes to the wave's tile (16-byte units
+//      XOR-swizzled by row); the sparse residual is applied in place,
+//      K[idx] = fp16(K[idx] + val).
+//   2. Scores on MFMA 16x16x32 f16: A = 16 tile rows ordered so that token
+//      16u+4i+g of half u lands in row 4g+i, B = the query heads replicated
+//      over 4 columns each; fp32 accumulation.  Lane (g, n) receives the
+//      scores of tokens 16u+4i+g (i = 0..3) for query head n/4.
+//   3. Online softmax in base 2 on those registers; the running max is only
+//      reduced across lanes when some score exceeds it.
 //   4. V^ tile built like K^.
-//   5. P.V on MFMA 16x16x16 f16 with A = V^ rows read as (subspace group x
-//      (token, coordinate)) and B = P placed on the coordinate diagonal, so
-//      that no transpose of V^ is needed; P is scaled by 2^14 before the fp16
-//      conversion to keep small weights out of the fp16 subnormal range.
+//   5. P.V on MFMA 16x16x16 f16: A = V^ rows read as (subspace x (token,
+//      coordinate)), B = the lane's own probability placed on the coordinate
+//      diagonal (the score layout of step 2 is already the B layout, so P
+//      never moves between lanes); a second MFMA with A = 1 accumulates the
+//      softmax denominator.  P is produced as p * 2^14 before the fp16
+//      conversion, keeping small weights out of the fp16 subnormal range;
+//      the factor cancels in out = acc / l.
 // Split partials (m, l, acc) are merged by merge_partials_kernel.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
@@ -31,19 +40,24 @@
 namespace rfsn {
 namespace {
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTile = 32;                 // tokens per wave tile
-constexpr int kWaves = 4;                 // waves per block
-constexpr int kD = 64;                    // head_dim of the fused kernel
-constexpr int kTileHalves = kTile * kD;   // 4 KB per wave
-constexpr int kDepth = 4;                 // tiles whose codes are in flight per wave
-constexpr int kCbHalves = 256 * kD;       // one codebook table in LDS (256 entries x D halves)
-constexpr size_t kDummyBytes = 4096;      // workspace head read by idle prefetch slots
-constexpr float kPScale = 16384.0f;       // 2^14
-constexpr float kPScaleInv = 1.0f / 16384.0f;
+constexpr int kTile = 32;                           // tokens per wave tile
+constexpr int kWaves = 8;                           // waves per block (2 per SIMD)
+constexpr int kThreads = kWaves * 64;
+constexpr int kD = 64;                              // head_dim of the fused kernel
+constexpr int kDepth = 4;                           // tiles whose codes are in flight per wave
+constexpr int kEntryBytes = 256;                    // one codebook entry: PQ slots, then RVQ slots
+constexpr int kRvqSlot = 128;                       // byte offset of the RVQ slots in an entry
+constexpr int kTableBytes = 256 * kEntryBytes;      // one K or V table, 64 KB
+constexpr int kTileBytes = kTile * kD * 2;          // 4 KB per wave
+constexpr int kTilesBase = 2 * kTableBytes;         // tiles follow the K and V tables
+constexpr size_t kLdsBytes = (size_t)kTilesBase + (size_t)kWaves * kTileBytes;  // 160 KB
+constexpr size_t kDummyBytes = 4096;                // workspace head read by idle prefetch slots
+constexpr float kPScaleLog2 = 14.0f;                // P is produced as p * 2^14
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Order LDS traffic between the lanes of one wave.  A wave's LDS instructions
@@ -57,34 +71,18 @@ __device__ __forceinline__ void wave_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Offset (in halves) of 8-byte chunk c (0..15) of tile row t.
-__device__ __forceinline__ int chunk_off(int t, int c) { return t * kD + ((c ^ (t & 15)) << 2); }
+__device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float bitsf(uint32_t v) { return __builtin_bit_cast(float, v); }
 
-// DPP lane exchanges (VALU, no LDS round trip)
-template <int Ctrl>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Ctrl, 0xf, 0xf, false));
+// max over lanes l, l^16 (resp. l^32): v_permlane16/32_swap exchange the rows
+// (halves) of the wave in one VALU op each.
+__device__ __forceinline__ float xmax16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false);
+  return fmaxf(bitsf(r[0]), bitsf(r[1]));
 }
-__device__ __forceinline__ float swz16(float v) {
-  // ds_swizzle bit mode: lane i reads lane i ^ 16 inside each group of 32
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
-}
-
-// max / sum over each group of 32 lanes: quad xor 1, quad xor 2, half-row
-// mirror, row mirror (16 lanes), then the swizzle across the two rows
-__device__ __forceinline__ float max32(float v) {
-  v = fmaxf(v, dpp<0xb1>(v));
-  v = fmaxf(v, dpp<0x4e>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return fmaxf(v, swz16(v));
-}
-__device__ __forceinline__ float sum32(float v) {
-  v += dpp<0xb1>(v);
-  v += dpp<0x4e>(v);
-  v += dpp<0x141>(v);
-  v += dpp<0x140>(v);
-  return v + swz16(v);
+__device__ __forceinline__ float xmax32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
+  return fmaxf(bitsf(r[0]), bitsf(r[1]));
 }
 
 __device__ __forceinline__ uint32_t add_h2(uint32_t a, uint32_t b) {
@@ -93,21 +91,32 @@ __device__ __forceinline__ uint32_t add_h2(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, x + y);  // v_pk_add_f16, IEEE round to nearest even
 }
 
+// Tile layout: row t (token) holds 64 fp16 = 8 units of 16 bytes; unit c of
+// row t sits at unit c ^ row_swz(t).  row_swz is chosen so that the 16 lanes
+// of every access pattern used below hit distinct banks: 16 chunks of one
+// row (gather stores, V operand reads), the 8-row passes of the score
+// operand reads (rows 4(r&3)+(r>>2)), and 8 units of one row (hot stores).
+__device__ __forceinline__ int row_swz(int t) { return ((t >> 2) & 3) | ((t & 1) << 2); }
+// byte offset of 8-byte chunk c (0..15) of row t
+__device__ __forceinline__ int tile_chunk(int t, int c) {
+  return t * 128 + ((((c >> 1) ^ row_swz(t)) << 4) | ((c & 1) << 3));
+}
+
+// LDS byte address of the codebook entry selected by byte k of the code word
+// w: code * 256 + lc.byte0 (the lane's subspace slot) + lc.byte2 * 65536 (the
+// K or V table).  v_perm_b32 byte selectors: 4 -> lc.byte0, k -> w.byte k,
+// 6 -> lc.byte2, 12 -> 0x00.
+__device__ __forceinline__ uint32_t entry_addr(uint32_t w, uint32_t lc, int k) {
+  return __builtin_amdgcn_perm(lc, w, 0x0C060004u | ((uint32_t)k << 8));
+}
+
 struct TileSrc {
-  int kind;        // 0 hot, 1 segment
+  int kind;        // 0 hot, 1 segment, -1 idle slot
   int seg;         // segment index
   int off;         // first token of the tile inside its source
   int count;       // valid tokens (1..32)
   int pos0;        // window position of the tile's first token
 };
-
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ const void* uni(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
-}
 
 // Global-address-space views: loads through these are global_load (counted by
 // vmcnt only), never flat loads, which would also count against lgkmcnt and
@@ -171,7 +180,7 @@ struct TileRegs {
   uint32_t sval;  // KS/2 fp16 values
 };
 
-// Issue one tile's loads.  The same loads are issued for every slot (invalid
+// Issue one tile's loads.  The same loads are issued for every slot (idle
 // and hot slots read a dummy address), so the compiler can count outstanding
 // loads exactly and wait only for the tile about to be used.
 template <int M, bool RVQ, int KS>
@@ -213,63 +222,55 @@ __device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc
 // Copy one exact (hot) tile into the wave's LDS tile: rows [off, off+count)
 // of hot[...][D]; rows past count -> 0.  All four loads are issued before any
 // is used (rows past count re-read the last valid row and are zeroed after).
-__device__ __forceinline__ void build_hot_tile(uint16_t* __restrict__ tile, const TileSrc& src,
+__device__ __forceinline__ void build_hot_tile(uint8_t* __restrict__ tile, const TileSrc& src,
                                                const uint16_t* __restrict__ hot, int lane) {
   uint4 v[4];
-  const int c16 = lane & 7;
+  const int u16 = lane & 7;  // 16-byte unit of the row
 #pragma unroll
   for (int k4 = 0; k4 < 4; ++k4) {
     const int row = min((lane >> 3) + 8 * k4, src.count - 1);
-    v[k4] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + c16 * 8);
+    v[k4] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + u16 * 8);
   }
 #pragma unroll
   for (int k4 = 0; k4 < 4; ++k4) {
     const int row = (lane >> 3) + 8 * k4;
     if (row >= src.count) v[k4] = make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint2*>(tile + chunk_off(row, 2 * c16)) = make_uint2(v[k4].x, v[k4].y);
-    *reinterpret_cast<uint2*>(tile + chunk_off(row, 2 * c16 + 1)) = make_uint2(v[k4].z, v[k4].w);
+    *reinterpret_cast<uint4*>(tile + row * 128 + ((u16 ^ row_swz(row)) << 4)) = v[k4];
   }
 }
 
-// Build one reconstructed K^ or V^ tile in LDS (per wave) from prefetched codes.
+// Build one reconstructed K^ or V^ tile in the wave's LDS tile from prefetched
+// codes.  M = 16: lane (j, m) = (lane / 16, lane % 16) gathers the 8-byte
+// entry of subspace m for tokens 4i + j; M = 8: lane (lane / 8, lane % 8)
+// gathers 16-byte entries for tokens 8i + j.  waddr holds the lane's store
+// offsets for the row patterns of consecutive i (4 for M = 16, 2 for M = 8).
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void build_tile(uint16_t* __restrict__ tile, const TileSrc& src,
-                                           const TileRegs<M, RVQ, KS>& regs, const uint16_t* __restrict__ cb_pq,
-                                           const uint16_t* __restrict__ cb_rvq, int C, int Cr, int lane) {
-  constexpr int d = kD / M;
-  constexpr int TPI = 64 / M;
-  constexpr int IPT = kTile / TPI;
-  const uint32_t* pc = regs.pq;
-  const uint32_t* rc = regs.rvq;
-  const int j = lane / M;
-  const int m = lane % M;
+__device__ __forceinline__ void build_tile(const uint8_t* __restrict__ lds, uint8_t* __restrict__ tile,
+                                           const TileSrc& src, const TileRegs<M, RVQ, KS>& regs, uint32_t lc,
+                                           const int (&waddr)[4], int lane) {
+  if constexpr (M == 16) {
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int t = TPI * i + j;
-    // every code byte indexes a 256-entry LDS table (entries >= C are zero)
-    const uint32_t code = (pc[i >> 2] >> ((i & 3) * 8)) & 0xffu;
-    const uint16_t* ep = cb_pq + (code * M + m) * d;
-    if constexpr (d == 4) {
-      uint2 e = *reinterpret_cast<const uint2*>(ep);
-      if (RVQ) {
-        const uint32_t rcode = (rc[i >> 2] >> ((i & 3) * 8)) & 0xffu;
-        const uint2 r = *reinterpret_cast<const uint2*>(cb_rvq + (rcode * M + m) * d);
+    for (int i = 0; i < 8; ++i) {
+      uint2 e = *reinterpret_cast<const uint2*>(lds + entry_addr(regs.pq[i >> 2], lc, i & 3));
+      if constexpr (RVQ) {
+        const uint2 r = *reinterpret_cast<const uint2*>(lds + entry_addr(regs.rvq[i >> 2], lc, i & 3) + kRvqSlot);
         e.x = add_h2(e.x, r.x);
         e.y = add_h2(e.y, r.y);
       }
-      *reinterpret_cast<uint2*>(tile + chunk_off(t, m)) = e;
-    } else {
-      uint4 e = *reinterpret_cast<const uint4*>(ep);
-      if (RVQ) {
-        const uint32_t rcode = (rc[i >> 2] >> ((i & 3) * 8)) & 0xffu;
-        const uint4 r = *reinterpret_cast<const uint4*>(cb_rvq + (rcode * M + m) * d);
+      *reinterpret_cast<uint2*>(tile + waddr[i & 3] + i * 512) = e;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint4 e = *reinterpret_cast<const uint4*>(lds + entry_addr(regs.pq[0], lc, i));
+      if constexpr (RVQ) {
+        const uint4 r = *reinterpret_cast<const uint4*>(lds + entry_addr(regs.rvq[0], lc, i) + kRvqSlot);
         e.x = add_h2(e.x, r.x);
         e.y = add_h2(e.y, r.y);
         e.z = add_h2(e.z, r.z);
         e.w = add_h2(e.w, r.w);
       }
-      *reinterpret_cast<uint2*>(tile + chunk_off(t, 2 * m)) = make_uint2(e.x, e.y);
-      *reinterpret_cast<uint2*>(tile + chunk_off(t, 2 * m + 1)) = make_uint2(e.z, e.w);
+      *reinterpret_cast<uint4*>(tile + waddr[i & 1] + i * 1024) = e;
     }
   }
   if constexpr (KS > 0) {
@@ -281,17 +282,19 @@ __device__ __forceinline__ void build_tile(uint16_t* __restrict__ tile, const Ti
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int idx = (regs.sidx >> (8 * e)) & (kD - 1);
-        const int o = chunk_off(t, idx >> 2) + (idx & 3);
-        tile[o] = hadd_bits(tile[o], (uint16_t)(regs.sval >> (16 * e)));
+        uint16_t* o = reinterpret_cast<uint16_t*>(tile + tile_chunk(t, idx >> 2) + (idx & 3) * 2);
+        *o = hadd_bits(*o, (uint16_t)(regs.sval >> (16 * e)));
       }
     }
   }
 }
 
 template <int M, bool RVQ, int KS, int NHG>
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(kThreads, 1)
 fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
-  extern __shared__ uint16_t lds[];
+  // static allocation: its base address is known at compile time, so LDS
+  // addresses built in registers need no base add
+  __shared__ __align__(16) uint8_t lds[kLdsBytes];
   // XCD-aware block mapping: consecutive hardware block ids go to different
   // XCDs; give each XCD a contiguous range of (sequence, head, split) units so
   // that one sequence's codebooks are fetched into one L2.
@@ -306,36 +309,26 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int G = p.q_heads / p.kv_heads;
   const int C = p.fmt.pq_centroids, Cr = RVQ ? p.fmt.rvq_centroids : 0;
-  (void)C;
-  (void)Cr;
+  constexpr int d = kD / M;
 
-  // LDS: 256-entry codebook tables (K-PQ, V-PQ[, K-RVQ, V-RVQ]), then the
-  // per-wave tiles and P buffers
-  uint16_t* cbKp = lds;
-  uint16_t* cbVp = cbKp + kCbHalves;
-  uint16_t* cbKr = cbVp + kCbHalves;
-  uint16_t* cbVr = cbKr + (RVQ ? kCbHalves : 0);
-  uint16_t* tiles = cbVr + (RVQ ? kCbHalves : 0);
-  uint16_t* tile = tiles + wave * kTileHalves;
-  uint16_t* pb = tiles + kWaves * kTileHalves + wave * (NHG * 128);
+  uint8_t* tile = lds + kTilesBase + wave * kTileBytes;
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.workspace);  // readable scratch for idle slots
   const cseg segs = (cseg)(p.segments + (int64_t)b * p.max_segments);
   const int nseg = p.num_segments ? p.num_segments[b] : 0;
 
-  // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [e][m][d]
+  // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [table][e][PQ m | RVQ m][d]
   {
-    constexpr int d = kD / M;
     const uint16_t* srcs[4] = {(const uint16_t*)p.k_pq_cb + (int64_t)b * p.pq_cb_stride,
                                (const uint16_t*)p.v_pq_cb + (int64_t)b * p.pq_cb_stride,
                                RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : nullptr,
                                RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : nullptr};
-    uint16_t* dsts[4] = {cbKp, cbVp, cbKr, cbVr};
 #pragma unroll
     for (int c = 0; c < (RVQ ? 4 : 2); ++c) {
       const int n = c < 2 ? C : Cr;
-      for (int idx = threadIdx.x; idx < M * 256; idx += blockDim.x) {
-        const int m = idx / 256, e = idx % 256;
-        uint16_t* t = dsts[c] + (e * M + m) * d;
+      uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
+      for (int idx = threadIdx.x; idx < M * 256; idx += kThreads) {
+        const int e = idx / M, m = idx % M;  // consecutive lanes store consecutive slots of one entry
+        uint8_t* t = dst + e * kEntryBytes + m * d * 2;
         if constexpr (d == 4) {
           uint2 v = make_uint2(0, 0);
           if (e < n) v = *reinterpret_cast<const uint2*>(srcs[c] + ((int64_t)m * n + e) * d);
@@ -349,26 +342,70 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     }
   }
 
-  // ---- query registers (4x4x4 A operand): lane l -> head group hgl, head r = l & 3
-  const int hgl = (NHG == 2) ? (lane >> 5) : 0;
-  const int myhead = hgl * 4 + (lane & 3);
-  half4_t qa[16];
+  // ---- lane constants
+  const int g = lane >> 4;   // k-group of the 16x16 MFMA operands
+  const int n = lane & 15;   // column (B, D) / row (A)
+  // gather lane (jg, mg) and its codebook slot; store offsets for the row
+  // patterns of consecutive gathers
+  const int jg = lane / M, mg = lane % M;
+  const uint32_t lc_k = (uint32_t)(mg * d * 2);
+  const uint32_t lc_v = lc_k | (1u << 16);
+  int waddr[4];
+  if constexpr (M == 16) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      waddr[a] = jg * 128 + (((((mg >> 1) ^ ((jg & 1) << 2)) ^ a) << 4) | ((mg & 1) << 3));
+  } else {
+#pragma unroll
+    for (int a = 0; a < 2; ++a) waddr[a] = jg * 128 + ((mg ^ (((2 * a + (jg >> 2)) & 3) | ((jg & 1) << 2))) << 4);
+    waddr[2] = waddr[0];
+    waddr[3] = waddr[1];
+  }
+  // V operand reads of P.V MFMA i: row 4i + g, chunk n (same pattern as the M = 16 stores)
+  int paddr[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) paddr[a] = g * 128 + (((((n >> 1) ^ ((g & 1) << 2)) ^ a) << 4) | ((n & 1) << 3));
+  // score operand reads: row 4(n&3) + (n>>2) of half u, 16-byte unit 4c + g
+  int raddr[2];
   {
-    const bool qv = myhead < G;
-    const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + h * G + (qv ? myhead : 0)) * kD;
+    const int f = (n & 3) | (((n >> 2) & 1) << 2);
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      uint2 w = qv ? *reinterpret_cast<const uint2*>(qrow + 4 * s) : make_uint2(0, 0);
-      qa[s] = __builtin_bit_cast(half4_t, w);
+    for (int c = 0; c < 2; ++c) raddr[c] = (4 * (n & 3) + (n >> 2)) * 128 + (((4 * c + g) ^ f) << 4);
+  }
+  // B operand of P.V: the lane's fp16 probability at coordinate n & 3 of its k-group
+  const int ep = n & 3;
+  const uint32_t sel_lo = ep == 0 ? 0x0C0C0100u : (ep == 1 ? 0x01000C0Cu : 0x0C0C0C0Cu);
+  const uint32_t sel_hi = ep == 2 ? 0x0C0C0100u : (ep == 3 ? 0x01000C0Cu : 0x0C0C0C0Cu);
+
+  // ---- query operands and per-head state: lane column n serves head hg*4 + n/4
+  half8_t qb[NHG][2];
+  float bias[NHG], bias_m[NHG], m_run[NHG];
+  int qpl[NHG];
+  float4_t acc[NHG], lsum[NHG];
+#pragma unroll
+  for (int hg = 0; hg < NHG; ++hg) {
+    const int hh = hg * 4 + (n >> 2);
+    const bool valid = hh < G;
+    const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + h * G + (valid ? hh : 0)) * kD;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      uint4 w = valid ? *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g) : make_uint4(0, 0, 0, 0);
+      qb[hg][c] = __builtin_bit_cast(half8_t, w);
     }
+    bias[hg] = valid ? 0.f : -__builtin_inff();
+    bias_m[hg] = valid ? __builtin_inff() : -__builtin_inff();  // forces the first max update
+    m_run[hg] = -__builtin_inff();
+    qpl[hg] = (p.causal && p.qpos && valid) ? p.qpos[(int64_t)b * p.q_heads + h * G + hh] : 0x7fffffff;
+    acc[hg] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lsum[hg] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
-  int qp[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hh = hgl * 4 + r;
-    qp[r] = (p.causal && p.qpos && hh < G) ? p.qpos[(int64_t)b * p.q_heads + h * G + hh] : 0x7fffffff;
-  }
+  // smallest query position of this KV head's query heads (uniform)
+  int qmin = 0x7fffffff;
+  if (p.causal && p.qpos)
+    for (int hh = 0; hh < G; ++hh) qmin = min(qmin, p.qpos[(int64_t)b * p.q_heads + h * G + hh]);
   const float scale_log2 = p.scale * kLog2e;
+  const half4_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+
   const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
   int total_tiles = hot_tiles;
   for (int i = 0; i < nseg; ++i) total_tiles += (segs[i].len + kTile - 1) / kTile;
@@ -377,20 +414,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
   const uint16_t* hotv = (const uint16_t*)p.hot_v + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
 
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m_run[r] = -__builtin_inff();
-    l_run[r] = 0.f;
-  }
-  float4_t acc[NHG];
-#pragma unroll
-  for (int g = 0; g < NHG; ++g) acc[g] = float4_t{0.f, 0.f, 0.f, 0.f};
-
   __syncthreads();
 
-  const int jq = lane >> 4;  // k-group of the 16x16x16 operands
-  const int cq = lane & 15;  // column (B) / row (A)
   using Regs = TileRegs<M, RVQ, KS>;
   // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves
   TileSrc srcs[kDepth];
@@ -412,77 +437,94 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     if constexpr (HOT) {
       build_hot_tile(tile, src, hotk, lane);
     } else {
-      build_tile<M, RVQ, KS>(tile, src, rk, cbKp, cbKr, C, Cr, lane);
+      build_tile<M, RVQ, KS>(lds, tile, src, rk, lc_k, waddr, lane);
     }
     wave_sync();
-    float4_t sc = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int trow = lane & (kTile - 1);
+    float4_t sc[NHG][2];
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const half4_t kv = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(tile + chunk_off(trow, s)));
-      sc = __builtin_amdgcn_mfma_f32_4x4x4f16(qa[s], kv, sc, 0, 0, 0);
-    }
-    // ---- online softmax (lane = token trow, register r = head hgl*4 + r)
-    const int pos = src.pos0 + trow;
-    float corr[4];
-    uint16_t p16[4];
-    bool rescaled = false;
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool allowed = trow < src.count && (hgl * 4 + r) < G && pos >= 0 && pos <= qp[r];
-      const float sv = allowed ? sc[r] * scale_log2 : -__builtin_inff();
-      // The running max only moves when some lane exceeds it; most tiles skip
-      // the cross-lane reduction and the rescale (any max gives the same
-      // softmax, the running one only keeps exp2 in range).
-      float mn = m_run[r];
-      corr[r] = 1.f;
-      if (__ballot(sv > mn)) {
-        mn = fmaxf(m_run[r], max32(sv));
-        corr[r] = (m_run[r] > -__builtin_inff()) ? __builtin_amdgcn_exp2f(m_run[r] - mn) : 0.f;
-        rescaled = true;
+      for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const half8_t a = *reinterpret_cast<const half8_t*>(tile + raddr[c] + u * 2048);
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[hg][c], sc[hg][u], 0, 0, 0);
       }
-      const float pv = allowed ? __builtin_amdgcn_exp2f(sv - mn) : 0.f;
-      p16[r] = f2h(pv * kPScale);
-      const float pr = h2f(p16[r]) * kPScaleInv;
-      l_run[r] = l_run[r] * corr[r] + pr;  // per-lane partial sum, reduced once at the end
-      m_run[r] = mn;
     }
-    if (NHG == 2 || lane < 32) {
+    // ---- online softmax: lane (g, n), register i of half u = token 16u + 4i + g
+    // uniform: nothing masked (a segment may start before the window, with
+    // negative positions for the tokens to skip)
+    const bool full = src.count == kTile && src.pos0 >= 0 && src.pos0 + kTile - 1 <= qmin;
+    uint32_t pbl[NHG][8], pbh[NHG][8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) pb[((hgl * 4 + (trow & 3)) * 4 + r) * 8 + (trow >> 2)] = p16[r];
+    for (int hg = 0; hg < NHG; ++hg) {
+      float arg[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) arg[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias_m[hg]);
+      if (!full) {  // uniform: partial tile or causal boundary
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
+          const int pos = src.pos0 + tok;
+          arg[r] = (tok < src.count && pos >= 0 && pos <= qpl[hg]) ? arg[r] : -__builtin_inff();
+        }
+      }
+      bool up = false;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) up |= arg[r] > kPScaleLog2;
+      // The running max only moves when some score exceeds it; most tiles
+      // skip the cross-lane reduction and the rescale (any max gives the same
+      // softmax, the running one only keeps exp2 in range).
+      if (__builtin_amdgcn_ballot_w64(up)) {
+        float mx = -__builtin_inff();
+        float sv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
+          sv[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]);
+          const int pos = src.pos0 + tok;
+          sv[r] = (full || (tok < src.count && pos >= 0 && pos <= qpl[hg])) ? sv[r] : -__builtin_inff();
+          mx = fmaxf(mx, sv[r]);
+        }
+        mx = xmax32(xmax16(mx));  // the 4 k-groups holding this head's tokens
+        const float mn = fmaxf(m_run[hg], mx);
+        const float corr = mn == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m_run[hg] - mn);
+        acc[hg] *= corr;
+        lsum[hg] *= corr;
+        m_run[hg] = mn;
+        // exp2 argument = score - max + 14; a head with nothing allowed yet
+        // keeps -inf (its scores are -inf, so its probabilities stay 0)
+        const float dm = mn == -__builtin_inff() ? 0.f : kPScaleLog2 - mn;
+        bias_m[hg] = mn == -__builtin_inff() ? -__builtin_inff() : bias[hg] + dm;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) arg[r] = sv[r] + dm;
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(arg[r]);
+        const uint32_t h16 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)pv);
+        pbl[hg][r] = __builtin_amdgcn_perm(0u, h16, sel_lo);
+        pbh[hg][r] = __builtin_amdgcn_perm(0u, h16, sel_hi);
+      }
     }
     wave_sync();
     // ---- V^ tile
     if constexpr (HOT) {
       build_hot_tile(tile, src, hotv, lane);
     } else {
-      build_tile<M, RVQ, KS>(tile, src, rv, cbVp, cbVr, C, Cr, lane);
+      build_tile<M, RVQ, KS>(lds, tile, src, rv, lc_v, waddr, lane);
     }
     wave_sync();
-    // ---- rescale accumulators and P.V
+    // ---- P.V and the denominator; P.V MFMA i covers tokens 4i .. 4i+3
 #pragma unroll
-    for (int g = 0; g < NHG; ++g) {
-      const int hr = cq >> 2;
-      if (rescaled) {
-        float cg[4];
+    for (int i = 0; i < 8; ++i) {
+      const half4_t av = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(tile + paddr[i & 3] + i * 512));
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          cg[r] = (NHG == 1) ? corr[r]
-                             : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr[r]), g * 32));
-        const float f = hr == 0 ? cg[0] : hr == 1 ? cg[1] : hr == 2 ? cg[2] : cg[3];
-        acc[g] *= f;
-      }
-      const uint4 pw = *reinterpret_cast<const uint4*>(pb + ((g * 4 + jq) * 4 + hr) * 8);
-      const uint32_t pws[4] = {pw.x, pw.y, pw.z, pw.w};
-      const int u = cq & 3;
-#pragma unroll
-      for (int i = 0; i < kTile / 4; ++i) {
-        const half4_t av =
-            __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(tile + chunk_off(4 * i + jq, cq)));
-        const uint32_t ph = (pws[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-        const uint32_t sh = ph << ((u & 1) * 16);
-        const uint2 bw = (u < 2) ? make_uint2(sh, 0u) : make_uint2(0u, sh);
-        acc[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, __builtin_bit_cast(half4_t, bw), acc[g], 0, 0, 0);
+      for (int hg = 0; hg < NHG; ++hg) {
+        const half4_t bw = __builtin_bit_cast(half4_t, make_uint2(pbl[hg][i], pbh[hg][i]));
+        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bw, acc[hg], 0, 0, 0);
+        lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, bw, lsum[hg], 0, 0, 0);
       }
     }
     wave_sync();
@@ -512,22 +554,18 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   float* red_l = red + kWaves * 8;
   float* red_a = red + kWaves * 16;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) l_run[r] = sum32(l_run[r]);
-  if (lane == 0 || (NHG == 2 && lane == 32)) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      red_m[wave * 8 + hgl * 4 + r] = m_run[r];
-      red_l[wave * 8 + hgl * 4 + r] = l_run[r];
+  for (int hg = 0; hg < NHG; ++hg) {
+    const int hh = hg * 4 + (n >> 2);
+    if (g == 0 && ep == 0) {
+      red_m[wave * 8 + hh] = m_run[hg];
+      red_l[wave * 8 + hh] = lsum[hg][0];
     }
-  }
+    // D rows 4g + r = subspace m, column n = (head, coordinate ep): dim 4m + ep
 #pragma unroll
-  for (int g = 0; g < NHG; ++g) {
-    const int head = g * 4 + (cq >> 2);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red_a[(wave * 8 + head) * kD + 16 * jq + 4 * r + (cq & 3)] = acc[g][r] * kPScaleInv;
+    for (int r = 0; r < 4; ++r) red_a[(wave * 8 + hh) * kD + 4 * (4 * g + r) + ep] = acc[hg][r];
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * kD; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
     const int head = idx / kD, c = idx % kD;
     float Mx = -__builtin_inff();
     for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, red_m[w * 8 + head]);
@@ -555,12 +593,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   }
 }
 
-size_t fused_lds_bytes(const rfsn_format& f, int nhg) {
-  size_t cb = (size_t)(f.rvq_subspaces > 0 ? 4 : 2) * kCbHalves * 2;
-  size_t t = (size_t)kWaves * kTileHalves * 2 + (size_t)kWaves * nhg * 128 * 2;
-  size_t red = (size_t)kWaves * 16 * 4 + (size_t)kWaves * 8 * kD * 4;
-  return (cb + t) > red ? (cb + t) : red;
-}
+static_assert((size_t)kWaves * 16 * 4 + (size_t)kWaves * 8 * kD * 4 <= kLdsBytes,
+              "the wave combine reuses the codebook LDS");
 
 int total_tiles_host(const rfsn_fused_params* p) {
   // upper bound: hot tiles + tiles of max_tokens encoded tokens split over segments
@@ -573,7 +607,7 @@ int auto_splits(const rfsn_fused_params* p) {
   if (p->splits > 0) return p->splits;
   const int units = p->batch * p->kv_heads;
   const int tiles = total_tiles_host(p);
-  int s = (256 + units - 1) / units;          // one block per CU (LDS-bound occupancy)
+  int s = (256 + units - 1) / units;                // one block per CU (LDS-bound occupancy)
   const int max_s = (tiles + kWaves - 1) / kWaves;  // at least one tile per wave
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
@@ -586,11 +620,8 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   const int tiles = total_tiles_host(p);
   const int tps = (tiles + splits - 1) / splits;
   const int blocks = p->batch * p->kv_heads * splits;
-  const size_t lds = fused_lds_bytes(p->fmt, NHG);
-  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return fail(RFSN_ERR_HIP, std::string("fused: hipFuncSetAttribute: ") + hipGetErrorString(e));
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, s, *p, splits, tps, blocks);
+  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG>;  // 160 KB of static LDS
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kThreads), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
   if (st || splits == 1) return st;
   return launch_merge(reinterpret_cast<const float*>(reinterpret_cast<const char*>(p->workspace) + kDummyBytes),
