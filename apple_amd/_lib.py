@@ -71,6 +71,7 @@ SIGNATURES = {
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),
     "rfsn_rvq_encode_full": (i32, [vp, i64, i32, vp, i64, vp, i32, i32, vp, vp]),
     "rfsn_decode": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, i64, i32, vp]),
+    "rfsn_sparse_fold": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, vp]),
     "rfsn_decode_ref": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, i64, i32, i32, vp, vp, vp]),
     "rfsn_attention_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "rfsn_blockwise_attention": (i32, [vp, i32, i32, i32, vp, vp, i64, i32, i64, i64, f32, i32, vp, vp, vp, sz, vp]),

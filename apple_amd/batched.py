@@ -7,7 +7,9 @@ cache.  Here the HBM image of B sequences lives in shared device buffers:
 
 * hot tier: ``hot_k / hot_v`` fp16 ``[B, Hkv, hot_cap, D]`` (newest tokens);
 * warm tier: PQ / RVQ codes in the tiled layout ``[B, Hkv, cap*M]`` and the
-  sparse residual ``[B, Hkv, cap, k]`` (u8 index, fp16 value);
+  sparse residual ``[B, Hkv, cap, k]`` (u8 index, fp16 value), plus the
+  corrected coordinates fp16(K[idx] + val) the fused kernel streams in place
+  of the residual values;
 * codebooks per sequence, K and V separately: ``[B, M, C, d]``.
 
 Window order per sequence is warm (positions 0..W-1) then hot, the recency
@@ -57,6 +59,8 @@ class RFSNBatchedKVCache:
                                if fmt.sparse_k else None)
             c["sparse_val"] = (torch.zeros((B, H, cap, fmt.sparse_k), dtype=torch.float16, device=dev)
                                if fmt.sparse_k else None)
+            # corrected coordinates fp16(K[idx] + val): the sparse values the fused kernel streams
+            c["sparse_fold"] = torch.zeros_like(c["sparse_val"]) if fmt.sparse_k else None
             self.codes[kv] = c
         M, Cn, d = fmt.pq_subspaces, fmt.pq_centroids, D // fmt.pq_subspaces
         self.cb = {"k_pq": torch.zeros((B, M, Cn, d), dtype=torch.float16, device=dev)}
@@ -103,6 +107,10 @@ class RFSNBatchedKVCache:
             if fmt.sparse_k:
                 c["sparse_idx"][b, :, :nw] = out["sparse_idx"].view(self.H, nw, -1)
                 c["sparse_val"][b, :, :nw] = out["sparse_val"].view(self.H, nw, -1)
+                fold = K.sparse_fold(fmt, out["pq"], qz.pq.codebooks, out.get("rvq"),
+                                     qz.rvq.codebooks if fmt.rvq_subspaces else None, out["sparse_idx"],
+                                     out["sparse_val"])
+                c["sparse_fold"][b, :, :nw] = fold.view(self.H, nw, -1)
         self.num_hot[b] = nh
         self.num_warm[b] = nw
         self.quantizers[b] = (key_quantizer, value_quantizer)
@@ -113,8 +121,8 @@ class RFSNBatchedKVCache:
             t = K.SegmentTable(self.batch)
             for b in range(self.batch):
                 if self.num_warm[b]:
-                    kc = {k: (None if v is None else v[b]) for k, v in self.codes["k"].items()}
-                    vc = {k: (None if v is None else v[b]) for k, v in self.codes["v"].items()}
+                    kc = {k: (None if v is None else v[b]) for k, v in _kernel_view(self.codes["k"]).items()}
+                    vc = {k: (None if v is None else v[b]) for k, v in _kernel_view(self.codes["v"]).items()}
                     t.add(b, kc, vc, self.warm_cap, self.num_warm[b], 0)
             self._table = (t, t.to_device(self.device))
         return self._table
@@ -179,6 +187,12 @@ class RFSNBatchedKVCache:
         return K.decode(f, pq.reshape(self.H * nw, -1), qz.pq.codebooks,
                         None if rvq is None else rvq.reshape(self.H * nw, -1),
                         qz.rvq.codebooks if f.rvq_subspaces else None, sidx, sval)
+
+
+def _kernel_view(c: Dict[str, Optional[torch.Tensor]]) -> Dict[str, Optional[torch.Tensor]]:
+    """The arrays the fused kernel streams: tiled codes, sparse indices and
+    the corrected coordinates as its sparse values."""
+    return {"pq": c["pq"], "rvq": c["rvq"], "sparse_idx": c["sparse_idx"], "sparse_val": c["sparse_fold"]}
 
 
 def untile(tiled: torch.Tensor, M: int, T: int) -> torch.Tensor:

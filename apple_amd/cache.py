@@ -67,7 +67,10 @@ def _pair(q: QuantizerArg) -> Tuple[HybridQuantizerMLX, HybridQuantizerMLX]:
 
 
 class TiledCodes:
-    """Device codes of the subspace format in the fused kernel's tiled layout."""
+    """Device codes of the subspace format in the fused kernel's tiled layout.
+    Its ``sparse_val`` holds the corrected coordinates fp16(K[idx] + val)
+    (``kernels.sparse_fold``), which the kernel stores over the reconstructed
+    coordinate; the reference-layout stores keep the residuals."""
 
     def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0):
         self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
@@ -101,9 +104,16 @@ class TiledCodes:
         self.t, self.cap = new, cap
 
     def append(self, pq: torch.Tensor, rvq: Optional[torch.Tensor], sidx: Optional[torch.Tensor],
-               sval: Optional[torch.Tensor]) -> None:
-        """Append plain codes [H, T, *] (device) at token ``len``."""
+               sval: Optional[torch.Tensor], pq_cb: Optional[torch.Tensor] = None,
+               rvq_cb: Optional[torch.Tensor] = None) -> None:
+        """Append plain codes [H, T, *] (device) at token ``len``; the sparse
+        residuals ``sval`` are folded into corrected coordinates with the
+        stream's codebooks."""
         H, T, _ = pq.shape
+        if self.fmt.sparse_k and T:
+            f = self.fmt
+            flat = lambda t: None if t is None else t.reshape(H * T, -1)
+            sval = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval)).view(H, T, -1)
         need = self.len + T
         if need > self.cap:
             self._alloc(max(need, 2 * self.cap))
@@ -248,9 +258,9 @@ class RFSNv10KVCacheMLX:
             return
         if self._warm_tiled is None:
             self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
-        for tiled, store in zip(self._warm_tiled, (ck, cv)):
+        for tiled, store, qz in zip(self._warm_tiled, (ck, cv), (self._kq, self._vq)):
             if self._subspace:
-                tiled.append(*_plain_head_major(store))
+                tiled.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
             else:
                 tiled.append(store.pq_codes.permute(1, 0, 2).contiguous(), None, None, None)
 
@@ -434,9 +444,9 @@ class RFSNv10KVCacheMLX:
         if self._subspace:
             fmt = self._fmt()
             chunk = K.round_up(self.config.chunk_tokens, K.TILE)
-            for name, store in (("key", ck), ("value", cv)):
+            for name, store, qz in (("key", ck, self._kq), ("value", cv, self._vq)):
                 dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk)
-                dev_t.append(*_plain_head_major(store))
+                dev_t.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
                 host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk)
                 for key, t in dev_t.t.items():
                     if t is not None:

@@ -47,6 +47,29 @@ decode_ext_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C
   for (int e = 0; e < 4; ++e) o[e] = r[e];
 }
 
+// One thread per sparse entry (vector v, slot j): the corrected coordinate
+// fp16(K[idx] + val) with K = fp16(base + rvq), i.e. the value the warm decode
+// leaves at coordinate idx (the indices of one vector are distinct).
+__global__ void __launch_bounds__(256)
+sparse_fold_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C, const uint16_t* __restrict__ pq_cb,
+                   const uint8_t* __restrict__ rvq, int Mr, int Cr, const uint16_t* __restrict__ rvq_cb,
+                   const uint8_t* __restrict__ sidx, const uint16_t* __restrict__ sval, int k,
+                   uint16_t* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * k) return;
+  const int64_t v = gid / k;
+  const int i = min((int)sidx[gid], D - 1);
+  const int d = D / M;
+  const int m = i / d;
+  uint16_t val = pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)];
+  if (Mr > 0) {
+    const int dr = D / Mr;
+    const int mr = i / dr;
+    val = hadd_bits(val, rvq_cb[((size_t)mr * Cr + min((int)rvq[v * Mr + mr], Cr - 1)) * dr + (i - mr * dr)]);
+  }
+  out[gid] = hadd_bits(val, sval[gid]);
+}
+
 __global__ void __launch_bounds__(256)
 decode_ref_base_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C,
                        const uint16_t* __restrict__ pq_cb, uint16_t* __restrict__ out) {
@@ -131,6 +154,22 @@ extern "C" int rfsn_decode(const rfsn_format* f, const rfsn_codes* codes, int64_
                      f->rvq_subspaces, f->rvq_centroids, (const uint16_t*)rvq_cb, codes->sparse_idx,
                      (const uint16_t*)codes->sparse_val, f->sparse_k, add_zero, (uint16_t*)out, ldo);
   return check_launch("decode");
+}
+
+extern "C" int rfsn_sparse_fold(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
+                                const void* rvq_cb, void* out, void* stream) {
+  RFSN_REQUIRE(f && codes && codes->pq && pq_cb && out, "sparse_fold: null pointer");
+  RFSN_REQUIRE(f->sparse_k > 0 && codes->sparse_idx && codes->sparse_val, "sparse_fold: no sparse stage");
+  RFSN_REQUIRE(f->head_dim % f->pq_subspaces == 0, "sparse_fold: head_dim must be a multiple of num_subspaces");
+  RFSN_REQUIRE(f->rvq_subspaces == 0 || (codes->rvq && rvq_cb && f->head_dim % f->rvq_subspaces == 0),
+               "sparse_fold: RVQ stage needs codes and codebooks");
+  if (n == 0) return RFSN_OK;
+  const int64_t total = n * f->sparse_k;
+  hipLaunchKernelGGL(sparse_fold_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, n,
+                     f->head_dim, codes->pq, f->pq_subspaces, f->pq_centroids, (const uint16_t*)pq_cb, codes->rvq,
+                     f->rvq_subspaces, f->rvq_centroids, (const uint16_t*)rvq_cb, codes->sparse_idx,
+                     (const uint16_t*)codes->sparse_val, f->sparse_k, (uint16_t*)out);
+  return check_launch("sparse_fold");
 }
 
 extern "C" int rfsn_decode_ref(const uint8_t* pq, int64_t n, int32_t D, int32_t M, int32_t C, const void* pq_cb,

@@ -15,8 +15,8 @@
 //      (code * 256 + subspace slot), and the 16 lanes of an LDS pass read 16
 //      distinct bank pairs.  fp16(base + rvq) on v_pk_add_f16
 //      (quantization.py:317-319) goes to the wave's tile (16-byte units
-//      XOR-swizzled by row); the sparse residual is applied in place,
-//      K[idx] = fp16(K[idx] + val).
+//      XOR-swizzled by row); the sparse stage stores the segment's corrected
+//      coordinates fp16(K[idx] + val) over the reconstructed ones.
 //   2. Scores on MFMA 16x16x32 f16: A = 16 tile rows ordered so that token
 //      16u+4i+g of half u lands in row 4g+i, B = the query heads replicated
 //      over 4 columns each; fp32 accumulation.  Lane (g, n) receives the
@@ -92,11 +92,12 @@ __device__ __forceinline__ uint32_t add_h2(uint32_t a, uint32_t b) {
 }
 
 // Tile layout: row t (token) holds 64 fp16 = 8 units of 16 bytes; unit c of
-// row t sits at unit c ^ row_swz(t).  row_swz is chosen so that the 16 lanes
-// of every access pattern used below hit distinct banks: 16 chunks of one
-// row (gather stores, V operand reads), the 8-row passes of the score
-// operand reads (rows 4(r&3)+(r>>2)), and 8 units of one row (hot stores).
-__device__ __forceinline__ int row_swz(int t) { return ((t >> 2) & 3) | ((t & 1) << 2); }
+// row t sits at unit c ^ row_swz(t).  LDS serves 64 banks (256 bytes) per
+// pass, so a row's parity picks the bank half and row_swz must spread the
+// units of same-parity rows: every pass below is then conflict-free -- two
+// adjacent rows' chunks (gather stores, V operand reads, hot stores) and the
+// 16 rows 4(n&3)+(n>>2) of a score operand read.
+__device__ __forceinline__ int row_swz(int t) { return (t >> 1) & 7; }
 // byte offset of 8-byte chunk c (0..15) of row t
 __device__ __forceinline__ int tile_chunk(int t, int c) {
   return t * 128 + ((((c >> 1) ^ row_swz(t)) << 4) | ((c & 1) << 3));
@@ -123,7 +124,7 @@ struct TileSrc {
 // make every LDS wait drain the prefetched tiles.
 typedef const uint8_t __attribute__((address_space(1)))* gbytes;
 template <class T>
-__device__ __forceinline__ T gload(gbytes base, int64_t off) {
+__device__ __forceinline__ T gload(gbytes base, uint32_t off) {  // base uniform, off per lane
   return *reinterpret_cast<const T __attribute__((address_space(1)))*>(base + off);
 }
 __device__ __forceinline__ gbytes gview(const void* p) { return (gbytes)(p); }
@@ -133,9 +134,37 @@ __device__ __forceinline__ gbytes gview(const void* p) { return (gbytes)(p); }
 // tile up never waits on the vector-memory counter of the prefetched tiles.
 typedef const rfsn_segment __attribute__((address_space(4)))* cseg;
 
-// Tile tt of this (sequence, KV head): hot tiles first, then the segments in order.
+// The pointers and extent of one segment (scalar loads).
+struct SegView {
+  const void* pq[2];  // [K, V]
+  const void* rvq[2];
+  const void* si[2];
+  const void* sv[2];
+  int64_t hs;         // head stride in token rows
+  int len;
+  int pos0;
+};
+__device__ __forceinline__ SegView seg_view(cseg sg) {
+  SegView v;
+  v.pq[0] = sg->k.pq;
+  v.pq[1] = sg->v.pq;
+  v.rvq[0] = sg->k.rvq;
+  v.rvq[1] = sg->v.rvq;
+  v.si[0] = sg->k.sparse_idx;
+  v.si[1] = sg->v.sparse_idx;
+  v.sv[0] = sg->k.sparse_val;
+  v.sv[1] = sg->v.sparse_val;
+  v.hs = sg->head_stride;
+  v.len = sg->len;
+  v.pos0 = sg->pos0;
+  return v;
+}
+
+// Tile tt of this (sequence, KV head): hot tiles first, then the segments in
+// order.  Segment 0 (the only one in the common case) is resolved from
+// registers; later segments walk the table.
 __device__ __forceinline__ TileSrc locate_tile(const rfsn_fused_params& p, cseg segs, int tt, int hot_tiles,
-                                               int nseg) {
+                                               int nseg, const SegView& v0, int seg0_tiles) {
   TileSrc s;
   if (tt < hot_tiles) {
     s.kind = 0;
@@ -148,10 +177,17 @@ __device__ __forceinline__ TileSrc locate_tile(const rfsn_fused_params& p, cseg 
   int r = tt - hot_tiles;
   s.kind = 1;
   s.seg = 0;
+  if (r < seg0_tiles) {
+    s.off = r * kTile;
+    s.count = min(kTile, v0.len - s.off);
+    s.pos0 = v0.pos0 + s.off;
+    return s;
+  }
+  r -= seg0_tiles;
   s.off = 0;
   s.count = 0;
   s.pos0 = 0;
-  for (int i = 0; i < nseg; ++i) {
+  for (int i = 1; i < nseg; ++i) {
     const int len = segs[i].len;
     const int nt = (len + kTile - 1) / kTile;
     if (r < nt) {
@@ -182,38 +218,40 @@ struct TileRegs {
 
 // Issue one tile's loads.  The same loads are issued for every slot (idle
 // and hot slots read a dummy address), so the compiler can count outstanding
-// loads exactly and wait only for the tile about to be used.
+// loads exactly and wait only for the tile about to be used.  Base pointers
+// are uniform (scalar registers); lanes add 32-bit offsets.
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc& src, cseg sg, bool is_k, int h,
-                                          int lane, const uint8_t* dummy) {
+__device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc& src, const SegView& v, int kv,
+                                          int h, int lane, const uint8_t* dummy) {
   constexpr int IPT = TileRegs<M, RVQ, KS>::IPT;
   const bool real = src.kind == 1;
-  const gbytes pq = gview(real ? (const void*)(is_k ? sg->k.pq : sg->v.pq) : (const void*)dummy);
-  const gbytes rq = gview(real && RVQ ? (const void*)(is_k ? sg->k.rvq : sg->v.rvq) : (const void*)dummy);
-  const int64_t hs = real ? sg->head_stride : 0;
-  const int tile_in_seg = real ? src.off / kTile : 0;
-  const int hh = real ? h : 0;
-  const int64_t base = (int64_t)hh * hs * M + (int64_t)tile_in_seg * kTile * M + lane * IPT;
+  const int64_t row = real ? (int64_t)h * v.hs + src.off : 0;  // token row of the tile's first token
+  const gbytes pq = gview(real ? v.pq[kv] : (const void*)dummy) + row * M;
+  const uint32_t lo = (uint32_t)(lane * IPT);
   if constexpr (IPT == 8) {
-    const uint64_t a = gload<uint64_t>(pq, base);
+    const uint64_t a = gload<uint64_t>(pq, lo);
     r.pq[0] = (uint32_t)a;
     r.pq[1] = (uint32_t)(a >> 32);
     if constexpr (RVQ) {
-      const uint64_t c = gload<uint64_t>(rq, base);
+      const gbytes rq = gview(real ? v.rvq[kv] : (const void*)dummy) + row * M;
+      const uint64_t c = gload<uint64_t>(rq, lo);
       r.rvq[0] = (uint32_t)c;
       r.rvq[1] = (uint32_t)(c >> 32);
     }
   } else {
-    r.pq[0] = gload<uint32_t>(pq, base);
-    if constexpr (RVQ) r.rvq[0] = gload<uint32_t>(rq, base);
+    r.pq[0] = gload<uint32_t>(pq, lo);
+    if constexpr (RVQ) {
+      const gbytes rq = gview(real ? v.rvq[kv] : (const void*)dummy) + row * M;
+      r.rvq[0] = gload<uint32_t>(rq, lo);
+    }
   }
   if constexpr (KS > 0) {
     static_assert(KS == 4, "fused kernel carries 4 sparse entries");
-    const gbytes si = gview(real ? (const void*)(is_k ? sg->k.sparse_idx : sg->v.sparse_idx) : (const void*)dummy);
-    const gbytes sv = gview(real ? (const void*)(is_k ? sg->k.sparse_val : sg->v.sparse_val) : (const void*)dummy);
+    const gbytes si = gview(real ? v.si[kv] : (const void*)dummy) + row * KS;
+    const gbytes sv = gview(real ? v.sv[kv] : (const void*)dummy) + row * KS * 2;
     const int t = lane & (kTile - 1);
     const int tc = real ? min(t, src.count - 1) : t;  // rows past count re-read the last row
-    const int64_t e0 = ((int64_t)hh * hs + (real ? src.off : 0) + tc) * KS + (lane >> 5) * 2;
+    const uint32_t e0 = (uint32_t)(tc * KS + (lane >> 5) * 2);
     r.sidx = gload<uint16_t>(si, e0);
     r.sval = gload<uint32_t>(sv, e0 * 2);
   }
@@ -222,7 +260,7 @@ __device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc
 // Copy one exact (hot) tile into the wave's LDS tile: rows [off, off+count)
 // of hot[...][D]; rows past count -> 0.  All four loads are issued before any
 // is used (rows past count re-read the last valid row and are zeroed after).
-__device__ __forceinline__ void build_hot_tile(uint8_t* __restrict__ tile, const TileSrc& src,
+__device__ __forceinline__ void build_hot_tile(uint8_t* __restrict__ lds, int tbase, const TileSrc& src,
                                                const uint16_t* __restrict__ hot, int lane) {
   uint4 v[4];
   const int u16 = lane & 7;  // 16-byte unit of the row
@@ -235,56 +273,97 @@ __device__ __forceinline__ void build_hot_tile(uint8_t* __restrict__ tile, const
   for (int k4 = 0; k4 < 4; ++k4) {
     const int row = (lane >> 3) + 8 * k4;
     if (row >= src.count) v[k4] = make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(tile + row * 128 + ((u16 ^ row_swz(row)) << 4)) = v[k4];
+    *reinterpret_cast<uint4*>(lds + tbase + row * 128 + ((u16 ^ row_swz(row)) << 4)) = v[k4];
   }
 }
 
-// Build one reconstructed K^ or V^ tile in the wave's LDS tile from prefetched
-// codes.  M = 16: lane (j, m) = (lane / 16, lane % 16) gathers the 8-byte
-// entry of subspace m for tokens 4i + j; M = 8: lane (lane / 8, lane % 8)
-// gathers 16-byte entries for tokens 8i + j.  waddr holds the lane's store
-// offsets for the row patterns of consecutive i (4 for M = 16, 2 for M = 8).
+// Codebook entries gathered for one K^ or V^ tile, held in registers until
+// they are summed and stored (the gathers of one tile are issued while the
+// previous phase of the pipeline still computes).
+template <int M, bool RVQ>
+struct RawTile {
+  static constexpr int N = M == 16 ? 8 : 4;  // gathers per lane and stream
+  typedef typename std::conditional<M == 16, uint2, uint4>::type E;
+  E a[N];
+  E b[RVQ ? N : 1];
+};
+
+// Gather one tile's codebook entries.  M = 16: lane (j, m) = (lane / 16,
+// lane % 16) reads the 8-byte entry of subspace m for tokens 4i + j; M = 8:
+// lane (lane / 8, lane % 8) reads 16-byte entries for tokens 8i + j.  One LDS
+// pass serves two adjacent j, which share subspace slots; lanes with odd j
+// therefore read their RVQ entry first (slot half lc1 = +128) and their PQ
+// entry second (lc2), so each pass covers all 64 banks (fp16 addition
+// commutes, the sum is the same).  Without an RVQ stage the upper slot half
+// holds a copy of the PQ table for the odd lanes.
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void build_tile(const uint8_t* __restrict__ lds, uint8_t* __restrict__ tile,
-                                           const TileSrc& src, const TileRegs<M, RVQ, KS>& regs, uint32_t lc,
-                                           const int (&waddr)[4], int lane) {
+__device__ __forceinline__ void gather_tile(const uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs,
+                                            uint32_t lc1, uint32_t lc2, bool odd, RawTile<M, RVQ>& raw) {
+  constexpr int NW = TileRegs<M, RVQ, KS>::NW;
+  using E = typename RawTile<M, RVQ>::E;
+  uint32_t wa[NW], wb[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    if constexpr (RVQ) {
+      wa[w] = odd ? regs.rvq[w] : regs.pq[w];
+      wb[w] = odd ? regs.pq[w] : regs.rvq[w];
+    } else {
+      wa[w] = regs.pq[w];
+      wb[w] = 0;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RawTile<M, RVQ>::N; ++i) {
+    constexpr int per = 4;  // code bytes per word
+    raw.a[i] = *reinterpret_cast<const E*>(lds + entry_addr(wa[i / per], lc1, i % per));
+    if constexpr (RVQ) raw.b[i] = *reinterpret_cast<const E*>(lds + entry_addr(wb[i / per], lc2, i % per));
+  }
+}
+
+// Sum the gathered entries (fp16(base + rvq), quantization.py:317-319), store
+// them to the wave's tile, then store the sparse stage's corrected
+// coordinates over them.  waddr holds the lane's LDS store addresses for the
+// row patterns of consecutive i (4 for M = 16, 2 for M = 8).  A wave's LDS
+// operations execute in issue order, so no wait separates these stores from
+// earlier reads of the tile or later reads of these values.
+template <int M, bool RVQ, int KS>
+__device__ __forceinline__ void store_tile(uint8_t* __restrict__ lds, int tbase, const TileRegs<M, RVQ, KS>& regs,
+                                           const RawTile<M, RVQ>& raw, const int (&waddr)[4], int lane) {
   if constexpr (M == 16) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      uint2 e = *reinterpret_cast<const uint2*>(lds + entry_addr(regs.pq[i >> 2], lc, i & 3));
+      uint2 e = raw.a[i];
       if constexpr (RVQ) {
-        const uint2 r = *reinterpret_cast<const uint2*>(lds + entry_addr(regs.rvq[i >> 2], lc, i & 3) + kRvqSlot);
-        e.x = add_h2(e.x, r.x);
-        e.y = add_h2(e.y, r.y);
+        e.x = add_h2(e.x, raw.b[i].x);
+        e.y = add_h2(e.y, raw.b[i].y);
       }
-      *reinterpret_cast<uint2*>(tile + waddr[i & 3] + i * 512) = e;
+      *reinterpret_cast<uint2*>(lds + waddr[i & 3] + i * 512) = e;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint4 e = *reinterpret_cast<const uint4*>(lds + entry_addr(regs.pq[0], lc, i));
+      uint4 e = raw.a[i];
       if constexpr (RVQ) {
-        const uint4 r = *reinterpret_cast<const uint4*>(lds + entry_addr(regs.rvq[0], lc, i) + kRvqSlot);
-        e.x = add_h2(e.x, r.x);
-        e.y = add_h2(e.y, r.y);
-        e.z = add_h2(e.z, r.z);
-        e.w = add_h2(e.w, r.w);
+        e.x = add_h2(e.x, raw.b[i].x);
+        e.y = add_h2(e.y, raw.b[i].y);
+        e.z = add_h2(e.z, raw.b[i].z);
+        e.w = add_h2(e.w, raw.b[i].w);
       }
-      *reinterpret_cast<uint4*>(tile + waddr[i & 1] + i * 1024) = e;
+      *reinterpret_cast<uint4*>(lds + waddr[i & 1] + i * 1024) = e;
     }
   }
   if constexpr (KS > 0) {
-    // sparse residual in place: K[idx] = fp16(K[idx] + val); the indices of
-    // one token are distinct, so the two lanes of a token never collide
-    wave_sync();
+    // sparse stage: the segment carries the corrected coordinates
+    // fp16(K[idx] + val), stored over the reconstructed ones.  The indices of
+    // one token are distinct, so the two lanes of a token never collide; rows
+    // past count repeat the last row's entries and are masked out of the
+    // softmax.
     const int t = lane & (kTile - 1);
-    if (t < src.count) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int idx = (regs.sidx >> (8 * e)) & (kD - 1);
-        uint16_t* o = reinterpret_cast<uint16_t*>(tile + tile_chunk(t, idx >> 2) + (idx & 3) * 2);
-        *o = hadd_bits(*o, (uint16_t)(regs.sval >> (16 * e)));
-      }
+    for (int e = 0; e < 2; ++e) {
+      const int idx = (regs.sidx >> (8 * e)) & (kD - 1);
+      *reinterpret_cast<uint16_t*>(lds + tbase + tile_chunk(t, idx >> 2) + (idx & 3) * 2) =
+          (uint16_t)(regs.sval >> (16 * e));
     }
   }
 }
@@ -311,20 +390,21 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int C = p.fmt.pq_centroids, Cr = RVQ ? p.fmt.rvq_centroids : 0;
   constexpr int d = kD / M;
 
-  uint8_t* tile = lds + kTilesBase + wave * kTileBytes;
+  const int tbase = kTilesBase + wave * kTileBytes;  // this wave's tile (LDS byte address)
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.workspace);  // readable scratch for idle slots
   const cseg segs = (cseg)(p.segments + (int64_t)b * p.max_segments);
   const int nseg = p.num_segments ? p.num_segments[b] : 0;
 
   // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [table][e][PQ m | RVQ m][d]
+  // (without an RVQ stage the upper slot half holds a second copy of the PQ table)
   {
-    const uint16_t* srcs[4] = {(const uint16_t*)p.k_pq_cb + (int64_t)b * p.pq_cb_stride,
-                               (const uint16_t*)p.v_pq_cb + (int64_t)b * p.pq_cb_stride,
-                               RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : nullptr,
-                               RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : nullptr};
+    const uint16_t* kp = (const uint16_t*)p.k_pq_cb + (int64_t)b * p.pq_cb_stride;
+    const uint16_t* vp = (const uint16_t*)p.v_pq_cb + (int64_t)b * p.pq_cb_stride;
+    const uint16_t* srcs[4] = {kp, vp, RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : kp,
+                               RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : vp};
 #pragma unroll
-    for (int c = 0; c < (RVQ ? 4 : 2); ++c) {
-      const int n = c < 2 ? C : Cr;
+    for (int c = 0; c < 4; ++c) {
+      const int n = (c < 2 || !RVQ) ? C : Cr;
       uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
       for (int idx = threadIdx.x; idx < M * 256; idx += kThreads) {
         const int e = idx / M, m = idx % M;  // consecutive lanes store consecutive slots of one entry
@@ -348,29 +428,33 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // gather lane (jg, mg) and its codebook slot; store offsets for the row
   // patterns of consecutive gathers
   const int jg = lane / M, mg = lane % M;
-  const uint32_t lc_k = (uint32_t)(mg * d * 2);
-  const uint32_t lc_v = lc_k | (1u << 16);
+  const bool odd = (jg & 1) != 0;
+  const uint32_t slot = (uint32_t)(mg * d * 2);
+  const uint32_t lc1_k = slot | (odd ? kRvqSlot : 0u), lc2_k = slot | (odd ? 0u : kRvqSlot);
+  const uint32_t lc1_v = lc1_k | (1u << 16), lc2_v = lc2_k | (1u << 16);
+  // row_swz(4i + j) = 2(i&3) + (j>>1) (M = 16); row_swz(8i + j) = 4(i&1) + (j>>1) (M = 8)
   int waddr[4];
   if constexpr (M == 16) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-      waddr[a] = jg * 128 + (((((mg >> 1) ^ ((jg & 1) << 2)) ^ a) << 4) | ((mg & 1) << 3));
+      waddr[a] = tbase + jg * 128 + ((((mg >> 1) ^ (2 * a + (jg >> 1))) << 4) | ((mg & 1) << 3));
   } else {
 #pragma unroll
-    for (int a = 0; a < 2; ++a) waddr[a] = jg * 128 + ((mg ^ (((2 * a + (jg >> 2)) & 3) | ((jg & 1) << 2))) << 4);
+    for (int a = 0; a < 2; ++a) waddr[a] = tbase + jg * 128 + ((mg ^ (4 * a + (jg >> 1))) << 4);
     waddr[2] = waddr[0];
     waddr[3] = waddr[1];
   }
   // V operand reads of P.V MFMA i: row 4i + g, chunk n (same pattern as the M = 16 stores)
   int paddr[4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) paddr[a] = g * 128 + (((((n >> 1) ^ ((g & 1) << 2)) ^ a) << 4) | ((n & 1) << 3));
-  // score operand reads: row 4(n&3) + (n>>2) of half u, 16-byte unit 4c + g
+  for (int a = 0; a < 4; ++a)
+    paddr[a] = tbase + g * 128 + ((((n >> 1) ^ (2 * a + (g >> 1))) << 4) | ((n & 1) << 3));
+  // score operand reads: row 4(n&3) + (n>>2) of half u (row_swz = 2(n&3) + (n>>3)), 16-byte unit 4c + g
   int raddr[2];
   {
-    const int f = (n & 3) | (((n >> 2) & 1) << 2);
+    const int f = 2 * (n & 3) + (n >> 3);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) raddr[c] = (4 * (n & 3) + (n >> 2)) * 128 + (((4 * c + g) ^ f) << 4);
+    for (int c = 0; c < 2; ++c) raddr[c] = tbase + (4 * (n & 3) + (n >> 2)) * 128 + (((4 * c + g) ^ f) << 4);
   }
   // B operand of P.V: the lane's fp16 probability at coordinate n & 3 of its k-group
   const int ep = n & 3;
@@ -407,8 +491,11 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const half4_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
   const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
-  int total_tiles = hot_tiles;
-  for (int i = 0; i < nseg; ++i) total_tiles += (segs[i].len + kTile - 1) / kTile;
+  SegView v0 = {};
+  if (nseg > 0) v0 = seg_view(segs);
+  const int seg0_tiles = nseg > 0 ? (v0.len + kTile - 1) / kTile : 0;
+  int total_tiles = hot_tiles + seg0_tiles;
+  for (int i = 1; i < nseg; ++i) total_tiles += (segs[i].len + kTile - 1) / kTile;
   const int t_begin = split * tiles_per_split;
   const int t_end = min(total_tiles, t_begin + tiles_per_split);
   const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
@@ -422,41 +509,37 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   Regs kr[kDepth], vr[kDepth];
   auto fetch = [&](TileSrc& s, Regs& rk, Regs& rv, int tt) {
     if (tt < t_end) {
-      s = locate_tile(p, segs, tt, hot_tiles, nseg);
+      s = locate_tile(p, segs, tt, hot_tiles, nseg, v0, seg0_tiles);
     } else {
       s.kind = -1;
       s.seg = 0;
     }
-    const cseg sg = segs + s.seg;
-    load_tile<M, RVQ, KS>(rk, s, sg, true, h, lane, dummy);
-    load_tile<M, RVQ, KS>(rv, s, sg, false, h, lane, dummy);
+    SegView v = v0;
+    if (s.kind == 1 && s.seg != 0) v = seg_view(segs + s.seg);  // uniform, rare
+    load_tile<M, RVQ, KS>(rk, s, v, 0, h, lane, dummy);
+    load_tile<M, RVQ, KS>(rv, s, v, 1, h, lane, dummy);
   };
-  auto process = [&](auto hot_tag, const TileSrc& src, const Regs& rk, const Regs& rv) {
-    constexpr bool HOT = decltype(hot_tag)::value;
-    // ---- K^ tile and scores
-    if constexpr (HOT) {
-      build_hot_tile(tile, src, hotk, lane);
-    } else {
-      build_tile<M, RVQ, KS>(lds, tile, src, rk, lc_k, waddr, lane);
-    }
-    wave_sync();
-    float4_t sc[NHG][2];
+  // scores of the tile in LDS: lane (g, n), register i of half u = token 16u + 4i + g
+  auto scores = [&](float4_t (&sc)[NHG][2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(tile + raddr[c] + u * 2048);
+        const half8_t a = *reinterpret_cast<const half8_t*>(lds + raddr[c] + u * 2048);
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[hg][c], sc[hg][u], 0, 0, 0);
       }
     }
-    // ---- online softmax: lane (g, n), register i of half u = token 16u + 4i + g
+  };
+  // online softmax in base 2; produces the B operands of P.V (probability at
+  // coordinate n & 3 of the lane's k-group)
+  auto softmax = [&](const TileSrc& src, const float4_t (&sc)[NHG][2], uint32_t (&pbl)[NHG][8],
+                     uint32_t (&pbh)[NHG][8]) {
     // uniform: nothing masked (a segment may start before the window, with
     // negative positions for the tokens to skip)
     const bool full = src.count == kTile && src.pos0 >= 0 && src.pos0 + kTile - 1 <= qmin;
-    uint32_t pbl[NHG][8], pbh[NHG][8];
 #pragma unroll
     for (int hg = 0; hg < NHG; ++hg) {
       float arg[8];
@@ -470,13 +553,12 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
           arg[r] = (tok < src.count && pos >= 0 && pos <= qpl[hg]) ? arg[r] : -__builtin_inff();
         }
       }
-      bool up = false;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) up |= arg[r] > kPScaleLog2;
+      const float amax = fmaxf(fmaxf(fmaxf(arg[0], arg[1]), fmaxf(arg[2], arg[3])),
+                               fmaxf(fmaxf(arg[4], arg[5]), fmaxf(arg[6], arg[7])));
       // The running max only moves when some score exceeds it; most tiles
       // skip the cross-lane reduction and the rescale (any max gives the same
       // softmax, the running one only keeps exp2 in range).
-      if (__builtin_amdgcn_ballot_w64(up)) {
+      if (__builtin_amdgcn_ballot_w64(amax > kPScaleLog2)) {
         float mx = -__builtin_inff();
         float sv[8];
 #pragma unroll
@@ -508,41 +590,71 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
         pbh[hg][r] = __builtin_amdgcn_perm(0u, h16, sel_hi);
       }
     }
-    wave_sync();
-    // ---- V^ tile
-    if constexpr (HOT) {
-      build_hot_tile(tile, src, hotv, lane);
-    } else {
-      build_tile<M, RVQ, KS>(lds, tile, src, rv, lc_v, waddr, lane);
-    }
-    wave_sync();
-    // ---- P.V and the denominator; P.V MFMA i covers tokens 4i .. 4i+3
+  };
+  // P.V and the denominator over the V^ tile in LDS; MFMA i covers tokens 4i .. 4i+3
+  auto pv_operands = [&](half4_t (&av)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      av[i] = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(lds + paddr[i & 3] + i * 512));
+  };
+  auto pv = [&](const half4_t (&av)[8], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const half4_t av = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(tile + paddr[i & 3] + i * 512));
 #pragma unroll
       for (int hg = 0; hg < NHG; ++hg) {
         const half4_t bw = __builtin_bit_cast(half4_t, make_uint2(pbl[hg][i], pbh[hg][i]));
-        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bw, acc[hg], 0, 0, 0);
+        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[i], bw, acc[hg], 0, 0, 0);
         lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, bw, lsum[hg], 0, 0, 0);
       }
     }
-    wave_sync();
   };
+
   // Phase 1: exact (hot) tiles, loaded synchronously (a few percent of tiles).
   const int hot_end = min(t_end, hot_tiles);
   for (int tt = t_begin + wave; tt < hot_end; tt += kWaves) {
-    const TileSrc src = locate_tile(p, segs, tt, hot_tiles, nseg);
-    process(std::true_type{}, src, kr[0], vr[0]);
+    const TileSrc src = locate_tile(p, segs, tt, hot_tiles, nseg, v0, seg0_tiles);
+    float4_t sc[NHG][2];
+    uint32_t pbl[NHG][8], pbh[NHG][8];
+    half4_t av[8];
+    build_hot_tile(lds, tbase, src, hotk, lane);
+    wave_sync();
+    scores(sc);
+    softmax(src, sc, pbl, pbh);
+    wave_sync();
+    build_hot_tile(lds, tbase, src, hotv, lane);
+    wave_sync();
+    pv_operands(av);
+    pv(av, pbl, pbh);
+    wave_sync();
   }
-  // Phase 2: encoded tiles, kDepth tiles of codes in flight per wave.
+
+  // Phase 2: encoded tiles, kDepth tiles of codes in flight per wave, and a
+  // software pipeline over the tile's LDS phases: the V^ gathers are issued
+  // under the score MFMAs and the softmax, and the next tile's K^ gathers
+  // under the P.V MFMAs.  LDS operations of a wave execute in order, so the
+  // tile buffer is reused without waits; the compiler's counters only wait
+  // for the data each step consumes.
   const int seg_begin = max(t_begin, hot_tiles);
 #pragma unroll
   for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+  RawTile<M, RVQ> rawk, rawv;
+  gather_tile<M, RVQ, KS>(lds, kr[0], lc1_k, lc2_k, odd, rawk);
   for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
     for (int s = 0; s < kDepth; ++s) {
-      if (srcs[s].kind >= 0) process(std::false_type{}, srcs[s], kr[s], vr[s]);
+      if (srcs[s].kind >= 0) {
+        float4_t sc[NHG][2];
+        uint32_t pbl[NHG][8], pbh[NHG][8];
+        half4_t av[8];
+        store_tile<M, RVQ, KS>(lds, tbase, kr[s], rawk, waddr, lane);
+        scores(sc);
+        gather_tile<M, RVQ, KS>(lds, vr[s], lc1_v, lc2_v, odd, rawv);
+        softmax(srcs[s], sc, pbl, pbh);
+        store_tile<M, RVQ, KS>(lds, tbase, vr[s], rawv, waddr, lane);
+        pv_operands(av);
+        gather_tile<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], lc1_k, lc2_k, odd, rawk);  // next tile
+        pv(av, pbl, pbh);
+      }
       fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
     }
   }

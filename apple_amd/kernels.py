@@ -178,6 +178,26 @@ def decode(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional
     return out
 
 
+def sparse_fold(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional[torch.Tensor],
+                rvq_cb: Optional[torch.Tensor], sparse_idx: torch.Tensor, sparse_val: torch.Tensor) -> torch.Tensor:
+    """Corrected coordinates fp16(K[idx] + val) of the sparse stage, [N, k] fp16:
+    the sparse values the fused kernel's layout carries (a store per entry
+    instead of a read-modify-write)."""
+    _dev(pq, "sparse_fold")
+    pq = _contig(pq)
+    n = pq.shape[0]
+    out = torch.empty((n, fmt.sparse_k), dtype=torch.float16, device=pq.device)
+    if n == 0:
+        return out
+    rvq = None if rvq is None else _contig(rvq)
+    sidx, sval = _contig(sparse_idx), _contig(sparse_val)
+    codes = L.Codes(pq.data_ptr(), L.ptr(rvq), sidx.data_ptr(), sval.data_ptr())
+    f = fmt.c()
+    L.call("rfsn_sparse_fold", C.byref(f), C.byref(codes), n, _contig(pq_cb).data_ptr(),
+           L.ptr(None if rvq_cb is None else _contig(rvq_cb)), out.data_ptr(), _stream(pq))
+    return out
+
+
 def decode_ref(pq: torch.Tensor, pq_cb: torch.Tensor, rvq_codes: torch.Tensor, offsets: torch.Tensor,
                rvq_cb: torch.Tensor) -> torch.Tensor:
     """Reference-format hybrid decode (quantization.py:310-319) -> fp16 [N, D]."""

@@ -111,6 +111,15 @@ int rfsn_decode(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
                 const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, int64_t ldo,
                 int32_t add_zero_correction, void* stream);
 
+/* Corrected coordinates of the sparse stage: out[v][j] = fp16(K[idx] + val)
+ * with K = fp16(base + rvq) and idx = sparse_idx[v][j], val = sparse_val[v][j],
+ * i.e. the value rfsn_decode leaves at coordinate idx.  out is [N][k] fp16.
+ * The fused kernel's segments carry these values in place of the residuals
+ * (rfsn_segment), so that it applies the sparse stage by one store per entry.
+ * No reference symbol (the sparse stage extends quantization.py:317-319). */
+int rfsn_sparse_fold(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
+                     const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, void* stream);
+
 /* Reference-format hybrid decode (quantization.py:310-319): base =
  * C_pq[pq_codes]; corr = fp16(sum_l C_l[rvq_codes[a][l]]) scattered to rows
  * offsets[a]; out = fp16(base + corr) (corr = +0 for inactive rows). */
@@ -153,8 +162,11 @@ int rfsn_pack_codes(const uint8_t* src_dev, int64_t src_head_stride, int64_t T, 
  * A segment is a run of encoded tokens of one sequence for all KV heads.
  * PQ and RVQ codes are in the tiled layout (head h at byte h*head_stride*M
  * resp. h*head_stride*M_r); sparse arrays are plain rows, (head h, token t)
- * at row h*head_stride + t.  head_stride is a multiple of 32.
- * Segment window positions are pos0 .. pos0+len-1 (used by causal masking). */
+ * at row h*head_stride + t.  head_stride is a multiple of 32.  The sparse
+ * values of a segment are the corrected coordinates of rfsn_sparse_fold
+ * (fp16(K[idx] + residual)), not the residuals.
+ * Segment window positions are pos0 .. pos0+len-1 (used by causal masking;
+ * tokens at negative positions are skipped). */
 typedef struct rfsn_segment {
   rfsn_codes k;
   rfsn_codes v;

@@ -85,6 +85,27 @@ def test_warm_encode_bit_exact(device, M, Mr, k):
     assert np.array_equal(H(dec).view(np.uint16), rdec.view(np.uint16))
 
 
+@pytest.mark.parametrize("M,Mr", [(16, 16), (8, 8), (16, 0)])
+def test_sparse_fold_bit_exact(device, M, Mr):
+    """Corrected coordinates fp16(K[idx] + val) equal the warm decode's value
+    at each sparse index."""
+    from apple_amd import kernels as K
+
+    g = rng(200 + M + Mr)
+    n, D, k = 517, 64, 4
+    x = randn16(g, n, D)
+    pq_cb = rand_codebooks(g, M, 256, D // M)
+    rvq_cb = rand_codebooks(g, Mr, 256, D // Mr) * np.float16(0.3) if Mr else None
+    fmt = K.WarmFormat(D, M, 256, Mr, 256 if Mr else 0, k)
+    ref = nx.ext_encode(x, pq_cb, rvq_cb, k)
+    dec = nx.ext_decode(ref["pq_codes"], pq_cb, ref.get("rvq_codes"), rvq_cb, ref["sparse_idx"], ref["sparse_val"])
+    want = np.take_along_axis(dec, ref["sparse_idx"].astype(np.int64), axis=1)
+    got = K.sparse_fold(fmt, T(ref["pq_codes"], device), T(pq_cb, device),
+                        T(ref["rvq_codes"], device) if Mr else None, T(rvq_cb, device) if Mr else None,
+                        T(ref["sparse_idx"], device), T(ref["sparse_val"], device))
+    assert np.array_equal(H(got).view(np.uint16), want.view(np.uint16))
+
+
 @pytest.mark.parametrize("thr", [0.25, 5.0, float("inf"), 0.0])
 def test_rvq_full_bit_exact(device, thr):
     from apple_amd import kernels as K
