@@ -6,24 +6,25 @@
 // reconstructed window to HBM.
 //
 // Work decomposition: one block = (sequence b, KV head h, token split) with
-// 8 waves, two per SIMD; each wave streams 32-token tiles of the split.
-// LDS holds the sequence's codebooks as two 64 KB tables (K, V), entry-major
-// with 256-byte entries [PQ entries of the M subspaces | RVQ entries], then
-// one 4 KB tile per wave (160 KB in total).  Per tile:
-//   1. K^ rows: one lane per (token, subspace) and gather; the LDS address of
-//      a codebook entry is built from the code byte with one v_perm_b32
-//      (code * 256 + subspace slot), and the 16 lanes of an LDS pass read 16
-//      distinct bank pairs.  fp16(base + rvq) on v_pk_add_f16
-//      (quantization.py:317-319) goes to the wave's tile (16-byte units
-//      XOR-swizzled by row); the sparse stage stores the segment's corrected
-//      coordinates fp16(K[idx] + val) over the reconstructed ones.
-//   2. Scores on MFMA 16x16x32 f16: A = 16 tile rows ordered so that token
-//      16u+4i+g of half u lands in row 4g+i, B = the query heads replicated
-//      over 4 columns each; fp32 accumulation.  Lane (g, n) receives the
-//      scores of tokens 16u+4i+g (i = 0..3) for query head n/4.
+// 12 waves, three per SIMD; each wave streams 32-token tiles of the split and
+// passes each through a 2 KB LDS buffer in 16-token halves.  LDS holds the
+// sequence's codebooks as two 64 KB tables (K, V), entry-major with 256-byte
+// entries [PQ entries of the M subspaces | RVQ entries], then the waves'
+// half-tile buffers (152 KB in total).  Per tile:
+//   1. K^ rows, per half: one lane per (token, subspace) and gather; the LDS
+//      address of a codebook entry is built from the code byte with one
+//      v_perm_b32 (code * 256 + subspace slot), and each LDS pass reads all 64
+//      banks.  fp16(base + rvq) on v_pk_add_f16 (quantization.py:317-319)
+//      goes to the wave's buffer (16-byte units XOR-swizzled by row); the
+//      sparse stage stores the segment's corrected coordinates
+//      fp16(K[idx] + val) over the reconstructed ones.
+//   2. Scores on MFMA 16x16x32 f16: A = the 16 buffer rows ordered so that
+//      token 16u+4i+g of half u lands in row 4g+i, B = the query heads
+//      replicated over 4 columns each; fp32 accumulation.  Lane (g, n)
+//      receives the scores of tokens 16u+4i+g (i = 0..3) for query head n/4.
 //   3. Online softmax in base 2 on those registers; the running max is only
 //      reduced across lanes when some score exceeds it.
-//   4. V^ tile built like K^.
+//   4. V^ halves built like K^.
 //   5. P.V on MFMA 16x16x16 f16: A = V^ rows read as (subspace x (token,
 //      coordinate)), B = the lane's own probability placed on the coordinate
 //      diagonal (the score layout of step 2 is already the B layout, so P
@@ -31,6 +32,8 @@
 //      softmax denominator.  P is produced as p * 2^14 before the fp16
 //      conversion, keeping small weights out of the fp16 subnormal range;
 //      the factor cancels in out = acc / l.
+// The steps are software-pipelined: every gather is issued one step before
+// the store that consumes it.
 // Split partials (m, l, acc) are merged by merge_partials_kernel.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
@@ -46,30 +49,20 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 32;                           // tokens per wave tile
-constexpr int kWaves = 8;                           // waves per block (2 per SIMD)
+constexpr int kWaves = 12;                          // waves per block (3 per SIMD)
 constexpr int kThreads = kWaves * 64;
 constexpr int kD = 64;                              // head_dim of the fused kernel
-constexpr int kDepth = 4;                           // tiles whose codes are in flight per wave
+constexpr int kDepth = 3;                           // tiles whose codes are in flight per wave
 constexpr int kEntryBytes = 256;                    // one codebook entry: PQ slots, then RVQ slots
 constexpr int kRvqSlot = 128;                       // byte offset of the RVQ slots in an entry
 constexpr int kTableBytes = 256 * kEntryBytes;      // one K or V table, 64 KB
-constexpr int kTileBytes = kTile * kD * 2;          // 4 KB per wave
+constexpr int kHalf = 16;                           // tokens per LDS half tile
+constexpr int kBufBytes = kHalf * kD * 2;           // 2 KB half-tile buffer per wave
 constexpr int kTilesBase = 2 * kTableBytes;         // tiles follow the K and V tables
-constexpr size_t kLdsBytes = (size_t)kTilesBase + (size_t)kWaves * kTileBytes;  // 160 KB
+constexpr size_t kLdsBytes = (size_t)kTilesBase + (size_t)kWaves * kBufBytes;  // 152 KB
 constexpr size_t kDummyBytes = 4096;                // workspace head read by idle prefetch slots
 constexpr float kPScaleLog2 = 14.0f;                // P is produced as p * 2^14
 constexpr float kLog2e = 1.4426950408889634f;
-
-// Order LDS traffic between the lanes of one wave.  A wave's LDS instructions
-// execute in issue order, so it is enough that the compiler keeps program
-// order (signal fences) and that earlier LDS operations have returned
-// (lgkmcnt(0)); global loads in flight (vmcnt) are deliberately not waited on,
-// so the tiles prefetched ahead keep streaming.
-__device__ __forceinline__ void wave_sync() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 __device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ float bitsf(uint32_t v) { return __builtin_bit_cast(float, v); }
@@ -98,10 +91,6 @@ __device__ __forceinline__ uint32_t add_h2(uint32_t a, uint32_t b) {
 // adjacent rows' chunks (gather stores, V operand reads, hot stores) and the
 // 16 rows 4(n&3)+(n>>2) of a score operand read.
 __device__ __forceinline__ int row_swz(int t) { return (t >> 1) & 7; }
-// byte offset of 8-byte chunk c (0..15) of row t
-__device__ __forceinline__ int tile_chunk(int t, int c) {
-  return t * 128 + ((((c >> 1) ^ row_swz(t)) << 4) | ((c & 1) << 3));
-}
 
 // LDS byte address of the codebook entry selected by byte k of the code word
 // w: code * 256 + lc.byte0 (the lane's subspace slot) + lc.byte2 * 65536 (the
@@ -257,115 +246,121 @@ __device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc
   }
 }
 
-// Copy one exact (hot) tile into the wave's LDS tile: rows [off, off+count)
-// of hot[...][D]; rows past count -> 0.  All four loads are issued before any
-// is used (rows past count re-read the last valid row and are zeroed after).
-__device__ __forceinline__ void build_hot_tile(uint8_t* __restrict__ lds, int tbase, const TileSrc& src,
-                                               const uint16_t* __restrict__ hot, int lane) {
-  uint4 v[4];
+// Copy rows [16u, 16u+16) of one exact (hot) tile into the wave's half-tile
+// buffer: rows [off, off+count) of hot[...][D]; rows past count -> 0.  Both
+// loads are issued before either is used (rows past count re-read the last
+// valid row and are zeroed after).
+__device__ __forceinline__ void build_hot_half(uint8_t* __restrict__ lds, int tbase, const TileSrc& src,
+                                               const uint16_t* __restrict__ hot, int lane, int u) {
+  uint4 v[2];
   const int u16 = lane & 7;  // 16-byte unit of the row
 #pragma unroll
-  for (int k4 = 0; k4 < 4; ++k4) {
-    const int row = min((lane >> 3) + 8 * k4, src.count - 1);
-    v[k4] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + u16 * 8);
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int row = min(16 * u + (lane >> 3) + 8 * k2, src.count - 1);
+    v[k2] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + u16 * 8);
   }
 #pragma unroll
-  for (int k4 = 0; k4 < 4; ++k4) {
-    const int row = (lane >> 3) + 8 * k4;
-    if (row >= src.count) v[k4] = make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(lds + tbase + row * 128 + ((u16 ^ row_swz(row)) << 4)) = v[k4];
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int r = (lane >> 3) + 8 * k2;  // buffer row
+    if (16 * u + r >= src.count) v[k2] = make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(lds + tbase + r * 128 + ((u16 ^ row_swz(r)) << 4)) = v[k2];
   }
 }
 
-// Codebook entries gathered for one K^ or V^ tile, held in registers until
-// they are summed and stored (the gathers of one tile are issued while the
-// previous phase of the pipeline still computes).
+// Codebook entries gathered for one half (16 tokens) of a K^ or V^ tile, held
+// in registers until they are summed and stored: the gathers are issued one
+// pipeline step ahead of their use.
 template <int M, bool RVQ>
-struct RawTile {
-  static constexpr int N = M == 16 ? 8 : 4;  // gathers per lane and stream
+struct RawHalf {
+  static constexpr int N = M == 16 ? 4 : 2;  // gathers per lane and stream
   typedef typename std::conditional<M == 16, uint2, uint4>::type E;
   E a[N];
   E b[RVQ ? N : 1];
 };
 
-// Gather one tile's codebook entries.  M = 16: lane (j, m) = (lane / 16,
-// lane % 16) reads the 8-byte entry of subspace m for tokens 4i + j; M = 8:
-// lane (lane / 8, lane % 8) reads 16-byte entries for tokens 8i + j.  One LDS
-// pass serves two adjacent j, which share subspace slots; lanes with odd j
-// therefore read their RVQ entry first (slot half lc1 = +128) and their PQ
-// entry second (lc2), so each pass covers all 64 banks (fp16 addition
-// commutes, the sum is the same).  Without an RVQ stage the upper slot half
-// holds a copy of the PQ table for the odd lanes.
+// Gather half u of one tile's codebook entries.  M = 16: lane (j, m) =
+// (lane / 16, lane % 16) reads the 8-byte entry of subspace m for tokens 4i + j
+// (i = 4u .. 4u+3); M = 8: lane (lane / 8, lane % 8) reads 16-byte entries for
+// tokens 8i + j (i = 2u, 2u+1).  One LDS pass serves two adjacent j, which
+// share subspace slots; lanes with odd j therefore read their RVQ entry first
+// (slot half lc1 = +128) and their PQ entry second (lc2), so each pass covers
+// all 64 banks (fp16 addition commutes, the sum is the same).  Without an RVQ
+// stage the upper slot half holds a copy of the PQ table for the odd lanes.
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void gather_tile(const uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs,
-                                            uint32_t lc1, uint32_t lc2, bool odd, RawTile<M, RVQ>& raw) {
-  constexpr int NW = TileRegs<M, RVQ, KS>::NW;
-  using E = typename RawTile<M, RVQ>::E;
-  uint32_t wa[NW], wb[NW];
+__device__ __forceinline__ void gather_half(const uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs, int u,
+                                            uint32_t lc1, uint32_t lc2, bool odd, RawHalf<M, RVQ>& raw) {
+  using E = typename RawHalf<M, RVQ>::E;
+  constexpr int N = RawHalf<M, RVQ>::N;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) {
+  for (int k = 0; k < N; ++k) {
+    const int i = N * u + k;  // gather group in the tile
+    const uint32_t pw = regs.pq[i >> 2];
+    uint32_t wa = pw, wb = 0;
     if constexpr (RVQ) {
-      wa[w] = odd ? regs.rvq[w] : regs.pq[w];
-      wb[w] = odd ? regs.pq[w] : regs.rvq[w];
-    } else {
-      wa[w] = regs.pq[w];
-      wb[w] = 0;
+      const uint32_t rw = regs.rvq[i >> 2];
+      wa = odd ? rw : pw;
+      wb = odd ? pw : rw;
     }
-  }
-#pragma unroll
-  for (int i = 0; i < RawTile<M, RVQ>::N; ++i) {
-    constexpr int per = 4;  // code bytes per word
-    raw.a[i] = *reinterpret_cast<const E*>(lds + entry_addr(wa[i / per], lc1, i % per));
-    if constexpr (RVQ) raw.b[i] = *reinterpret_cast<const E*>(lds + entry_addr(wb[i / per], lc2, i % per));
+    raw.a[k] = *reinterpret_cast<const E*>(lds + entry_addr(wa, lc1, i & 3));
+    if constexpr (RVQ) raw.b[k] = *reinterpret_cast<const E*>(lds + entry_addr(wb, lc2, i & 3));
   }
 }
 
-// Sum the gathered entries (fp16(base + rvq), quantization.py:317-319), store
-// them to the wave's tile, then store the sparse stage's corrected
-// coordinates over them.  waddr holds the lane's LDS store addresses for the
-// row patterns of consecutive i (4 for M = 16, 2 for M = 8).  A wave's LDS
-// operations execute in issue order, so no wait separates these stores from
-// earlier reads of the tile or later reads of these values.
+// Sum the gathered entries of half u (fp16(base + rvq), quantization.py:
+// 317-319), store them to the wave's buffer, then store the sparse stage's
+// corrected coordinates over them.  waddr holds the lane's LDS store addresses
+// for the row patterns of consecutive gathers (4 for M = 16, 2 for M = 8).  A
+// wave's LDS operations execute in issue order, so no wait separates these
+// stores from earlier reads of the buffer or later reads of these values.
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void store_tile(uint8_t* __restrict__ lds, int tbase, const TileRegs<M, RVQ, KS>& regs,
-                                           const RawTile<M, RVQ>& raw, const int (&waddr)[4], int lane) {
+__device__ __forceinline__ void store_half(uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs,
+                                           const RawHalf<M, RVQ>& raw, int u, const int (&waddr)[4],
+                                           const uint32_t (&saddr)[2], bool shalf) {
   if constexpr (M == 16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint2 e = raw.a[i];
+    for (int k = 0; k < 4; ++k) {
+      uint2 e = raw.a[k];
       if constexpr (RVQ) {
-        e.x = add_h2(e.x, raw.b[i].x);
-        e.y = add_h2(e.y, raw.b[i].y);
+        e.x = add_h2(e.x, raw.b[k].x);
+        e.y = add_h2(e.y, raw.b[k].y);
       }
-      *reinterpret_cast<uint2*>(lds + waddr[i & 3] + i * 512) = e;
+      *reinterpret_cast<uint2*>(lds + waddr[k] + k * 512) = e;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint4 e = raw.a[i];
+    for (int k = 0; k < 2; ++k) {
+      uint4 e = raw.a[k];
       if constexpr (RVQ) {
-        e.x = add_h2(e.x, raw.b[i].x);
-        e.y = add_h2(e.y, raw.b[i].y);
-        e.z = add_h2(e.z, raw.b[i].z);
-        e.w = add_h2(e.w, raw.b[i].w);
+        e.x = add_h2(e.x, raw.b[k].x);
+        e.y = add_h2(e.y, raw.b[k].y);
+        e.z = add_h2(e.z, raw.b[k].z);
+        e.w = add_h2(e.w, raw.b[k].w);
       }
-      *reinterpret_cast<uint4*>(lds + waddr[i & 1] + i * 1024) = e;
+      *reinterpret_cast<uint4*>(lds + waddr[k] + k * 1024) = e;
     }
   }
   if constexpr (KS > 0) {
     // sparse stage: the segment carries the corrected coordinates
-    // fp16(K[idx] + val), stored over the reconstructed ones.  The indices of
-    // one token are distinct, so the two lanes of a token never collide; rows
-    // past count repeat the last row's entries and are masked out of the
-    // softmax.
-    const int t = lane & (kTile - 1);
+    // fp16(K[idx] + val), stored over the reconstructed ones by the lanes of
+    // this half's tokens (saddr from sparse_addrs).  The indices of one token
+    // are distinct, so the two lanes of a token never collide; rows past count
+    // repeat the last row's entries and are masked out of the softmax.
+    if (shalf == (u != 0)) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int idx = (regs.sidx >> (8 * e)) & (kD - 1);
-      *reinterpret_cast<uint16_t*>(lds + tbase + tile_chunk(t, idx >> 2) + (idx & 3) * 2) =
-          (uint16_t)(regs.sval >> (16 * e));
+      for (int e = 0; e < 2; ++e) *reinterpret_cast<uint16_t*>(lds + saddr[e]) = (uint16_t)(regs.sval >> (16 * e));
     }
   }
+}
+
+// LDS addresses of the lane's two sparse entries in the half-tile buffer.
+// Coordinate idx of buffer row r sits at byte
+//   128 r + 16 ((idx >> 3) ^ row_swz(r)) + 2 (idx & 7) = sbase ^ (2 idx)
+// with sbase = buffer base + 128 r + 16 row_swz(r): the index bits land below
+// the row bits, and bits 4-6 of 2 idx XOR into the unit swizzle.
+template <int M, bool RVQ, int KS>
+__device__ __forceinline__ void sparse_addrs(const TileRegs<M, RVQ, KS>& regs, uint32_t sbase, uint32_t (&sa)[2]) {
+  sa[0] = sbase ^ ((regs.sidx << 1) & 0x7Eu);
+  sa[1] = sbase ^ ((regs.sidx >> 7) & 0x7Eu);
 }
 
 template <int M, bool RVQ, int KS, int NHG>
@@ -390,7 +385,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int C = p.fmt.pq_centroids, Cr = RVQ ? p.fmt.rvq_centroids : 0;
   constexpr int d = kD / M;
 
-  const int tbase = kTilesBase + wave * kTileBytes;  // this wave's tile (LDS byte address)
+  const int tbase = kTilesBase + wave * kBufBytes;  // this wave's half-tile buffer (LDS byte address)
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.workspace);  // readable scratch for idle slots
   const cseg segs = (cseg)(p.segments + (int64_t)b * p.max_segments);
   const int nseg = p.num_segments ? p.num_segments[b] : 0;
@@ -432,7 +427,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const uint32_t slot = (uint32_t)(mg * d * 2);
   const uint32_t lc1_k = slot | (odd ? kRvqSlot : 0u), lc2_k = slot | (odd ? 0u : kRvqSlot);
   const uint32_t lc1_v = lc1_k | (1u << 16), lc2_v = lc2_k | (1u << 16);
-  // row_swz(4i + j) = 2(i&3) + (j>>1) (M = 16); row_swz(8i + j) = 4(i&1) + (j>>1) (M = 8)
+  // Store addresses of gather k of a half: buffer row 4k + j (M = 16), with
+  // row_swz = 2k + (j>>1); row 8k + j (M = 8), with row_swz = 4k + (j>>1).
   int waddr[4];
   if constexpr (M == 16) {
 #pragma unroll
@@ -444,12 +440,15 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     waddr[2] = waddr[0];
     waddr[3] = waddr[1];
   }
-  // V operand reads of P.V MFMA i: row 4i + g, chunk n (same pattern as the M = 16 stores)
+  // sparse stores: token t = lane & 31 lives in half t >> 4
+  const bool shalf = (lane & 16) != 0;
+  const uint32_t sbase = (uint32_t)(tbase + (lane & 15) * 128 + (row_swz(lane & 15) << 4));
+  // V operand reads of P.V MFMA k of a half: buffer row 4k + g, chunk n (the M = 16 store pattern)
   int paddr[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
     paddr[a] = tbase + g * 128 + ((((n >> 1) ^ (2 * a + (g >> 1))) << 4) | ((n & 1) << 3));
-  // score operand reads: row 4(n&3) + (n>>2) of half u (row_swz = 2(n&3) + (n>>3)), 16-byte unit 4c + g
+  // score operand reads: buffer row 4(n&3) + (n>>2) (row_swz = 2(n&3) + (n>>3)), 16-byte unit 4c + g
   int raddr[2];
   {
     const int f = 2 * (n & 3) + (n >> 3);
@@ -519,18 +518,18 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     load_tile<M, RVQ, KS>(rk, s, v, 0, h, lane, dummy);
     load_tile<M, RVQ, KS>(rv, s, v, 1, h, lane, dummy);
   };
-  // scores of the tile in LDS: lane (g, n), register i of half u = token 16u + 4i + g
-  auto scores = [&](float4_t (&sc)[NHG][2]) {
+  // score operands of the half in the buffer, then the scores: lane (g, n),
+  // register i of half u = token 16u + 4i + g
+  auto score_operands = [&](half8_t (&a)[2]) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int c = 0; c < 2; ++c) a[c] = *reinterpret_cast<const half8_t*>(lds + raddr[c]);
+  };
+  auto scores = [&](const half8_t (&a)[2], float4_t (&sc)[NHG][2], int u) {
 #pragma unroll
-      for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int hg = 0; hg < NHG; ++hg) {
+      sc[hg][u] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(lds + raddr[c] + u * 2048);
-#pragma unroll
-        for (int hg = 0; hg < NHG; ++hg) sc[hg][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[hg][c], sc[hg][u], 0, 0, 0);
-      }
+      for (int c = 0; c < 2; ++c) sc[hg][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], qb[hg][c], sc[hg][u], 0, 0, 0);
     }
   };
   // online softmax in base 2; produces the B operands of P.V (probability at
@@ -564,9 +563,9 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
           const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
-          sv[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]);
           const int pos = src.pos0 + tok;
-          sv[r] = (full || (tok < src.count && pos >= 0 && pos <= qpl[hg])) ? sv[r] : -__builtin_inff();
+          const bool ok = full || (tok < src.count && pos >= 0 && pos <= qpl[hg]);
+          sv[r] = ok ? fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]) : -__builtin_inff();
           mx = fmaxf(mx, sv[r]);
         }
         mx = xmax32(xmax16(mx));  // the 4 k-groups holding this head's tokens
@@ -591,19 +590,20 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       }
     }
   };
-  // P.V and the denominator over the V^ tile in LDS; MFMA i covers tokens 4i .. 4i+3
-  auto pv_operands = [&](half4_t (&av)[8]) {
+  // P.V and the denominator over the V^ half in the buffer; MFMA k of half u
+  // covers tokens 16u + 4k .. 16u + 4k + 3
+  auto pv_operands = [&](half4_t (&av)[4]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      av[i] = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(lds + paddr[i & 3] + i * 512));
+    for (int k = 0; k < 4; ++k)
+      av[k] = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(lds + paddr[k] + k * 512));
   };
-  auto pv = [&](const half4_t (&av)[8], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8]) {
+  auto pv = [&](const half4_t (&av)[4], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8], int u) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int k = 0; k < 4; ++k) {
 #pragma unroll
       for (int hg = 0; hg < NHG; ++hg) {
-        const half4_t bw = __builtin_bit_cast(half4_t, make_uint2(pbl[hg][i], pbh[hg][i]));
-        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[i], bw, acc[hg], 0, 0, 0);
+        const half4_t bw = __builtin_bit_cast(half4_t, make_uint2(pbl[hg][4 * u + k], pbh[hg][4 * u + k]));
+        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[k], bw, acc[hg], 0, 0, 0);
         lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, bw, lsum[hg], 0, 0, 0);
       }
     }
@@ -615,45 +615,64 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     const TileSrc src = locate_tile(p, segs, tt, hot_tiles, nseg, v0, seg0_tiles);
     float4_t sc[NHG][2];
     uint32_t pbl[NHG][8], pbh[NHG][8];
-    half4_t av[8];
-    build_hot_tile(lds, tbase, src, hotk, lane);
-    wave_sync();
-    scores(sc);
+    half8_t a[2];
+    half4_t av[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      build_hot_half(lds, tbase, src, hotk, lane, u);
+      score_operands(a);
+      scores(a, sc, u);
+    }
     softmax(src, sc, pbl, pbh);
-    wave_sync();
-    build_hot_tile(lds, tbase, src, hotv, lane);
-    wave_sync();
-    pv_operands(av);
-    pv(av, pbl, pbh);
-    wave_sync();
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      build_hot_half(lds, tbase, src, hotv, lane, u);
+      pv_operands(av);
+      pv(av, pbl, pbh, u);
+    }
   }
 
   // Phase 2: encoded tiles, kDepth tiles of codes in flight per wave, and a
-  // software pipeline over the tile's LDS phases: the V^ gathers are issued
-  // under the score MFMAs and the softmax, and the next tile's K^ gathers
-  // under the P.V MFMAs.  LDS operations of a wave execute in order, so the
-  // tile buffer is reused without waits; the compiler's counters only wait
-  // for the data each step consumes.
+  // software pipeline over the tile's LDS steps: every gather is issued one
+  // step ahead of the store that consumes it (the next tile's first K^ half
+  // under this tile's last P.V MFMAs).  LDS operations of a wave execute in
+  // order, so the buffer is reused without waits; the compiler's counters
+  // only wait for the data each step consumes.
   const int seg_begin = max(t_begin, hot_tiles);
 #pragma unroll
   for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
-  RawTile<M, RVQ> rawk, rawv;
-  gather_tile<M, RVQ, KS>(lds, kr[0], lc1_k, lc2_k, odd, rawk);
+  RawHalf<M, RVQ> ra, rb;
+  gather_half<M, RVQ, KS>(lds, kr[0], 0, lc1_k, lc2_k, odd, ra);
   for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
     for (int s = 0; s < kDepth; ++s) {
       if (srcs[s].kind >= 0) {
         float4_t sc[NHG][2];
         uint32_t pbl[NHG][8], pbh[NHG][8];
-        half4_t av[8];
-        store_tile<M, RVQ, KS>(lds, tbase, kr[s], rawk, waddr, lane);
-        scores(sc);
-        gather_tile<M, RVQ, KS>(lds, vr[s], lc1_v, lc2_v, odd, rawv);
+        half8_t a[2];
+        half4_t av[4];
+        uint32_t sak[2] = {0, 0}, sav[2] = {0, 0};
+        if constexpr (KS > 0) {
+          sparse_addrs(kr[s], sbase, sak);
+          sparse_addrs(vr[s], sbase, sav);
+        }
+        store_half<M, RVQ, KS>(lds, kr[s], ra, 0, waddr, sak, shalf);
+        score_operands(a);
+        gather_half<M, RVQ, KS>(lds, kr[s], 1, lc1_k, lc2_k, odd, rb);
+        scores(a, sc, 0);
+        store_half<M, RVQ, KS>(lds, kr[s], rb, 1, waddr, sak, shalf);
+        score_operands(a);
+        gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
+        scores(a, sc, 1);
         softmax(srcs[s], sc, pbl, pbh);
-        store_tile<M, RVQ, KS>(lds, tbase, vr[s], rawv, waddr, lane);
+        store_half<M, RVQ, KS>(lds, vr[s], ra, 0, waddr, sav, shalf);
         pv_operands(av);
-        gather_tile<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], lc1_k, lc2_k, odd, rawk);  // next tile
-        pv(av, pbl, pbh);
+        gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
+        pv(av, pbl, pbh, 0);
+        store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
+        pv_operands(av);
+        gather_half<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], 0, lc1_k, lc2_k, odd, ra);  // next tile
+        pv(av, pbl, pbh, 1);
       }
       fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
     }
