@@ -6,11 +6,12 @@
 // reconstructed window to HBM.
 //
 // Work decomposition: one block = (sequence b, KV head h, token split) with
-// 12 waves, three per SIMD; each wave streams 32-token tiles of the split and
+// 16 waves, four per SIMD (12 when a KV head serves 8 query heads); each
+// wave streams 32-token tiles of the split and
 // passes each through a 2 KB LDS buffer in 16-token halves.  LDS holds the
 // sequence's codebooks as two 64 KB tables (K, V), entry-major with 256-byte
 // entries [PQ entries of the M subspaces | RVQ entries], then the waves'
-// half-tile buffers (152 KB in total).  Per tile:
+// half-tile buffers (up to 160 KB in total).  Per tile:
 //   1. K^ rows, per half: one lane per (token, subspace) and gather; the LDS
 //      address of a codebook entry is built from the code byte with one
 //      v_perm_b32 (code * 256 + subspace slot), and each LDS pass reads all 64
@@ -49,17 +50,25 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 32;                           // tokens per wave tile
-constexpr int kWaves = 12;                          // waves per block (3 per SIMD)
-constexpr int kThreads = kWaves * 64;
 constexpr int kD = 64;                              // head_dim of the fused kernel
-constexpr int kDepth = 3;                           // tiles whose codes are in flight per wave
+constexpr int kDepth = 2;                           // tiles whose codes are in flight per wave
 constexpr int kEntryBytes = 256;                    // one codebook entry: PQ slots, then RVQ slots
 constexpr int kRvqSlot = 128;                       // byte offset of the RVQ slots in an entry
 constexpr int kTableBytes = 256 * kEntryBytes;      // one K or V table, 64 KB
 constexpr int kHalf = 16;                           // tokens per LDS half tile
 constexpr int kBufBytes = kHalf * kD * 2;           // 2 KB half-tile buffer per wave
 constexpr int kTilesBase = 2 * kTableBytes;         // tiles follow the K and V tables
-constexpr size_t kLdsBytes = (size_t)kTilesBase + (size_t)kWaves * kBufBytes;  // 152 KB
+// Waves per block: 16 (4 per SIMD, 160 KB of LDS) when a KV head serves at
+// most 4 query heads; 12 when it serves 8 (the second head group's registers
+// must fit 170 VGPRs instead of 128).
+template <int NHG>
+struct BlockShape {
+  static constexpr int W = NHG == 1 ? 16 : 12;
+  static constexpr int T = W * 64;
+  static constexpr size_t L = (size_t)kTilesBase + (size_t)W * kBufBytes;
+  static_assert(L <= 160 * 1024, "LDS per CU");
+  static_assert((size_t)W * 16 * 4 + (size_t)W * 8 * kD * 4 <= L, "the wave combine reuses the codebook LDS");
+};
 constexpr size_t kDummyBytes = 4096;                // workspace head read by idle prefetch slots
 constexpr float kPScaleLog2 = 14.0f;                // P is produced as p * 2^14
 constexpr float kLog2e = 1.4426950408889634f;
@@ -364,11 +373,13 @@ __device__ __forceinline__ void sparse_addrs(const TileRegs<M, RVQ, KS>& regs, u
 }
 
 template <int M, bool RVQ, int KS, int NHG>
-__global__ void __launch_bounds__(kThreads, 1)
+__global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
 fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
   // static allocation: its base address is known at compile time, so LDS
   // addresses built in registers need no base add
-  __shared__ __align__(16) uint8_t lds[kLdsBytes];
+  constexpr int kWaves = BlockShape<NHG>::W;
+  constexpr int kThreads = BlockShape<NHG>::T;
+  __shared__ __align__(16) uint8_t lds[BlockShape<NHG>::L];
   // XCD-aware block mapping: consecutive hardware block ids go to different
   // XCDs; give each XCD a contiguous range of (sequence, head, split) units so
   // that one sequence's codebooks are fetched into one L2.
@@ -724,8 +735,9 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   }
 }
 
-static_assert((size_t)kWaves * 16 * 4 + (size_t)kWaves * 8 * kD * 4 <= kLdsBytes,
-              "the wave combine reuses the codebook LDS");
+int waves_for(const rfsn_fused_params* p) {
+  return p->q_heads / p->kv_heads <= 4 ? BlockShape<1>::W : BlockShape<2>::W;
+}
 
 int total_tiles_host(const rfsn_fused_params* p) {
   // upper bound: hot tiles + tiles of max_tokens encoded tokens split over segments
@@ -739,7 +751,8 @@ int auto_splits(const rfsn_fused_params* p) {
   const int units = p->batch * p->kv_heads;
   const int tiles = total_tiles_host(p);
   int s = (256 + units - 1) / units;                // one block per CU (LDS-bound occupancy)
-  const int max_s = (tiles + kWaves - 1) / kWaves;  // at least one tile per wave
+  const int waves = waves_for(p);
+  const int max_s = (tiles + waves - 1) / waves;    // at least one tile per wave
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
   return s;
@@ -752,7 +765,7 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   const int tps = (tiles + splits - 1) / splits;
   const int blocks = p->batch * p->kv_heads * splits;
   auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG>;  // 160 KB of static LDS
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kThreads), 0, s, *p, splits, tps, blocks);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(BlockShape<NHG>::T), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
   if (st || splits == 1) return st;
   return launch_merge(reinterpret_cast<const float*>(reinterpret_cast<const char*>(p->workspace) + kDummyBytes),

@@ -180,19 +180,20 @@ def main(argv=None) -> int:
     for _ in range(args.warmup):
         launch()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # HIP events on the launch stream bracket the timed region; the kernel
+    # time per step is their interval over the K back-to-back launches
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record()
+    start.record()
+    for _ in range(args.steps):
         launch()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
-    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    kernel_ms = start.elapsed_time(end) / args.steps
     step_bytes = w.bytes_per_step()
     achieved = step_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = traffic_from_profiles(w.name)
