@@ -24,10 +24,13 @@
 //      replicated over 4 columns each; fp32 accumulation.  Lane (g, n)
 //      receives the scores of tokens 16u+4i+g (i = 0..3) for query head n/4.
 //   3. Online softmax in base 2 on those registers; the running max is only
-//      reduced across lanes when some score exceeds it.
-//   4. V^ halves built like K^.
-//   5. P.V on MFMA 16x16x16 f16: A = V^ rows read as (subspace x (token,
-//      coordinate)), B = the lane's own probability placed on the coordinate
+//      reduced across lanes when some score exceeds it by more than the fp16
+//      headroom of P.
+//   4. V^ halves built like K^; with 16 subspaces the gather registers are
+//      already the P.V A operands and only pass through the buffer (lane-major,
+//      one 16-byte store and load per operand) for the sparse stage.
+//   5. P.V on MFMA 16x16x32 f16: A = V^ rows read as (subspace x (token,
+//      coordinate)), B = the lane's own probabilities placed on the coordinate
 //      diagonal (the score layout of step 2 is already the B layout, so P
 //      never moves between lanes); a second MFMA with A = 1 accumulates the
 //      softmax denominator.  P is produced as p * 2^14 before the fp16
@@ -69,8 +72,10 @@ struct BlockShape {
   static_assert(L <= 160 * 1024, "LDS per CU");
   static_assert((size_t)W * 16 * 4 + (size_t)W * 8 * kD * 4 <= L, "the wave combine reuses the codebook LDS");
 };
-constexpr size_t kDummyBytes = 4096;                // workspace head read by idle prefetch slots
 constexpr float kPScaleLog2 = 14.0f;                // P is produced as p * 2^14
+// A score may exceed the running max by this much (log2 units) before the max
+// is moved: P then stays below 2^15.75 < 65504, the fp16 maximum.
+constexpr float kSlackLog2 = 1.75f;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
@@ -132,56 +137,55 @@ __device__ __forceinline__ gbytes gview(const void* p) { return (gbytes)(p); }
 // tile up never waits on the vector-memory counter of the prefetched tiles.
 typedef const rfsn_segment __attribute__((address_space(4)))* cseg;
 
-// The pointers and extent of one segment (scalar loads).
-struct SegView {
-  const void* pq[2];  // [K, V]
-  const void* rvq[2];
-  const void* si[2];
-  const void* sv[2];
-  int64_t hs;         // head stride in token rows
+// This KV head's rows of one segment: base addresses of its code and sparse
+// streams [K, V] (scalar registers) and the segment's extent.  Tiles of the
+// segment are then addressed with 32-bit offsets from these bases.
+struct WarmBase {
+  gbytes pq[2];
+  gbytes rvq[2];
+  gbytes si[2];
+  gbytes sv[2];
   int len;
   int pos0;
 };
-__device__ __forceinline__ SegView seg_view(cseg sg) {
-  SegView v;
-  v.pq[0] = sg->k.pq;
-  v.pq[1] = sg->v.pq;
-  v.rvq[0] = sg->k.rvq;
-  v.rvq[1] = sg->v.rvq;
-  v.si[0] = sg->k.sparse_idx;
-  v.si[1] = sg->v.sparse_idx;
-  v.sv[0] = sg->k.sparse_val;
-  v.sv[1] = sg->v.sparse_val;
-  v.hs = sg->head_stride;
-  v.len = sg->len;
-  v.pos0 = sg->pos0;
-  return v;
+template <int M, bool RVQ, int KS>
+__device__ __forceinline__ WarmBase warm_base(cseg sg, int h) {
+  WarmBase w;
+  const int64_t row = (int64_t)h * sg->head_stride;  // first token row of head h
+  const void* pq[2] = {sg->k.pq, sg->v.pq};
+  const void* rvq[2] = {sg->k.rvq, sg->v.rvq};
+  const void* si[2] = {sg->k.sparse_idx, sg->v.sparse_idx};
+  const void* sv[2] = {sg->k.sparse_val, sg->v.sparse_val};
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    w.pq[kv] = gview(pq[kv]) + row * M;
+    w.rvq[kv] = RVQ ? gview(rvq[kv]) + row * M : w.pq[kv];
+    w.si[kv] = KS ? gview(si[kv]) + row * KS : w.pq[kv];
+    w.sv[kv] = KS ? gview(sv[kv]) + row * KS * 2 : w.pq[kv];
+  }
+  w.len = sg->len;
+  w.pos0 = sg->pos0;
+  return w;
 }
 
-// Tile tt of this (sequence, KV head): hot tiles first, then the segments in
-// order.  Segment 0 (the only one in the common case) is resolved from
-// registers; later segments walk the table.
-__device__ __forceinline__ TileSrc locate_tile(const rfsn_fused_params& p, cseg segs, int tt, int hot_tiles,
-                                               int nseg, const SegView& v0, int seg0_tiles) {
+// Hot tile tt of this (sequence, KV head).
+__device__ __forceinline__ TileSrc hot_tile(const rfsn_fused_params& p, int tt) {
   TileSrc s;
-  if (tt < hot_tiles) {
-    s.kind = 0;
-    s.seg = 0;
-    s.off = tt * kTile;
-    s.count = min(kTile, p.hot_len - s.off);
-    s.pos0 = p.hot_pos0 + s.off;
-    return s;
-  }
-  int r = tt - hot_tiles;
-  s.kind = 1;
+  s.kind = 0;
   s.seg = 0;
-  if (r < seg0_tiles) {
-    s.off = r * kTile;
-    s.count = min(kTile, v0.len - s.off);
-    s.pos0 = v0.pos0 + s.off;
-    return s;
-  }
-  r -= seg0_tiles;
+  s.off = tt * kTile;
+  s.count = min(kTile, p.hot_len - s.off);
+  s.pos0 = p.hot_pos0 + s.off;
+  return s;
+}
+
+// Encoded tile r of segments 1..nseg-1 (r counted from the first tile of
+// segment 1), walking the table (uniform, rare: the common cache has one warm
+// segment).  r must lie inside the table.
+__device__ __forceinline__ TileSrc walk_segments(cseg segs, int nseg, int r) {
+  TileSrc s;
+  s.kind = 1;
+  s.seg = nseg - 1;
   s.off = 0;
   s.count = 0;
   s.pos0 = 0;
@@ -193,7 +197,7 @@ __device__ __forceinline__ TileSrc locate_tile(const rfsn_fused_params& p, cseg 
       s.off = r * kTile;
       s.count = min(kTile, len - s.off);
       s.pos0 = segs[i].pos0 + s.off;
-      return s;
+      break;
     }
     r -= nt;
   }
@@ -214,44 +218,36 @@ struct TileRegs {
   uint32_t sval;  // KS/2 fp16 values
 };
 
-// Issue one tile's loads.  The same loads are issued for every slot (idle
-// and hot slots read a dummy address), so the compiler can count outstanding
-// loads exactly and wait only for the tile about to be used.  Base pointers
-// are uniform (scalar registers); lanes add 32-bit offsets.
+// Issue one tile's loads: the tile starting at token off (a multiple of 32)
+// of the segment whose bases are w, count valid tokens.  Bases are uniform
+// (scalar registers); lanes add 32-bit offsets.  Every slot issues the same
+// loads (idle slots re-read a real tile), so the compiler counts outstanding
+// loads exactly and waits only for the tile about to be used.
 template <int M, bool RVQ, int KS>
-__device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const TileSrc& src, const SegView& v, int kv,
-                                          int h, int lane, const uint8_t* dummy) {
+__device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const WarmBase& w, int kv, int off, int count,
+                                          int lane) {
   constexpr int IPT = TileRegs<M, RVQ, KS>::IPT;
-  const bool real = src.kind == 1;
-  const int64_t row = real ? (int64_t)h * v.hs + src.off : 0;  // token row of the tile's first token
-  const gbytes pq = gview(real ? v.pq[kv] : (const void*)dummy) + row * M;
-  const uint32_t lo = (uint32_t)(lane * IPT);
+  // tiled codes: tile off/32 starts at byte off * M of the head's stream
+  const uint32_t lo = (uint32_t)(off * M) + (uint32_t)(lane * IPT);
   if constexpr (IPT == 8) {
-    const uint64_t a = gload<uint64_t>(pq, lo);
+    const uint64_t a = gload<uint64_t>(w.pq[kv], lo);
     r.pq[0] = (uint32_t)a;
     r.pq[1] = (uint32_t)(a >> 32);
     if constexpr (RVQ) {
-      const gbytes rq = gview(real ? v.rvq[kv] : (const void*)dummy) + row * M;
-      const uint64_t c = gload<uint64_t>(rq, lo);
+      const uint64_t c = gload<uint64_t>(w.rvq[kv], lo);
       r.rvq[0] = (uint32_t)c;
       r.rvq[1] = (uint32_t)(c >> 32);
     }
   } else {
-    r.pq[0] = gload<uint32_t>(pq, lo);
-    if constexpr (RVQ) {
-      const gbytes rq = gview(real ? v.rvq[kv] : (const void*)dummy) + row * M;
-      r.rvq[0] = gload<uint32_t>(rq, lo);
-    }
+    r.pq[0] = gload<uint32_t>(w.pq[kv], lo);
+    if constexpr (RVQ) r.rvq[0] = gload<uint32_t>(w.rvq[kv], lo);
   }
   if constexpr (KS > 0) {
     static_assert(KS == 4, "fused kernel carries 4 sparse entries");
-    const gbytes si = gview(real ? v.si[kv] : (const void*)dummy) + row * KS;
-    const gbytes sv = gview(real ? v.sv[kv] : (const void*)dummy) + row * KS * 2;
-    const int t = lane & (kTile - 1);
-    const int tc = real ? min(t, src.count - 1) : t;  // rows past count re-read the last row
-    const uint32_t e0 = (uint32_t)(tc * KS + (lane >> 5) * 2);
-    r.sidx = gload<uint16_t>(si, e0);
-    r.sval = gload<uint32_t>(sv, e0 * 2);
+    const int t = min(lane & (kTile - 1), count - 1);  // rows past count re-read the last row
+    const uint32_t e0 = (uint32_t)((off + t) * KS + (lane >> 5) * 2);
+    r.sidx = gload<uint16_t>(w.si[kv], e0);
+    r.sval = gload<uint32_t>(w.sv[kv], e0 * 2);
   }
 }
 
@@ -315,12 +311,28 @@ __device__ __forceinline__ void gather_half(const uint8_t* __restrict__ lds, con
   }
 }
 
+// The sparse stage of half u: the segment carries the corrected coordinates
+// fp16(X[idx] + val), stored over the reconstructed ones by the lanes of
+// this half's tokens (two entries each, addresses from sparse_addrs).  The
+// indices of one token are distinct, so the two lanes of a token never
+// collide; rows past count repeat the last row's entries and get zero weight.
+template <int M, bool RVQ, int KS>
+__device__ __forceinline__ void sparse_stage(uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs, int u,
+                                             const uint32_t (&saddr)[2], bool shalf) {
+  if constexpr (KS > 0) {
+    if (shalf == (u != 0)) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) *reinterpret_cast<uint16_t*>(lds + saddr[e]) = (uint16_t)(regs.sval >> (16 * e));
+    }
+  }
+}
+
 // Sum the gathered entries of half u (fp16(base + rvq), quantization.py:
-// 317-319), store them to the wave's buffer, then store the sparse stage's
-// corrected coordinates over them.  waddr holds the lane's LDS store addresses
-// for the row patterns of consecutive gathers (4 for M = 16, 2 for M = 8).  A
-// wave's LDS operations execute in issue order, so no wait separates these
-// stores from earlier reads of the buffer or later reads of these values.
+// 317-319), store them to the wave's buffer, then run the sparse stage over
+// them.  waddr holds the lane's LDS store addresses for the row patterns of
+// consecutive gathers (4 for M = 16, 2 for M = 8).  A wave's LDS operations
+// execute in issue order, so no wait separates these stores from earlier
+// reads of the buffer or later reads of these values.
 template <int M, bool RVQ, int KS>
 __device__ __forceinline__ void store_half(uint8_t* __restrict__ lds, const TileRegs<M, RVQ, KS>& regs,
                                            const RawHalf<M, RVQ>& raw, int u, const int (&waddr)[4],
@@ -348,17 +360,55 @@ __device__ __forceinline__ void store_half(uint8_t* __restrict__ lds, const Tile
       *reinterpret_cast<uint4*>(lds + waddr[k] + k * 1024) = e;
     }
   }
-  if constexpr (KS > 0) {
-    // sparse stage: the segment carries the corrected coordinates
-    // fp16(K[idx] + val), stored over the reconstructed ones by the lanes of
-    // this half's tokens (saddr from sparse_addrs).  The indices of one token
-    // are distinct, so the two lanes of a token never collide; rows past count
-    // repeat the last row's entries and are masked out of the softmax.
-    if (shalf == (u != 0)) {
+  sparse_stage<M, RVQ, KS>(lds, regs, u, saddr, shalf);
+}
+
+// M = 16 without a sparse stage: the gathered entries of half u are already
+// the P.V MFMA's A operands (lane (j, m) holds subspace m of token
+// 16u + 4k + j for gather k, the 16x16x32 A layout of MFMA k/2), so V^ skips
+// the buffer: av[j] = fp16(base + rvq) of gathers 2j, 2j + 1.
+template <bool RVQ>
+__device__ __forceinline__ void direct_half(const RawHalf<16, RVQ>& raw, half8_t (&av)[2]) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) *reinterpret_cast<uint16_t*>(lds + saddr[e]) = (uint16_t)(regs.sval >> (16 * e));
+  for (int j = 0; j < 2; ++j) {
+    uint2 lo = raw.a[2 * j], hi = raw.a[2 * j + 1];
+    if constexpr (RVQ) {
+      lo = make_uint2(add_h2(lo.x, raw.b[2 * j].x), add_h2(lo.y, raw.b[2 * j].y));
+      hi = make_uint2(add_h2(hi.x, raw.b[2 * j + 1].x), add_h2(hi.y, raw.b[2 * j + 1].y));
     }
+    av[j] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
   }
+}
+
+// M = 16 with a sparse stage: V^ halves pass through the buffer lane-major
+// (the gather lane already holds the P.V A operands, only the sparse stage
+// needs the buffer): lane l's slots k = 0..3 (tokens 16u + 4k + l/16 of
+// subspace l%16) sit at byte (k >> 1) * 1024 + 16 l + 8 (k & 1), so a lane
+// stores and reloads each 16x16x32 A operand with one 16-byte access (64
+// lanes x 16 B contiguous: no bank conflicts).
+__device__ __forceinline__ void store_lanes(uint8_t* __restrict__ lds, int tbase, int lane, const half8_t (&av)[2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) *reinterpret_cast<half8_t*>(lds + tbase + j * 1024 + lane * 16) = av[j];
+}
+__device__ __forceinline__ void load_lanes(const uint8_t* __restrict__ lds, int tbase, int lane, half8_t (&av)[2]) {
+  // A lane reloads the bytes it stored, which other lanes' sparse stores may
+  // have changed: keep the compiler from forwarding the stored registers
+  // (the wave's LDS operations execute in order, so no wait is needed).
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 2; ++j) av[j] = *reinterpret_cast<const half8_t*>(lds + tbase + j * 1024 + lane * 16);
+}
+// Sparse entry addresses in that layout: token t' = 4k + g of the half and
+// coordinate idx land in lane 16 g + idx / 4, slot k, so the byte is
+//   vtok(t') | 16 (idx >> 2) | 2 (idx & 3),
+//   vtok(t') = buffer + 1024 (t' >> 3) + 256 (t' & 3) + 8 ((t' >> 2) & 1)
+// (disjoint bits).  Both entries of the lane at once from the two index bytes.
+template <int M, bool RVQ, int KS>
+__device__ __forceinline__ void sparse_addrs_lanes(const TileRegs<M, RVQ, KS>& regs, uint32_t vtok, uint32_t (&sa)[2]) {
+  const uint32_t x = regs.sidx;  // two index bytes
+  const uint32_t y = ((x & 0x3C3Cu) << 2) | ((x & 0x0303u) << 1);
+  sa[0] = vtok | (y & 0xFFu);
+  sa[1] = vtok | (y >> 8);
 }
 
 // LDS addresses of the lane's two sparse entries in the half-tile buffer.
@@ -397,7 +447,6 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   constexpr int d = kD / M;
 
   const int tbase = kTilesBase + wave * kBufBytes;  // this wave's half-tile buffer (LDS byte address)
-  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(p.workspace);  // readable scratch for idle slots
   const cseg segs = (cseg)(p.segments + (int64_t)b * p.max_segments);
   const int nseg = p.num_segments ? p.num_segments[b] : 0;
 
@@ -454,6 +503,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // sparse stores: token t = lane & 31 lives in half t >> 4
   const bool shalf = (lane & 16) != 0;
   const uint32_t sbase = (uint32_t)(tbase + (lane & 15) * 128 + (row_swz(lane & 15) << 4));
+  const int tq = lane & 15;  // the sparse lane's token within its half
+  const uint32_t vtok = (uint32_t)(tbase + 1024 * (tq >> 3) + 256 * (tq & 3) + 8 * ((tq >> 2) & 1));
   // V operand reads of P.V MFMA k of a half: buffer row 4k + g, chunk n (the M = 16 store pattern)
   int paddr[4];
 #pragma unroll
@@ -498,12 +549,13 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   if (p.causal && p.qpos)
     for (int hh = 0; hh < G; ++hh) qmin = min(qmin, p.qpos[(int64_t)b * p.q_heads + h * G + hh]);
   const float scale_log2 = p.scale * kLog2e;
-  const half4_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+  const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                        (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
   const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
-  SegView v0 = {};
-  if (nseg > 0) v0 = seg_view(segs);
-  const int seg0_tiles = nseg > 0 ? (v0.len + kTile - 1) / kTile : 0;
+  WarmBase w0 = {};
+  if (nseg > 0) w0 = warm_base<M, RVQ, KS>(segs, h);
+  const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
   int total_tiles = hot_tiles + seg0_tiles;
   for (int i = 1; i < nseg; ++i) total_tiles += (segs[i].len + kTile - 1) / kTile;
   const int t_begin = split * tiles_per_split;
@@ -514,24 +566,36 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   __syncthreads();
 
   using Regs = TileRegs<M, RVQ, KS>;
-  // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves
+  // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves.  Only
+  // encoded tiles go through slots (tt >= hot_tiles); a slot past the split
+  // is idle and re-reads the split's last tile, which is encoded.
   TileSrc srcs[kDepth];
   Regs kr[kDepth], vr[kDepth];
   auto fetch = [&](TileSrc& s, Regs& rk, Regs& rv, int tt) {
-    if (tt < t_end) {
-      s = locate_tile(p, segs, tt, hot_tiles, nseg, v0, seg0_tiles);
-    } else {
-      s.kind = -1;
+    const int r = min(tt, t_end - 1) - hot_tiles;
+    if (r < seg0_tiles) {  // uniform; segment 0 from registers
+      s.kind = 1;
       s.seg = 0;
+      s.off = r * kTile;
+      s.count = min(kTile, w0.len - s.off);
+      s.pos0 = w0.pos0 + s.off;
+      load_tile<M, RVQ, KS>(rk, w0, 0, s.off, s.count, lane);
+      load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
+    } else {
+      s = walk_segments(segs, nseg, r - seg0_tiles);
+      const WarmBase w = warm_base<M, RVQ, KS>(segs + s.seg, h);
+      load_tile<M, RVQ, KS>(rk, w, 0, s.off, s.count, lane);
+      load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
     }
-    SegView v = v0;
-    if (s.kind == 1 && s.seg != 0) v = seg_view(segs + s.seg);  // uniform, rare
-    load_tile<M, RVQ, KS>(rk, s, v, 0, h, lane, dummy);
-    load_tile<M, RVQ, KS>(rv, s, v, 1, h, lane, dummy);
+    if (tt >= t_end) s.kind = -1;
   };
   // score operands of the half in the buffer, then the scores: lane (g, n),
   // register i of half u = token 16u + 4i + g
+  // Operand reads of data other lanes stored: a compiler barrier first, so
+  // that no lane's own stored registers are forwarded past the other lanes'
+  // stores (the wave's LDS operations execute in order: no wait is needed).
   auto score_operands = [&](half8_t (&a)[2]) {
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int c = 0; c < 2; ++c) a[c] = *reinterpret_cast<const half8_t*>(lds + raddr[c]);
   };
@@ -552,43 +616,46 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     const bool full = src.count == kTile && src.pos0 >= 0 && src.pos0 + kTile - 1 <= qmin;
 #pragma unroll
     for (int hg = 0; hg < NHG; ++hg) {
+      // masked scores -> -inf (uniform branch: partial tile or causal boundary)
+      auto mask = [&](float (&v)[8]) {
+        if (!full) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
+            const int pos = src.pos0 + tok;
+            v[r] = (tok < src.count && pos >= 0 && pos <= qpl[hg]) ? v[r] : -__builtin_inff();
+          }
+        }
+      };
       float arg[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) arg[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias_m[hg]);
-      if (!full) {  // uniform: partial tile or causal boundary
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
-          const int pos = src.pos0 + tok;
-          arg[r] = (tok < src.count && pos >= 0 && pos <= qpl[hg]) ? arg[r] : -__builtin_inff();
-        }
-      }
+      mask(arg);
       const float amax = fmaxf(fmaxf(fmaxf(arg[0], arg[1]), fmaxf(arg[2], arg[3])),
                                fmaxf(fmaxf(arg[4], arg[5]), fmaxf(arg[6], arg[7])));
-      // The running max only moves when some score exceeds it; most tiles
-      // skip the cross-lane reduction and the rescale (any max gives the same
-      // softmax, the running one only keeps exp2 in range).
-      if (__builtin_amdgcn_ballot_w64(amax > kPScaleLog2)) {
-        float mx = -__builtin_inff();
+      // The running max only moves when some score exceeds it by more than
+      // the fp16 headroom of P (any max gives the same softmax, the running
+      // one only keeps exp2 in range); most tiles skip the cross-lane
+      // reduction and the rescale.
+      if (__builtin_amdgcn_ballot_w64(amax > kPScaleLog2 + kSlackLog2)) {
         float sv[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const int tok = 16 * (r >> 2) + 4 * (r & 3) + g;
-          const int pos = src.pos0 + tok;
-          const bool ok = full || (tok < src.count && pos >= 0 && pos <= qpl[hg]);
-          sv[r] = ok ? fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]) : -__builtin_inff();
-          mx = fmaxf(mx, sv[r]);
-        }
+        for (int r = 0; r < 8; ++r) sv[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]);
+        mask(sv);
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
         mx = xmax32(xmax16(mx));  // the 4 k-groups holding this head's tokens
         const float mn = fmaxf(m_run[hg], mx);
-        const float corr = mn == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m_run[hg] - mn);
+        // a head with nothing allowed yet keeps m = -inf, probabilities 0 and
+        // bias_m (+inf for a real head, so its first allowed score rescales)
+        const bool none = mn == -__builtin_inff();
+        const float corr = none ? 1.f : __builtin_amdgcn_exp2f(m_run[hg] - mn);
         acc[hg] *= corr;
         lsum[hg] *= corr;
         m_run[hg] = mn;
-        // exp2 argument = score - max + 14; a head with nothing allowed yet
-        // keeps -inf (its scores are -inf, so its probabilities stay 0)
-        const float dm = mn == -__builtin_inff() ? 0.f : kPScaleLog2 - mn;
-        bias_m[hg] = mn == -__builtin_inff() ? -__builtin_inff() : bias[hg] + dm;
+        // exp2 argument = score - max + 14
+        const float dm = none ? 0.f : kPScaleLog2 - mn;
+        bias_m[hg] = none ? bias_m[hg] : bias[hg] + dm;
 #pragma unroll
         for (int r = 0; r < 8; ++r) arg[r] = sv[r] + dm;
       }
@@ -601,21 +668,29 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       }
     }
   };
-  // P.V and the denominator over the V^ half in the buffer; MFMA k of half u
-  // covers tokens 16u + 4k .. 16u + 4k + 3
-  auto pv_operands = [&](half4_t (&av)[4]) {
+  // P.V and the denominator over the V^ half in the buffer on MFMA 16x16x32:
+  // MFMA j of half u covers tokens 16u + 8j + 4t + g (t = 0, 1), k index
+  // 8g + 4t + c (coordinate c); lane (n, g) holds V^ rows of subspace n for
+  // its two tokens, and the B operand the lane's probabilities of the same
+  // two tokens (score registers 4u + 2j + t) on the coordinate diagonal.
+  auto pv_operands = [&](half8_t (&av)[2]) {
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      av[k] = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(lds + paddr[k] + k * 512));
+    for (int j = 0; j < 2; ++j) {
+      const uint2 lo = *reinterpret_cast<const uint2*>(lds + paddr[2 * j] + 2 * j * 512);
+      const uint2 hi = *reinterpret_cast<const uint2*>(lds + paddr[2 * j + 1] + (2 * j + 1) * 512);
+      av[j] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    }
   };
-  auto pv = [&](const half4_t (&av)[4], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8], int u) {
+  auto pv = [&](const half8_t (&av)[2], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8], int u) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int hg = 0; hg < NHG; ++hg) {
-        const half4_t bw = __builtin_bit_cast(half4_t, make_uint2(pbl[hg][4 * u + k], pbh[hg][4 * u + k]));
-        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[k], bw, acc[hg], 0, 0, 0);
-        lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, bw, lsum[hg], 0, 0, 0);
+        const int r = 4 * u + 2 * j;
+        const half8_t bw = __builtin_bit_cast(half8_t, make_uint4(pbl[hg][r], pbh[hg][r], pbl[hg][r + 1], pbh[hg][r + 1]));
+        acc[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j], bw, acc[hg], 0, 0, 0);
+        lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, bw, lsum[hg], 0, 0, 0);
       }
     }
   };
@@ -623,11 +698,11 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // Phase 1: exact (hot) tiles, loaded synchronously (a few percent of tiles).
   const int hot_end = min(t_end, hot_tiles);
   for (int tt = t_begin + wave; tt < hot_end; tt += kWaves) {
-    const TileSrc src = locate_tile(p, segs, tt, hot_tiles, nseg, v0, seg0_tiles);
+    const TileSrc src = hot_tile(p, tt);
     float4_t sc[NHG][2];
     uint32_t pbl[NHG][8], pbh[NHG][8];
     half8_t a[2];
-    half4_t av[4];
+    half8_t av[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       build_hot_half(lds, tbase, src, hotk, lane, u);
@@ -649,43 +724,68 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // under this tile's last P.V MFMAs).  LDS operations of a wave execute in
   // order, so the buffer is reused without waits; the compiler's counters
   // only wait for the data each step consumes.
+  // With 16 subspaces V^ goes from the gather registers into P.V (through
+  // the buffer lane-major only for its sparse stage); with 8 its halves pass
+  // through the buffer like K^.
   const int seg_begin = max(t_begin, hot_tiles);
+  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
 #pragma unroll
-  for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
-  RawHalf<M, RVQ> ra, rb;
-  gather_half<M, RVQ, KS>(lds, kr[0], 0, lc1_k, lc2_k, odd, ra);
-  for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
+    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+    RawHalf<M, RVQ> ra, rb;
+    gather_half<M, RVQ, KS>(lds, kr[0], 0, lc1_k, lc2_k, odd, ra);
+    for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
-      if (srcs[s].kind >= 0) {
-        float4_t sc[NHG][2];
-        uint32_t pbl[NHG][8], pbh[NHG][8];
-        half8_t a[2];
-        half4_t av[4];
-        uint32_t sak[2] = {0, 0}, sav[2] = {0, 0};
-        if constexpr (KS > 0) {
-          sparse_addrs(kr[s], sbase, sak);
-          sparse_addrs(vr[s], sbase, sav);
+      for (int s = 0; s < kDepth; ++s) {
+        if (srcs[s].kind >= 0) {
+          float4_t sc[NHG][2];
+          uint32_t pbl[NHG][8], pbh[NHG][8];
+          half8_t a[2];
+          half8_t av[2];
+          uint32_t sak[2] = {0, 0}, sav[2] = {0, 0};
+          if constexpr (KS > 0) {
+            sparse_addrs(kr[s], sbase, sak);
+            if constexpr (M != 16) sparse_addrs(vr[s], sbase, sav);
+          }
+          store_half<M, RVQ, KS>(lds, kr[s], ra, 0, waddr, sak, shalf);
+          score_operands(a);
+          gather_half<M, RVQ, KS>(lds, kr[s], 1, lc1_k, lc2_k, odd, rb);
+          scores(a, sc, 0);
+          store_half<M, RVQ, KS>(lds, kr[s], rb, 1, waddr, sak, shalf);
+          score_operands(a);
+          gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
+          scores(a, sc, 1);
+          softmax(srcs[s], sc, pbl, pbh);
+          if constexpr (M == 16 && KS == 0) {
+            direct_half<RVQ>(ra, av);
+            gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
+            pv(av, pbl, pbh, 0);
+            direct_half<RVQ>(rb, av);
+          } else if constexpr (M == 16) {
+            uint32_t svl[2];
+            sparse_addrs_lanes(vr[s], vtok, svl);
+            direct_half<RVQ>(ra, av);
+            store_lanes(lds, tbase, lane, av);
+            sparse_stage<M, RVQ, KS>(lds, vr[s], 0, svl, shalf);
+            load_lanes(lds, tbase, lane, av);
+            gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
+            pv(av, pbl, pbh, 0);
+            direct_half<RVQ>(rb, av);
+            store_lanes(lds, tbase, lane, av);
+            sparse_stage<M, RVQ, KS>(lds, vr[s], 1, svl, shalf);
+            load_lanes(lds, tbase, lane, av);
+          } else {
+            store_half<M, RVQ, KS>(lds, vr[s], ra, 0, waddr, sav, shalf);
+            pv_operands(av);
+            gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
+            pv(av, pbl, pbh, 0);
+            store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
+            pv_operands(av);
+          }
+          gather_half<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], 0, lc1_k, lc2_k, odd, ra);  // next tile
+          pv(av, pbl, pbh, 1);
         }
-        store_half<M, RVQ, KS>(lds, kr[s], ra, 0, waddr, sak, shalf);
-        score_operands(a);
-        gather_half<M, RVQ, KS>(lds, kr[s], 1, lc1_k, lc2_k, odd, rb);
-        scores(a, sc, 0);
-        store_half<M, RVQ, KS>(lds, kr[s], rb, 1, waddr, sak, shalf);
-        score_operands(a);
-        gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
-        scores(a, sc, 1);
-        softmax(srcs[s], sc, pbl, pbh);
-        store_half<M, RVQ, KS>(lds, vr[s], ra, 0, waddr, sav, shalf);
-        pv_operands(av);
-        gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
-        pv(av, pbl, pbh, 0);
-        store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
-        pv_operands(av);
-        gather_half<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], 0, lc1_k, lc2_k, odd, ra);  // next tile
-        pv(av, pbl, pbh, 1);
+        fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
       }
-      fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
     }
   }
 
@@ -725,7 +825,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       o[c] = f2h(Ls > 0.f ? A / Ls : 0.f);
       continue;
     }
-    float* out = reinterpret_cast<float*>(reinterpret_cast<char*>(p.workspace) + kDummyBytes) +
+    float* out = reinterpret_cast<float*>(p.workspace) +
                  (((int64_t)b * p.q_heads + h * G + head) * splits + split) * (kD + 2);
     if (c == 0) {
       out[0] = Mx;
@@ -768,7 +868,7 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(BlockShape<NHG>::T), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
   if (st || splits == 1) return st;
-  return launch_merge(reinterpret_cast<const float*>(reinterpret_cast<const char*>(p->workspace) + kDummyBytes),
+  return launch_merge(reinterpret_cast<const float*>(p->workspace),
                       (int64_t)p->batch * p->q_heads, splits, kD, p->out, s);
 }
 
@@ -796,7 +896,8 @@ using namespace rfsn;
 extern "C" size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p) {
   if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0) return 0;
   const int splits = auto_splits(p);
-  return kDummyBytes + (size_t)p->batch * p->q_heads * splits * (kD + 2) * sizeof(float);
+  if (splits == 1) return 0;  // one split writes the output directly
+  return (size_t)p->batch * p->q_heads * splits * (kD + 2) * sizeof(float);
 }
 
 extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream) {
@@ -819,7 +920,8 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   RFSN_REQUIRE(p->max_segments >= 0 && (p->max_segments == 0 || (p->segments && p->num_segments)),
                "fused: bad segment table");
   RFSN_REQUIRE(p->max_tokens >= p->hot_len, "fused: max_tokens must cover the hot tier");
-  RFSN_REQUIRE(p->workspace && p->workspace_bytes >= rfsn_fused_workspace_bytes(p), "fused: workspace too small");
+  const size_t wsb = rfsn_fused_workspace_bytes(p);
+  RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;
   const bool rvq = f.rvq_subspaces > 0;
   if (f.pq_subspaces == 16) return rvq ? dispatch_ks<16, true>(p, s) : dispatch_ks<16, false>(p, s);

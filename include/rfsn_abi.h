@@ -207,8 +207,8 @@ typedef struct rfsn_fused_params {
   int64_t rvq_cb_stride;
   int32_t max_tokens;     /* upper bound on hot_len + sum of segment lengths */
   int32_t splits;         /* token splits per (sequence, KV head); 0 = auto  */
-  void* workspace;
-  size_t workspace_bytes;
+  void* workspace;        /* split partials; may be NULL when           */
+  size_t workspace_bytes; /* rfsn_fused_workspace_bytes() returns 0     */
 } rfsn_fused_params;
 
 size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);

@@ -92,7 +92,10 @@ def test_fused_cache_attention(device, case):
     B = 3
     q = randn16(g, B, Hq, 64)
     Ttot = nw + nh
-    for causal, qp in ((True, None), (False, None), (True, g.integers(-1, Ttot, (B,)).astype(np.int32))):
+    # per-head positions: in one wave some heads have nothing allowed in the
+    # first tiles (the hot tier holds the latest positions) while others do
+    for causal, qp in ((True, None), (False, None), (True, g.integers(-1, Ttot, (B,)).astype(np.int32)),
+                       (True, g.integers(-1, Ttot, (B, Hq)).astype(np.int32))):
         out = cache.attention_forward(T(q, device), causal=causal, query_positions=None if qp is None else T(qp, device))
         ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, causal, qp)
         err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
