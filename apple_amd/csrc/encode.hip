@@ -269,6 +269,225 @@ sparse_topk_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx
   }
 }
 
+// ---------------------------------------------------------------------------
+// Nearest-centroid search on MFMA (subspace dims d = 4 and d = 8).
+//
+// Half the squared distance is one MFMA dot product of augmented operands:
+//   centroid row  [ c_j (d) | rh_j  rl_j  1  1 | 0 ... ]   (A, 32 centroids)
+//   vector column [ -x  (d) | 1     1  lh  ll  | 0 ... ]   (B, 32 vectors)
+//   z_j = -x.c_j + (rh_j + rl_j) + (lh + ll) ~= (L - 2 X_j + R_j) / 2
+// with R_j / 2 = rh_j + rl_j and L / 2 = lh + ll split into fp16 pairs
+// (22 significant bits).  The products are exact in fp32 and the MFMA
+// accumulates in fp32, so |z_j - dist_j / 2| <= E with dist_j the canonical
+// distance and E = 2^-17 (L + R_max) + 2^-22, four times the worst-case sum
+// of the accumulation (d + 4 terms), split-representation and canonical
+// rounding errors.
+//
+// Each lane keeps the three smallest keys (z with its low byte replaced by
+// the centroid index) of its 128 (vector, centroid) pairs; the two lanes of a
+// vector merge theirs.  With v1 <= v2 <= v3 the key values and t the key
+// truncation (2^-14 |v|):
+//   v2 - v1 > 2E + t  -> the smallest key's centroid is the canonical code;
+//   v3 - v1 > 2E + t  -> only the two smallest can be the code: both are
+//                        rescored exactly (the duplicate-centroid case);
+//   otherwise (or non-finite values) the exact canonical scan over all C.
+// The exact rescoring uses the float64 chain of pq_encode_kernel, so codes
+// are identical to it (and to the oracle) by construction.
+constexpr int kMfmaVecsPerWave = 32;
+constexpr int kMfmaThreads = 256;
+
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef float mf16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int med3i(int a, int b, int c) { return max(min(a, b), min(max(a, b), c)); }
+// insert key k into the sorted triple (m1 <= m2 <= m3)
+__device__ __forceinline__ void top3_insert(int& m1, int& m2, int& m3, int k) {
+  const int n3 = med3i(m2, m3, k);
+  const int n2 = med3i(m1, m2, k);
+  m1 = min(m1, k);
+  m2 = n2;
+  m3 = n3;
+}
+__device__ __forceinline__ float key_value(int k) { return __builtin_bit_cast(float, k & (int)0xFFFFFF00); }
+constexpr int kNoKey = 0x7F8000FF;  // value +inf, above every finite key
+
+template <int DS>
+__global__ void __launch_bounds__(kMfmaThreads)
+pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, int64_t x_gstride,
+                      const uint16_t* __restrict__ cb, int M, int C, int64_t cb_gstride,
+                      uint8_t* __restrict__ codes, int64_t ldc, int64_t codes_gstride,
+                      uint16_t* __restrict__ resid, int64_t ldr, int64_t resid_gstride) {
+  constexpr int K = DS == 4 ? 8 : 16;  // MFMA depth: 32x32x8 (d = 4) or 32x32x16 (d = 8)
+  constexpr int KH = K / 2;            // operand halves per lane
+  __shared__ __align__(16) _Float16 tab[256 * K];  // augmented centroid rows
+  __shared__ float Rs[256];                        // canonical R_j
+  __shared__ float rmax_s;
+  const int m = blockIdx.y, g = blockIdx.z;
+  const uint16_t* cbm = cb + (size_t)g * cb_gstride + (size_t)m * C * DS;
+  const int nch = (C + 31) / 32;  // 32-centroid chunks
+  if (threadIdx.x == 0) rmax_s = 0.f;
+  __syncthreads();
+  for (int j = threadIdx.x; j < 32 * nch; j += kMfmaThreads) {
+    _Float16* row = tab + j * K;
+    if (j < C) {
+      double acc = 0.0;
+#pragma unroll
+      for (int u = 0; u < DS; ++u) {
+        const double c = (double)h2f(cbm[j * DS + u]);
+        acc = __builtin_fma(c, c, acc);
+        const uint16_t cu = cbm[j * DS + u];
+        row[u] = __builtin_bit_cast(_Float16, cu);
+      }
+      const float R = (float)acc;
+      const float half_r = 0.5f * R;
+      const _Float16 rh = (_Float16)half_r;
+      const _Float16 rl = (_Float16)(half_r - (float)rh);
+      row[KH] = rh;
+      row[KH + 1] = rl;
+      row[KH + 2] = (_Float16)1.0f;
+      row[KH + 3] = (_Float16)1.0f;
+      Rs[j] = R;
+      atomicMax(reinterpret_cast<int*>(&rmax_s), __builtin_bit_cast(int, R));  // R >= 0: int order = float order
+    } else {
+      for (int u = 0; u < KH + 4; ++u) row[u] = (_Float16)0.0f;
+    }
+    for (int u = KH + 4; u < K; ++u) row[u] = (_Float16)0.0f;
+    if (DS < KH) {
+      for (int u = DS; u < KH; ++u) row[u] = (_Float16)0.0f;
+    }
+  }
+  __syncthreads();
+  const float rmax = rmax_s;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, hi = lane >> 5;
+  const int64_t v = ((int64_t)blockIdx.x * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
+  const bool live = v < n;
+  // the lane's vector: canonical L and the B operand
+  double xs[DS];
+  double lacc = 0.0;
+  const uint16_t* xv = x + (size_t)g * x_gstride + (live ? v : 0) * ldx + (size_t)m * DS;
+#pragma unroll
+  for (int u = 0; u < DS; ++u) {
+    xs[u] = live ? (double)h2f(xv[u]) : 0.0;
+    lacc = __builtin_fma(xs[u], xs[u], lacc);
+  }
+  const float L = (float)lacc;
+  const float half_l = 0.5f * L;
+  const _Float16 lh = (_Float16)half_l;
+  const _Float16 ll = (_Float16)(half_l - (float)lh);
+  _Float16 bop[KH];
+#pragma unroll
+  for (int u = 0; u < KH; ++u) bop[u] = (_Float16)0.0f;
+  if (hi == 0) {
+#pragma unroll
+    for (int u = 0; u < DS; ++u) bop[u] = (_Float16)(-(float)xs[u]);
+  } else {
+    bop[0] = (_Float16)1.0f;
+    bop[1] = (_Float16)1.0f;
+    bop[2] = lh;
+    bop[3] = ll;
+  }
+
+  // screen: the three smallest keys of the lane's rows 8(r/4) + 4 hi + r%4
+  int m1 = kNoKey, m2 = kNoKey, m3 = kNoKey;
+  auto chunk = [&](int t, bool partial) {
+    mf16 acc = {};
+    const _Float16* arow = tab + (32 * t + col) * K + KH * hi;
+    if constexpr (DS == 4) {
+      mh4 a, b;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[u] = arow[u];
+        b[u] = bop[u];
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, acc, 0, 0, 0);
+    } else {
+      mh8 a, b;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a[u] = arow[u];
+        b[u] = bop[u];
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int jl = 32 * t + 8 * (r >> 2) + (r & 3);  // centroid index without the lane's 4 hi
+      // the element goes through a scalar first: bit-casting a vector element
+      // subscript in place reads element 0 with this compiler
+      const float z = acc[r];
+      int key = (__builtin_bit_cast(int, z) & (int)0xFFFFFF00) | jl;
+      if (partial && jl + 4 * hi >= C) key = kNoKey;
+      top3_insert(m1, m2, m3, key);
+    }
+  };
+  const int nfull = C / 32;
+  for (int t = 0; t < nfull; ++t) chunk(t, false);
+  if (nfull < nch) chunk(nfull, true);  // uniform: the last, partial chunk
+  // add the lane's row offset, then merge with the other lane of the vector
+  if (m1 != kNoKey) m1 |= 4 * hi;
+  if (m2 != kNoKey) m2 |= 4 * hi;
+  if (m3 != kNoKey) m3 |= 4 * hi;
+  {
+    const int o1 = __shfl_xor(m1, 32, 64), o2 = __shfl_xor(m2, 32, 64), o3 = __shfl_xor(m3, 32, 64);
+    top3_insert(m1, m2, m3, o1);
+    top3_insert(m1, m2, m3, o2);
+    top3_insert(m1, m2, m3, o3);
+  }
+  const float v1 = key_value(m1), v2 = key_value(m2), v3 = key_value(m3);
+  const float E = 0x1p-17f * (L + rmax) + 0x1p-22f;
+  const bool unique = v2 - v1 > 2.0f * E + 0x1p-14f * (fabsf(v1) + fabsf(v2));
+  const bool pair = v3 - v1 > 2.0f * E + 0x1p-14f * (fabsf(v1) + fabsf(v3));
+  const bool safe = rmax < 120000.0f;  // R / 2 representable in fp16 for every centroid
+
+  // canonical distance of centroid j (the float64 chain of pq_encode_kernel)
+  auto exact = [&](int j) {
+    double acc = 0.0;
+#pragma unroll
+    for (int u = 0; u < DS; ++u) acc = __builtin_fma(xs[u], (double)(float)tab[j * K + u], acc);
+    const float X = (float)acc;
+    return __fadd_rn(__fsub_rn(L, 2.0f * X), Rs[j]);
+  };
+  int code;
+  if (safe && unique) {
+    code = m1 & 0xFF;
+  } else if (safe && pair) {
+    const int ja = min(m1 & 0xFF, m2 & 0xFF), jb = max(m1 & 0xFF, m2 & 0xFF);
+    const float da = exact(ja), db = exact(jb);
+    code = db < da ? jb : ja;  // first min: ties keep the lower index
+  } else {
+    float best = __builtin_inff();
+    code = 0;
+    for (int j = 0; j < C; ++j) {
+      const float dj = exact(j);
+      if (dj < best) {
+        best = dj;
+        code = j;
+      }
+    }
+  }
+  if (!live || hi != 0) return;
+  codes[(size_t)g * codes_gstride + v * ldc + m] = (uint8_t)code;
+  if (resid != nullptr) {
+    uint16_t* rv = resid + (size_t)g * resid_gstride + v * ldr + (size_t)m * DS;
+#pragma unroll
+    for (int u = 0; u < DS; ++u) rv[u] = f2h(__fsub_rn((float)xs[u], (float)tab[code * K + u]));
+  }
+}
+
+template <int DS>
+int launch_pq_mfma(const void* x, int64_t n, int64_t ldx, int64_t xg, const void* cb, int M, int C, int64_t cbg,
+                   uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg, int groups,
+                   hipStream_t s) {
+  constexpr int per_block = (kMfmaThreads / 64) * kMfmaVecsPerWave;
+  dim3 grid((unsigned)ceil_div(n, per_block), (unsigned)M, (unsigned)groups);
+  hipLaunchKernelGGL(pq_encode_mfma_kernel<DS>, grid, dim3(kMfmaThreads), 0, s, (const uint16_t*)x, n, ldx, xg,
+                     (const uint16_t*)cb, M, C, cbg, codes, ldc, cg, (uint16_t*)resid, ldr, rg);
+  return check_launch("pq_encode");
+}
+
 template <int DSUB>
 int launch_pq(const void* x, int64_t n, int64_t ldx, int64_t xg, const void* cb, int M, int C, int d, int64_t cbg,
               uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg, int groups,
@@ -298,8 +517,8 @@ int pq_encode_impl(const void* x, int64_t n, int D, int64_t ldx, int64_t xg, con
   RFSN_REQUIRE(d <= 32, "pq_encode: subspace_dim > 32 unsupported");
   if (n == 0) return RFSN_OK;
   switch (d) {
-    case 4: return launch_pq<4>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
-    case 8: return launch_pq<8>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    case 4: return launch_pq_mfma<4>(x, n, ldx, xg, cb, M, C, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    case 8: return launch_pq_mfma<8>(x, n, ldx, xg, cb, M, C, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
     case 16: return launch_pq<16>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
     default: return launch_pq<0>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
   }

@@ -59,6 +59,52 @@ def test_pq_encode_known_answers(device):
     assert not H(zc).any()
 
 
+@pytest.mark.parametrize("d", [4, 8])
+@pytest.mark.parametrize("C", [1, 16, 100, 256])
+def test_pq_encode_screening_paths(device, d, C):
+    """The MFMA search (d = 4, 8) through each of its decisions: a unique
+    screened minimum, duplicated centroids (two exact ties), a triplicated
+    centroid and exactly equidistant centroid pairs (wider near-ties), vectors
+    whose |x|^2 / 2 overflows fp16, and codebooks with |c|^2 / 2 beyond fp16;
+    codes and residuals bit-exact against the oracle."""
+    from apple_amd import kernels as K
+
+    g = rng(300 + 7 * d + C)
+    M = 4
+    cb = rand_codebooks(g, M, C, d)
+    rows = [randn16(g, 64, M * d)]
+    if C >= 16:
+        cb[:, 5] = cb[:, 2]                      # a pair
+        cb[:, 9] = cb[:, 2]                      # ... a triple
+        cb[:, C - 1] = cb[:, 7]                  # a pair across chunks
+        rows.append(np.concatenate([cb[m][[2, 7, 9, 5, 0, C - 1]] for m in range(M)], axis=1))
+        # centroids 11, 12 at exactly +-delta from a vector along coordinate 0
+        base = randn16(g, 1, d)[0]
+        delta = np.float16(0.25)
+        for m in range(M):
+            cb[m, 11] = base
+            cb[m, 12] = base
+            cb[m, 11, 0] = base[0] + delta
+            cb[m, 12, 0] = base[0] - delta
+        rows.append(np.tile(base, (3, M)))
+        # near the pair, perturbed in the last fp16 bit
+        near = np.tile(base, (8, M)).view(np.uint16)
+        near[np.arange(8), np.arange(8) % (M * d)] ^= 1
+        rows.append(near.view(np.float16))
+    rows.append((randn16(g, 16, M * d).astype(np.float32) * 300.0).astype(np.float16))  # L / 2 > 65504
+    x = np.concatenate(rows, 0)
+    codes, resid = K.pq_encode(T(x, device), T(cb, device))
+    rc, rr = nx.pq_encode(x, cb)
+    assert np.array_equal(H(codes), rc)
+    assert np.array_equal(H(resid).view(np.uint16), rr.view(np.uint16))
+    big = cb.copy()
+    big[:, 0] = (big[:, 0].astype(np.float32) * 200.0).astype(np.float16)  # R / 2 > 60000 for centroid 0
+    codes, resid = K.pq_encode(T(x, device), T(big, device))
+    rc, rr = nx.pq_encode(x, big)
+    assert np.array_equal(H(codes), rc)
+    assert np.array_equal(H(resid).view(np.uint16), rr.view(np.uint16))
+
+
 @pytest.mark.parametrize("M,Mr,k", [(16, 16, 4), (8, 8, 4), (8, 0, 0), (16, 16, 0), (16, 0, 4)])
 def test_warm_encode_bit_exact(device, M, Mr, k):
     from apple_amd import kernels as K
