@@ -33,11 +33,14 @@ FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
+# per-source additions: the encode kernels keep MFMA results in VGPRs (the
+# argmin reads every accumulator element once; AGPRs would add a copy each)
+FILE_FLAGS = {"encode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")

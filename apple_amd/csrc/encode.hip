@@ -10,6 +10,8 @@
 // (mx.argmin, quantization.py:139; strict-< chunk merge, quantization.py:244).
 #include "rfsn_common.h"
 
+#include <type_traits>
+
 namespace rfsn {
 
 namespace {
@@ -322,21 +324,32 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
   constexpr int KH = K / 2;            // operand halves per lane
   __shared__ __align__(16) _Float16 tab[256 * K];  // augmented centroid rows
   __shared__ float Rs[256];                        // canonical R_j
-  __shared__ float rmax_s;
+  __shared__ uint32_t rmax_s[kMfmaThreads / 64];
   const int m = blockIdx.y, g = blockIdx.z;
   const uint16_t* cbm = cb + (size_t)g * cb_gstride + (size_t)m * C * DS;
   const int nch = (C + 31) / 32;  // 32-centroid chunks
-  if (threadIdx.x == 0) rmax_s = 0.f;
-  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, hi = lane >> 5;
+  const int64_t v = ((int64_t)blockIdx.x * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
+  const bool live = v < n;
+  // the lane's vector slice, loaded ahead of the codebook staging
+  uint16_t xr[DS];
+  const uint16_t* xv = x + (size_t)g * x_gstride + (live ? v : 0) * ldx + (size_t)m * DS;
+#pragma unroll
+  for (int u = 0; u < DS; ++u) xr[u] = live ? xv[u] : (uint16_t)0;
+
+  uint32_t rmax_t = 0;  // this thread's largest R_j, as bits (R >= 0; NaN above +inf)
   for (int j = threadIdx.x; j < 32 * nch; j += kMfmaThreads) {
-    _Float16* row = tab + j * K;
+    _Float16 row[K];  // built in registers, stored as 16-byte units
+#pragma unroll
+    for (int u = 0; u < K; ++u) row[u] = (_Float16)0.0f;
     if (j < C) {
       double acc = 0.0;
 #pragma unroll
       for (int u = 0; u < DS; ++u) {
-        const double c = (double)h2f(cbm[j * DS + u]);
-        acc = __builtin_fma(c, c, acc);
         const uint16_t cu = cbm[j * DS + u];
+        const double c = (double)h2f(cu);
+        acc = __builtin_fma(c, c, acc);
         row[u] = __builtin_bit_cast(_Float16, cu);
       }
       const float R = (float)acc;
@@ -348,29 +361,32 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       row[KH + 2] = (_Float16)1.0f;
       row[KH + 3] = (_Float16)1.0f;
       Rs[j] = R;
-      atomicMax(reinterpret_cast<int*>(&rmax_s), __builtin_bit_cast(int, R));  // R >= 0: int order = float order
-    } else {
-      for (int u = 0; u < KH + 4; ++u) row[u] = (_Float16)0.0f;
+      rmax_t = max(rmax_t, __builtin_bit_cast(uint32_t, R) & 0x7FFFFFFFu);
     }
-    for (int u = KH + 4; u < K; ++u) row[u] = (_Float16)0.0f;
-    if (DS < KH) {
-      for (int u = DS; u < KH; ++u) row[u] = (_Float16)0.0f;
+#pragma unroll
+    for (int c = 0; c < K / 8; ++c) {
+      mh8 w;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = row[8 * c + u];
+      *reinterpret_cast<mh8*>(tab + j * K + 8 * c) = w;
     }
   }
+  // block max of R_j (a NaN R makes every lane take the exact path)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) rmax_t = max(rmax_t, (uint32_t)__shfl_xor((int)rmax_t, o, 64));
+  if ((threadIdx.x & 63) == 0) rmax_s[threadIdx.x >> 6] = rmax_t;
   __syncthreads();
-  const float rmax = rmax_s;
+  uint32_t rmax_b = rmax_s[0];
+#pragma unroll
+  for (int w = 1; w < kMfmaThreads / 64; ++w) rmax_b = max(rmax_b, rmax_s[w]);
+  const float rmax = __builtin_bit_cast(float, rmax_b);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = lane & 31, hi = lane >> 5;
-  const int64_t v = ((int64_t)blockIdx.x * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
-  const bool live = v < n;
   // the lane's vector: canonical L and the B operand
   double xs[DS];
   double lacc = 0.0;
-  const uint16_t* xv = x + (size_t)g * x_gstride + (live ? v : 0) * ldx + (size_t)m * DS;
 #pragma unroll
   for (int u = 0; u < DS; ++u) {
-    xs[u] = live ? (double)h2f(xv[u]) : 0.0;
+    xs[u] = (double)h2f(xr[u]);
     lacc = __builtin_fma(xs[u], xs[u], lacc);
   }
   const float L = (float)lacc;
@@ -390,8 +406,14 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
     bop[3] = ll;
   }
 
+  // residual rows take one DS*2-byte store when the output is aligned for it
+  const bool vec_ok = resid != nullptr && ldr % DS == 0 && (reinterpret_cast<uintptr_t>(resid) % (2 * DS)) == 0 &&
+                      (resid_gstride % DS) == 0;
+
   // screen: the three smallest keys of the lane's rows 8(r/4) + 4 hi + r%4
+  // two independent lists (even / odd accumulator registers) for more ILP
   int m1 = kNoKey, m2 = kNoKey, m3 = kNoKey;
+  int n1 = kNoKey, n2 = kNoKey, n3 = kNoKey;
   auto chunk = [&](int t, bool partial) {
     mf16 acc = {};
     const _Float16* arow = tab + (32 * t + col) * K + KH * hi;
@@ -420,12 +442,18 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       const float z = acc[r];
       int key = (__builtin_bit_cast(int, z) & (int)0xFFFFFF00) | jl;
       if (partial && jl + 4 * hi >= C) key = kNoKey;
-      top3_insert(m1, m2, m3, key);
+      if (r & 1)
+        top3_insert(n1, n2, n3, key);
+      else
+        top3_insert(m1, m2, m3, key);
     }
   };
   const int nfull = C / 32;
   for (int t = 0; t < nfull; ++t) chunk(t, false);
   if (nfull < nch) chunk(nfull, true);  // uniform: the last, partial chunk
+  top3_insert(m1, m2, m3, n1);
+  top3_insert(m1, m2, m3, n2);
+  top3_insert(m1, m2, m3, n3);
   // add the lane's row offset, then merge with the other lane of the vector
   if (m1 != kNoKey) m1 |= 4 * hi;
   if (m2 != kNoKey) m2 |= 4 * hi;
@@ -472,8 +500,20 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
   codes[(size_t)g * codes_gstride + v * ldc + m] = (uint8_t)code;
   if (resid != nullptr) {
     uint16_t* rv = resid + (size_t)g * resid_gstride + v * ldr + (size_t)m * DS;
+    uint16_t r[DS];
 #pragma unroll
-    for (int u = 0; u < DS; ++u) rv[u] = f2h(__fsub_rn((float)xs[u], (float)tab[code * K + u]));
+    for (int u = 0; u < DS; ++u) r[u] = f2h(__fsub_rn((float)xs[u], (float)tab[code * K + u]));
+    if (vec_ok) {
+      if constexpr (DS == 4) {
+        *reinterpret_cast<uint2*>(rv) = make_uint2(r[0] | ((uint32_t)r[1] << 16), r[2] | ((uint32_t)r[3] << 16));
+      } else {
+        *reinterpret_cast<uint4*>(rv) = make_uint4(r[0] | ((uint32_t)r[1] << 16), r[2] | ((uint32_t)r[3] << 16),
+                                                   r[4] | ((uint32_t)r[5] << 16), r[6] | ((uint32_t)r[7] << 16));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < DS; ++u) rv[u] = r[u];
+    }
   }
 }
 
@@ -486,6 +526,101 @@ int launch_pq_mfma(const void* x, int64_t n, int64_t ldx, int64_t xg, const void
   hipLaunchKernelGGL(pq_encode_mfma_kernel<DS>, grid, dim3(kMfmaThreads), 0, s, (const uint16_t*)x, n, ldx, xg,
                      (const uint16_t*)cb, M, C, cbg, codes, ldc, cg, (uint16_t*)resid, ldr, rg);
   return check_launch("pq_encode");
+}
+
+// Top-k |r2| for head_dim 64: four lanes per vector, 16 coordinates each,
+// then the lanes' lists merge across the quad.  Order and tie rule are those
+// of sparse_topk_kernel (|r2| descending, ties to the lower coordinate, NaN
+// never enters, unused slots (index 0, value 0)).  An entry is one 64-bit key
+//   |r2| bits (32) | 64 - index (16) | fp16(r2) (16),
+// so the rank order is the unsigned key order (|r2| >= 0; the index field
+// breaks ties toward the lower coordinate) and the stored value rides along;
+// every entry is nonzero, so 0 marks an unused slot.  A sorted insert is then
+// a max/min network with static indices.
+template <int K>
+__device__ __forceinline__ void topk_insert(uint64_t (&t)[K], uint64_t x) {
+#pragma unroll
+  for (int j = K - 1; j > 0; --j) t[j] = __builtin_elementwise_max(t[j], __builtin_elementwise_min(t[j - 1], x));
+  t[0] = __builtin_elementwise_max(t[0], x);
+}
+
+template <int K, int DS, bool RVQ>
+__global__ void __launch_bounds__(256)
+sparse_topk64_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, const uint8_t* __restrict__ pq, int M,
+                     int C, const uint16_t* __restrict__ pq_cb, const uint8_t* __restrict__ rvq, int Cr,
+                     const uint16_t* __restrict__ rvq_cb, uint8_t* __restrict__ idx_out,
+                     uint16_t* __restrict__ val_out) {
+  constexpr int NS = 16 / DS;  // subspaces of the lane's 16 coordinates (same split for both stages)
+  typedef typename std::conditional<DS == 4, uint2, uint4>::type E;
+  const int64_t v = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 2;
+  const int q = threadIdx.x & 3;  // quarter: coordinates 16q .. 16q + 15
+  const bool live = v < n;
+  const int64_t vv = live ? v : 0;
+  const int m0 = q * NS;
+  // all loads first: the vector's 16 coordinates, its codes and the centroid entries
+  const uint4* xq = reinterpret_cast<const uint4*>(x + vv * ldx + 16 * q);
+  const uint4 xa = xq[0], xb = xq[1];
+  E pe[NS], re[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    pe[s] = *reinterpret_cast<const E*>(pq_cb + ((size_t)(m0 + s) * C + pq[vv * M + m0 + s]) * DS);
+    if constexpr (RVQ) re[s] = *reinterpret_cast<const E*>(rvq_cb + ((size_t)(m0 + s) * Cr + rvq[vv * M + m0 + s]) * DS);
+  }
+  const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  uint32_t pw[8], rw[8];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if constexpr (DS == 4) {
+      pw[2 * s] = pe[s].x;
+      pw[2 * s + 1] = pe[s].y;
+      if constexpr (RVQ) {
+        rw[2 * s] = re[s].x;
+        rw[2 * s + 1] = re[s].y;
+      }
+    } else {
+      pw[4 * s] = pe[s].x;
+      pw[4 * s + 1] = pe[s].y;
+      pw[4 * s + 2] = pe[s].z;
+      pw[4 * s + 3] = pe[s].w;
+      if constexpr (RVQ) {
+        rw[4 * s] = re[s].x;
+        rw[4 * s + 1] = re[s].y;
+        rw[4 * s + 2] = re[s].z;
+        rw[4 * s + 3] = re[s].w;
+      }
+    }
+  }
+  uint64_t t[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) t[j] = 0;  // unused slot, below every entry
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const uint16_t xh = (uint16_t)(xw[u >> 1] >> (16 * (u & 1)));
+    uint16_t rec = (uint16_t)(pw[u >> 1] >> (16 * (u & 1)));
+    if constexpr (RVQ) rec = hadd_bits(rec, (uint16_t)(rw[u >> 1] >> (16 * (u & 1))));
+    const float r2 = __fsub_rn(h2f(xh), h2f(rec));
+    const uint32_t mb = __builtin_bit_cast(uint32_t, r2) & 0x7FFFFFFFu;
+    if (mb <= 0x7F800000u) {  // NaN never enters
+      const int i = 16 * q + u;
+      topk_insert(t, ((uint64_t)mb << 32) | ((uint64_t)(64 - i) << 16) | f2h(r2));
+    }
+  }
+  // merge across the quad (lanes 4v' .. 4v'+3 of the wave)
+#pragma unroll
+  for (int o = 1; o < 4; o <<= 1) {
+    uint64_t ot[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) ot[j] = __shfl_xor(t[j], o, 64);
+#pragma unroll
+    for (int j = 0; j < K; ++j) topk_insert(t, ot[j]);
+  }
+  if (!live || q != 0) return;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const bool real = t[j] != 0;
+    idx_out[v * K + j] = real ? (uint8_t)(64 - (int)((t[j] >> 16) & 0xFFFF)) : (uint8_t)0;
+    val_out[v * K + j] = real ? (uint16_t)(t[j] & 0xFFFF) : (uint16_t)0;
+  }
 }
 
 template <int DSUB>
@@ -527,6 +662,25 @@ int pq_encode_impl(const void* x, int64_t n, int D, int64_t ldx, int64_t xg, con
 int sparse_topk_impl(const void* x, int64_t n, int D, int64_t ldx, const uint8_t* pq, int M, int C,
                      const void* pq_cb, const uint8_t* rvq, int Mr, int Cr, const void* rvq_cb, int k,
                      uint8_t* idx, void* val, hipStream_t s) {
+  // head_dim 64, 4- or 8-dim subspaces, an RVQ stage of the same split or
+  // none, k = 4, 16-byte aligned rows: four lanes per vector
+  const int d = D / M;
+  const bool fast = D == 64 && k == 4 && (d == 4 || d == 8) && (Mr == 0 || Mr == M) && ldx % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(pq_cb) % 16 == 0 &&
+                    (Mr == 0 || reinterpret_cast<uintptr_t>(rvq_cb) % 16 == 0);
+  if (fast) {
+    dim3 grid4((unsigned)ceil_div(n * 4, 256));
+#define RFSN_TOPK64(DS, R)                                                                                          \
+  hipLaunchKernelGGL((sparse_topk64_kernel<4, DS, R>), grid4, dim3(256), 0, s, (const uint16_t*)x, n, ldx, pq, M, C, \
+                     (const uint16_t*)pq_cb, rvq, Cr, (const uint16_t*)rvq_cb, idx, (uint16_t*)val)
+    if (d == 4) {
+      if (Mr) RFSN_TOPK64(4, true); else RFSN_TOPK64(4, false);
+    } else {
+      if (Mr) RFSN_TOPK64(8, true); else RFSN_TOPK64(8, false);
+    }
+#undef RFSN_TOPK64
+    return check_launch("sparse_topk");
+  }
   dim3 grid((unsigned)ceil_div(n, 256));
 #define RFSN_TOPK(KK)                                                                                  \
   hipLaunchKernelGGL(sparse_topk_kernel<KK>, grid, dim3(256), 0, s, (const uint16_t*)x, n, D, ldx, pq, M, C, \

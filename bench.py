@@ -146,6 +146,81 @@ def cpu_baseline(w, cache, q, gpu_out, sample, repeats):
             "seconds": round(total, 2)}, max_err
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+
+
+def bench_encode(w, args, dev) -> dict:
+    """Warm-tier compression throughput: one step encodes one chunk of
+    ``w.context`` tokens x ``w.kv_heads`` heads for K and for V (PQ, then the
+    subspace RVQ stage on the PQ residual, then the top-k sparse residual)."""
+    import torch
+    from apple_amd import kernels as K
+    from apple_amd.workloads import make_sequence
+
+    cfg = w.config()
+    k, v, _, g = make_sequence(w, 0)
+    kd, vd = k.to(dev), v.to(dev)
+    kq = fit_quantizer(cfg, kd, g, w, dev)
+    vq = fit_quantizer(cfg, vd, g, w, dev)
+    fmt = kq.warm_format()
+    xs = [(t.reshape(-1, w.head_dim).contiguous(), qz) for t, qz in ((kd, kq), (vd, vq))]
+    cbs = [(qz.pq.codebooks, qz.rvq.codebooks if fmt.rvq_subspaces else None) for _, qz in xs]
+
+    def step():
+        for (x, _), (pcb, rcb) in zip(xs, cbs):
+            K.warm_encode(x, fmt, pcb, rcb)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"timing {args.steps} encode steps")
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    kernel_ms = start.elapsed_time(end) / args.steps
+    vectors = 2 * w.context * w.kv_heads
+    # algorithmic contraction flops: 2 * C * D per vector and stage
+    flops = vectors * 2 * w.head_dim * (w.pq_centroids + (w.rvq_centroids if w.rvq_subspaces else 0))
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    result = {
+        "metric": "warm-tier encode vectors/s (PQ+RVQ+top-k, MFMA nearest-centroid search), 1 GPU",
+        "value": round(vectors / (kernel_ms * 1e-3), 1),
+        "unit": "vectors/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) K/V with per-channel scale U(0.5,2); k-means codebooks)",
+        "config": {"workload": w.name, "chunk_tokens": w.context, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+                   "vectors_per_step": vectors,
+                   "format": f"PQ M{w.pq_subspaces}x{w.pq_centroids}"
+                             + (f" + RVQ M{w.rvq_subspaces}x{w.rvq_centroids}" if w.rvq_subspaces else "")
+                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else "")},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 5), "traffic": None, "kernel_ms": round(kernel_ms, 5),
+                     "flops_per_step": flops},
+    }
+    if not args.no_cpu:
+        log("CPU baseline")
+        from oracle import numerics as nx
+
+        n = min(args.cpu_sample * 512, w.context * w.kv_heads)
+        x = xs[0][0][:n].cpu().numpy()
+        pcb, rcb = (t.cpu().numpy() if t is not None else None for t in cbs[0])
+        t0 = time.perf_counter()
+        nx.ext_encode(x, pcb, rcb, fmt.sparse_k)
+        sec = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(n / sec, 1), "unit": "vectors/s", "cores": 1, "kind": "port",
+                                  "sample": f"{n} key vectors of the chunk through the oracle's numpy encode "
+                                            f"(float64 brute-force distances), one process",
+                                  "seconds": round(sec, 2)}
+    return result
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per launch measured by rocprofv3 PMC runs, if committed."""
     p = ROOT / "profiles" / f"fused_decode_attn_{workload}_traffic.md"
@@ -170,9 +245,12 @@ def main(argv=None) -> int:
     from apple_amd.workloads import WORKLOADS
 
     w = WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    if w.name == "encode_4k":
+        print(json.dumps(bench_encode(w, args, dev)), flush=True)
+        return 0
     if w.hot + w.warm != w.context or w.cold:
         raise SystemExit(f"workload {w.name} is not a hot+warm decode workload")
-    dev = torch.device("cuda", 0)
     log(f"workload {w.name}: B={w.batch} ctx={w.context} Hq={w.q_heads} Hkv={w.kv_heads} hot={w.hot} warm={w.warm}")
     cache, q = setup_decode(w, dev)
     out = torch.empty_like(q)
