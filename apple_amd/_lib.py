@@ -52,7 +52,8 @@ class FusedParams(C.Structure):
                 ("segments", vp), ("num_segments", vp), ("max_segments", i32),
                 ("k_pq_cb", vp), ("k_rvq_cb", vp), ("v_pq_cb", vp), ("v_rvq_cb", vp),
                 ("pq_cb_stride", i64), ("rvq_cb_stride", i64),
-                ("max_tokens", i32), ("splits", i32), ("workspace", vp), ("workspace_bytes", sz)]
+                ("max_tokens", i32), ("splits", i32), ("workspace", vp), ("workspace_bytes", sz),
+                ("part_base", i32), ("part_slots", i32), ("merge", i32)]
 
 
 class Copy(C.Structure):
@@ -76,6 +77,7 @@ SIGNATURES = {
     "rfsn_attention_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "rfsn_blockwise_attention": (i32, [vp, i32, i32, i32, vp, vp, i64, i32, i64, i64, f32, i32, vp, vp, vp, sz, vp]),
     "rfsn_pack_codes": (i32, [vp, i64, i64, i32, i32, vp, i64, i64, vp]),
+    "rfsn_fused_splits": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_workspace_bytes": (sz, [C.POINTER(FusedParams)]),
     "rfsn_fused_decode_attention": (i32, [C.POINTER(FusedParams), vp]),
     "rfsn_kmeans_workspace_bytes": (sz, [i32, i32, i32]),
@@ -108,7 +110,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 1:
+    if lib.rfsn_abi_version() != 2:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

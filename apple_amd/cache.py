@@ -72,14 +72,47 @@ class TiledCodes:
     (``kernels.sparse_fold``), which the kernel stores over the reconstructed
     coordinate; the reference-layout stores keep the residuals."""
 
-    def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0):
+    def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0,
+                 backing: Optional[torch.Tensor] = None):
+        """``backing``: a uint8 buffer of at least ``nbytes(fmt, heads, cap)``
+        that holds every array (fixed capacity), so that one copy moves the
+        whole set; otherwise each array is its own growable allocation."""
         self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
         self.cap = 0
         self.len = 0
         self.t: Dict[str, Optional[torch.Tensor]] = {}
+        self._backing = backing
+        self._carved = 0
         self._alloc(cap)
 
+    @staticmethod
+    def _arrays(fmt: K.WarmFormat, heads: int, cap: int):
+        f, H = fmt, heads
+        return {"pq": ((H, cap * f.pq_subspaces), torch.uint8),
+                "rvq": ((H, cap * f.rvq_subspaces), torch.uint8) if f.rvq_subspaces else None,
+                "sparse_idx": ((H, cap, f.sparse_k), torch.uint8) if f.sparse_k else None,
+                "sparse_val": ((H, cap, f.sparse_k), torch.float16) if f.sparse_k else None}
+
+    @staticmethod
+    def nbytes(fmt: K.WarmFormat, heads: int, cap: int) -> int:
+        """Bytes of one backing buffer: every array, each at a 256-byte boundary."""
+        total = 0
+        for spec in TiledCodes._arrays(fmt, heads, K.round_up(max(cap, 0), K.TILE)).values():
+            if spec is not None:
+                shape, dtype = spec
+                n = shape[0] * shape[1] * (shape[2] if len(shape) > 2 else 1) * (2 if dtype == torch.float16 else 1)
+                total += K.round_up(n, 256)
+        return total
+
     def _new(self, shape, dtype):
+        if self._backing is not None:
+            n = 1
+            for s in shape:
+                n *= s
+            nb = n * (2 if dtype == torch.float16 else 1)
+            view = self._backing[self._carved:self._carved + nb]
+            self._carved += K.round_up(nb, 256)
+            return view.view(dtype).view(shape)
         if self.pinned:
             return torch.zeros(shape, dtype=dtype, pin_memory=True)
         return torch.zeros(shape, dtype=dtype, device=self.device)
@@ -88,11 +121,13 @@ class TiledCodes:
         cap = K.round_up(max(cap, 0), K.TILE)
         if cap <= self.cap and self.t:
             return
-        f, H = self.fmt, self.heads
-        new = {"pq": self._new((H, cap * f.pq_subspaces), torch.uint8),
-               "rvq": self._new((H, cap * f.rvq_subspaces), torch.uint8) if f.rvq_subspaces else None,
-               "sparse_idx": self._new((H, cap, f.sparse_k), torch.uint8) if f.sparse_k else None,
-               "sparse_val": self._new((H, cap, f.sparse_k), torch.float16) if f.sparse_k else None}
+        if self._backing is not None:
+            if self.t:
+                raise ValueError("a TiledCodes set in one backing buffer has a fixed capacity")
+            if self._backing.numel() < TiledCodes.nbytes(self.fmt, self.heads, cap):
+                raise ValueError("backing buffer too small for the tiled arrays")
+        new = {key: (None if spec is None else self._new(*spec))
+               for key, spec in TiledCodes._arrays(self.fmt, self.heads, cap).items()}
         if self.t and self.cap:
             for key, old in self.t.items():
                 if old is None:
@@ -136,6 +171,55 @@ class TiledCodes:
         return out
 
 
+def plan_slot_windows(slot_cid: Sequence[int], lru: Sequence[int], wanted: set, missing: Sequence[int],
+                      arena: int) -> List[Tuple[int, List[int]]]:
+    """Where missing cold chunks go in a pool of ``len(slot_cid)`` device slots.
+
+    slot_cid[j]: the chunk in slot j (-1 free); lru: occupied slots, least
+    recently used first; wanted: every chunk of the window (their slots are
+    never taken); missing: the chunks to copy in.  Missing ids form runs of
+    consecutive ids inside one pinned arena of ``arena`` ids; each run takes
+    the longest window of consecutive usable slots (free, or holding no
+    wanted chunk), preferring fewer occupied slots, then older occupants, and
+    is split only when no window is long enough.  Returns (first slot, chunk
+    ids) per window, one copy each."""
+    S = len(slot_cid)
+    rank = {s: r for r, s in enumerate(lru)}
+    taken = set()
+
+    def usable(j: int) -> bool:
+        return j not in taken and (slot_cid[j] < 0 or slot_cid[j] not in wanted)
+
+    runs: List[List[int]] = []
+    for cid in sorted(missing):
+        if runs and cid == runs[-1][-1] + 1 and cid // arena == runs[-1][0] // arena:
+            runs[-1].append(cid)
+        else:
+            runs.append([cid])
+    out = []
+    for run in runs:
+        while run:
+            best = None
+            for j in range(S):
+                n = 0
+                while n < len(run) and j + n < S and usable(j + n):
+                    n += 1
+                if n == 0:
+                    continue
+                occupied = sum(1 for x in range(j, j + n) if slot_cid[x] >= 0)
+                newest = max((rank.get(x, -1) for x in range(j, j + n)), default=-1)
+                cost = (-n, occupied, newest)
+                if best is None or cost < best[0]:
+                    best = (cost, j, n)
+            if best is None:
+                raise ValueError("more wanted cold chunks than device slots")
+            _, j, n = best
+            taken.update(range(j, j + n))
+            out.append((j, run[:n]))
+            run = run[n:]
+    return out
+
+
 def _plain_head_major(store: CompressedTensorMLX):
     """Reference-layout subspace codes [T, H, *] -> head-major [H, T, *]."""
     pm = lambda t: None if t is None else t.permute(1, 0, 2).contiguous()
@@ -168,7 +252,10 @@ class RFSNv10KVCacheMLX:
         self.cold_chunk_paths_by_id: Dict[int, Path] = {}
         self.cold_chunk_metadata: List[dict] = []
         self._cold_pinned: Dict[int, dict] = {}
-        self._cold_slots: "OrderedDict[int, dict]" = OrderedDict()
+        self._cold_slots: "OrderedDict[int, dict]" = OrderedDict()  # chunk id -> device slot, LRU first
+        self._cold_arena: Dict[int, torch.Tensor] = {}
+        self._slot_buf: Optional[torch.Tensor] = None
+        self._slot_cid: List[int] = []
         self._cold_slot_limit = cold_slots
         self._side: Optional[K.SideStream] = None
 
@@ -428,31 +515,58 @@ class RFSNv10KVCacheMLX:
             cv = _append_compressed_tensor(_to_device_store(old["value"], self.device), cv)
             meta["end_token"] += n
             meta["num_tokens"] += n
-            self._cold_slots.pop(cid, None)
+            stale = self._cold_slots.pop(cid, None)
+            if stale is not None:
+                self._slot_cid[stale["slot"]] = -1
+            if self._side is not None:
+                self._side.synchronize()  # a queued copy may still read the pinned bytes rewritten below
         else:
             meta = {"chunk_id": cid, "start_token": cstart, "end_token": cstart + n, "num_tokens": n,
                     "path": f"pinned:{cid}"}
             self.cold_chunk_metadata.append(meta)
             self.cold_chunk_metadata.sort(key=lambda m: m["start_token"])
-        self._cold_pinned[cid] = self._pin_chunk(ck, cv)
+        self._cold_pinned[cid] = self._pin_chunk(cid, ck, cv)
 
-    def _pin_chunk(self, ck: CompressedTensorMLX, cv: CompressedTensorMLX) -> dict:
+    # Pinned chunks live in arenas of ARENA_CHUNKS consecutive chunk ids and
+    # device slots in one buffer of cold_slots slots, so that a run of
+    # consecutive chunks copied into consecutive slots is one hipMemcpyAsync.
+    ARENA_CHUNKS = 64
+
+    def _chunk_bytes(self) -> int:
+        """Bytes of one chunk's tiled K and V codes (its pinned buffer and device slot)."""
+        chunk = K.round_up(self.config.chunk_tokens, K.TILE)
+        return 2 * TiledCodes.nbytes(self._fmt(), self.H, chunk)
+
+    def _arena_view(self, cid: int) -> torch.Tensor:
+        nb = self._chunk_bytes()
+        blk = cid // self.ARENA_CHUNKS
+        arena = self._cold_arena.get(blk)
+        if arena is None:
+            arena = torch.zeros(self.ARENA_CHUNKS * nb, dtype=torch.uint8, pin_memory=True)
+            self._cold_arena[blk] = arena
+        o = (cid % self.ARENA_CHUNKS) * nb
+        return arena[o:o + nb]
+
+    def _pin_chunk(self, cid: int, ck: CompressedTensorMLX, cv: CompressedTensorMLX) -> dict:
         """Keep a chunk in pinned host memory: the reference layout (for decode
         and NPZ export) and, for the subspace format, the tiled layout that
-        prefetch copies into device slots."""
+        prefetch copies into device slots (K then V in one buffer)."""
         entry = {"key": _to_host_store(ck), "value": _to_host_store(cv)}
         if self._subspace:
             fmt = self._fmt()
             chunk = K.round_up(self.config.chunk_tokens, K.TILE)
-            for name, store, qz in (("key", ck, self._kq), ("value", cv, self._vq)):
-                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk)
+            half = self._chunk_bytes() // 2
+            dev_buf = torch.zeros(2 * half, dtype=torch.uint8, device=self.device)
+            host_buf = self._arena_view(cid)
+            for i, (name, store, qz) in enumerate((("key", ck, self._kq), ("value", cv, self._vq))):
+                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk, backing=dev_buf[i * half:(i + 1) * half])
                 dev_t.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
-                host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk)
-                for key, t in dev_t.t.items():
-                    if t is not None:
-                        host_t.t[key].copy_(t)
+                host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk,
+                                    backing=host_buf[i * half:(i + 1) * half])
                 host_t.len = dev_t.len
                 entry[f"{name}_tiled"] = host_t
+            host_buf.copy_(dev_buf)
+            entry["tiled_buf"] = host_buf
         return entry
 
     def has_cold_chunk(self, chunk_id: int) -> bool:
@@ -472,43 +586,89 @@ class RFSNv10KVCacheMLX:
             return _to_device_store(loaded[prefix], self.device)
         return compressed_tensor_from_loaded(loaded, prefix)
 
-    def prefetch_cold_chunks(self, chunk_ids: Sequence[int]) -> Dict[int, dict]:
-        """Make pinned chunks resident in device slots; copies are issued with
-        hipMemcpyAsync on a side stream and the current stream waits on its event."""
+    def _slot_pool(self) -> torch.Tensor:
+        if self._slot_buf is None:
+            self._slot_buf = torch.empty(self._cold_slot_limit * self._chunk_bytes(), dtype=torch.uint8,
+                                         device=self.device)
+            self._slot_cid = [-1] * self._cold_slot_limit
+        return self._slot_buf
+
+    def _slot_entry(self, cid: int, slot: int) -> dict:
+        nb = self._chunk_bytes()
+        half = nb // 2
+        pool = self._slot_pool()
+        e = self._cold_pinned[cid]
+        dev = {"slot": slot}
+        for i, name in enumerate(("key", "value")):
+            host_t: TiledCodes = e[f"{name}_tiled"]
+            o = slot * nb + i * half
+            dt = TiledCodes(self._fmt(), self.H, self.device, cap=host_t.cap, backing=pool[o:o + half])
+            dt.len = host_t.len
+            dev[name] = dt
+        return dev
+
+    def _stage_cold(self, chunk_ids: Sequence[int]) -> Tuple[Dict[int, dict], List[int], list]:
+        """Device slots for ``chunk_ids``: (slots by id, ids still to copy,
+        their (dst, src, bytes) copies).  Resident chunks keep their slot and
+        become the most recently used.  The missing ones, in runs of
+        consecutive ids inside one pinned arena, take the longest windows of
+        consecutive slots that hold no chunk of ``chunk_ids`` (preferring free
+        slots, then the least recently used), so that each window is one copy."""
         if self.config.cold_medium != "pinned":
-            raise RuntimeError("prefetch_cold_chunks needs cold_medium='pinned'")
-        if self._side is None:
-            self._side = K.SideStream()
-        copies = []
+            raise RuntimeError("cold-chunk prefetch needs cold_medium='pinned'")
+        ids = list(dict.fromkeys(int(c) for c in chunk_ids))
+        S = self._cold_slot_limit
+        if len(ids) > S:
+            raise ValueError(f"{len(ids)} cold chunks requested; the device slot pool holds "
+                             f"{S} (raise cold_slots)")
         out: Dict[int, dict] = {}
-        self._side.wait_for_current(self.device)
-        for cid in chunk_ids:
+        for cid in ids:
             if cid in self._cold_slots:
                 self._cold_slots.move_to_end(cid)
                 out[cid] = self._cold_slots[cid]
-                continue
-            e = self._cold_pinned[cid]
-            slot = None
-            if len(self._cold_slots) >= self._cold_slot_limit:
-                _, slot = self._cold_slots.popitem(last=False)
-            dev = {}
-            for name in ("key", "value"):
-                host_t: TiledCodes = e[f"{name}_tiled"]
-                if slot is not None and slot[name].cap == host_t.cap:
-                    dt = slot[name]
-                else:
-                    dt = TiledCodes(host_t.fmt, self.H, self.device, cap=host_t.cap)
-                dt.len = host_t.len
-                for key, t in host_t.t.items():
-                    if t is not None:
-                        copies.append((dt.t[key].data_ptr(), t.data_ptr(), t.numel() * t.element_size()))
-                dev[name] = dt
-            self._cold_slots[cid] = dev
-            out[cid] = dev
+        missing = sorted(cid for cid in ids if cid not in out)
+        if not missing:
+            return out, [], []
+        pool = self._slot_pool()
+        nb = self._chunk_bytes()
+        lru = [d["slot"] for d in self._cold_slots.values()]
+        fetched, copies = [], []
+        for j, part in plan_slot_windows(self._slot_cid, lru, set(ids), missing, self.ARENA_CHUNKS):
+            for t, cid in enumerate(part):
+                old = self._slot_cid[j + t]
+                if old >= 0:
+                    del self._cold_slots[old]
+                self._slot_cid[j + t] = cid
+                dev = self._slot_entry(cid, j + t)
+                self._cold_slots[cid] = dev
+                out[cid] = dev
+                fetched.append(cid)
+            src = self._cold_pinned[part[0]]["tiled_buf"]
+            copies.append((pool.data_ptr() + j * nb, src.data_ptr(), len(part) * nb))
+        return out, fetched, copies
+
+    def _side_stream(self) -> K.SideStream:
+        if self._side is None:
+            self._side = K.SideStream()
+        return self._side
+
+    def prefetch_cold_chunks(self, chunk_ids: Sequence[int]) -> Dict[int, dict]:
+        """Make pinned chunks resident in device slots; copies are issued with
+        hipMemcpyAsync on a side stream (after the work already queued on the
+        current stream, which may still read a reused slot) and the current
+        stream waits on its event."""
+        out, _, copies = self._stage_cold(chunk_ids)
         if copies:
-            self._side.prefetch(copies)
-        self._side.make_current_wait(self.device)
+            side = self._side_stream()
+            side.wait_for_current(self.device)
+            side.prefetch(copies)
+            side.make_current_wait(self.device)
         return out
+
+    def evict_cold_slots(self) -> None:
+        """Drop every chunk from the device slots (the slot buffer is kept)."""
+        self._cold_slots.clear()
+        self._slot_cid = [-1] * len(self._slot_cid)
 
     # ------------------------------------------------------------------ windows
     def _max_query_position(self, query_positions, current_position) -> int:
@@ -687,7 +847,26 @@ class RFSNv10KVCacheMLX:
                                               query_positions=adjusted)
         return self._fused_forward(q, causal, query_positions, router, current_position, context_window, cold_chunks)
 
-    def _fused_forward(self, q, causal, query_positions, router, current_position, context_window, cold_chunks):
+    def prepare(self, q: torch.Tensor, causal: bool = True, query_positions=None,
+                router: Optional[AsyncHierarchicalRouterMLX] = None, current_position: Optional[int] = None,
+                context_window: Optional[int] = None, cold_chunks: Optional[Sequence[int]] = None,
+                splits: int = 0, out: Optional[torch.Tensor] = None) -> "K.PrefetchedStep":
+        """A reusable fused decode step over this window (``q`` is read at
+        launch time, so a decode loop refills it in place).  Cold chunks not
+        resident in device slots are copied in by every call of the step,
+        overlapped with the attention over the resident part; with all of
+        them resident the step is one launch.  The step stays valid until
+        another call changes the cache or its device slots."""
+        if not self._fused_ok():
+            raise ValueError("prepare() needs a cache format the fused kernel serves")
+        step = self._fused_forward(q, causal, query_positions, router, current_position, context_window,
+                                   cold_chunks, launch=False, splits=splits, out=out)
+        if step is None:
+            raise ValueError("the window is empty")
+        return step
+
+    def _fused_forward(self, q, causal, query_positions, router, current_position, context_window, cold_chunks,
+                       launch: bool = True, splits: int = 0, out: Optional[torch.Tensor] = None):
         start, end, adjusted = self._window_bounds(query_positions, context_window, current_position)
         stats = self._empty_access_stats()
         stats["window_start"], stats["window_end"] = start, end
@@ -699,54 +878,86 @@ class RFSNv10KVCacheMLX:
         self.last_access_stats = dict(stats)
         B, Hq, D = q.shape
         if not plan:
-            return torch.zeros_like(q)
-        qh = q.to(self.device, torch.float16)
+            return torch.zeros_like(q) if launch else None
+        qh = q if (q.device == self.device and q.dtype == torch.float16) else q.to(self.device, torch.float16)
         spans = self._tier_spans()
         fmt = self._fmt()
-        table = K.SegmentTable(B)
+        # the resident part of the window (hot, warm, cold chunks already in
+        # device slots) and the chunks still to copy in
+        resident, incoming = K.SegmentTable(B), K.SegmentTable(B)
         hot_len, hot_pos0, hot_off = 0, 0, 0
-        max_tokens = 0
+        res_tokens, in_tokens = 0, 0
         cold_ids = [x[0]["chunk_id"] for kind, x in plan if kind == "cold"]
-        if len(cold_ids) > self._cold_slot_limit:
-            raise ValueError(f"window touches {len(cold_ids)} cold chunks; the device slot pool holds "
-                             f"{self._cold_slot_limit} (raise cold_slots)")
-        slots = self.prefetch_cold_chunks(cold_ids) if cold_ids else {}
+        slots, fetched, copies = self._stage_cold(cold_ids) if cold_ids else ({}, [], [])
+        fetched = set(fetched)
         for kind, x in plan:
             if kind == "hot":
                 hot_off = x[0] - spans["hot"][0]
                 hot_len = x[1] - x[0]
                 hot_pos0 = x[0] - start
-                max_tokens += hot_len
+                res_tokens += hot_len
             elif kind == "warm":
                 a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
                 skip = a // K.TILE
                 kt, vt = self._warm_tiled
                 for bi in range(B):
-                    table.add(bi, kt.codes(skip), vt.codes(skip), kt.cap, b - skip * K.TILE,
-                              spans["warm"][0] + skip * K.TILE - start)
-                max_tokens += b - skip * K.TILE
+                    resident.add(bi, kt.codes(skip), vt.codes(skip), kt.cap, b - skip * K.TILE,
+                                 spans["warm"][0] + skip * K.TILE - start)
+                res_tokens += b - skip * K.TILE
             else:
                 meta, ov, _ = x
                 dev = slots[meta["chunk_id"]]
                 a, b = ov[0] - meta["start_token"], ov[1] - meta["start_token"]
                 skip = a // K.TILE
+                table = incoming if meta["chunk_id"] in fetched else resident
                 for bi in range(B):
                     table.add(bi, dev["key"].codes(skip), dev["value"].codes(skip), dev["key"].cap,
                               b - skip * K.TILE, meta["start_token"] + skip * K.TILE - start)
-                max_tokens += b - skip * K.TILE
+                if meta["chunk_id"] in fetched:
+                    in_tokens += b - skip * K.TILE
+                else:
+                    res_tokens += b - skip * K.TILE
         qpos = adjusted
         if causal:
             qpos = _normalize_query_positions(adjusted, B, Hq, stats["window_tokens"] - 1, self.device)
         hk = self._hot_k[:, hot_off:] if hot_len else None
         hv = self._hot_v[:, hot_off:] if hot_len else None
-        return K.fused_attention(
-            qh, fmt, kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos if causal else None,
-            hot_k=hk, hot_v=hv, hot_len=hot_len, hot_pos0=hot_pos0, hot_seq_stride=0, segments=table,
-            k_pq_cb=self._kq.pq.codebooks, v_pq_cb=self._vq.pq.codebooks,
-            k_rvq_cb=self._kq.rvq.codebooks if fmt.rvq_subspaces else None,
-            v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
-            cb_batch_stride=False, max_tokens=max(max_tokens, 1), hot_cap=int(self._hot_k.shape[1]),
-        ).to(q.dtype)
+        if out is None:
+            out = torch.empty((B, Hq, D), dtype=torch.float16, device=self.device)
+        common = dict(kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos if causal else None,
+                      hot_seq_stride=0, k_pq_cb=self._kq.pq.codebooks, v_pq_cb=self._vq.pq.codebooks,
+                      k_rvq_cb=self._kq.rvq.codebooks if fmt.rvq_subspaces else None,
+                      v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
+                      cb_batch_stride=False, hot_cap=int(self._hot_k.shape[1]), out=out, launch=False)
+        has_resident = hot_len > 0 or not resident.empty
+        if not fetched or not has_resident:
+            # one launch; with chunks to copy it waits for them (nothing to overlap)
+            table = resident if not fetched else incoming
+            fl = K.fused_attention(qh, fmt, hot_k=hk, hot_v=hv, hot_len=hot_len, hot_pos0=hot_pos0,
+                                   segments=table, max_tokens=max(res_tokens + in_tokens, 1), splits=splits,
+                                   **common)
+            step = K.PrefetchedStep(self._side_stream(), copies, [fl], wait_at=0) if copies else fl
+        else:
+            # attend the resident part while the side stream copies the
+            # missing chunks, then the copied chunks; partials merge at the end
+            sa = K.fused_splits(B, Hq, self.H, hot_len, max(res_tokens, 1), resident.max_rows, splits)
+            sb = K.fused_splits(B, Hq, self.H, 0, max(in_tokens, 1), incoming.max_rows, splits)
+            ws = torch.empty(B * Hq * (sa + sb) * (D + 2) * 4, dtype=torch.uint8, device=self.device)
+            fa = K.fused_attention(qh, fmt, hot_k=hk, hot_v=hv, hot_len=hot_len, hot_pos0=hot_pos0,
+                                   segments=resident, max_tokens=max(res_tokens, 1), splits=sa, workspace=ws,
+                                   part=(0, sa + sb, False), **common)
+            fb = K.fused_attention(qh, fmt, hot_k=None, hot_v=None, hot_len=0, hot_pos0=0, segments=incoming,
+                                   max_tokens=max(in_tokens, 1), splits=sb, workspace=ws,
+                                   part=(sa, sa + sb, True), **common)
+            step = K.PrefetchedStep(self._side_stream(), copies, [fa, fb], wait_at=1)
+        if not launch:
+            if copies:
+                # the staged slots count as resident from now on: fill them
+                # before any other call reads them
+                step.issue_copies()
+                self._side_stream().make_current_wait(self.device)
+            return step
+        return step().to(q.dtype)
 
     def memory_usage_bytes(self) -> Dict[str, int]:
         """cache.py:430-440.  Subspace format: warm_rvq_bytes counts the RVQ

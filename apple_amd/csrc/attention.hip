@@ -147,31 +147,69 @@ exact_attn_kernel(const uint16_t* __restrict__ q, int Hq, const uint16_t* __rest
 
 }  // namespace
 
-// Merge split partials (m, l, acc[D]) into fp16 outputs: one block per
-// (sequence, query head).
-__global__ void merge_partials_kernel(const float* __restrict__ partial, int splits, int D,
-                                      uint16_t* __restrict__ out) {
-  const int64_t bh = blockIdx.x;
-  const float* p = partial + bh * splits * (D + 2);
-  float M = -__builtin_inff();
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, p[s * (D + 2)]);
-  float L = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float m = p[s * (D + 2)];
-    if (m > -__builtin_inff()) L += p[s * (D + 2) + 1] * exp2f(m - M);
+// Merge split partials (m, l, acc[D]) into fp16 outputs: one block of 256
+// threads per (sequence, query head).  The split weights exp2(m_s - max) go
+// to LDS once; then 256/D groups of D threads each sum a share of the splits
+// with independent loads, and the groups are added in LDS.  A split with
+// m_s = -inf (no allowed key) has weight 0.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxSplits = 8192;
+
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float y = __shfl_xor(v, o);
+    v = is_max ? fmaxf(v, y) : v + y;
   }
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
-    float a = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const float m = p[s * (D + 2)];
-      if (m > -__builtin_inff()) a += p[s * (D + 2) + 2 + c] * exp2f(m - M);
-    }
-    out[bh * D + c] = f2h(L > 0.f ? a / L : 0.f);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kMergeThreads / 64; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(kMergeThreads) merge_partials_kernel(const float* __restrict__ partial, int splits,
+                                                                      int D, uint16_t* __restrict__ out) {
+  extern __shared__ float weight[];  // [splits]
+  __shared__ float red[kMergeThreads / 64];
+  __shared__ float part[kMergeThreads];
+  const int64_t bh = blockIdx.x;
+  const int t = threadIdx.x;
+  const float* p = partial + bh * splits * (D + 2);
+  float mx = -__builtin_inff();
+  for (int s = t; s < splits; s += kMergeThreads) mx = fmaxf(mx, p[s * (D + 2)]);
+  mx = block_reduce(mx, red, true);
+  float l = 0.f;
+  for (int s = t; s < splits; s += kMergeThreads) {
+    const float m = p[s * (D + 2)];
+    const float w = m > -__builtin_inff() ? exp2f(m - mx) : 0.f;
+    weight[s] = w;
+    l += p[s * (D + 2) + 1] * w;
+  }
+  l = block_reduce(l, red, false);  // its barriers also publish weight[]
+  const int groups = kMergeThreads / D, g = t / D, c = t % D;
+  float a = 0.f;
+  if (g < groups) {
+#pragma unroll 8
+    for (int s = g; s < splits; s += groups) a += weight[s] * p[s * (D + 2) + 2 + c];
+  }
+  part[t] = a;
+  __syncthreads();
+  if (t < D) {
+    float sum = 0.f;
+    for (int k = 0; k < groups; ++k) sum += part[k * D + t];
+    out[bh * D + t] = f2h(l > 0.f ? sum / l : 0.f);
   }
 }
 
 int launch_merge(const float* partial, int64_t bh, int splits, int D, void* out, hipStream_t s) {
-  hipLaunchKernelGGL(merge_partials_kernel, dim3((unsigned)bh), dim3(64), 0, s, partial, splits, D, (uint16_t*)out);
+  RFSN_REQUIRE(D > 0 && D <= kMergeThreads && kMergeThreads % D == 0, "merge: head_dim must divide 256");
+  RFSN_REQUIRE(splits > 0 && splits <= kMergeMaxSplits, "merge: at most 8192 split partials per row");
+  hipLaunchKernelGGL(merge_partials_kernel, dim3((unsigned)bh), dim3(kMergeThreads), (size_t)splits * sizeof(float),
+                     s, partial, splits, D, (uint16_t*)out);
   return check_launch("merge_partials");
 }
 

@@ -180,8 +180,9 @@ __device__ __forceinline__ TileSrc hot_tile(const rfsn_fused_params& p, int tt) 
 }
 
 // Encoded tile r of segments 1..nseg-1 (r counted from the first tile of
-// segment 1), walking the table (uniform, rare: the common cache has one warm
-// segment).  r must lie inside the table.
+// segment 1), walking the table (uniform).  The lengths of 8 segments are read
+// per step, with no data dependence between the reads, so a walk costs one
+// scalar-memory round trip per 8 segments.  r must lie inside the table.
 __device__ __forceinline__ TileSrc walk_segments(cseg segs, int nseg, int r) {
   TileSrc s;
   s.kind = 1;
@@ -189,19 +190,47 @@ __device__ __forceinline__ TileSrc walk_segments(cseg segs, int nseg, int r) {
   s.off = 0;
   s.count = 0;
   s.pos0 = 0;
-  for (int i = 1; i < nseg; ++i) {
-    const int len = segs[i].len;
-    const int nt = (len + kTile - 1) / kTile;
-    if (r < nt) {
-      s.seg = i;
+  for (int i0 = 1; i0 < nseg; i0 += 8) {
+    int nt[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = min(i0 + j, nseg - 1);  // entries past the table count no tiles
+      const int n = (segs[i].len + kTile - 1) / kTile;
+      nt[j] = i0 + j < nseg ? n : 0;
+    }
+    int found = -1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (found < 0) {
+        if (r < nt[j]) found = j;
+        else r -= nt[j];
+      }
+    }
+    if (found >= 0) {
+      const int seg = i0 + found;
+      const int len = segs[seg].len;
+      s.seg = seg;
       s.off = r * kTile;
       s.count = min(kTile, len - s.off);
-      s.pos0 = segs[i].pos0 + s.off;
-      break;
+      s.pos0 = segs[seg].pos0 + s.off;
+      return s;
     }
-    r -= nt;
   }
   return s;
+}
+
+// Tiles of segments 1..nseg-1, 8 independent reads per step.
+__device__ __forceinline__ int tail_tiles(cseg segs, int nseg) {
+  int total = 0;
+  for (int i0 = 1; i0 < nseg; i0 += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = min(i0 + j, nseg - 1);
+      const int n = (segs[i].len + kTile - 1) / kTile;
+      total += i0 + j < nseg ? n : 0;
+    }
+  }
+  return total;
 }
 
 // One tile's encoded data for one lane (K or V): IPT code bytes of the PQ and
@@ -457,22 +486,30 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     const uint16_t* vp = (const uint16_t*)p.v_pq_cb + (int64_t)b * p.pq_cb_stride;
     const uint16_t* srcs[4] = {kp, vp, RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : kp,
                                RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : vp};
+    // every load of this thread is issued before its first LDS store, so the
+    // block waits for one memory round trip rather than one per entry
+    using Vec = typename std::conditional<d == 4, uint2, uint4>::type;
+    constexpr int kIters = (M * 256 + kThreads - 1) / kThreads;
+    Vec v[4][kIters];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int n = (c < 2 || !RVQ) ? C : Cr;
-      uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
-      for (int idx = threadIdx.x; idx < M * 256; idx += kThreads) {
+#pragma unroll
+      for (int i = 0; i < kIters; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
         const int e = idx / M, m = idx % M;  // consecutive lanes store consecutive slots of one entry
-        uint8_t* t = dst + e * kEntryBytes + m * d * 2;
-        if constexpr (d == 4) {
-          uint2 v = make_uint2(0, 0);
-          if (e < n) v = *reinterpret_cast<const uint2*>(srcs[c] + ((int64_t)m * n + e) * d);
-          *reinterpret_cast<uint2*>(t) = v;
-        } else {
-          uint4 v = make_uint4(0, 0, 0, 0);
-          if (e < n) v = *reinterpret_cast<const uint4*>(srcs[c] + ((int64_t)m * n + e) * d);
-          *reinterpret_cast<uint4*>(t) = v;
-        }
+        v[c][i] = Vec{};
+        if (idx < M * 256 && e < n) v[c][i] = *reinterpret_cast<const Vec*>(srcs[c] + ((int64_t)m * n + e) * d);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
+#pragma unroll
+      for (int i = 0; i < kIters; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        const int e = idx / M, m = idx % M;
+        if (idx < M * 256) *reinterpret_cast<Vec*>(dst + e * kEntryBytes + m * d * 2) = v[c][i];
       }
     }
   }
@@ -557,7 +594,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   if (nseg > 0) w0 = warm_base<M, RVQ, KS>(segs, h);
   const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
   int total_tiles = hot_tiles + seg0_tiles;
-  for (int i = 1; i < nseg; ++i) total_tiles += (segs[i].len + kTile - 1) / kTile;
+  total_tiles += tail_tiles(segs, nseg);
   const int t_begin = split * tiles_per_split;
   const int t_end = min(total_tiles, t_begin + tiles_per_split);
   const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
@@ -818,15 +855,17 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       Ls += red_l[w * 8 + head] * f;
       A += red_a[(w * 8 + head) * kD + c] * f;
     }
-    if (splits == 1) {
+    if (splits == 1 && p.part_slots == 0) {
       // whole (sequence, KV head) in this block: normalise and write fp16 directly
       // (a query with no allowed key returns zeros, attention.py:104-105)
       uint16_t* o = (uint16_t*)p.out + ((int64_t)b * p.q_heads + h * G + head) * kD;
       o[c] = f2h(Ls > 0.f ? A / Ls : 0.f);
       continue;
     }
+    // partial slot: this call's split, after the slots of earlier calls in partial mode
+    const int slots = p.part_slots ? p.part_slots : splits;
     float* out = reinterpret_cast<float*>(p.workspace) +
-                 (((int64_t)b * p.q_heads + h * G + head) * splits + split) * (kD + 2);
+                 (((int64_t)b * p.q_heads + h * G + head) * slots + p.part_base + split) * (kD + 2);
     if (c == 0) {
       out[0] = Mx;
       out[1] = Ls;
@@ -867,7 +906,13 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG>;  // 160 KB of static LDS
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(BlockShape<NHG>::T), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
-  if (st || splits == 1) return st;
+  if (st) return st;
+  if (p->part_slots > 0) {
+    if (!p->merge) return RFSN_OK;
+    return launch_merge(reinterpret_cast<const float*>(p->workspace),
+                        (int64_t)p->batch * p->q_heads, p->part_slots, kD, p->out, s);
+  }
+  if (splits == 1) return RFSN_OK;
   return launch_merge(reinterpret_cast<const float*>(p->workspace),
                       (int64_t)p->batch * p->q_heads, splits, kD, p->out, s);
 }
@@ -893,11 +938,17 @@ int dispatch_ks(const rfsn_fused_params* p, hipStream_t s) {
 
 using namespace rfsn;
 
+extern "C" int32_t rfsn_fused_splits(const rfsn_fused_params* p) {
+  if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0) return 0;
+  return auto_splits(p);
+}
+
 extern "C" size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p) {
   if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0) return 0;
   const int splits = auto_splits(p);
-  if (splits == 1) return 0;  // one split writes the output directly
-  return (size_t)p->batch * p->q_heads * splits * (kD + 2) * sizeof(float);
+  const int slots = p->part_slots > 0 ? p->part_slots : splits;
+  if (p->part_slots <= 0 && splits == 1) return 0;  // one split writes the output directly
+  return (size_t)p->batch * p->q_heads * slots * (kD + 2) * sizeof(float);
 }
 
 extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream) {
@@ -920,6 +971,17 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   RFSN_REQUIRE(p->max_segments >= 0 && (p->max_segments == 0 || (p->segments && p->num_segments)),
                "fused: bad segment table");
   RFSN_REQUIRE(p->max_tokens >= p->hot_len, "fused: max_tokens must cover the hot tier");
+  RFSN_REQUIRE(p->part_slots >= 0 && p->part_base >= 0 && (p->merge == 0 || p->merge == 1),
+               "fused: bad partial-mode fields");
+  RFSN_REQUIRE(p->part_slots > 0 || (p->part_base == 0 && p->merge == 0),
+               "fused: part_base and merge need part_slots > 0");
+  RFSN_REQUIRE(p->part_slots <= 8192 && auto_splits(p) <= 8192, "fused: at most 8192 split partials");
+  if (p->part_slots > 0) {
+    const int splits = auto_splits(p);
+    RFSN_REQUIRE(p->part_base + splits <= p->part_slots, "fused: part_base + splits exceeds part_slots");
+    RFSN_REQUIRE(!p->merge || p->part_base + splits == p->part_slots,
+                 "fused: the merging call must fill the last slots (part_base + splits == part_slots)");
+  }
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;

@@ -280,6 +280,15 @@ class SegmentTable:
                            L.ptr(c.get("sparse_val")))
         self.rows[b].append(L.Segment(codes(k), codes(v), head_stride, length, pos0))
 
+    @property
+    def max_rows(self) -> int:
+        """Segments of the longest row (the table's max_segments, at least 1)."""
+        return max(1, max(len(r) for r in self.rows))
+
+    @property
+    def empty(self) -> bool:
+        return all(not r for r in self.rows)
+
     def to_device(self, device) -> Tuple[torch.Tensor, torch.Tensor, int]:
         maxs = max(1, max(len(r) for r in self.rows))
         size = C.sizeof(L.Segment)
@@ -301,13 +310,20 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
                     v_rvq_cb: Optional[torch.Tensor], cb_batch_stride: bool, max_tokens: int,
                     splits: int = 0, table: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
                     workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                    hot_cap: Optional[int] = None, launch: bool = True):
+                    hot_cap: Optional[int] = None, launch: bool = True,
+                    part: Optional[Tuple[int, int, bool]] = None):
     """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
 
     hot_k/hot_v: [.., Hkv, hot_cap, D] fp16 (sequence stride ``hot_seq_stride``
     elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
     else [M, C, d] shared.  With ``launch=False`` returns a ``FusedLaunch``
     that re-issues the same launch (same buffers) without rebuilding it.
+
+    ``part = (base, slots, merge)`` attends one part of a window split over
+    several calls on one stream: the call's split partials go to slots
+    base .. base+splits-1 of ``slots`` in ``workspace`` (shared by the calls,
+    which must pass ``splits`` explicitly), and the call with ``merge`` writes
+    ``out`` from all slots.
     """
     _dev(q, "fused_attention")
     q = _contig(q)
@@ -336,9 +352,15 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
     p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
     p.max_tokens, p.splits = max_tokens, splits
+    if part is not None:
+        if splits <= 0 or workspace is None:
+            raise ValueError("partial calls need explicit splits and a shared workspace")
+        p.part_base, p.part_slots, p.merge = int(part[0]), int(part[1]), int(bool(part[2]))
     lib = L.load()
     wsb = lib.rfsn_fused_workspace_bytes(C.byref(p))
     if workspace is None or workspace.numel() < wsb:
+        if part is not None:
+            raise ValueError(f"partial calls share a workspace of at least {wsb} bytes")
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
     fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments, *cbs], out, _stream(q))
@@ -346,6 +368,16 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
         return fl
     fl()
     return out
+
+
+def fused_splits(batch: int, q_heads: int, kv_heads: int, hot_len: int, max_tokens: int, max_segments: int,
+                 splits: int = 0) -> int:
+    """Token splits per (sequence, KV head) the fused kernel uses for a call
+    of this shape (``splits`` if positive, else its automatic choice)."""
+    p = L.FusedParams()
+    p.batch, p.q_heads, p.kv_heads = batch, q_heads, kv_heads
+    p.hot_len, p.max_tokens, p.max_segments, p.splits = hot_len, max_tokens, max_segments, splits
+    return int(L.load().rfsn_fused_splits(C.byref(p)))
 
 
 class FusedLaunch:
@@ -365,6 +397,52 @@ class FusedLaunch:
         st = self._fn(self._ref, self.stream)
         if st:
             L.check(st, "rfsn_fused_decode_attention")
+        return self.out
+
+
+class PrefetchedStep:
+    """A decode step whose window includes chunks still in pinned host memory.
+
+    ``__call__`` waits (on the host) for the work already on the launch stream,
+    which may read the destination slots, queues the host-to-device ``copies``
+    (dst, src, bytes) on the side stream, runs ``launches[:wait_at]`` (the
+    resident part of the window) while they are in flight, makes the launch
+    stream wait for the copies, then runs ``launches[wait_at:]`` (the copied
+    chunks, ending with the merge).  Every call re-issues the copies it was
+    built with."""
+
+    def __init__(self, side: SideStream, copies: Sequence[Tuple[int, int, int]], launches: Sequence[FusedLaunch],
+                 wait_at: int, keep: Optional[list] = None):
+        if not launches:
+            raise ValueError("a decode step needs at least one launch")
+        self.side = side
+        self.launches = list(launches)
+        self.wait_at = wait_at
+        self.stream = self.launches[0].stream
+        self.out = self.launches[-1].out
+        self.ncopies = len(copies)
+        self._copies = (L.Copy * max(1, self.ncopies))()
+        for i, (dst, src, nbytes) in enumerate(copies):
+            self._copies[i] = L.Copy(dst, src, nbytes)
+        self.copy_bytes = sum(int(c[2]) for c in copies)
+        self._keep = keep
+
+    def issue_copies(self) -> None:
+        """The copies alone, once the work already on the launch stream (which
+        may read the destination slots) is done; their event recorded."""
+        self.side.drain(self.stream)
+        L.call("rfsn_prefetch_h2d", self._copies, self.ncopies, self.side.stream)
+        L.call("rfsn_event_record", self.side.event, self.side.stream)
+
+    def __call__(self) -> torch.Tensor:
+        if self.ncopies:
+            self.issue_copies()
+        for i, fl in enumerate(self.launches):
+            if i == self.wait_at and self.ncopies:
+                L.call("rfsn_stream_wait_event", self.stream, self.side.event)
+            fl()
+        if self.wait_at >= len(self.launches) and self.ncopies:
+            L.call("rfsn_stream_wait_event", self.stream, self.side.event)
         return self.out
 
 
@@ -404,10 +482,21 @@ class SideStream:
         L.call("rfsn_event_create", C.byref(e2))
         self.main_event = e2.value
 
+    def drain(self, stream: int) -> None:
+        """Block the host until the work queued so far on ``stream`` is done.
+
+        Copies into device buffers that queued kernels may still read are
+        ordered this way, on the host, rather than by making the side stream
+        wait on an event of ``stream``: on MI355X a copy-engine transfer
+        that waits on a compute-queue event costs about 130 us more than the
+        2.9 MB transfer itself (60 us), while the launch stream waiting on the
+        copy's event costs a few."""
+        L.call("rfsn_event_record", self.main_event, stream)
+        L.call("rfsn_event_synchronize", self.main_event)
+
     def wait_for_current(self, device=None) -> None:
-        """Order the side stream after all work already queued on the current stream."""
-        L.call("rfsn_event_record", self.main_event, L.stream_handle(device))
-        L.call("rfsn_stream_wait_event", self.stream, self.main_event)
+        """Order later side-stream copies after the work queued on the current stream."""
+        self.drain(L.stream_handle(device))
 
     def prefetch(self, copies: Sequence[Tuple[int, int, int]]) -> None:
         arr = (L.Copy * max(1, len(copies)))()
@@ -418,6 +507,10 @@ class SideStream:
 
     def make_current_wait(self, device=None) -> None:
         L.call("rfsn_stream_wait_event", L.stream_handle(device), self.event)
+
+    def synchronize(self) -> None:
+        """Block the host until the copies recorded so far have finished."""
+        L.call("rfsn_event_synchronize", self.event)
 
     def close(self) -> None:
         for name in ("event", "main_event"):

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 1
+#define RFSN_ABI_VERSION 2
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -209,8 +209,22 @@ typedef struct rfsn_fused_params {
   int32_t splits;         /* token splits per (sequence, KV head); 0 = auto  */
   void* workspace;        /* split partials; may be NULL when           */
   size_t workspace_bytes; /* rfsn_fused_workspace_bytes() returns 0     */
+  /* Partial mode (part_slots > 0): one window attended over several calls
+   * on one stream, e.g. the resident segments while a side stream copies
+   * cold chunks in, then the copied chunks.  The call writes its split
+   * partials (running max, sum, unnormalised output) into slots
+   * [part_base, part_base + splits) of part_slots per (sequence, query head)
+   * of the workspace; with merge = 1 (only when part_base + splits ==
+   * part_slots) it then merges all part_slots slots into out.  Every slot
+   * must have been written by a call queued earlier on the stream.  Calls
+   * that share one workspace share B and Hq.  part_slots = 0: one call. */
+  int32_t part_base;
+  int32_t part_slots;
+  int32_t merge;
 } rfsn_fused_params;
 
+/* Token splits the call would use (p->splits, or the automatic choice when 0). */
+int32_t rfsn_fused_splits(const rfsn_fused_params* p);
 size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);
 int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
 

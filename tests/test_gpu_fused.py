@@ -144,3 +144,138 @@ def test_batched_matches_per_sequence(device):
         assert np.array_equal(H(mv).view(np.uint16), refs[b][1].view(np.uint16))
         ref = nx.blockwise_attention(q[b:b + 1], refs[b][0], refs[b][1], 0.125, 256, False, None)
         assert np.abs(out[b:b + 1].astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
+def _cold_cache(device, seed, total, nh, nw, chunk, Hq=32, Hkv=4, cold_slots=32):
+    """A recency cache (PQ M16 + RVQ M16 + top-4) whose oldest tokens sit in
+    pinned cold chunks of ``chunk`` tokens, filled by two appends (the second
+    spills warm tokens into a partly filled chunk), with the oracle's decode
+    of every token."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    g = rng(seed)
+    D, M = 64, 16
+    keys, values = _kv(g, total, Hkv, D)
+    cbs = {n: rand_codebooks(g, M, 256, D // M) for n in ("kp", "vp")}
+    cbs.update({n: rand_codebooks(g, M, 256, D // M) * np.float16(0.35) for n in ("kr", "vr")})
+    cfg = RFSNConfig(num_heads=Hq, head_dim=D, num_subspaces=M, subspace_dim=D // M, num_rvq_layers=1,
+                     rvq_codebook_size=256, rvq_sparsity_threshold=0.005, hot_capacity=nh, warm_capacity=nw,
+                     block_size_seq=128, num_kv_heads=Hkv, rvq_subspaces=M, sparse_topk=4, tier_policy="recency",
+                     cold_medium="pinned", cold_chunk_tokens=chunk)
+    kq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["kp"]), rvq_codebooks=torch.from_numpy(cbs["kr"]))
+    vq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["vp"]), rvq_codebooks=torch.from_numpy(cbs["vr"]))
+    cache = RFSNv10KVCacheMLX(cfg, device=device, cold_slots=cold_slots)
+    cut = total - 300
+    cache.update(T(keys[:cut], device), T(values[:cut], device), (kq, vq))
+    cache.update(T(keys[cut:], device), T(values[cut:], device), (kq, vq))
+    dec = []
+    for x, p, r in ((keys, cbs["kp"], cbs["kr"]), (values, cbs["vp"], cbs["vr"])):
+        enc = nx.ext_encode(x.reshape(-1, D), p, r, 4)
+        dec.append(nx.ext_decode(enc["pq_codes"], p, enc["rvq_codes"], r, enc["sparse_idx"],
+                                 enc["sparse_val"]).reshape(total, Hkv, D))
+    return g, cfg, cache, keys, values, dec
+
+
+def _cold_window(ids, chunk, ncold, total, nh, keys, values, dec):
+    """Positions and oracle K/V of [chosen cold chunks | warm | hot], in position order."""
+    pos = np.concatenate([np.arange(c * chunk, min((c + 1) * chunk, ncold)) for c in sorted(ids)]
+                         + [np.arange(ncold, total)])
+    hot = (pos >= total - nh)[:, None, None]
+    return pos, np.where(hot, keys[pos], dec[0][pos]), np.where(hot, values[pos], dec[1][pos])
+
+
+def test_fused_cold_pinned_prefetch(device):
+    """Pinned cold chunks chosen by the router's ranking (and an arbitrary
+    set): the fused path with every chunk copied in during the step (resident
+    part attended while the copies run, partials merged), with every chunk
+    resident (one launch), and with half of them resident; prepared steps of
+    both kinds; materialized windows bit-exact."""
+    from apple_amd import kernels as K
+    from apple_amd.storage import AsyncHierarchicalRouterMLX
+
+    total, nh, nw, chunk = 1664, 64, 600, 100
+    ncold = total - nh - nw
+    g, cfg, cache, keys, values, dec = _cold_cache(device, 90, total, nh, nw, chunk)
+    assert (cache.num_hot, cache.num_warm, cache.num_cold) == (nh, nw, ncold)
+    assert [m["chunk_id"] for m in cache.cold_chunk_metadata] == list(range(10))
+    router = AsyncHierarchicalRouterMLX(cfg).bind(cache)
+    near = router.rank(total - 1, total)[:4]
+    assert near == [9, 8, 7, 6]
+    B, Hq = 2, 32
+    q = randn16(g, B, Hq, 64)
+    qd = T(q, device)
+    qp = g.integers(-1, total, (B, Hq)).astype(np.int32)
+    qp[0, 0] = total - 1  # the window ends at the newest token
+    for ids in (near, [0, 3, 7]):
+        pos, wk, wv = _cold_window(ids, chunk, ncold, total, nh, keys, values, dec)
+        mk, mv, _ = cache.materialize_window(cold_chunks=ids)
+        assert np.array_equal(H(mk).view(np.uint16), wk.view(np.uint16))
+        assert np.array_equal(H(mv).view(np.uint16), wv.view(np.uint16))
+        qidx = (np.searchsorted(pos, qp, side="right") - 1).astype(np.int32)
+        for mode in ("copied", "resident", "half"):
+            for causal, qpa, rqp in ((False, None, None), (True, None, None), (True, qp, qidx)):
+                if mode == "copied":
+                    cache.evict_cold_slots()
+                elif mode == "half":
+                    cache.evict_cold_slots()
+                    cache.prefetch_cold_chunks(ids[::2])
+                out = cache.attention_forward(qd, causal=causal, cold_chunks=ids,
+                                              query_positions=None if qpa is None else T(qpa, device))
+                st = cache.get_last_access_stats()
+                assert st["cold_chunks_touched"] == len(ids)
+                ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, causal, rqp)
+                err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
+                assert err <= TOL, (ids, mode, causal, qpa is None, err)
+        # prepared steps: copies re-issued by every call, then all resident
+        ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, True, None)
+        cache.evict_cold_slots()
+        step = cache.prepare(qd, causal=True, cold_chunks=ids)
+        assert isinstance(step, K.PrefetchedStep) and step.copy_bytes == len(ids) * cache._chunk_bytes()
+        assert step.ncopies == (1 if ids == near else len(ids))  # consecutive chunks move in one copy
+        for _ in range(2):
+            err = np.abs(H(step()).astype(np.float32) - ref.astype(np.float32)).max()
+            assert err <= TOL
+        one = cache.prepare(qd, causal=True, cold_chunks=ids)
+        assert isinstance(one, K.FusedLaunch)
+        for _ in range(2):
+            assert np.abs(H(one()).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
+def test_fused_cold_slot_limit_and_partial_contract(device):
+    """More chunks than device slots is a ValueError; partial-mode calls whose
+    slots do not fit are rejected before any launch."""
+    from apple_amd import kernels as K
+
+    total, nh, nw, chunk = 900, 32, 200, 64
+    g, cfg, cache, keys, values, dec = _cold_cache(device, 91, total, nh, nw, chunk, Hq=8, Hkv=4, cold_slots=3)
+    q = T(randn16(g, 1, 8, 64), device)
+    with pytest.raises(ValueError):
+        cache.attention_forward(q, cold_chunks=[0, 1, 2, 3])
+    out = cache.attention_forward(q, cold_chunks=[0, 1, 2])
+    assert out.shape == (1, 8, 64)
+    fmt = cache._fmt()
+    kt, vt = cache._warm_tiled
+    table = K.SegmentTable(1)
+    table.add(0, kt.codes(0), vt.codes(0), kt.cap, nw, 0)
+    ws = torch.empty(1 << 16, dtype=torch.uint8, device=device)
+    common = dict(kv_heads=4, scale=0.125, causal=False, qpos=None, hot_k=None, hot_v=None, hot_len=0,
+                  hot_pos0=0, hot_seq_stride=0, segments=table, k_pq_cb=cache._kq.pq.codebooks,
+                  v_pq_cb=cache._vq.pq.codebooks, k_rvq_cb=cache._kq.rvq.codebooks,
+                  v_rvq_cb=cache._vq.rvq.codebooks, cb_batch_stride=False, max_tokens=nw, workspace=ws)
+    with pytest.raises(ValueError):
+        K.fused_attention(q, fmt, splits=4, part=(2, 5, False), **common)   # 2 + 4 > 5 slots
+    with pytest.raises(ValueError):
+        K.fused_attention(q, fmt, splits=2, part=(0, 4, True), **common)    # merging call not last
+    # two partial calls over two halves of the warm tier equal one call
+    half = K.round_up(nw // 2, K.TILE)
+    t1, t2 = K.SegmentTable(1), K.SegmentTable(1)
+    t1.add(0, kt.codes(0), vt.codes(0), kt.cap, half, 0)
+    t2.add(0, kt.codes(half // K.TILE), vt.codes(half // K.TILE), kt.cap, nw - half, half)
+    whole = K.fused_attention(q, fmt, splits=0, **{**common, "workspace": None})
+    out = torch.empty_like(q)
+    K.fused_attention(q, fmt, splits=3, part=(0, 5, False), out=out, **{**common, "segments": t1, "max_tokens": half})
+    K.fused_attention(q, fmt, splits=2, part=(3, 5, True), out=out,
+                      **{**common, "segments": t2, "max_tokens": nw - half})
+    assert float((out.float() - whole.float()).abs().max()) <= 1e-3

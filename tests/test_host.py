@@ -155,3 +155,56 @@ def test_product_path_refuses_cpu_tensors():
     cb = torch.zeros((16, 256, 4), dtype=torch.float16)
     with pytest.raises(RuntimeError, match="GPU only"):
         K.pq_encode(x, cb)
+
+
+def _check_windows(slot_cid, wanted, missing, arena, windows):
+    used = set()
+    got = []
+    for j, part in windows:
+        assert part and all(b == a + 1 for a, b in zip(part, part[1:]))          # consecutive ids
+        assert len({c // arena for c in part}) == 1                               # one pinned arena
+        slots = range(j, j + len(part))
+        assert 0 <= j and j + len(part) <= len(slot_cid)
+        assert not used.intersection(slots)
+        used.update(slots)
+        assert all(slot_cid[s] < 0 or slot_cid[s] not in wanted for s in slots)  # no wanted chunk evicted
+        got += part
+    assert sorted(got) == sorted(missing)
+
+
+def test_cold_slot_windows():
+    """Placement of missing cold chunks in the device slot pool: the router's
+    16 consecutive chunks in an empty pool are one copy; a run that crosses a
+    pinned arena is two; wanted resident chunks split a run around them; the
+    least recently used occupants are evicted first; random pool states keep
+    every invariant."""
+    from apple_amd.cache import plan_slot_windows
+
+    free = [-1] * 32
+    ids = list(range(208, 224))
+    assert plan_slot_windows(free, [], set(ids), ids, 64) == [(0, ids)]
+    w = plan_slot_windows(free, [], {62, 63, 64, 65}, [62, 63, 64, 65], 64)
+    assert w == [(0, [62, 63]), (2, [64, 65])]
+    pool = [-1] * 16
+    pool[4], pool[10] = 100, 101                       # wanted and resident
+    w = plan_slot_windows(pool, [4, 10], {100, 101, *range(6)}, list(range(6)), 64)
+    _check_windows(pool, {100, 101, *range(6)}, list(range(6)), 64, w)
+    assert [len(p) for _, p in w] == [5, 1]
+    full = list(range(50, 58))                         # 8 slots, all unwanted occupants
+    lru = [6, 7, 0, 1, 2, 3, 4, 5]                     # slots 6 and 7 hold the oldest chunks
+    assert plan_slot_windows(full, lru, {0, 1}, [0, 1], 64) == [(6, [0, 1])]
+    g = np.random.default_rng(5)
+    for _ in range(300):
+        S = int(g.integers(1, 40))
+        slot_cid = [-1] * S
+        occ = g.choice(1000, size=int(g.integers(0, S + 1)), replace=False)
+        for s, c in zip(g.permutation(S)[:len(occ)], occ):
+            slot_cid[s] = int(c)
+        resident = [c for c in slot_cid if c >= 0]
+        keep = [c for c in resident if g.random() < 0.4]
+        room = S - len(keep)
+        missing = sorted({int(x) for x in g.integers(1000, 1100, int(g.integers(0, room + 1)))})
+        wanted = set(keep) | set(missing)
+        lru = [s for s in g.permutation(S) if slot_cid[s] >= 0]
+        arena = int(g.integers(1, 70))
+        _check_windows(slot_cid, wanted, missing, arena, plan_slot_windows(slot_cid, lru, wanted, missing, arena))
