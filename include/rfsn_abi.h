@@ -223,7 +223,9 @@ typedef struct rfsn_fused_params {
   int32_t merge;
 } rfsn_fused_params;
 
-/* Token splits the call would use (p->splits, or the automatic choice when 0). */
+/* Token splits the call would use (p->splits, or the automatic choice when 0);
+ * sizes partial-mode slots.  Part of the attention_forward replacement
+ * (cache.py:395-428). */
 int32_t rfsn_fused_splits(const rfsn_fused_params* p);
 size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);
 int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
