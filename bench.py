@@ -107,13 +107,14 @@ def setup_decode(w, dev):
     return cache, torch.stack(qs).to(dev)
 
 
-def cpu_baseline(w, cache, q, gpu_out, sample, repeats):
-    """Time the torch-CPU restatement of the path on a bounded sample."""
+def cpu_baseline(w, cache, q, gpu_out, sample, repeats, threads=None):
+    """Time the torch-CPU restatement of the path on a bounded sample, on
+    every host core (or ``threads``)."""
     import torch
     from apple_amd.batched import untile
     from oracle import cpu_baseline as cb
 
-    cores = len(os.sched_getaffinity(0))
+    cores = threads or len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     f = cache.fmt
     total, n, max_err = 0.0, 0, 0.0
@@ -140,6 +141,7 @@ def cpu_baseline(w, cache, q, gpu_out, sample, repeats):
         max_err = max(max_err, float((out.float() - gpu_out[b:b + 1].float().cpu()).abs().max()))
     per_token = total / n
     return {"value": 1.0 / per_token, "unit": "decode tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{min(sample, w.batch)} of {w.batch} sequences x {repeats} repeats, one decode step each "
                       f"(full {w.context}-token window, torch-CPU F.embedding decode + fp32 blockwise "
                       f"attention, block {w.block})",
@@ -173,16 +175,18 @@ def bench_encode(w, args, dev) -> dict:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    steps = max(args.steps, 256)  # one chunk is microseconds: time at least 256 back to back
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"timing {args.steps} encode steps")
+    log(f"timing {steps} encode steps")
     t0 = time.perf_counter()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     end.record()
     torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    kernel_ms = start.elapsed_time(end) / args.steps
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    kernel_ms = start.elapsed_time(end) / steps
+    pct = step_percentiles(step, steps)
     vectors = 2 * w.context * w.kv_heads
     # algorithmic contraction flops: 2 * C * D per vector and stage
     flops = vectors * 2 * w.head_dim * (w.pq_centroids + (w.rvq_centroids if w.rvq_subspaces else 0))
@@ -191,7 +195,7 @@ def bench_encode(w, args, dev) -> dict:
         "metric": "warm-tier encode vectors/s (PQ+RVQ+top-k, MFMA nearest-centroid search), 1 GPU",
         "value": round(vectors / (kernel_ms * 1e-3), 1),
         "unit": "vectors/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded N(0,1) K/V with per-channel scale U(0.5,2); k-means codebooks)",
@@ -202,6 +206,7 @@ def bench_encode(w, args, dev) -> dict:
                              + (f" + top-{w.sparse_k} sparse" if w.sparse_k else "")},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_PEAK_TFLOPS, 5), "traffic": None, "kernel_ms": round(kernel_ms, 5),
+                     "kernel_ms_percentiles": pct,
                      "flops_per_step": flops},
     }
     if not args.no_cpu:
@@ -219,6 +224,54 @@ def bench_encode(w, args, dev) -> dict:
                                             f"(float64 brute-force distances), one process",
                                   "seconds": round(sec, 2)}
     return result
+
+
+def step_percentiles(fn, steps):
+    """p10 / p50 / p90 of per-call times (ms), from one event between each
+    pair of back-to-back calls on the launch stream (a pass of its own)."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    d = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    pick = lambda f: round(d[min(len(d) - 1, int(f * len(d)))], 5)
+    return {"p10": pick(0.1), "p50": pick(0.5), "p90": pick(0.9)}
+
+
+def device_copy_gbs(mib: int = 1024, reps: int = 10) -> float:
+    """Measured device-to-device copy bandwidth, read + write bytes per second (GB/s)."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    gbs = 2 * n * reps / (s.elapsed_time(e) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(gbs, 1)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _timed(fn, steps, stream=None):
@@ -274,6 +327,7 @@ def bench_longctx(w, args, dev) -> dict:
         launch()
     log(f"timing {args.steps} steps (cold chunks resident)")
     ms_per_step, kernel_ms = _timed(launch, args.steps)
+    pct = step_percentiles(launch, args.steps)
 
     # every step copies the chunks in: resident part || copies, then the copied chunks + merge
     cache.evict_cold_slots()
@@ -314,7 +368,7 @@ def bench_longctx(w, args, dev) -> dict:
         "bytes_per_step": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(w.name),
-                     "kernel_ms": round(kernel_ms, 5)},
+                     "kernel_ms": round(kernel_ms, 5), "kernel_ms_percentiles": pct},
         "cold_copy_step": {
             "ms_per_step": round(refetch_ms, 5), "host_ms_per_step": round(refetch_host_ms, 5),
             "copy_bytes": step.copy_bytes, "copies": step.ncopies,
@@ -419,6 +473,8 @@ def main(argv=None) -> int:
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     kernel_ms = start.elapsed_time(end) / args.steps
+    pct = step_percentiles(launch, args.steps)
+    copy_gbs = device_copy_gbs()
     step_bytes = w.bytes_per_step()
     achieved = step_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = traffic_from_profiles(w.name)
@@ -444,11 +500,14 @@ def main(argv=None) -> int:
         "bytes_per_step": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel_ms": round(kernel_ms, 5)},
+                     "kernel_ms": round(kernel_ms, 5), "kernel_ms_percentiles": pct,
+                     "device_copy_gbs": copy_gbs, "frac_of_device_copy": round(achieved / copy_gbs, 4)},
     }
     if not args.no_cpu:
         log("CPU baseline")
         cpu, err = cpu_baseline(w, cache, q, out, args.cpu_sample, args.cpu_repeats)
+        four, _ = cpu_baseline(w, cache, q, out, args.cpu_sample, max(4, args.cpu_repeats // 4), threads=4)
+        cpu["at_4_threads"] = {k: four[k] for k in ("value", "cores", "seconds")}
         result["cpu_baseline"] = cpu
         result["check_max_abs_vs_cpu"] = err
     print(json.dumps(result), flush=True)
