@@ -80,6 +80,7 @@ class TiledCodes:
         self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
         self.cap = 0
         self.len = 0
+        self.head = 0  # tiles before the oldest live token (pop_front_tiles)
         self.t: Dict[str, Optional[torch.Tensor]] = {}
         self._backing = backing
         self._carved = 0
@@ -129,14 +130,33 @@ class TiledCodes:
         new = {key: (None if spec is None else self._new(*spec))
                for key, spec in TiledCodes._arrays(self.fmt, self.heads, cap).items()}
         if self.t and self.cap:
-            for key, old in self.t.items():
-                if old is None:
-                    continue
-                if key in ("pq", "rvq"):
-                    new[key][:, : old.shape[1]] = old
-                else:
-                    new[key][:, : self.cap] = old
-        self.t, self.cap = new, cap
+            self._move_live(self.t, new)
+        self.t, self.cap, self.head = new, cap, 0
+
+    def _live_tiles(self) -> int:
+        return (self.len + K.TILE - 1) // K.TILE
+
+    def _move_live(self, src: Dict[str, Optional[torch.Tensor]], dst: Dict[str, Optional[torch.Tensor]]) -> None:
+        """Copy the live tiles (from tile ``head``) of ``src`` to tile 0 of ``dst``."""
+        f = self.fmt
+        t0, nt = self.head * K.TILE, self._live_tiles() * K.TILE
+        for key, old in src.items():
+            if old is None:
+                continue
+            if key in ("pq", "rvq"):
+                m = f.pq_subspaces if key == "pq" else f.rvq_subspaces
+                live = old[:, t0 * m:(t0 + nt) * m]
+                dst[key][:, :nt * m] = live.clone() if dst[key] is old else live
+            else:
+                live = old[:, t0:t0 + nt]
+                dst[key][:, :nt] = live.clone() if dst[key] is old else live
+
+    def pop_front_tiles(self, n: int) -> None:
+        """Drop the n oldest whole tiles (32 n tokens)."""
+        if n < 0 or n * K.TILE > self.len:
+            raise ValueError("pop_front_tiles: more tiles than held")
+        self.head += n
+        self.len -= n * K.TILE
 
     def append(self, pq: torch.Tensor, rvq: Optional[torch.Tensor], sidx: Optional[torch.Tensor],
                sval: Optional[torch.Tensor], pq_cb: Optional[torch.Tensor] = None,
@@ -150,24 +170,97 @@ class TiledCodes:
             flat = lambda t: None if t is None else t.reshape(H * T, -1)
             sval = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval)).view(H, T, -1)
         need = self.len + T
-        if need > self.cap:
-            self._alloc(max(need, 2 * self.cap))
-        K.pack_codes(pq, self.t["pq"], self.len)
+        if self.head * K.TILE + need > self.cap:
+            if self._backing is None and self.head and 2 * K.round_up(need, K.TILE) <= self.cap:
+                self._move_live(self.t, self.t)  # the live tiles move to the front
+                self.head = 0
+            else:
+                self._alloc(max(need, 2 * self.cap))
+        t_base = self.head * K.TILE + self.len
+        K.pack_codes(pq, self.t["pq"], t_base)
         if self.fmt.rvq_subspaces:
-            K.pack_codes(rvq, self.t["rvq"], self.len)
+            K.pack_codes(rvq, self.t["rvq"], t_base)
         if self.fmt.sparse_k:
-            self.t["sparse_idx"][:, self.len:need] = sidx
-            self.t["sparse_val"][:, self.len:need] = sval
+            self.t["sparse_idx"][:, t_base:t_base + T] = sidx
+            self.t["sparse_val"][:, t_base:t_base + T] = sval
         self.len = need
 
     def codes(self, tile_skip: int = 0) -> Dict[str, Optional[torch.Tensor]]:
-        """Per-array views starting at tile ``tile_skip`` (head stride unchanged)."""
+        """Per-array views starting at live tile ``tile_skip`` (head stride unchanged)."""
         f = self.fmt
-        o = tile_skip * K.TILE
+        o = (self.head + tile_skip) * K.TILE
         out = {"pq": self.t["pq"][:, o * f.pq_subspaces:]}
         out["rvq"] = self.t["rvq"][:, o * f.rvq_subspaces:] if f.rvq_subspaces else None
         out["sparse_idx"] = self.t["sparse_idx"][:, o:] if f.sparse_k else None
         out["sparse_val"] = self.t["sparse_val"][:, o:] if f.sparse_k else None
+        return out
+
+
+class _RingStore:
+    """Subspace-format codes in token-major device buffers with a live range
+    [head, head + n).  Appends write at the tail (when the tail reaches the
+    end the live range moves to the front, or the buffers double) and pops
+    advance the head, so an append or a migration to the cold tier costs its
+    own tokens, not the tier's length (the reference concatenates,
+    quantization.py:346-361)."""
+
+    FIELDS = ("pq_codes", "rvq_codes", "rvq_mask", "sparse_idx", "sparse_val")
+
+    def __init__(self, empty: CompressedTensorMLX):
+        self.heads = empty.num_heads
+        self.offsets = empty.rvq_offsets
+        self.buf = {f: getattr(empty, f) for f in self.FIELDS}
+        self.head = 0
+        self.n = 0
+
+    def _cap(self) -> int:
+        return int(self.buf["pq_codes"].shape[0])
+
+    def view(self, a: int = 0, b: Optional[int] = None) -> CompressedTensorMLX:
+        b = self.n if b is None else b
+        lo, hi = self.head + a, self.head + b
+        sl = {f: (None if t is None else t[lo:hi]) for f, t in self.buf.items()}
+        return CompressedTensorMLX(pq_codes=sl["pq_codes"], rvq_codes=sl["rvq_codes"], rvq_mask=sl["rvq_mask"],
+                                   rvq_offsets=self.offsets, num_heads=self.heads, sparse_idx=sl["sparse_idx"],
+                                   sparse_val=sl["sparse_val"])
+
+    def append(self, st: CompressedTensorMLX) -> None:
+        T = st.num_tokens
+        if T == 0:
+            return
+        need = self.n + T
+        if self.head + need > self._cap():
+            live = {f: (None if t is None else t[self.head:self.head + self.n]) for f, t in self.buf.items()}
+            if 2 * need <= self._cap():
+                for f, t in live.items():
+                    if t is not None:
+                        self.buf[f][:self.n] = t.clone()
+            else:
+                cap = max(need, 2 * self._cap(), 64)
+                for f, t in live.items():
+                    if t is not None:
+                        nb = torch.empty((cap, *t.shape[1:]), dtype=t.dtype, device=t.device)
+                        nb[:self.n] = t
+                        self.buf[f] = nb
+            self.head = 0
+        o = self.head + self.n
+        for f in self.FIELDS:
+            if self.buf[f] is not None:
+                self.buf[f][o:o + T] = getattr(st, f)
+        self.n = need
+
+    def pop_front(self, m: int) -> CompressedTensorMLX:
+        """Remove the m oldest tokens and return them (copies)."""
+        if m < 0 or m > self.n:
+            raise ValueError("pop_front: more tokens than held")
+        out = self.view(0, m)
+        out = CompressedTensorMLX(
+            pq_codes=out.pq_codes.clone(), rvq_codes=out.rvq_codes.clone(), rvq_mask=out.rvq_mask.clone(),
+            rvq_offsets=self.offsets, num_heads=self.heads,
+            sparse_idx=None if out.sparse_idx is None else out.sparse_idx.clone(),
+            sparse_val=None if out.sparse_val is None else out.sparse_val.clone())
+        self.head += m
+        self.n -= m
         return out
 
 
@@ -241,11 +334,19 @@ class RFSNv10KVCacheMLX:
         self.device = torch.device(device)
         self.H = config.kv_heads
         self.D = config.head_dim
+        # hot tier: [H, cap, D] buffers, live tokens [_hot_head, _hot_head + num_hot)
         self._hot_k = torch.zeros((self.H, 0, self.D), dtype=torch.float16, device=self.device)
         self._hot_v = torch.zeros_like(self._hot_k)
+        self._hot_head = 0
 
-        self.warm_keys = CompressedTensorMLX.empty(config, self.H, self.device)
-        self.warm_values = CompressedTensorMLX.empty(config, self.H, self.device)
+        # warm tier: the subspace format keeps its codes in rings (appends and
+        # migrations cost their own tokens); the reference format concatenates
+        if config.ext_format:
+            self._wk = _RingStore(CompressedTensorMLX.empty(config, self.H, self.device))
+            self._wv = _RingStore(CompressedTensorMLX.empty(config, self.H, self.device))
+        else:
+            self._wk = CompressedTensorMLX.empty(config, self.H, self.device)
+            self._wv = CompressedTensorMLX.empty(config, self.H, self.device)
         self._warm_tiled: Optional[Tuple[TiledCodes, TiledCodes]] = None
 
         self.cold_chunk_paths: List[Path] = []
@@ -293,11 +394,30 @@ class RFSNv10KVCacheMLX:
     @property
     def hot_keys(self) -> torch.Tensor:
         """[T_hot, H, D] view of the hot tier (oldest first)."""
-        return self._hot_k[:, : self.num_hot].permute(1, 0, 2)
+        h = self._hot_head
+        return self._hot_k[:, h:h + self.num_hot].permute(1, 0, 2)
 
     @property
     def hot_values(self) -> torch.Tensor:
-        return self._hot_v[:, : self.num_hot].permute(1, 0, 2)
+        h = self._hot_head
+        return self._hot_v[:, h:h + self.num_hot].permute(1, 0, 2)
+
+    @property
+    def warm_keys(self) -> CompressedTensorMLX:
+        """The warm tier's key codes (cache.py:45-46), oldest first."""
+        return self._wk.view() if isinstance(self._wk, _RingStore) else self._wk
+
+    @warm_keys.setter
+    def warm_keys(self, store: CompressedTensorMLX) -> None:
+        self._wk = store
+
+    @property
+    def warm_values(self) -> CompressedTensorMLX:
+        return self._wv.view() if isinstance(self._wv, _RingStore) else self._wv
+
+    @warm_values.setter
+    def warm_values(self, store: CompressedTensorMLX) -> None:
+        self._wv = store
 
     # ------------------------------------------------------------------ helpers
     @property
@@ -312,28 +432,37 @@ class RFSNv10KVCacheMLX:
         return self._kq.warm_format()
 
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Append [T, H, D] tokens to the hot tier."""
+        """Append [T, H, D] tokens to the hot tier.  The buffers hold up to
+        twice the hot capacity under the recency policy, so the live range
+        moves to the front only once per hot_capacity appended tokens."""
         T = int(k.shape[0])
         need = self.num_hot + T
-        if need > self._hot_k.shape[1]:
-            cap = max(need, min(self.hot_capacity, 2 * self._hot_k.shape[1]))
-            nk = torch.zeros((self.H, cap, self.D), dtype=torch.float16, device=self.device)
-            nv = torch.zeros_like(nk)
-            nk[:, : self.num_hot] = self._hot_k[:, : self.num_hot]
-            nv[:, : self.num_hot] = self._hot_v[:, : self.num_hot]
-            self._hot_k, self._hot_v = nk, nv
-        self._hot_k[:, self.num_hot:need] = k.permute(1, 0, 2).to(self.device, torch.float16)
-        self._hot_v[:, self.num_hot:need] = v.permute(1, 0, 2).to(self.device, torch.float16)
+        h = self._hot_head
+        cap = int(self._hot_k.shape[1])
+        if h + need > cap:
+            target = 2 * self.hot_capacity if self._recency else self.hot_capacity
+            if need <= cap and 2 * need <= cap:
+                self._hot_k[:, :self.num_hot] = self._hot_k[:, h:h + self.num_hot].clone()
+                self._hot_v[:, :self.num_hot] = self._hot_v[:, h:h + self.num_hot].clone()
+            else:
+                cap = max(need, min(max(target, need), max(2 * cap, 32)))
+                nk = torch.zeros((self.H, cap, self.D), dtype=torch.float16, device=self.device)
+                nv = torch.zeros_like(nk)
+                nk[:, : self.num_hot] = self._hot_k[:, h:h + self.num_hot]
+                nv[:, : self.num_hot] = self._hot_v[:, h:h + self.num_hot]
+                self._hot_k, self._hot_v = nk, nv
+            self._hot_head = h = 0
+        self._hot_k[:, h + self.num_hot:h + need] = k.permute(1, 0, 2).to(self.device, torch.float16)
+        self._hot_v[:, h + self.num_hot:h + need] = v.permute(1, 0, 2).to(self.device, torch.float16)
         self.num_hot = need
 
     def _hot_pop_oldest(self, n: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Remove and return the n oldest hot tokens as [n, H, D]."""
-        k = self._hot_k[:, :n].permute(1, 0, 2).clone()
-        v = self._hot_v[:, :n].permute(1, 0, 2).clone()
-        rest = self.num_hot - n
-        self._hot_k[:, :rest] = self._hot_k[:, n:self.num_hot].clone()
-        self._hot_v[:, :rest] = self._hot_v[:, n:self.num_hot].clone()
-        self.num_hot = rest
+        h = self._hot_head
+        k = self._hot_k[:, h:h + n].permute(1, 0, 2).clone()
+        v = self._hot_v[:, h:h + n].permute(1, 0, 2).clone()
+        self._hot_head += n
+        self.num_hot -= n
         return k, v
 
     def _warm_tiled_append(self, ck: CompressedTensorMLX, cv: CompressedTensorMLX) -> None:
@@ -384,14 +513,22 @@ class RFSNv10KVCacheMLX:
 
     append = update
 
+    HOT_BLOCK = 32  # hot tokens are demoted in multiples of one tile
+
     def _update_recency(self, keys, values, disk_dir) -> None:
-        """Hot keeps the newest ``hot_capacity`` tokens; demoted tokens go to
-        warm; warm overflow moves the oldest warm tokens to cold."""
+        """Hot keeps the newest tokens, at most ``hot_capacity``; when an
+        append overflows it, the oldest hot tokens are demoted to warm in
+        multiples of HOT_BLOCK (a block of new tokens is demoted as it is).
+        When warm overflows, its oldest tokens move to cold up to the next
+        cold chunk boundary, so migrations move whole chunks.  A bulk fill of
+        T >= hot_capacity tokens leaves exactly hot_capacity hot."""
         T = int(keys.shape[0])
         # tokens that never stay hot go straight to warm/cold, in order
         keep_new = min(T, self.hot_capacity)
         direct = T - keep_new
         overflow_hot = max(self.num_hot + keep_new - self.hot_capacity, 0)
+        if overflow_hot and self.hot_capacity >= self.HOT_BLOCK:
+            overflow_hot = -(-overflow_hot // self.HOT_BLOCK) * self.HOT_BLOCK
         demoted_k, demoted_v = [], []
         if overflow_hot:
             k_old, v_old = self._hot_pop_oldest(min(overflow_hot, self.num_hot))
@@ -401,18 +538,20 @@ class RFSNv10KVCacheMLX:
             demoted_k.append(keys[:direct])
             demoted_v.append(values[:direct])
         if demoted_k:
-            dk = torch.cat(demoted_k, 0)
-            dv = torch.cat(demoted_v, 0)
+            dk = demoted_k[0] if len(demoted_k) == 1 else torch.cat(demoted_k, 0)
+            dv = demoted_v[0] if len(demoted_v) == 1 else torch.cat(demoted_v, 0)
             n = int(dk.shape[0])
-            # oldest demoted tokens beyond the warm capacity go to cold first
-            warm_room = self.warm_capacity - self.num_warm
-            if n > warm_room:
-                # move old warm tokens out to make room, then cold-store what still does not fit
-                spill_warm = min(self.num_warm, n - warm_room)
+            excess = self.num_warm + n - self.warm_capacity
+            if excess > 0:
+                # the oldest tokens (warm first, then demoted) move to cold up
+                # to the next chunk boundary of their absolute positions
+                chunk = self.config.chunk_tokens
+                cut = -(-(self.num_cold + excess) // chunk) * chunk - self.num_cold
+                cut = min(cut, self.num_warm + n)
+                spill_warm = min(self.num_warm, cut)
                 if spill_warm:
                     self._warm_to_cold(spill_warm, disk_dir)
-                warm_room = self.warm_capacity - self.num_warm
-                to_cold = max(n - warm_room, 0)
+                to_cold = cut - spill_warm
                 if to_cold:
                     self._add_to_cold(dk[:to_cold], dv[:to_cold], disk_dir)
                     dk, dv = dk[to_cold:], dv[to_cold:]
@@ -424,25 +563,37 @@ class RFSNv10KVCacheMLX:
         """cache.py:122-132."""
         ck = _compress_tensor_sequence(keys, self._kq)
         cv = _compress_tensor_sequence(values, self._vq)
-        self.warm_keys = _append_compressed_tensor(self.warm_keys, ck)
-        self.warm_values = _append_compressed_tensor(self.warm_values, cv)
+        if isinstance(self._wk, _RingStore):
+            self._wk.append(ck)
+            self._wv.append(cv)
+        else:
+            self.warm_keys = _append_compressed_tensor(self.warm_keys, ck)
+            self.warm_values = _append_compressed_tensor(self.warm_values, cv)
         self._warm_tiled_append(ck, cv)
         self.num_warm += int(keys.shape[0])
 
     def _warm_to_cold(self, n: int, disk_dir) -> None:
-        """Move the n oldest warm tokens (already encoded) to the cold tier."""
-        ck = _slice_compressed_tensor(self.warm_keys, 0, n)
-        cv = _slice_compressed_tensor(self.warm_values, 0, n)
-        rest_k = _slice_compressed_tensor(self.warm_keys, n, self.num_warm)
-        rest_v = _slice_compressed_tensor(self.warm_values, n, self.num_warm)
+        """Move the n oldest warm tokens (already encoded) to the cold tier.
+        Whole tiles leave the tiled store by moving its head; otherwise the
+        tiled store is rebuilt from the remaining codes."""
+        if isinstance(self._wk, _RingStore):
+            ck, cv = self._wk.pop_front(n), self._wv.pop_front(n)
+        else:
+            ck = _slice_compressed_tensor(self.warm_keys, 0, n)
+            cv = _slice_compressed_tensor(self.warm_values, 0, n)
+            self.warm_keys = _slice_compressed_tensor(self.warm_keys, n, self.num_warm)
+            self.warm_values = _slice_compressed_tensor(self.warm_values, n, self.num_warm)
         self._store_cold(ck, cv, disk_dir)
-        self.warm_keys, self.warm_values = rest_k, rest_v
         self.num_warm -= n
         if self._warm_tiled is not None:
-            fmt = self._fmt()
-            self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
-            if self.num_warm:
-                self._warm_tiled_append(rest_k, rest_v)
+            if n % K.TILE == 0:
+                for t in self._warm_tiled:
+                    t.pop_front_tiles(n // K.TILE)
+            else:
+                fmt = self._fmt()
+                self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
+                if self.num_warm:
+                    self._warm_tiled_append(self.warm_keys, self.warm_values)
 
     # ------------------------------------------------------------------ cold tier
     def _cold_start_token(self) -> int:
@@ -787,8 +938,9 @@ class RFSNv10KVCacheMLX:
         for kind, x in plan:
             if kind == "hot":
                 a, b = x[0] - spans["hot"][0], x[1] - spans["hot"][0]
-                ks.append(self._hot_k[:, a:b].permute(1, 0, 2))
-                vs.append(self._hot_v[:, a:b].permute(1, 0, 2))
+                h = self._hot_head
+                ks.append(self._hot_k[:, h + a:h + b].permute(1, 0, 2))
+                vs.append(self._hot_v[:, h + a:h + b].permute(1, 0, 2))
             elif kind == "warm":
                 a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
                 ks.append(_decode_compressed_tensor(_slice_compressed_tensor(self.warm_keys, a, b), self._kq))
@@ -892,7 +1044,7 @@ class RFSNv10KVCacheMLX:
         fetched = set(fetched)
         for kind, x in plan:
             if kind == "hot":
-                hot_off = x[0] - spans["hot"][0]
+                hot_off = self._hot_head + x[0] - spans["hot"][0]
                 hot_len = x[1] - x[0]
                 hot_pos0 = x[0] - start
                 res_tokens += hot_len

@@ -273,6 +273,19 @@ class SegmentTable:
     def add(self, b: int, k: Dict[str, Optional[torch.Tensor]], v: Dict[str, Optional[torch.Tensor]],
             head_stride: int, length: int, pos0: int) -> None:
         def codes(c):
+            # the kernel reads whole 32-token tiles of the tiled code rows: the
+            # segment must fit the views it is given
+            tiles = (length + 31) // 32
+            for key in ("pq", "rvq"):
+                t = c.get(key)
+                if t is not None and length > 0:
+                    m = t.stride(0) // head_stride if head_stride > 0 else 0
+                    if m <= 0 or tiles * 32 * m > t.shape[1]:
+                        raise ValueError(f"segment of {length} tokens exceeds its {key} code rows")
+            for key in ("sparse_idx", "sparse_val"):
+                t = c.get(key)
+                if t is not None and length > t.shape[1]:
+                    raise ValueError(f"segment of {length} tokens exceeds its {key} rows")
             for t in c.values():
                 if t is not None:
                     self.keep.append(t)

@@ -40,6 +40,8 @@ def parse_args(argv=None):
     ap.add_argument("--splits", type=int, default=0, help="token splits per (sequence, KV head); 0 = auto")
     ap.add_argument("--cpu-sample", type=int, default=4, help="sequences timed on the CPU baseline")
     ap.add_argument("--cpu-repeats", type=int, default=32)
+    ap.add_argument("--stream-steps", type=int, default=600,
+                    help="long-context workload: streaming appends timed after the decode line (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (the known-size kernel that scales "
@@ -381,7 +383,47 @@ def bench_longctx(w, args, dev) -> dict:
         log("CPU baseline")
         result["cpu_baseline"], result["check_max_abs_vs_cpu"] = cpu_baseline_longctx(
             w, cache, ids, qd, out, args.cpu_repeats)
+    if args.stream_steps:
+        result["stream"] = bench_stream(w, cache, router, (kq, vq), qd, args.stream_steps, dev)
     return result
+
+
+def bench_stream(w, cache, router, quantizers, q, steps, dev) -> dict:
+    """The decode loop's streaming path on the filled cache: each step appends
+    one new token (hot ring; every 32 tokens a block is encoded into warm;
+    whole chunks move from warm to pinned cold as warm fills), then attends
+    hot + warm + the router's nearest cold chunks.  Wall-clock per step with
+    the GPU synchronized at the end (the host issues everything)."""
+    import torch
+    from apple_amd.workloads import make_sequence
+
+    kn, vn, _, _ = make_sequence(w, 1, tokens=2 * steps)
+    kn, vn = kn.to(dev), vn.to(dev)
+    chunks0, tok0 = len(cache.cold_chunk_metadata), cache.total_tokens
+    log(f"streaming {steps} appends")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        cache.update(kn[i:i + 1], vn[i:i + 1], quantizers)
+    torch.cuda.synchronize()
+    append_ms = (time.perf_counter() - t0) * 1e3 / steps
+    chunks1 = len(cache.cold_chunk_metadata)
+    log(f"streaming {steps} decode steps (append + attention)")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps, 2 * steps):
+        cache.update(kn[i:i + 1], vn[i:i + 1], quantizers)
+        pos = cache.total_tokens - 1
+        ids = router.rank(pos, cache.total_tokens)[:w.cold_attended]
+        cache.attention_forward(q, causal=True, cold_chunks=ids)
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"append_ms_per_token": round(append_ms, 4), "decode_step_ms": round(step_ms, 4),
+            "decode_tokens_per_s": round(1e3 / step_ms, 1), "steps": steps,
+            "tokens_appended": cache.total_tokens - tok0,
+            "chunks_moved_to_cold": len(cache.cold_chunk_metadata) - chunks0,
+            "chunks_moved_during_appends": chunks1 - chunks0,
+            "tiers_after": {"hot": cache.num_hot, "warm": cache.num_warm, "cold": cache.num_cold}}
 
 
 def cpu_baseline_longctx(w, cache, ids, q, gpu_out, repeats, budget_s=20.0):
@@ -402,7 +444,7 @@ def cpu_baseline_longctx(w, cache, ids, q, gpu_out, repeats, budget_s=20.0):
                      for i, name in enumerate(("pq", "rvq", "sparse_idx", "sparse_val"))}
     cbs = {"k_pq": cache._kq.pq.codebooks.cpu(), "v_pq": cache._vq.pq.codebooks.cpu(),
            "k_rvq": cache._kq.rvq.codebooks.cpu(), "v_rvq": cache._vq.rvq.codebooks.cpu()}
-    hk, hv = cache._hot_k.cpu(), cache._hot_v.cpu()
+    hk, hv = cache.hot_keys.permute(1, 0, 2).cpu(), cache.hot_values.permute(1, 0, 2).cpu()
     qc = q.cpu()
     out = cb.decode_step(qc, hk, hv, codes["k"], codes["v"], cbs, w.head_dim ** -0.5, w.block)  # warm-up
     n, t0 = 0, time.perf_counter()

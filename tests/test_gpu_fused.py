@@ -148,9 +148,8 @@ def test_batched_matches_per_sequence(device):
 
 def _cold_cache(device, seed, total, nh, nw, chunk, Hq=32, Hkv=4, cold_slots=32):
     """A recency cache (PQ M16 + RVQ M16 + top-4) whose oldest tokens sit in
-    pinned cold chunks of ``chunk`` tokens, filled by two appends (the second
-    spills warm tokens into a partly filled chunk), with the oracle's decode
-    of every token."""
+    pinned cold chunks of ``chunk`` tokens, filled by two appends, with the
+    oracle's decode of every token."""
     from apple_amd.cache import RFSNv10KVCacheMLX
     from apple_amd.quantization import HybridQuantizerMLX
     from apple_amd.storage import RFSNConfig
@@ -257,6 +256,10 @@ def test_fused_cold_slot_limit_and_partial_contract(device):
     assert out.shape == (1, 8, 64)
     fmt = cache._fmt()
     kt, vt = cache._warm_tiled
+    nw = cache.num_warm  # whole-chunk migrations leave fewer than the capacity
+    assert nw > 64
+    with pytest.raises(ValueError):  # a segment longer than its code rows is refused on the host
+        K.SegmentTable(1).add(0, kt.codes(0), vt.codes(0), kt.cap, kt.cap + 1, 0)
     table = K.SegmentTable(1)
     table.add(0, kt.codes(0), vt.codes(0), kt.cap, nw, 0)
     ws = torch.empty(1 << 16, dtype=torch.uint8, device=device)
@@ -279,3 +282,79 @@ def test_fused_cold_slot_limit_and_partial_contract(device):
     K.fused_attention(q, fmt, splits=2, part=(3, 5, True), out=out,
                       **{**common, "segments": t2, "max_tokens": nw - half})
     assert float((out.float() - whole.float()).abs().max()) <= 1e-3
+
+
+def _policy_counts(appends, hc, wc, chunk, block=32):
+    """Tier sizes under the recency policy, restated in plain arithmetic:
+    hot overflow demoted in multiples of ``block``, warm overflow moved to
+    cold up to the next chunk boundary."""
+    hot = warm = cold = 0
+    for T in appends:
+        keep = min(T, hc)
+        direct = T - keep
+        ov = max(hot + keep - hc, 0)
+        if ov and hc >= block:
+            ov = -(-ov // block) * block
+        pop = min(ov, hot)
+        hot -= pop
+        n = pop + direct
+        if n:
+            excess = warm + n - wc
+            if excess > 0:
+                cut = min(-(-(cold + excess) // chunk) * chunk - cold, warm + n)
+                moved = min(warm, cut)
+                warm, cold = warm - moved, cold + moved
+                cold += cut - moved
+                n -= cut - moved
+            warm += n
+        hot += keep
+    return hot, warm, cold
+
+
+@pytest.mark.parametrize("chunk,wc", [(64, 256), (100, 256), (64, 40)])
+def test_streaming_appends(device, chunk, wc):
+    """Token-by-token and ragged appends into a recency cache with a pinned
+    cold tier: tier sizes follow the policy, every cold chunk but the last is
+    whole, the materialized window is bit-exact against the oracle's decode
+    of every token (exact where hot), and the fused attention over the whole
+    context (every cold chunk) is within 2e-3.  With 64-token chunks the
+    tiled warm store migrates by moving its head (no rebuild); with 100 it
+    takes the rebuild path whenever a move is not whole tiles; a warm tier
+    smaller than a chunk leaves partial chunks that later moves complete
+    (merge-on-append into pinned chunks)."""
+    total, hc = 1500, 64
+    g, cfg, bulk, keys, values, dec = _cold_cache(device, 92 + chunk, total, hc, wc, chunk, Hq=8, Hkv=4)
+    # _cold_cache filled ``bulk`` with two appends; start again from empty with ragged ones
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    cache = RFSNv10KVCacheMLX(cfg, device=device, cold_slots=32)
+    kq, vq = bulk._kq, bulk._vq
+    sizes, done = [], 0
+    pick = [1, 1, 1, 3, 17, 64, 100, 1, 5]
+    while done < total:
+        s = min(pick[len(sizes) % len(pick)], total - done)
+        sizes.append(s)
+        done += s
+    o = 0
+    heads_moved = False
+    for s in sizes:
+        cache.update(T(keys[o:o + s], device), T(values[o:o + s], device), (kq, vq))
+        o += s
+        heads_moved |= cache._warm_tiled is not None and cache._warm_tiled[0].head > 0
+    assert (cache.num_hot, cache.num_warm, cache.num_cold) == _policy_counts(sizes, hc, wc, chunk)
+    if chunk % 32 == 0 and wc >= chunk:
+        assert heads_moved
+    lens = [m["num_tokens"] for m in cache.cold_chunk_metadata]
+    assert all(n == chunk for n in lens[:-1]) and sum(lens) == cache.num_cold
+    ids = [m["chunk_id"] for m in cache.cold_chunk_metadata]
+    enc = cache.num_cold + cache.num_warm
+    wk = np.concatenate([dec[0][:enc], keys[enc:]], 0)
+    wv = np.concatenate([dec[1][:enc], values[enc:]], 0)
+    mk, mv, _ = cache.materialize_window(cold_chunks=ids)
+    assert np.array_equal(H(mk).view(np.uint16), wk.view(np.uint16))
+    assert np.array_equal(H(mv).view(np.uint16), wv.view(np.uint16))
+    q = randn16(g, 2, 8, 64)
+    for causal in (False, True):
+        out = cache.attention_forward(T(q, device), causal=causal, cold_chunks=ids)
+        ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, causal, None)
+        assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
