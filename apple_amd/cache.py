@@ -9,11 +9,13 @@ materialization order and access counters (cache.py:250-393),
 (cache.py:430-440).  ``append`` is an alias of ``update``.
 
 MI355X design:
-* the hot tier is a head-major device buffer ``[Hkv, cap, D]`` fp16;
-* warm codes stay in the reference layout (``CompressedTensorMLX``) and, for
-  the subspace format, are also packed into the tiled layout streamed by the
-  fused dequant-attention kernel (one pass over hot + warm + attended cold
-  chunks, no window written to HBM);
+* the hot tier is a head-major device buffer ``[Hkv, cap, D]`` fp16 whose
+  live range moves: appends write at the tail, demotions advance the head;
+* warm codes are kept in the reference layout (``CompressedTensorMLX``; for
+  the subspace format in token rings) and, for the subspace format, also in
+  the tiled layout streamed by the fused dequant-attention kernel (one pass
+  over hot + warm + attended cold chunks, no window written to HBM); under
+  the recency policy whole cold chunks leave warm by moving ring heads;
 * cold chunks go either to NPZ files (reference schema, storage.py:113-151)
   or to pinned host memory; attended pinned chunks are copied into device
   slots with hipMemcpyAsync on a side stream, ordered by events.
@@ -34,6 +36,7 @@ from typing import Any, Dict, List, Optional, Sequence, Tuple, Union
 import numpy as np
 import torch
 
+from . import _lib as L
 from . import kernels as K
 from .attention import _blockwise_exact_attention, _normalize_query_positions
 from .quantization import (
@@ -184,6 +187,18 @@ class TiledCodes:
             self.t["sparse_idx"][:, t_base:t_base + T] = sidx
             self.t["sparse_val"][:, t_base:t_base + T] = sval
         self.len = need
+
+    def seg(self, tile_skip: int = 0):
+        """(rfsn_codes addresses from live tile ``tile_skip``, the arrays to
+        keep alive, tokens available from there): a segment without building
+        tensor views."""
+        f = self.fmt
+        o = (self.head + tile_skip) * K.TILE
+        t = self.t
+        ptr = lambda key, scale: None if t[key] is None else t[key].data_ptr() + o * scale
+        codes = L.Codes(ptr("pq", f.pq_subspaces), ptr("rvq", f.rvq_subspaces),
+                          ptr("sparse_idx", f.sparse_k), ptr("sparse_val", 2 * f.sparse_k))
+        return codes, [x for x in t.values() if x is not None], self.cap - o
 
     def codes(self, tile_skip: int = 0) -> Dict[str, Optional[torch.Tensor]]:
         """Per-array views starting at live tile ``tile_skip`` (head stride unchanged)."""
@@ -1052,9 +1067,10 @@ class RFSNv10KVCacheMLX:
                 a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
                 skip = a // K.TILE
                 kt, vt = self._warm_tiled
+                (kc, kk, avail), (vc, vk, _) = kt.seg(skip), vt.seg(skip)
                 for bi in range(B):
-                    resident.add(bi, kt.codes(skip), vt.codes(skip), kt.cap, b - skip * K.TILE,
-                                 spans["warm"][0] + skip * K.TILE - start)
+                    resident.add_codes(bi, kc, vc, kk + vk, kt.cap, b - skip * K.TILE,
+                                       spans["warm"][0] + skip * K.TILE - start, avail)
                 res_tokens += b - skip * K.TILE
             else:
                 meta, ov, _ = x
@@ -1062,9 +1078,10 @@ class RFSNv10KVCacheMLX:
                 a, b = ov[0] - meta["start_token"], ov[1] - meta["start_token"]
                 skip = a // K.TILE
                 table = incoming if meta["chunk_id"] in fetched else resident
+                (kc, kk, avail), (vc, vk, _) = dev["key"].seg(skip), dev["value"].seg(skip)
                 for bi in range(B):
-                    table.add(bi, dev["key"].codes(skip), dev["value"].codes(skip), dev["key"].cap,
-                              b - skip * K.TILE, meta["start_token"] + skip * K.TILE - start)
+                    table.add_codes(bi, kc, vc, kk + vk, dev["key"].cap, b - skip * K.TILE,
+                                    meta["start_token"] + skip * K.TILE - start, avail)
                 if meta["chunk_id"] in fetched:
                     in_tokens += b - skip * K.TILE
                 else:

@@ -293,6 +293,15 @@ class SegmentTable:
                            L.ptr(c.get("sparse_val")))
         self.rows[b].append(L.Segment(codes(k), codes(v), head_stride, length, pos0))
 
+    def add_codes(self, b: int, k: "L.Codes", v: "L.Codes", keep: Sequence[torch.Tensor], head_stride: int,
+                  length: int, pos0: int, available: int) -> None:
+        """Like ``add`` from precomputed addresses (``TiledCodes.seg``);
+        ``available`` = tokens of the code rows from the segment's start."""
+        if length > 0 and (length + 31) // 32 * 32 > available:
+            raise ValueError(f"segment of {length} tokens exceeds its {available} available code rows")
+        self.keep.extend(keep)
+        self.rows[b].append(L.Segment(k, v, head_stride, length, pos0))
+
     @property
     def max_rows(self) -> int:
         """Segments of the longest row (the table's max_segments, at least 1)."""
@@ -303,17 +312,22 @@ class SegmentTable:
         return all(not r for r in self.rows)
 
     def to_device(self, device) -> Tuple[torch.Tensor, torch.Tensor, int]:
+        """(segment table, segment counts, max_segments) in device memory.
+        Table and counts travel in one asynchronous copy from pinned memory,
+        so building a launch never waits for the work already queued."""
         maxs = max(1, max(len(r) for r in self.rows))
         size = C.sizeof(L.Segment)
+        nb = size * len(self.rows) * maxs
         host = (L.Segment * (len(self.rows) * maxs))()
         for b, r in enumerate(self.rows):
             for s, seg in enumerate(r):
                 host[b * maxs + s] = seg
-        raw = torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8).clone()
-        table = raw.to(device, non_blocking=False)
-        nseg = torch.tensor([len(r) for r in self.rows], dtype=torch.int32).to(device)
-        assert table.numel() == size * len(self.rows) * maxs
-        return table, nseg, maxs
+        counts = (C.c_int32 * len(self.rows))(*[len(r) for r in self.rows])
+        staged = torch.empty(nb + C.sizeof(counts), dtype=torch.uint8, pin_memory=True)
+        C.memmove(staged.data_ptr(), host, nb)
+        C.memmove(staged.data_ptr() + nb, counts, C.sizeof(counts))
+        dev = staged.to(device, non_blocking=True)
+        return dev[:nb], dev[nb:].view(torch.int32), maxs
 
 
 def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: float, causal: bool,
