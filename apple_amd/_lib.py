@@ -92,6 +92,8 @@ SIGNATURES = {
     "rfsn_event_record": (i32, [vp, vp]),
     "rfsn_stream_wait_event": (i32, [vp, vp]),
     "rfsn_event_synchronize": (i32, [vp]),
+    "rfsn_event_query": (i32, [vp]),
+    "rfsn_stream_query": (i32, [vp]),
 }
 
 _lib: Optional[C.CDLL] = None

@@ -28,6 +28,7 @@ explicit cold chunk sets (``attention_forward(..., cold_chunks=[...])``).
 
 from __future__ import annotations
 
+import ctypes as C
 import logging
 from collections import OrderedDict
 from pathlib import Path
@@ -280,23 +281,27 @@ class _RingStore:
 
 
 def plan_slot_windows(slot_cid: Sequence[int], lru: Sequence[int], wanted: set, missing: Sequence[int],
-                      arena: int) -> List[Tuple[int, List[int]]]:
+                      arena: int, busy: frozenset = frozenset()) -> List[Tuple[int, List[int]]]:
     """Where missing cold chunks go in a pool of ``len(slot_cid)`` device slots.
 
     slot_cid[j]: the chunk in slot j (-1 free); lru: occupied slots, least
     recently used first; wanted: every chunk of the window (their slots are
-    never taken); missing: the chunks to copy in.  Missing ids form runs of
-    consecutive ids inside one pinned arena of ``arena`` ids; each run takes
-    the longest window of consecutive usable slots (free, or holding no
-    wanted chunk), preferring fewer occupied slots, then older occupants, and
-    is split only when no window is long enough.  Returns (first slot, chunk
-    ids) per window, one copy each."""
+    never taken); missing: the chunks to copy in; busy: slots that queued
+    launches may still read (a copy into one first waits for them).  Usable
+    slots rank free and idle, free and busy, holding an unwanted chunk and
+    idle, holding one and busy.  Missing ids form runs of consecutive ids
+    inside one pinned arena of ``arena`` ids; each run takes the longest
+    window of consecutive slots of the best rank that has any (older
+    occupants first among equals), and the rest of the run continues the
+    same way.  Returns (first slot, chunk ids) per window, one copy each."""
     S = len(slot_cid)
     rank = {s: r for r, s in enumerate(lru)}
     taken = set()
 
-    def usable(j: int) -> bool:
-        return j not in taken and (slot_cid[j] < 0 or slot_cid[j] not in wanted)
+    def klass(j: int) -> int:
+        if j in taken or (slot_cid[j] >= 0 and slot_cid[j] in wanted):
+            return 4  # unusable
+        return (0 if slot_cid[j] < 0 else 2) + (1 if j in busy else 0)
 
     runs: List[List[int]] = []
     for cid in sorted(missing):
@@ -307,18 +312,27 @@ def plan_slot_windows(slot_cid: Sequence[int], lru: Sequence[int], wanted: set, 
     out = []
     for run in runs:
         while run:
+            cls = [klass(j) for j in range(S)]
             best = None
-            for j in range(S):
-                n = 0
-                while n < len(run) and j + n < S and usable(j + n):
-                    n += 1
-                if n == 0:
-                    continue
-                occupied = sum(1 for x in range(j, j + n) if slot_cid[x] >= 0)
-                newest = max((rank.get(x, -1) for x in range(j, j + n)), default=-1)
-                cost = (-n, occupied, newest)
-                if best is None or cost < best[0]:
-                    best = (cost, j, n)
+            for limit in range(4):
+                j = 0
+                while j < S:  # each maximal stretch of slots of rank <= limit
+                    if cls[j] > limit:
+                        j += 1
+                        continue
+                    a = j
+                    while j < S and cls[j] <= limit:
+                        j += 1
+                    n = min(len(run), j - a)
+                    for off in range(a, j - n + 1):
+                        newest = max((rank.get(x, -1) for x in range(off, off + n)), default=-1)
+                        cost = (-n, newest)
+                        if best is None or cost < best[0]:
+                            best = (cost, off, n)
+                        if newest < 0:
+                            break  # free slots: the first window of the stretch is as good as any
+                if best is not None:
+                    break
             if best is None:
                 raise ValueError("more wanted cold chunks than device slots")
             _, j, n = best
@@ -372,6 +386,13 @@ class RFSNv10KVCacheMLX:
         self._cold_arena: Dict[int, torch.Tensor] = {}
         self._slot_buf: Optional[torch.Tensor] = None
         self._slot_cid: List[int] = []
+        self._slot_views: Dict[int, Tuple[TiledCodes, TiledCodes]] = {}
+        # per slot: event recorded after the last launches that read it (None:
+        # no reader; PREPARED: read by prepared steps, whose calls are not tracked)
+        self._slot_reader: List[Any] = []
+        self._read_events: List[int] = []
+        self._read_next = 0
+        self._copies_pending = False  # copies queued without the launch stream waiting on them
         self._cold_slot_limit = cold_slots
         self._side: Optional[K.SideStream] = None
 
@@ -757,29 +778,95 @@ class RFSNv10KVCacheMLX:
             self._slot_buf = torch.empty(self._cold_slot_limit * self._chunk_bytes(), dtype=torch.uint8,
                                          device=self.device)
             self._slot_cid = [-1] * self._cold_slot_limit
+            self._slot_reader = [None] * self._cold_slot_limit
         return self._slot_buf
 
-    def _slot_entry(self, cid: int, slot: int) -> dict:
-        nb = self._chunk_bytes()
-        half = nb // 2
-        pool = self._slot_pool()
-        e = self._cold_pinned[cid]
-        dev = {"slot": slot}
-        for i, name in enumerate(("key", "value")):
-            host_t: TiledCodes = e[f"{name}_tiled"]
-            o = slot * nb + i * half
-            dt = TiledCodes(self._fmt(), self.H, self.device, cap=host_t.cap, backing=pool[o:o + half])
-            dt.len = host_t.len
-            dev[name] = dt
-        return dev
+    PREPARED = "prepared"
+    READ_EVENTS = 8
 
-    def _stage_cold(self, chunk_ids: Sequence[int]) -> Tuple[Dict[int, dict], List[int], list]:
+    def _reader_done(self, ev, cache: Dict[Any, bool]) -> bool:
+        if ev is None:
+            return True
+        if ev == self.PREPARED:
+            return False
+        if ev not in cache:
+            st = L.load().rfsn_event_query(ev)
+            if st < 0:
+                L.check(st, "rfsn_event_query")
+            cache[ev] = st == 1
+        return cache[ev]
+
+    def _busy_slots(self) -> set:
+        """Slots whose last readers may still be running.  Slots read by
+        prepared steps count as idle once the launch stream has drained
+        (queried, without waiting)."""
+        if self.PREPARED in self._slot_reader:
+            st = L.load().rfsn_stream_query(L.stream_handle(self.device))
+            if st < 0:
+                L.check(st, "rfsn_stream_query")
+            if st == 1:
+                self._slot_reader = [None if ev == self.PREPARED else ev for ev in self._slot_reader]
+        seen: Dict[Any, bool] = {}
+        return {j for j, ev in enumerate(self._slot_reader) if not self._reader_done(ev, seen)}
+
+    def _wait_readers(self, slots: Sequence[int], stream: Optional[int] = None) -> None:
+        """Block the host until the launches that read ``slots`` are done
+        (the copies that overwrite them are then queued with no device wait,
+        see ``SideStream.drain``)."""
+        seen: Dict[Any, bool] = {}
+        evs = {self._slot_reader[j] for j in slots}
+        if self.PREPARED in evs:
+            self._side_stream().drain(L.stream_handle(self.device) if stream is None else stream)
+            return
+        for ev in evs:
+            if not self._reader_done(ev, seen):
+                L.call("rfsn_event_synchronize", ev)
+
+    def _record_reads(self, slots: Sequence[int], prepared: bool = False) -> None:
+        """Mark ``slots`` as read by the launches just queued on the current stream."""
+        if not slots:
+            return
+        if prepared:
+            for j in slots:
+                self._slot_reader[j] = self.PREPARED
+            return
+        if len(self._read_events) < self.READ_EVENTS:
+            e = C.c_void_p()
+            L.call("rfsn_event_create", C.byref(e))
+            self._read_events.append(e.value)
+            ev = e.value
+        else:
+            # re-recording an event only moves it later: its slots wait longer, never less
+            ev = self._read_events[self._read_next]
+            self._read_next = (self._read_next + 1) % self.READ_EVENTS
+        L.call("rfsn_event_record", ev, L.stream_handle(self.device))
+        for j in slots:
+            self._slot_reader[j] = ev
+
+    def _slot_entry(self, cid: int, slot: int) -> dict:
+        """The slot's K and V views (built once per slot) holding chunk ``cid``."""
+        if slot not in self._slot_views:
+            nb = self._chunk_bytes()
+            half = nb // 2
+            pool = self._slot_pool()
+            cap = K.round_up(self.config.chunk_tokens, K.TILE)
+            self._slot_views[slot] = tuple(
+                TiledCodes(self._fmt(), self.H, self.device, cap=cap, backing=pool[o:o + half])
+                for o in (slot * nb, slot * nb + half))
+        e = self._cold_pinned[cid]
+        kt, vt = self._slot_views[slot]
+        kt.len, vt.len = e["key_tiled"].len, e["value_tiled"].len
+        return {"slot": slot, "key": kt, "value": vt}
+
+    def _stage_cold(self, chunk_ids: Sequence[int]) -> Tuple[Dict[int, dict], List[int], list, List[int]]:
         """Device slots for ``chunk_ids``: (slots by id, ids still to copy,
-        their (dst, src, bytes) copies).  Resident chunks keep their slot and
-        become the most recently used.  The missing ones, in runs of
-        consecutive ids inside one pinned arena, take the longest windows of
-        consecutive slots that hold no chunk of ``chunk_ids`` (preferring free
-        slots, then the least recently used), so that each window is one copy."""
+        their (dst, src, bytes) copies, the slots those copies overwrite).
+        Resident chunks keep their slot and become the most recently used.
+        The missing ones, in runs of consecutive ids inside one pinned arena,
+        take the longest windows of consecutive slots that hold no chunk of
+        ``chunk_ids``, avoiding slots whose readers may still run, then
+        preferring free slots and the least recently used; each window is
+        one copy."""
         if self.config.cold_medium != "pinned":
             raise RuntimeError("cold-chunk prefetch needs cold_medium='pinned'")
         ids = list(dict.fromkeys(int(c) for c in chunk_ids))
@@ -794,12 +881,14 @@ class RFSNv10KVCacheMLX:
                 out[cid] = self._cold_slots[cid]
         missing = sorted(cid for cid in ids if cid not in out)
         if not missing:
-            return out, [], []
+            return out, [], [], []
         pool = self._slot_pool()
         nb = self._chunk_bytes()
         lru = [d["slot"] for d in self._cold_slots.values()]
-        fetched, copies = [], []
-        for j, part in plan_slot_windows(self._slot_cid, lru, set(ids), missing, self.ARENA_CHUNKS):
+        fetched, copies, targets = [], [], []
+        busy = self._busy_slots()
+        for j, part in plan_slot_windows(self._slot_cid, lru, set(ids), missing, self.ARENA_CHUNKS, busy):
+            targets.extend(range(j, j + len(part)))
             for t, cid in enumerate(part):
                 old = self._slot_cid[j + t]
                 if old >= 0:
@@ -811,30 +900,63 @@ class RFSNv10KVCacheMLX:
                 fetched.append(cid)
             src = self._cold_pinned[part[0]]["tiled_buf"]
             copies.append((pool.data_ptr() + j * nb, src.data_ptr(), len(part) * nb))
-        return out, fetched, copies
+        return out, fetched, copies, targets
 
     def _side_stream(self) -> K.SideStream:
         if self._side is None:
             self._side = K.SideStream()
         return self._side
 
-    def prefetch_cold_chunks(self, chunk_ids: Sequence[int]) -> Dict[int, dict]:
-        """Make pinned chunks resident in device slots; copies are issued with
-        hipMemcpyAsync on a side stream (after the work already queued on the
-        current stream, which may still read a reused slot) and the current
-        stream waits on its event."""
-        out, _, copies = self._stage_cold(chunk_ids)
+    def prefetch_cold_chunks(self, chunk_ids: Sequence[int], wait: bool = True) -> Dict[int, dict]:
+        """Make pinned chunks resident in device slots.  The copies are
+        issued with hipMemcpyAsync on a side stream once the launches that
+        last read the slots they overwrite are done (slots no queued launch
+        reads are preferred).  With ``wait`` the current stream waits on
+        them now; otherwise the next attention call does (a prefetch one
+        decode step ahead, overlapped with the current step)."""
+        out, _, copies, targets = self._stage_cold(chunk_ids)
         if copies:
             side = self._side_stream()
-            side.wait_for_current(self.device)
+            self._wait_readers(targets)
             side.prefetch(copies)
-            side.make_current_wait(self.device)
+            if wait:
+                side.make_current_wait(self.device)
+            else:
+                self._copies_pending = True
         return out
 
-    def evict_cold_slots(self) -> None:
-        """Drop every chunk from the device slots (the slot buffer is kept)."""
-        self._cold_slots.clear()
-        self._slot_cid = [-1] * len(self._slot_cid)
+    def _order_after_copies(self) -> None:
+        """The current stream waits for every copy queued so far (cheap)."""
+        if self._copies_pending:
+            self._side_stream().make_current_wait(self.device)
+            self._copies_pending = False
+
+    def resident_cold_chunk(self, chunk_id: int) -> Optional[dict]:
+        """The device slot holding a pinned chunk, or None."""
+        return self._cold_slots.get(int(chunk_id))
+
+    def evict_cold_slots(self, chunk_ids: Optional[Sequence[int]] = None) -> None:
+        """Drop chunks (every chunk by default) from the device slots; the
+        slot buffer is kept and its last readers are still tracked."""
+        if chunk_ids is None:
+            self._cold_slots.clear()
+            self._slot_cid = [-1] * len(self._slot_cid)
+            return
+        for cid in chunk_ids:
+            dev = self._cold_slots.pop(int(cid), None)
+            if dev is not None:
+                self._slot_cid[dev["slot"]] = -1
+
+    def note_reads(self, chunk_ids: Sequence[int]) -> None:
+        """Record that the launches just queued on the current stream (a
+        prepared step, which does not record it itself) read these chunks'
+        slots, so that later copies wait only for those launches."""
+        self._record_reads([self._cold_slots[int(c)]["slot"] for c in chunk_ids if int(c) in self._cold_slots])
+
+    def wait_for_prefetch(self) -> None:
+        """Order the current stream after the copies of ``prefetch_cold_chunks(wait=False)``
+        (attention calls do this themselves; prepared launches need it)."""
+        self._order_after_copies()
 
     # ------------------------------------------------------------------ windows
     def _max_query_position(self, query_positions, current_position) -> int:
@@ -1055,8 +1177,10 @@ class RFSNv10KVCacheMLX:
         hot_len, hot_pos0, hot_off = 0, 0, 0
         res_tokens, in_tokens = 0, 0
         cold_ids = [x[0]["chunk_id"] for kind, x in plan if kind == "cold"]
-        slots, fetched, copies = self._stage_cold(cold_ids) if cold_ids else ({}, [], [])
+        slots, fetched, copies, targets = self._stage_cold(cold_ids) if cold_ids else ({}, [], [], [])
         fetched = set(fetched)
+        read_slots = [slots[c]["slot"] for c in cold_ids]
+        self._order_after_copies()  # resident chunks may still be arriving from a prefetch
         for kind, x in plan:
             if kind == "hot":
                 hot_off = self._hot_head + x[0] - spans["hot"][0]
@@ -1122,11 +1246,20 @@ class RFSNv10KVCacheMLX:
         if not launch:
             if copies:
                 # the staged slots count as resident from now on: fill them
-                # before any other call reads them
-                step.issue_copies()
+                # before any other call reads them (a prepared step re-issues
+                # its copies after draining the launch stream)
+                self._wait_readers(targets)
+                step.issue_copies(drain=False)
                 self._side_stream().make_current_wait(self.device)
+            self._record_reads(read_slots, prepared=True)
             return step
-        return step().to(q.dtype)
+        if copies:
+            self._wait_readers(targets)
+            step(drain=False)
+        else:
+            step()
+        self._record_reads(read_slots)
+        return out.to(q.dtype)
 
     def memory_usage_bytes(self) -> Dict[str, int]:
         """cache.py:430-440.  Subspace format: warm_rvq_bytes counts the RVQ

@@ -101,3 +101,18 @@ extern "C" int rfsn_event_synchronize(void* e) {
   RFSN_REQUIRE(e != nullptr, "event_synchronize: null event");
   return hip_status(hipEventSynchronize((hipEvent_t)e), "hipEventSynchronize");
 }
+
+extern "C" int rfsn_stream_query(void* s) {
+  const hipError_t r = hipStreamQuery((hipStream_t)s);
+  if (r == hipSuccess) return 1;
+  if (r == hipErrorNotReady) return 0;
+  return hip_status(r, "hipStreamQuery");
+}
+
+extern "C" int rfsn_event_query(void* e) {
+  RFSN_REQUIRE(e != nullptr, "event_query: null event");
+  const hipError_t r = hipEventQuery((hipEvent_t)e);
+  if (r == hipSuccess) return 1;
+  if (r == hipErrorNotReady) return 0;
+  return hip_status(r, "hipEventQuery");
+}

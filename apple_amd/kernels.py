@@ -454,16 +454,19 @@ class PrefetchedStep:
         self.copy_bytes = sum(int(c[2]) for c in copies)
         self._keep = keep
 
-    def issue_copies(self) -> None:
-        """The copies alone, once the work already on the launch stream (which
-        may read the destination slots) is done; their event recorded."""
-        self.side.drain(self.stream)
+    def issue_copies(self, drain: bool = True) -> None:
+        """The copies alone and their event.  With ``drain`` the host first
+        waits for the work already on the launch stream, which may read the
+        destination slots (the previous call of this step does); a caller
+        that has ordered the copies otherwise passes False."""
+        if drain:
+            self.side.drain(self.stream)
         L.call("rfsn_prefetch_h2d", self._copies, self.ncopies, self.side.stream)
         L.call("rfsn_event_record", self.side.event, self.side.stream)
 
-    def __call__(self) -> torch.Tensor:
+    def __call__(self, drain: bool = True) -> torch.Tensor:
         if self.ncopies:
-            self.issue_copies()
+            self.issue_copies(drain)
         for i, fl in enumerate(self.launches):
             if i == self.wait_at and self.ncopies:
                 L.call("rfsn_stream_wait_event", self.stream, self.side.event)

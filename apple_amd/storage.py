@@ -287,6 +287,16 @@ class AsyncHierarchicalRouterMLX:
 
     async def predict_and_prefetch(self, current_position: int, context_window: int, top_k: int = 2) -> List[int]:
         candidates = self.rank(current_position, context_window)
+        if self._bound is not None:
+            # pinned medium: the chunks not yet held move in one batch of copies
+            ids = candidates[:top_k]
+            new = [cid for cid in ids if cid not in self._cache]
+            if new:
+                slots = self._bound.prefetch_cold_chunks(new)
+                for cid in new:
+                    self._cache[cid] = slots[cid]
+            self._trim()
+            return ids
         loaded: List[int] = []
         for chunk_id in candidates[:top_k]:
             if chunk_id in self._cache:
@@ -300,10 +310,28 @@ class AsyncHierarchicalRouterMLX:
             loaded.append(chunk_id)
             if self.throttle > 0:
                 await asyncio.sleep(self.throttle)
+        self._trim()
+        return loaded
+
+    def _trim(self) -> None:
+        """FIFO of at most 16 chunks (storage.py:197-199)."""
         while len(self._cache) > self._max_cache_size:
             oldest_key = next(iter(self._cache))
             del self._cache[oldest_key]
-        return loaded
+
+    def prefetch_ahead(self, current_position: int, context_window: int, top_k: int = 2) -> List[int]:
+        """For a router bound to a pinned-medium cache: rank the chunks for
+        ``current_position`` and start their copies on the side stream
+        without waiting, one decode step ahead; the next attention call
+        orders itself after them.  Returns the ranked chunk ids."""
+        if self._bound is None:
+            raise RuntimeError("prefetch_ahead needs a router bound to a pinned-medium cache (bind)")
+        ids = self.rank(current_position, context_window)[:top_k]
+        slots = self._bound.prefetch_cold_chunks(ids, wait=False)
+        for cid in ids:
+            self._cache[cid] = slots[cid]
+        self._trim()
+        return ids
 
     def prefetch_sync(self, current_position: int, context_window: int, top_k: int = 2) -> List[int]:
         try:
@@ -316,9 +344,6 @@ class AsyncHierarchicalRouterMLX:
                 loop.close()
 
     async def _load_chunk(self, chunk_id: int) -> None:
-        if self._bound is not None:
-            self._cache[chunk_id] = self._bound.prefetch_cold_chunks([chunk_id])[chunk_id]
-            return
         loop = asyncio.get_running_loop()
         loaded = await loop.run_in_executor(None, self._load_chunk_sync, chunk_id)
         self._cache[chunk_id] = loaded
@@ -330,4 +355,7 @@ class AsyncHierarchicalRouterMLX:
         return load_compressed_chunk(path)
 
     def get_chunk(self, chunk_id: int) -> Optional[Dict[str, torch.Tensor]]:
+        if self._bound is not None and chunk_id in self._cache:
+            # a chunk the router fetched counts while it is still in a device slot
+            return self._bound.resident_cold_chunk(chunk_id)
         return self._cache.get(chunk_id)

@@ -350,6 +350,41 @@ def bench_longctx(w, args, dev) -> dict:
     torch.cuda.synchronize()
     diff = float((out2.float() - out.float()).abs().max())
 
+    # prefetch one step ahead: steps alternate between the router's 16 nearest
+    # chunks and the next 16; while a step runs, the other set (dropped from
+    # its slots first, so that it really moves) is copied in without the
+    # launch stream waiting, and the next step orders itself after the copy
+    sets = [ids, router.rank(w.context - 1, w.context)[w.cold_attended:2 * w.cold_attended]]
+    cache.evict_cold_slots()
+    outs = [torch.empty_like(qd), torch.empty_like(qd)]
+    launches = []
+    for k in range(2):
+        cache.prefetch_cold_chunks(sets[k])
+        launches.append(cache.prepare(qd, causal=True, cold_chunks=sets[k], out=outs[k]))
+        cache.note_reads(sets[k])  # the loop records each call's reads, so copies wait only for those
+    slots_of = [sorted(cache.resident_cold_chunk(c)["slot"] for c in st) for st in sets]
+
+    def ahead(i):
+        cache.wait_for_prefetch()
+        launches[i % 2]()
+        cache.note_reads(sets[i % 2])
+        nxt = sets[(i + 1) % 2]
+        cache.evict_cold_slots(nxt)
+        cache.prefetch_cold_chunks(nxt, wait=False)
+
+    for i in range(args.warmup):
+        ahead(i)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps (next step's chunks prefetched during the step)")
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ahead(i)
+    cache.wait_for_prefetch()
+    torch.cuda.synchronize()
+    ahead_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    same_slots = slots_of == [sorted(cache.resident_cold_chunk(c)["slot"] for c in st) for st in sets]
+    ahead_diff = float((outs[0].float() - out.float()).abs().max())
+
     step_bytes = w.bytes_per_step()
     achieved = step_bytes / (kernel_ms * 1e-3) / 1e9
     result = {
@@ -378,6 +413,10 @@ def bench_longctx(w, args, dev) -> dict:
             "resident_part_ms": round(resident_ms, 5), "copied_part_ms": round(incoming_ms, 5),
             "tokens_per_s": round(w.batch / (refetch_ms * 1e-3), 1),
             "max_abs_vs_resident": diff},
+        "prefetch_ahead_step": {
+            "ms_per_step": round(ahead_ms, 5), "tokens_per_s": round(w.batch / (ahead_ms * 1e-3), 1),
+            "copy_bytes_per_step": step.copy_bytes, "sets_kept_their_slots": same_slots,
+            "max_abs_vs_resident": ahead_diff},
     }
     if not args.no_cpu:
         log("CPU baseline")

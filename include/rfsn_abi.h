@@ -258,6 +258,10 @@ int rfsn_event_destroy(void* event);
 int rfsn_event_record(void* event, void* stream);
 int rfsn_stream_wait_event(void* stream, void* event);
 int rfsn_event_synchronize(void* event);
+/* 1 when the work recorded before the event has finished, 0 when not yet, <0 on error. */
+int rfsn_event_query(void* event);
+/* 1 when every operation queued on the stream has finished, 0 when not yet, <0 on error. */
+int rfsn_stream_query(void* stream);
 
 #ifdef __cplusplus
 }

@@ -358,3 +358,42 @@ def test_streaming_appends(device, chunk, wc):
         out = cache.attention_forward(T(q, device), causal=causal, cold_chunks=ids)
         ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, causal, None)
         assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
+def test_prefetch_ahead_decode_loop(device):
+    """Decode steps whose cold chunk sets alternate, each set's copies
+    started one step ahead without the launch stream waiting
+    (``prefetch_cold_chunks(wait=False)``, then the router's
+    ``prefetch_ahead``): every step equals the oracle over its window, and
+    the copies land in the half of the slot pool the running step does not
+    read."""
+    from apple_amd.storage import AsyncHierarchicalRouterMLX
+
+    total, nh, nw, chunk = 2600, 64, 256, 64
+    g, cfg, cache, keys, values, dec = _cold_cache(device, 93, total, nh, nw, chunk, Hq=8, Hkv=4, cold_slots=16)
+    ncold, hot = cache.num_cold, cache.num_hot
+    ids_all = [m["chunk_id"] for m in cache.cold_chunk_metadata]
+    sets = [ids_all[-8:], ids_all[-16:-8]]
+    q = randn16(g, 1, 8, 64)
+    qd = T(q, device)
+    cache.prefetch_cold_chunks(sets[0])
+    for i in range(6):
+        cur, nxt = sets[i % 2], sets[(i + 1) % 2]
+        out = cache.attention_forward(qd, causal=False, cold_chunks=cur)
+        cur_slots = {cache.resident_cold_chunk(c)["slot"] for c in cur}
+        cache.prefetch_cold_chunks(nxt, wait=False)
+        assert not cur_slots & {cache.resident_cold_chunk(c)["slot"] for c in nxt}
+        assert all(cache.resident_cold_chunk(c) is not None for c in cur)  # the running set kept its slots
+        pos, wk, wv = _cold_window(cur, chunk, ncold, total, hot, keys, values, dec)
+        ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, False, None)
+        assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL, i
+    router = AsyncHierarchicalRouterMLX(cfg).bind(cache)
+    cache.evict_cold_slots()
+    for step in range(3):
+        p = total - 1 - 700 * step
+        ids = router.prefetch_ahead(p, total, top_k=8)
+        assert ids == router.rank(p, total)[:8] and all(router.get_chunk(c) is not None for c in ids)
+        out = cache.attention_forward(qd, causal=False, cold_chunks=ids)
+        pos, wk, wv = _cold_window(ids, chunk, ncold, total, hot, keys, values, dec)
+        ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, False, None)
+        assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL, step

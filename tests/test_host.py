@@ -208,3 +208,28 @@ def test_cold_slot_windows():
         lru = [s for s in g.permutation(S) if slot_cid[s] >= 0]
         arena = int(g.integers(1, 70))
         _check_windows(slot_cid, wanted, missing, arena, plan_slot_windows(slot_cid, lru, wanted, missing, arena))
+        busy = frozenset(int(s) for s in g.permutation(S)[:int(g.integers(0, S + 1))])
+        w = plan_slot_windows(slot_cid, lru, wanted, missing, arena, busy)
+        _check_windows(slot_cid, wanted, missing, arena, w)
+        used = [j for s0, part in w for j in range(s0, s0 + len(part))]
+        free_idle = [j for j in range(S) if j not in busy and slot_cid[j] < 0]
+        if len(free_idle) >= len(missing):  # enough free idle slots: no eviction, no wait
+            assert all(j not in busy and slot_cid[j] < 0 for j in used)
+
+
+def test_cold_slot_windows_avoid_busy_slots():
+    """A prefetch one step ahead: the slots the running step reads are busy,
+    so the next window's chunks go to the other half of the pool; free slots
+    come before evicting a resident chunk, even when they are still busy."""
+    from apple_amd.cache import plan_slot_windows
+
+    pool = list(range(100, 116)) + [-1] * 16       # slots 0-15 hold the current window
+    busy = frozenset(range(16))
+    nxt = list(range(200, 216))
+    assert plan_slot_windows(pool, list(range(16)), set(nxt), nxt, 64, busy) == [(16, nxt)]
+    # without the busy set the least recently used (free) slots are the same here
+    pool2 = list(range(100, 132))                  # full pool of stale chunks, 0-15 busy
+    w = plan_slot_windows(pool2, list(range(32)), set(nxt), nxt, 64, busy)
+    assert w == [(16, nxt)]
+    pool3 = list(range(100, 116)) + [-1] * 16      # the other half is free but its last reader still runs
+    assert plan_slot_windows(pool3, list(range(16)), set(nxt), nxt, 64, frozenset(range(32))) == [(16, nxt)]
