@@ -768,6 +768,60 @@ class RFSNv10KVCacheMLX:
             return {"key": e["key"], "value": e["value"]}
         return load_compressed_chunk(self.cold_chunk_paths_by_id[chunk_id], self.device)
 
+    # ------------------------------------------------------------------ NPZ interop
+    def export_cold_chunks(self, directory: Union[str, Path]) -> List[Path]:
+        """Write every pinned cold chunk as ``layer{L}_chunk{id}.npz`` in the
+        reference's chunk schema (storage.py:113-135), which the reference's
+        ``load_compressed_chunk`` reads (the subspace format adds its sparse
+        arrays and keeps its own code shapes)."""
+        if self.config.cold_medium != "pinned":
+            raise RuntimeError("export_cold_chunks needs cold_medium='pinned' (NPZ caches already hold files)")
+        root = Path(directory)
+        paths = []
+        for m in self.cold_chunk_metadata:
+            e = self._cold_pinned[m["chunk_id"]]
+            path = chunk_file_path(root, self.layer_idx, m["chunk_id"])
+            save_compressed_chunk(path, e["key"], e["value"])
+            paths.append(path)
+        return paths
+
+    def import_cold_chunks(self, directory: Union[str, Path], quantizer: QuantizerArg) -> int:
+        """Load ``layer{L}_chunk{id}.npz`` files (the reference's chunk schema,
+        storage.py:113-151) into the pinned cold tier of an empty cache under
+        the recency policy: chunk ``id`` holds the tokens from
+        ``id * cold_chunk_tokens``, so the ids must run 0, 1, ... and every
+        chunk but the last must be full.  Later appends continue after them.
+        Returns the number of tokens loaded."""
+        if self.config.cold_medium != "pinned" or not self._recency:
+            raise RuntimeError("import_cold_chunks needs cold_medium='pinned' and tier_policy='recency'")
+        if self.total_tokens:
+            raise RuntimeError("import_cold_chunks loads into an empty cache")
+        chunk = self.config.chunk_tokens
+        prefix = f"layer{self.layer_idx}_chunk"
+        found = {}
+        for path in Path(directory).glob(f"{prefix}*.npz"):
+            tail = path.stem[len(prefix):]
+            if tail.isdigit():
+                found[int(tail)] = path
+        ids = sorted(found)
+        if ids != list(range(len(ids))):
+            raise ValueError(f"chunk files must be layer{self.layer_idx}_chunk0.npz, chunk1, ... without gaps")
+        self.quantizer = quantizer
+        self._kq, self._vq = _pair(quantizer)
+        for cid in ids:
+            loaded = load_compressed_chunk(found[cid], self.device)
+            ck = compressed_tensor_from_loaded(loaded, "key")
+            cv = compressed_tensor_from_loaded(loaded, "value")
+            if ck.num_heads != self.H or (ck.subspace != self._subspace):
+                raise ValueError(f"{found[cid].name}: heads or code format differ from this cache's")
+            n = ck.num_tokens
+            if n > chunk or (n < chunk and cid != ids[-1]) or cv.num_tokens != n:
+                raise ValueError(f"{found[cid].name}: every chunk but the last must hold {chunk} tokens")
+            self._store_cold_piece(cid, cid * chunk, ck, cv, None)
+            self.num_cold += n
+        self.total_tokens = self.num_cold
+        return self.num_cold
+
     def _chunk_store(self, loaded, prefix: str) -> CompressedTensorMLX:
         if self.config.cold_medium == "pinned":
             return _to_device_store(loaded[prefix], self.device)

@@ -397,3 +397,36 @@ def test_prefetch_ahead_decode_loop(device):
         pos, wk, wv = _cold_window(ids, chunk, ncold, total, hot, keys, values, dec)
         ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, False, None)
         assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL, step
+
+
+def test_cold_chunks_npz_roundtrip(device, tmp_path):
+    """The pinned cold tier written as the reference's chunk files
+    (layer{L}_chunk{id}.npz, its key names) and read back into an empty cache:
+    after the remaining tokens are appended the new cache materializes the
+    same window bit for bit and attends identically; gaps in the chunk ids
+    are refused."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    total, nh, nw, chunk = 1500, 64, 256, 64
+    g, cfg, cache, keys, values, dec = _cold_cache(device, 94, total, nh, nw, chunk, Hq=8, Hkv=4)
+    paths = cache.export_cold_chunks(tmp_path)
+    assert [p.name for p in paths] == [f"layer0_chunk{m['chunk_id']}.npz" for m in cache.cold_chunk_metadata]
+    with np.load(paths[0], allow_pickle=False) as z:
+        for key in ("num_tokens", "num_heads", "key_pq_codes", "key_rvq_codes", "key_rvq_mask", "key_rvq_offsets",
+                    "value_pq_codes", "value_rvq_codes", "value_rvq_mask", "value_rvq_offsets"):
+            assert key in z.files
+        assert int(z["num_tokens"][0]) == chunk and int(z["num_heads"][0]) == 4
+    again = RFSNv10KVCacheMLX(cfg, device=device)
+    assert again.import_cold_chunks(tmp_path, (cache._kq, cache._vq)) == cache.num_cold
+    rest = cache.num_cold
+    again.update(T(keys[rest:], device), T(values[rest:], device), (cache._kq, cache._vq))
+    assert (again.num_hot, again.num_warm, again.num_cold) == (cache.num_hot, cache.num_warm, cache.num_cold)
+    ids = [m["chunk_id"] for m in cache.cold_chunk_metadata]
+    a, b = cache.materialize_window(cold_chunks=ids), again.materialize_window(cold_chunks=ids)
+    assert np.array_equal(H(a[0]).view(np.uint16), H(b[0]).view(np.uint16))
+    assert np.array_equal(H(a[1]).view(np.uint16), H(b[1]).view(np.uint16))
+    q = T(randn16(g, 1, 8, 64), device)
+    assert torch.equal(cache.attention_forward(q, cold_chunks=ids), again.attention_forward(q, cold_chunks=ids))
+    paths[1].unlink()
+    with pytest.raises(ValueError):
+        RFSNv10KVCacheMLX(cfg, device=device).import_cold_chunks(tmp_path, (cache._kq, cache._vq))
