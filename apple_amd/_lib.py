@@ -53,7 +53,7 @@ class FusedParams(C.Structure):
                 ("k_pq_cb", vp), ("k_rvq_cb", vp), ("v_pq_cb", vp), ("v_rvq_cb", vp),
                 ("pq_cb_stride", i64), ("rvq_cb_stride", i64),
                 ("max_tokens", i32), ("splits", i32), ("workspace", vp), ("workspace_bytes", sz),
-                ("part_base", i32), ("part_slots", i32), ("merge", i32)]
+                ("part_base", i32), ("part_slots", i32), ("merge", i32), ("k_layout", i32)]
 
 
 class Copy(C.Structure):
@@ -73,10 +73,12 @@ SIGNATURES = {
     "rfsn_rvq_encode_full": (i32, [vp, i64, i32, vp, i64, vp, i32, i32, vp, vp]),
     "rfsn_decode": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, i64, i32, vp]),
     "rfsn_sparse_fold": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, vp]),
+    "rfsn_sparse_delta": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, vp]),
     "rfsn_decode_ref": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, i64, i32, i32, vp, vp, vp]),
     "rfsn_attention_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "rfsn_blockwise_attention": (i32, [vp, i32, i32, i32, vp, vp, i64, i32, i64, i64, f32, i32, vp, vp, vp, sz, vp]),
     "rfsn_pack_codes": (i32, [vp, i64, i64, i32, i32, vp, i64, i64, vp]),
+    "rfsn_pack_score_codes": (i32, [vp, vp, vp, vp, i32, i64, i32, vp, vp, vp, vp, i64, i64, vp]),
     "rfsn_fused_splits": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_workspace_bytes": (sz, [C.POINTER(FusedParams)]),
     "rfsn_fused_decode_attention": (i32, [C.POINTER(FusedParams), vp]),
@@ -112,7 +114,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 2:
+    if lib.rfsn_abi_version() != 3:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

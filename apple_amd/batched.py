@@ -9,7 +9,9 @@ cache.  Here the HBM image of B sequences lives in shared device buffers:
 * warm tier: PQ / RVQ codes in the tiled layout ``[B, Hkv, cap*M]`` and the
   sparse residual ``[B, Hkv, cap, k]`` (u8 index, fp16 value), plus the
   corrected coordinates fp16(K[idx] + val) the fused kernel streams in place
-  of the residual values;
+  of the residual values.  When the kernel can score K through q . centroid
+  tables (16 + 16 subspaces, at most 4 query heads per KV head), K codes are
+  score-table rows instead and K's streamed sparse values the score deltas;
 * codebooks per sequence, K and V separately: ``[B, M, C, d]``.
 
 Window order per sequence is warm (positions 0..W-1) then hot, the recency
@@ -47,6 +49,7 @@ class RFSNBatchedKVCache:
     def _alloc(self, fmt: K.WarmFormat) -> None:
         B, H, D, dev = self.batch, self.H, self.D, self.device
         self.fmt = fmt
+        self.k_layout = 1 if K.score_layout_ok(fmt, self.config.num_heads, H) else 0
         self.hot_k = torch.zeros((B, H, self.hot_cap, D), dtype=torch.float16, device=dev)
         self.hot_v = torch.zeros_like(self.hot_k)
         cap = self.warm_cap
@@ -60,7 +63,10 @@ class RFSNBatchedKVCache:
             c["sparse_val"] = (torch.zeros((B, H, cap, fmt.sparse_k), dtype=torch.float16, device=dev)
                                if fmt.sparse_k else None)
             # corrected coordinates fp16(K[idx] + val): the sparse values the fused kernel streams
+            # (score deltas for K in the score-table layout, with the indices in that layout)
             c["sparse_fold"] = torch.zeros_like(c["sparse_val"]) if fmt.sparse_k else None
+            c["sparse_idx_s"] = (torch.zeros_like(c["sparse_idx"])
+                                 if fmt.sparse_k and kv == "k" and self.k_layout == 1 else None)
             self.codes[kv] = c
         M, Cn, d = fmt.pq_subspaces, fmt.pq_centroids, D // fmt.pq_subspaces
         self.cb = {"k_pq": torch.zeros((B, M, Cn, d), dtype=torch.float16, device=dev)}
@@ -101,16 +107,26 @@ class RFSNBatchedKVCache:
             flat = x[:nw].permute(1, 0, 2).reshape(self.H * nw, self.D).contiguous()
             out = K.warm_encode(flat, fmt, qz.pq.codebooks, qz.rvq.codebooks if fmt.rvq_subspaces else None)
             c = self.codes[kv]
-            K.pack_codes(out["pq"].view(self.H, nw, -1), c["pq"][b], 0)
-            if fmt.rvq_subspaces:
-                K.pack_codes(out["rvq"].view(self.H, nw, -1), c["rvq"][b], 0)
+            score_rows = kv == "k" and self.k_layout == 1
+            fold = None
             if fmt.sparse_k:
                 c["sparse_idx"][b, :, :nw] = out["sparse_idx"].view(self.H, nw, -1)
                 c["sparse_val"][b, :, :nw] = out["sparse_val"].view(self.H, nw, -1)
                 fold = K.sparse_fold(fmt, out["pq"], qz.pq.codebooks, out.get("rvq"),
                                      qz.rvq.codebooks if fmt.rvq_subspaces else None, out["sparse_idx"],
-                                     out["sparse_val"])
-                c["sparse_fold"][b, :, :nw] = fold.view(self.H, nw, -1)
+                                     out["sparse_val"], delta=score_rows).view(self.H, nw, -1)
+            view3 = lambda t: None if t is None else t.view(self.H, nw, -1)
+            if score_rows:
+                dst = {"pq": c["pq"][b], "rvq": c["rvq"][b],
+                       "sparse_idx": c["sparse_idx_s"][b] if fmt.sparse_k else None,
+                       "sparse_val": c["sparse_fold"][b] if fmt.sparse_k else None}
+                K.pack_score_codes(view3(out["pq"]), view3(out["rvq"]), view3(out.get("sparse_idx")), fold, dst, 0)
+            else:
+                K.pack_codes(view3(out["pq"]), c["pq"][b], 0)
+                if fmt.rvq_subspaces:
+                    K.pack_codes(view3(out["rvq"]), c["rvq"][b], 0)
+                if fmt.sparse_k:
+                    c["sparse_fold"][b, :, :nw] = fold
         self.num_hot[b] = nh
         self.num_warm[b] = nw
         self.quantizers[b] = (key_quantizer, value_quantizer)
@@ -140,6 +156,9 @@ class RFSNBatchedKVCache:
             raise ValueError("q must be [B, Hq, D] with Hq a multiple of the KV heads")
         if len(set(self.num_hot)) != 1 or (causal and len(set(self.num_warm)) != 1):
             raise ValueError("every sequence must hold the same hot length (and warm length when causal)")
+        if self.k_layout == 1 and not K.score_layout_ok(self.fmt, q.shape[1], self.H):
+            raise ValueError(f"K codes are laid out for {self.config.num_heads} query heads; "
+                             f"got {q.shape[1]} (more than 4 per KV head)")
         table, dev_table = self._segment_table()
         f = self.fmt
         qpos = None
@@ -160,7 +179,7 @@ class RFSNBatchedKVCache:
             k_pq_cb=self.cb["k_pq"], v_pq_cb=self.cb["v_pq"], k_rvq_cb=self.cb.get("k_rvq"),
             v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True,
             max_tokens=max(h + w for h, w in zip(self.num_hot, self.num_warm)), splits=splits,
-            workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=launch)
+            workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=launch, k_layout=self.k_layout)
 
     def sequence_window(self, b: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Materialized (keys, values) [W, Hkv, D] of sequence b, warm then hot."""
@@ -175,24 +194,37 @@ class RFSNBatchedKVCache:
             outs.append(torch.cat(parts, 0).contiguous())
         return outs[0], outs[1]
 
-    def _decode_warm(self, kv: str, b: int, qz: HybridQuantizerMLX) -> torch.Tensor:
-        """Unpack the tiled codes of sequence b and decode them (head-major rows)."""
+    def plain_codes(self, kv: str, b: int) -> Dict[str, Optional[torch.Tensor]]:
+        """Warm codes of sequence b in the reference layout: pq / rvq [H, W, M]
+        and the sparse residual [H, W, k] (device tensors)."""
         f = self.fmt
         nw = self.num_warm[b]
         c = self.codes[kv]
-        pq = untile(c["pq"][b], f.pq_subspaces, nw)
-        rvq = untile(c["rvq"][b], f.rvq_subspaces, nw) if f.rvq_subspaces else None
-        sidx = c["sparse_idx"][b, :, :nw].reshape(self.H * nw, -1) if f.sparse_k else None
-        sval = c["sparse_val"][b, :, :nw].reshape(self.H * nw, -1) if f.sparse_k else None
-        return K.decode(f, pq.reshape(self.H * nw, -1), qz.pq.codebooks,
-                        None if rvq is None else rvq.reshape(self.H * nw, -1),
-                        qz.rvq.codebooks if f.rvq_subspaces else None, sidx, sval)
+        if kv == "k" and self.k_layout == 1:
+            pq, rvq, _, _ = K.unpack_score_codes({"pq": c["pq"][b], "rvq": c["rvq"][b]}, nw)
+        else:
+            pq = untile(c["pq"][b], f.pq_subspaces, nw)
+            rvq = untile(c["rvq"][b], f.rvq_subspaces, nw) if f.rvq_subspaces else None
+        return {"pq": pq, "rvq": rvq,
+                "sparse_idx": c["sparse_idx"][b, :, :nw] if f.sparse_k else None,
+                "sparse_val": c["sparse_val"][b, :, :nw] if f.sparse_k else None}
+
+    def _decode_warm(self, kv: str, b: int, qz: HybridQuantizerMLX) -> torch.Tensor:
+        """Decode the warm codes of sequence b (head-major rows)."""
+        f = self.fmt
+        nw = self.num_warm[b]
+        c = self.plain_codes(kv, b)
+        flat = lambda t: None if t is None else t.reshape(self.H * nw, -1)
+        return K.decode(f, flat(c["pq"]), qz.pq.codebooks, flat(c["rvq"]),
+                        qz.rvq.codebooks if f.rvq_subspaces else None, flat(c["sparse_idx"]),
+                        flat(c["sparse_val"]))
 
 
 def _kernel_view(c: Dict[str, Optional[torch.Tensor]]) -> Dict[str, Optional[torch.Tensor]]:
     """The arrays the fused kernel streams: tiled codes, sparse indices and
     the corrected coordinates as its sparse values."""
-    return {"pq": c["pq"], "rvq": c["rvq"], "sparse_idx": c["sparse_idx"], "sparse_val": c["sparse_fold"]}
+    si = c["sparse_idx_s"] if c.get("sparse_idx_s") is not None else c["sparse_idx"]
+    return {"pq": c["pq"], "rvq": c["rvq"], "sparse_idx": si, "sparse_val": c["sparse_fold"]}
 
 
 def untile(tiled: torch.Tensor, M: int, T: int) -> torch.Tensor:

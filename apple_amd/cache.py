@@ -74,14 +74,18 @@ class TiledCodes:
     """Device codes of the subspace format in the fused kernel's tiled layout.
     Its ``sparse_val`` holds the corrected coordinates fp16(K[idx] + val)
     (``kernels.sparse_fold``), which the kernel stores over the reconstructed
-    coordinate; the reference-layout stores keep the residuals."""
+    coordinate; the reference-layout stores keep the residuals.  With
+    ``score_rows`` (K codes the kernel scores through q . centroid tables)
+    codes and sparse entries are in the ``kernels.pack_score_codes`` layout
+    and ``sparse_val`` holds the score deltas."""
 
     def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0,
-                 backing: Optional[torch.Tensor] = None):
+                 backing: Optional[torch.Tensor] = None, score_rows: bool = False):
         """``backing``: a uint8 buffer of at least ``nbytes(fmt, heads, cap)``
         that holds every array (fixed capacity), so that one copy moves the
         whole set; otherwise each array is its own growable allocation."""
         self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
+        self.score_rows = score_rows
         self.cap = 0
         self.len = 0
         self.head = 0  # tiles before the oldest live token (pop_front_tiles)
@@ -172,7 +176,8 @@ class TiledCodes:
         if self.fmt.sparse_k and T:
             f = self.fmt
             flat = lambda t: None if t is None else t.reshape(H * T, -1)
-            sval = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval)).view(H, T, -1)
+            sval = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval),
+                                 delta=self.score_rows).view(H, T, -1)
         need = self.len + T
         if self.head * K.TILE + need > self.cap:
             if self._backing is None and self.head and 2 * K.round_up(need, K.TILE) <= self.cap:
@@ -181,10 +186,13 @@ class TiledCodes:
             else:
                 self._alloc(max(need, 2 * self.cap))
         t_base = self.head * K.TILE + self.len
-        K.pack_codes(pq, self.t["pq"], t_base)
-        if self.fmt.rvq_subspaces:
-            K.pack_codes(rvq, self.t["rvq"], t_base)
-        if self.fmt.sparse_k:
+        if self.score_rows:
+            K.pack_score_codes(pq, rvq, sidx, sval, self.t, t_base)
+        else:
+            K.pack_codes(pq, self.t["pq"], t_base)
+            if self.fmt.rvq_subspaces:
+                K.pack_codes(rvq, self.t["rvq"], t_base)
+        if self.fmt.sparse_k and not self.score_rows:
             self.t["sparse_idx"][:, t_base:t_base + T] = sidx
             self.t["sparse_val"][:, t_base:t_base + T] = sval
         self.len = need
@@ -467,6 +475,18 @@ class RFSNv10KVCacheMLX:
     def _fmt(self) -> K.WarmFormat:
         return self._kq.warm_format()
 
+    @property
+    def _k_layout(self) -> int:
+        """1 when K codes are score-table rows (subspace format, 16 + 16
+        subspaces, at most 4 query heads of the config per KV head)."""
+        return int(self._subspace and K.score_layout_ok(self._fmt(), self.config.num_heads, self.H))
+
+    def _tiled_pair(self, **kw) -> Tuple["TiledCodes", "TiledCodes"]:
+        """Empty (K, V) tiled code sets; K as score-table rows when the kernel scores K that way."""
+        fmt = self._fmt()
+        return (TiledCodes(fmt, self.H, self.device, score_rows=bool(self._k_layout), **kw),
+                TiledCodes(fmt, self.H, self.device, **kw))
+
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Append [T, H, D] tokens to the hot tier.  The buffers hold up to
         twice the hot capacity under the recency policy, so the live range
@@ -509,7 +529,7 @@ class RFSNv10KVCacheMLX:
         if not fmt.fused_ok:
             return
         if self._warm_tiled is None:
-            self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
+            self._warm_tiled = self._tiled_pair()
         for tiled, store, qz in zip(self._warm_tiled, (ck, cv), (self._kq, self._vq)):
             if self._subspace:
                 tiled.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
@@ -626,8 +646,7 @@ class RFSNv10KVCacheMLX:
                 for t in self._warm_tiled:
                     t.pop_front_tiles(n // K.TILE)
             else:
-                fmt = self._fmt()
-                self._warm_tiled = (TiledCodes(fmt, self.H, self.device), TiledCodes(fmt, self.H, self.device))
+                self._warm_tiled = self._tiled_pair()
                 if self.num_warm:
                     self._warm_tiled_append(self.warm_keys, self.warm_values)
 
@@ -746,7 +765,8 @@ class RFSNv10KVCacheMLX:
             dev_buf = torch.zeros(2 * half, dtype=torch.uint8, device=self.device)
             host_buf = self._arena_view(cid)
             for i, (name, store, qz) in enumerate((("key", ck, self._kq), ("value", cv, self._vq))):
-                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk, backing=dev_buf[i * half:(i + 1) * half])
+                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk, backing=dev_buf[i * half:(i + 1) * half],
+                                   score_rows=i == 0 and bool(self._k_layout))
                 dev_t.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
                 host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk,
                                     backing=host_buf[i * half:(i + 1) * half])
@@ -905,8 +925,9 @@ class RFSNv10KVCacheMLX:
             pool = self._slot_pool()
             cap = K.round_up(self.config.chunk_tokens, K.TILE)
             self._slot_views[slot] = tuple(
-                TiledCodes(self._fmt(), self.H, self.device, cap=cap, backing=pool[o:o + half])
-                for o in (slot * nb, slot * nb + half))
+                TiledCodes(self._fmt(), self.H, self.device, cap=cap, backing=pool[o:o + half],
+                           score_rows=i == 0 and bool(self._k_layout))
+                for i, o in enumerate((slot * nb, slot * nb + half)))
         e = self._cold_pinned[cid]
         kt, vt = self._slot_views[slot]
         kt.len, vt.len = e["key_tiled"].len, e["value_tiled"].len
@@ -1156,11 +1177,14 @@ class RFSNv10KVCacheMLX:
         return keys.contiguous(), values.contiguous(), adjusted
 
     # ------------------------------------------------------------------ attention
-    def _fused_ok(self) -> bool:
+    def _fused_ok(self, q_heads: Optional[int] = None) -> bool:
         """The fused kernel serves the long-context warm format, and the
         reference format while no warm vector carries an RVQ correction (the
-        reference's pq_only mode, threshold = inf)."""
+        reference's pq_only mode, threshold = inf).  K codes laid out as
+        score-table rows serve at most 4 query heads per KV head."""
         if self._kq is None or not self._fmt().fused_ok or self._kq.warm_format() != self._vq.warm_format():
+            return False
+        if q_heads is not None and self._k_layout and not K.score_layout_ok(self._fmt(), q_heads, self.H):
             return False
         if self.num_warm and self._warm_tiled is None:
             return False
@@ -1179,7 +1203,7 @@ class RFSNv10KVCacheMLX:
             raise RuntimeError("Cache cannot run attention before update() provides a quantizer")
         if q.shape[-1] != self.D or q.dim() != 3 or q.shape[1] % self.H:
             raise ValueError("q must be [B, Hq, D] with Hq a multiple of the cache's KV heads")
-        if not self._fused_ok():
+        if not self._fused_ok(int(q.shape[1])):
             keys, values, adjusted = self.materialize_window(query_positions, context_window, router,
                                                              current_position, cold_chunks)
             self.last_access_stats["query_tokens"] = int(q.shape[0])
@@ -1200,7 +1224,7 @@ class RFSNv10KVCacheMLX:
         overlapped with the attention over the resident part; with all of
         them resident the step is one launch.  The step stays valid until
         another call changes the cache or its device slots."""
-        if not self._fused_ok():
+        if not self._fused_ok(int(q.shape[1])):
             raise ValueError("prepare() needs a cache format the fused kernel serves")
         step = self._fused_forward(q, causal, query_positions, router, current_position, context_window,
                                    cold_chunks, launch=False, splits=splits, out=out)
@@ -1275,7 +1299,8 @@ class RFSNv10KVCacheMLX:
                       hot_seq_stride=0, k_pq_cb=self._kq.pq.codebooks, v_pq_cb=self._vq.pq.codebooks,
                       k_rvq_cb=self._kq.rvq.codebooks if fmt.rvq_subspaces else None,
                       v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
-                      cb_batch_stride=False, hot_cap=int(self._hot_k.shape[1]), out=out, launch=False)
+                      cb_batch_stride=False, hot_cap=int(self._hot_k.shape[1]), out=out, launch=False,
+                      k_layout=self._k_layout)
         has_resident = hot_len > 0 or not resident.empty
         if not fetched or not has_resident:
             # one launch; with chunks to copy it waits for them (nothing to overlap)

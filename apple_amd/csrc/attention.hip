@@ -230,6 +230,41 @@ __global__ void pack_codes_kernel(const uint8_t* __restrict__ src, int64_t src_h
   dst[(int64_t)h * dst_head_stride + off] = src[(int64_t)h * src_head_stride + gid];
 }
 
+// Score-table K layout (16 PQ + 16 RVQ subspaces, k sparse entries): token
+// t = 32 tau + 16 u + r of a head's stream.  Code byte j = 4 beta + b of its
+// row (in each array) sits at 512 tau + 32 r + 8 beta + 4 u + b and holds
+// subspace 4 beta + (b ^ ((r >> 2) & 3)); odd tokens keep their RVQ codes in
+// the PQ array and their PQ codes in the RVQ array.  Sparse entry e sits at
+// entry 32 k tau + 2 k r + 2 e + u.  One thread per (token, row byte j); the
+// threads j < k also move sparse entry j.
+__global__ void pack_score_codes_kernel(const uint8_t* __restrict__ pq, const uint8_t* __restrict__ rvq,
+                                        const uint8_t* __restrict__ sidx, const uint16_t* __restrict__ sval, int k,
+                                        int64_t T, uint8_t* __restrict__ dpq, uint8_t* __restrict__ drvq,
+                                        uint8_t* __restrict__ dsidx, uint16_t* __restrict__ dsval,
+                                        int64_t dst_tokens, int64_t t_base) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int h = blockIdx.y;
+  if (gid >= T * 16) return;
+  const int64_t tl = gid >> 4;
+  const int j = (int)(gid & 15);
+  const int64_t t = t_base + tl;
+  const int64_t tau = t >> 5;
+  const int u = (int)((t >> 4) & 1), r = (int)(t & 15);
+  const int m = (j & 12) | ((j & 3) ^ ((r >> 2) & 3));
+  const int64_t src = ((int64_t)h * T + tl) * 16 + m;
+  const uint8_t a = pq[src], c = rvq[src];
+  const int64_t dst = (int64_t)h * dst_tokens * 16 + tau * 512 + r * 32 + (j >> 2) * 8 + u * 4 + (j & 3);
+  const bool odd = (r & 1) != 0;
+  dpq[dst] = odd ? c : a;
+  drvq[dst] = odd ? a : c;
+  if (j < k) {
+    const int64_t se = ((int64_t)h * T + tl) * k + j;
+    const int64_t de = (int64_t)h * dst_tokens * k + tau * 32 * k + r * 2 * k + 2 * j + u;
+    dsidx[de] = sidx[se];
+    dsval[de] = sval[se];
+  }
+}
+
 }  // namespace rfsn
 
 using namespace rfsn;
@@ -306,4 +341,19 @@ extern "C" int rfsn_pack_codes(const uint8_t* src, int64_t src_head_stride, int6
   hipLaunchKernelGGL(pack_codes_kernel, dim3((unsigned)ceil_div(T * M, 256), (unsigned)heads), dim3(256), 0,
                      (hipStream_t)stream, src, src_head_stride, T, M, dst, dst_head_stride, t_base);
   return check_launch("pack_codes");
+}
+
+extern "C" int rfsn_pack_score_codes(const uint8_t* pq, const uint8_t* rvq, const uint8_t* sidx,
+                                     const uint16_t* sval, int32_t k, int64_t T, int32_t heads, uint8_t* dpq,
+                                     uint8_t* drvq, uint8_t* dsidx, uint16_t* dsval, int64_t dst_tokens,
+                                     int64_t t_base, void* stream) {
+  RFSN_REQUIRE(pq && rvq && dpq && drvq && heads > 0 && T >= 0 && t_base >= 0, "pack_score_codes: bad arguments");
+  RFSN_REQUIRE(k >= 0 && k <= 16 && (k == 0 || (sidx && sval && dsidx && dsval)),
+               "pack_score_codes: sparse entries need 0 <= k <= 16 and all four arrays");
+  RFSN_REQUIRE(dst_tokens % 32 == 0 && dst_tokens >= ceil_div(t_base + T, 32) * 32,
+               "pack_score_codes: destination too small (whole 32-token tiles)");
+  if (T == 0) return RFSN_OK;
+  hipLaunchKernelGGL(pack_score_codes_kernel, dim3((unsigned)ceil_div(T * 16, 256), (unsigned)heads), dim3(256), 0,
+                     (hipStream_t)stream, pq, rvq, sidx, sval, k, T, dpq, drvq, dsidx, dsval, dst_tokens, t_base);
+  return check_launch("pack_score_codes");
 }

@@ -50,6 +50,9 @@ decode_ext_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C
 // One thread per sparse entry (vector v, slot j): the corrected coordinate
 // fp16(K[idx] + val) with K = fp16(base + rvq), i.e. the value the warm decode
 // leaves at coordinate idx (the indices of one vector are distinct).
+// DELTA = false: the corrected coordinate c = fp16(fp16(base + rvq) + val);
+// DELTA = true: the score delta fp16(c - (float(base) + float(rvq))).
+template <bool DELTA>
 __global__ void __launch_bounds__(256)
 sparse_fold_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C, const uint16_t* __restrict__ pq_cb,
                    const uint8_t* __restrict__ rvq, int Mr, int Cr, const uint16_t* __restrict__ rvq_cb,
@@ -61,13 +64,21 @@ sparse_fold_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int 
   const int i = min((int)sidx[gid], D - 1);
   const int d = D / M;
   const int m = i / d;
-  uint16_t val = pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)];
+  const uint16_t base = pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)];
+  uint16_t corr = 0, val = base;
   if (Mr > 0) {
     const int dr = D / Mr;
     const int mr = i / dr;
-    val = hadd_bits(val, rvq_cb[((size_t)mr * Cr + min((int)rvq[v * Mr + mr], Cr - 1)) * dr + (i - mr * dr)]);
+    corr = rvq_cb[((size_t)mr * Cr + min((int)rvq[v * Mr + mr], Cr - 1)) * dr + (i - mr * dr)];
+    val = hadd_bits(base, corr);
   }
-  out[gid] = hadd_bits(val, sval[gid]);
+  const uint16_t c = hadd_bits(val, sval[gid]);
+  if constexpr (DELTA) {
+    const float exact = h2f(base) + (Mr > 0 ? h2f(corr) : 0.f);
+    out[gid] = f2h(h2f(c) - exact);
+  } else {
+    out[gid] = c;
+  }
 }
 
 __global__ void __launch_bounds__(256)
@@ -156,8 +167,10 @@ extern "C" int rfsn_decode(const rfsn_format* f, const rfsn_codes* codes, int64_
   return check_launch("decode");
 }
 
-extern "C" int rfsn_sparse_fold(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
-                                const void* rvq_cb, void* out, void* stream) {
+namespace rfsn {
+namespace {
+int sparse_fold_launch(bool delta, const char* name, const rfsn_format* f, const rfsn_codes* codes, int64_t n,
+                       const void* pq_cb, const void* rvq_cb, void* out, void* stream) {
   RFSN_REQUIRE(f && codes && codes->pq && pq_cb && out, "sparse_fold: null pointer");
   RFSN_REQUIRE(f->sparse_k > 0 && codes->sparse_idx && codes->sparse_val, "sparse_fold: no sparse stage");
   RFSN_REQUIRE(f->head_dim % f->pq_subspaces == 0, "sparse_fold: head_dim must be a multiple of num_subspaces");
@@ -165,11 +178,24 @@ extern "C" int rfsn_sparse_fold(const rfsn_format* f, const rfsn_codes* codes, i
                "sparse_fold: RVQ stage needs codes and codebooks");
   if (n == 0) return RFSN_OK;
   const int64_t total = n * f->sparse_k;
-  hipLaunchKernelGGL(sparse_fold_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, n,
+  auto kern = delta ? sparse_fold_kernel<true> : sparse_fold_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, n,
                      f->head_dim, codes->pq, f->pq_subspaces, f->pq_centroids, (const uint16_t*)pq_cb, codes->rvq,
                      f->rvq_subspaces, f->rvq_centroids, (const uint16_t*)rvq_cb, codes->sparse_idx,
                      (const uint16_t*)codes->sparse_val, f->sparse_k, (uint16_t*)out);
-  return check_launch("sparse_fold");
+  return check_launch(name);
+}
+}  // namespace
+}  // namespace rfsn
+
+extern "C" int rfsn_sparse_fold(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
+                                const void* rvq_cb, void* out, void* stream) {
+  return sparse_fold_launch(false, "sparse_fold", f, codes, n, pq_cb, rvq_cb, out, stream);
+}
+
+extern "C" int rfsn_sparse_delta(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
+                                 const void* rvq_cb, void* out, void* stream) {
+  return sparse_fold_launch(true, "sparse_delta", f, codes, n, pq_cb, rvq_cb, out, stream);
 }
 
 extern "C" int rfsn_decode_ref(const uint8_t* pq, int64_t n, int32_t D, int32_t M, int32_t C, const void* pq_cb,

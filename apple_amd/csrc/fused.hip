@@ -38,6 +38,16 @@
 //      the factor cancels in out = acc / l.
 // The steps are software-pipelined: every gather is issued one step before
 // the store that consumes it.
+// Score tables (k_layout 1: 16 PQ + 16 RVQ subspaces, at most 4 query heads
+// per KV head): the block first writes T[code][slot][head] = fp16(q_head .
+// centroid) over the 32 slots (PQ subspaces, then RVQ) into the K table's
+// place, same 256-byte entries.  K codes then arrive as plain rows and a
+// lane (row r, k-group kg) gathers 8 table entries of one token (4 slots x
+// both stages), which are directly a 16x16x32 A operand with k = (slot,
+// head); B selects head = k % 4 into the replicated score columns, so four
+// MFMAs per half tile sum the 32 slots in fp32 and K^ is never built.  The
+// sparse stage adds fp16(q[idx] * delta) through a fifth MFMA, q[idx] taken
+// from other lanes' registers by ds_bpermute.
 // Split partials (m, l, acc) are merged by merge_partials_kernel.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
@@ -340,6 +350,102 @@ __device__ __forceinline__ void gather_half(const uint8_t* __restrict__ lds, con
   }
 }
 
+// K codes of one tile for the score-table path (rfsn_pack_score_codes
+// layout): the lane's token row r = tokr (tokens 16u + tokr of the halves,
+// the score layout's row order) and code block beta: one 8-byte load per code
+// array gives bytes [4 beta, 4 beta + 4) of both halves' rows (u = 0 low word),
+// and one load each gives sparse entry kg = lane >> 4 of both tokens (index
+// bytes, delta halves; u = 0 low).
+struct LutRegs {
+  uint2 pq;
+  uint2 rvq;
+  uint32_t sidx;
+  uint32_t sval;
+};
+
+template <int KS>
+__device__ __forceinline__ void load_tile_lut(LutRegs& r, const WarmBase& w, int off, int tokr, uint32_t blk8,
+                                              int kg) {
+  // tile off / 32 of the head's block: 512 code bytes per array
+  const uint32_t co = (uint32_t)off * 16u + (uint32_t)tokr * 32u + blk8;
+  const uint64_t a = gload<uint64_t>(w.pq[0], co), c = gload<uint64_t>(w.rvq[0], co);
+  r.pq = make_uint2((uint32_t)a, (uint32_t)(a >> 32));
+  r.rvq = make_uint2((uint32_t)c, (uint32_t)(c >> 32));
+  if constexpr (KS > 0) {
+    // rows past count lie inside the tile (codes are allocated in whole
+    // tiles) and their scores are masked before the exponential
+    const uint32_t e = (uint32_t)off * (uint32_t)KS + (uint32_t)(tokr * 2 * KS + 2 * kg);
+    r.sidx = gload<uint16_t>(w.si[0], e);
+    r.sval = gload<uint32_t>(w.sv[0], e * 2);
+  }
+}
+
+// Gather the 8 score-table entries of half u: for k = 0..3 the entries of
+// code byte k of the lane's PQ-array word and of its RVQ-array word.  The
+// row layout permutes and swaps the codes so that byte k of a word is the
+// same subspace slot for every token of the lane: lca / lcb hold those slot
+// offsets (32 beta + 8 (k ^ ((t >> 2) & 3)) + stage * 128) in byte k, and one
+// v_perm_b32 builds code * 256 + offset.  Per LDS pass the 32 lanes read 32
+// distinct slots (all 64 banks).
+// e[2k] (PQ-array byte k) and e[2k + 1] (RVQ-array byte k) form the A
+// operand of score MFMA k.
+struct LutHalf {
+  uint4 e[4];
+};
+__device__ __forceinline__ void lut_gather(const uint8_t* __restrict__ lds, const LutRegs& r, int u, uint32_t lca,
+                                           uint32_t lcb, LutHalf& raw) {
+  const uint32_t wp = u ? r.pq.y : r.pq.x, wr = u ? r.rvq.y : r.rvq.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t sel = 0x0C0C0000u | ((uint32_t)k << 8) | (4u + (uint32_t)k);
+    const uint2 a = *reinterpret_cast<const uint2*>(lds + __builtin_amdgcn_perm(lca, wp, sel));
+    const uint2 b = *reinterpret_cast<const uint2*>(lds + __builtin_amdgcn_perm(lcb, wr, sel));
+    raw.e[k] = make_uint4(a.x, a.y, b.x, b.y);
+  }
+}
+
+// Sparse operand of half u for a 16x16x16 MFMA: fp16(q_j[idx] * delta) for
+// heads j = 0..3 at k = 4kg + j (entry kg of the lane's token).  Lane l holds
+// (q_0[l], q_1[l]) in qc0 and (q_2[l], q_3[l]) in qc1; ds_bpermute reads them
+// from lane idx.
+template <int KS>
+__device__ __forceinline__ half4_t lut_sparse(const LutRegs& r, int u, uint32_t qc0, uint32_t qc1) {
+  if constexpr (KS > 0) {
+    const int a = (int)(((r.sidx >> (8 * u)) & 63u) << 2);
+    const half2_t q01 = __builtin_bit_cast(half2_t, (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)qc0));
+    const half2_t q23 = __builtin_bit_cast(half2_t, (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)qc1));
+    const _Float16 dv = __builtin_bit_cast(_Float16, (uint16_t)(r.sval >> (16 * u)));
+    const half2_t dd = {dv, dv};
+    const half2_t p01 = q01 * dd, p23 = q23 * dd;  // v_pk_mul_f16
+    return half4_t{p01[0], p01[1], p23[0], p23[1]};
+  } else {
+    return half4_t{};
+  }
+}
+
+// Scores of both halves of a tile from their gathered score-table entries:
+// MFMA k of a half sums e[k] (k = (slot, head) pairs), B selects head k % 4
+// into the replicated score columns, and a 16x16x16 MFMA adds the sparse
+// operand (B = the first 4 rows of the same selection).  The two halves'
+// accumulation chains are interleaved, so that consecutive MFMAs are
+// independent.
+template <int KS>
+__device__ __forceinline__ void lut_mfma2(const LutHalf& h0, const LutHalf& h1, const half4_t& sp0,
+                                          const half4_t& sp1, const half8_t& bsel, float4_t& c0, float4_t& c1) {
+  c0 = float4_t{0.f, 0.f, 0.f, 0.f};
+  c1 = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, h0.e[k]), bsel, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, h1.e[k]), bsel, c1, 0, 0, 0);
+  }
+  if constexpr (KS > 0) {
+    const half4_t b4 = {bsel[0], bsel[1], bsel[2], bsel[3]};
+    c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(sp0, b4, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(sp1, b4, c1, 0, 0, 0);
+  }
+}
+
 // The sparse stage of half u: the segment carries the corrected coordinates
 // fp16(X[idx] + val), stored over the reconstructed ones by the lanes of
 // this half's tokens (two entries each, addresses from sparse_addrs).  The
@@ -451,9 +557,10 @@ __device__ __forceinline__ void sparse_addrs(const TileRegs<M, RVQ, KS>& regs, u
   sa[1] = sbase ^ ((regs.sidx >> 7) & 0x7Eu);
 }
 
-template <int M, bool RVQ, int KS, int NHG>
+template <int M, bool RVQ, int KS, int NHG, bool LUT>
 __global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
 fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
+  static_assert(!LUT || (M == 16 && RVQ && NHG == 1), "score tables: 16 + 16 subspaces, <= 4 heads per KV head");
   // static allocation: its base address is known at compile time, so LDS
   // addresses built in registers need no base add
   constexpr int kWaves = BlockShape<NHG>::W;
@@ -493,6 +600,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     Vec v[4][kIters];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      if (LUT && (c & 1) == 0) continue;  // the K tables become score tables below
       const int n = (c < 2 || !RVQ) ? C : Cr;
 #pragma unroll
       for (int i = 0; i < kIters; ++i) {
@@ -504,6 +612,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
+      if (LUT && (c & 1) == 0) continue;
       uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
 #pragma unroll
       for (int i = 0; i < kIters; ++i) {
@@ -511,6 +620,54 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
         const int e = idx / M, m = idx % M;
         if (idx < M * 256) *reinterpret_cast<Vec*>(dst + e * kEntryBytes + m * d * 2) = v[c][i];
       }
+    }
+  }
+  if constexpr (LUT) {
+    // score table T[c][s][j] = fp16(q_j . centroid c of slot s) in fp32
+    // (slot s < 16: PQ subspace s, else RVQ subspace s - 16; heads j >= G
+    // give 0, codes past the codebook 0).  Thread: slot tid % 32, codes
+    // tid / 32 + kRows * i; every load is issued before the first store.
+    constexpr int kRows = kThreads / 32;
+    constexpr int kPasses = 256 / kRows;
+    static_assert(256 % kRows == 0, "score table passes");
+    const int s = threadIdx.x & 31, m = s & 15;
+    const bool rv = s >= 16;
+    const uint16_t* cb = rv ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride
+                            : (const uint16_t*)p.k_pq_cb + (int64_t)b * p.pq_cb_stride;
+    const int nc = rv ? Cr : C;
+    uint2 qw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + h * G + min(j, G - 1)) * kD;
+      qw[j] = j < G ? *reinterpret_cast<const uint2*>(qrow + 4 * m) : make_uint2(0, 0);
+    }
+    uint2 e[kPasses];
+#pragma unroll
+    for (int i = 0; i < kPasses; ++i) {
+      const int c = (threadIdx.x >> 5) + kRows * i;
+      e[i] = c < nc ? *reinterpret_cast<const uint2*>(cb + ((int64_t)m * nc + c) * 4) : make_uint2(0, 0);
+    }
+    float qf[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half4_t hq = __builtin_bit_cast(half4_t, qw[j]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) qf[j][t] = (float)hq[t];
+    }
+#pragma unroll
+    for (int i = 0; i < kPasses; ++i) {
+      const int c = (threadIdx.x >> 5) + kRows * i;
+      const half4_t x = __builtin_bit_cast(half4_t, e[i]);
+      half4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float a = qf[j][0] * (float)x[0];
+        a = fmaf(qf[j][1], (float)x[1], a);
+        a = fmaf(qf[j][2], (float)x[2], a);
+        a = fmaf(qf[j][3], (float)x[3], a);
+        o[j] = (_Float16)a;
+      }
+      *reinterpret_cast<uint2*>(lds + c * kEntryBytes + s * 8) = __builtin_bit_cast(uint2, o);
     }
   }
 
@@ -558,6 +715,27 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int ep = n & 3;
   const uint32_t sel_lo = ep == 0 ? 0x0C0C0100u : (ep == 1 ? 0x01000C0Cu : 0x0C0C0C0Cu);
   const uint32_t sel_hi = ep == 2 ? 0x0C0C0100u : (ep == 3 ? 0x01000C0Cu : 0x0C0C0C0Cu);
+  // score-table lanes: row n holds token row tokr of each half (tokens
+  // t = 16u + tokr, so (t >> 2) & 3 = n & 3 and t & 1 = (n >> 2) & 1), k-group
+  // g the code block beta (4 subspaces of both stages), chosen so that the 8
+  // lanes of a block in one LDS pass differ in (n & 3, (n >> 2) & 1) and read
+  // 8 distinct slots
+  const int tokr = 4 * (n & 3) + (n >> 2);
+  const int beta = (g + 2 * (n >> 3)) & 3;
+  const bool todd = ((n >> 2) & 1) != 0;
+  const uint32_t blk8 = 8u * (uint32_t)beta;
+  uint32_t lca = 0, lcb = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot8 = 32 * beta + 8 * (i ^ (n & 3));
+    lca |= (uint32_t)(slot8 + (todd ? kRvqSlot : 0)) << (8 * i);
+    lcb |= (uint32_t)(slot8 + (todd ? 0 : kRvqSlot)) << (8 * i);
+  }
+  // B operand of the score-table MFMAs: k index 8g + e carries head e & 3,
+  // column n scores head n >> 2
+  half8_t bsel;
+#pragma unroll
+  for (int e2 = 0; e2 < 8; ++e2) bsel[e2] = (_Float16)((e2 & 3) == (n >> 2) ? 1.0f : 0.0f);
 
   // ---- query operands and per-head state: lane column n serves head hg*4 + n/4
   half8_t qb[NHG][2];
@@ -586,6 +764,18 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   if (p.causal && p.qpos)
     for (int hh = 0; hh < G; ++hh) qmin = min(qmin, p.qpos[(int64_t)b * p.q_heads + h * G + hh]);
   const float scale_log2 = p.scale * kLog2e;
+  // q columns of the score-table sparse stage: lane l holds q_j[l], j < 4
+  uint32_t qc0 = 0, qc1 = 0;
+  if constexpr (LUT && KS > 0) {
+    uint32_t qv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + h * G + min(j, G - 1)) * kD;
+      qv[j] = j < G ? (uint32_t)qrow[lane] : 0u;
+    }
+    qc0 = qv[0] | (qv[1] << 16);
+    qc1 = qv[2] | (qv[3] << 16);
+  }
   const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
                         (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
@@ -603,12 +793,18 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   __syncthreads();
 
   using Regs = TileRegs<M, RVQ, KS>;
+  using KRegs = typename std::conditional<LUT, LutRegs, Regs>::type;
   // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves.  Only
   // encoded tiles go through slots (tt >= hot_tiles); a slot past the split
   // is idle and re-reads the split's last tile, which is encoded.
   TileSrc srcs[kDepth];
-  Regs kr[kDepth], vr[kDepth];
-  auto fetch = [&](TileSrc& s, Regs& rk, Regs& rv, int tt) {
+  KRegs kr[kDepth];
+  Regs vr[kDepth];
+  auto load_k = [&](KRegs& rk, const WarmBase& w, int off, int count) __attribute__((always_inline)) {
+    if constexpr (LUT) load_tile_lut<KS>(rk, w, off, tokr, blk8, g);
+    else load_tile<M, RVQ, KS>(rk, w, 0, off, count, lane);
+  };
+  auto fetch = [&](TileSrc& s, KRegs& rk, Regs& rv, int tt) {
     const int r = min(tt, t_end - 1) - hot_tiles;
     if (r < seg0_tiles) {  // uniform; segment 0 from registers
       s.kind = 1;
@@ -616,12 +812,12 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       s.off = r * kTile;
       s.count = min(kTile, w0.len - s.off);
       s.pos0 = w0.pos0 + s.off;
-      load_tile<M, RVQ, KS>(rk, w0, 0, s.off, s.count, lane);
+      load_k(rk, w0, s.off, s.count);
       load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
     } else {
       s = walk_segments(segs, nseg, r - seg0_tiles);
       const WarmBase w = warm_base<M, RVQ, KS>(segs + s.seg, h);
-      load_tile<M, RVQ, KS>(rk, w, 0, s.off, s.count, lane);
+      load_k(rk, w, s.off, s.count);
       load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
     }
     if (tt >= t_end) s.kind = -1;
@@ -643,6 +839,17 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
       for (int c = 0; c < 2; ++c) sc[hg][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], qb[hg][c], sc[hg][u], 0, 0, 0);
     }
+  };
+  // scores of both halves from their gathered score-table entries (+ the sparse operands)
+  using KHalf = typename std::conditional<LUT, LutHalf, RawHalf<M, RVQ>>::type;
+  auto lut_scores = [&](const KHalf& h0, const KHalf& h1, const half4_t& sp0, const half4_t& sp1,
+                        float4_t (&sc)[NHG][2]) __attribute__((always_inline)) {
+    if constexpr (LUT) lut_mfma2<KS>(h0, h1, sp0, sp1, bsel, sc[0][0], sc[0][1]);
+  };
+  // K half u of the tile in slot ks: score-table or codebook gathers
+  auto gather_k = [&](const KRegs& rk, int u, KHalf& raw) __attribute__((always_inline)) {
+    if constexpr (LUT) lut_gather(lds, rk, u, lca, lcb, raw);
+    else gather_half<M, RVQ, KS>(lds, rk, u, lc1_k, lc2_k, odd, raw);
   };
   // online softmax in base 2; produces the B operands of P.V (probability at
   // coordinate n & 3 of the lane's k-group)
@@ -769,7 +976,9 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
     for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
     RawHalf<M, RVQ> ra, rb;
-    gather_half<M, RVQ, KS>(lds, kr[0], 0, lc1_k, lc2_k, odd, ra);
+    KHalf ka, kb;  // K halves of the score-table path (the codebook path gathers K into ra, rb)
+    if constexpr (LUT) gather_k(kr[0], 0, ka);
+    else gather_k(kr[0], 0, ra);
     for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
@@ -778,19 +987,26 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
           uint32_t pbl[NHG][8], pbh[NHG][8];
           half8_t a[2];
           half8_t av[2];
-          uint32_t sak[2] = {0, 0}, sav[2] = {0, 0};
-          if constexpr (KS > 0) {
-            sparse_addrs(kr[s], sbase, sak);
-            if constexpr (M != 16) sparse_addrs(vr[s], sbase, sav);
+          uint32_t sav[2] = {0, 0};
+          if constexpr (KS > 0 && M != 16) sparse_addrs(vr[s], sbase, sav);
+          if constexpr (LUT) {
+            gather_k(kr[s], 1, kb);
+            const half4_t sp0 = lut_sparse<KS>(kr[s], 0, qc0, qc1);
+            const half4_t sp1 = lut_sparse<KS>(kr[s], 1, qc0, qc1);
+            gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
+            lut_scores(ka, kb, sp0, sp1, sc);
+          } else {
+            uint32_t sak[2] = {0, 0};
+            if constexpr (KS > 0) sparse_addrs(kr[s], sbase, sak);
+            store_half<M, RVQ, KS>(lds, kr[s], ra, 0, waddr, sak, shalf);
+            score_operands(a);
+            gather_k(kr[s], 1, rb);
+            scores(a, sc, 0);
+            store_half<M, RVQ, KS>(lds, kr[s], rb, 1, waddr, sak, shalf);
+            score_operands(a);
+            gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
+            scores(a, sc, 1);
           }
-          store_half<M, RVQ, KS>(lds, kr[s], ra, 0, waddr, sak, shalf);
-          score_operands(a);
-          gather_half<M, RVQ, KS>(lds, kr[s], 1, lc1_k, lc2_k, odd, rb);
-          scores(a, sc, 0);
-          store_half<M, RVQ, KS>(lds, kr[s], rb, 1, waddr, sak, shalf);
-          score_operands(a);
-          gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
-          scores(a, sc, 1);
           softmax(srcs[s], sc, pbl, pbh);
           if constexpr (M == 16 && KS == 0) {
             direct_half<RVQ>(ra, av);
@@ -818,7 +1034,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
             store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
             pv_operands(av);
           }
-          gather_half<M, RVQ, KS>(lds, kr[(s + 1) % kDepth], 0, lc1_k, lc2_k, odd, ra);  // next tile
+          if constexpr (LUT) gather_k(kr[(s + 1) % kDepth], 0, ka);  // next tile
+          else gather_k(kr[(s + 1) % kDepth], 0, ra);
           pv(av, pbl, pbh, 1);
         }
         fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
@@ -897,13 +1114,13 @@ int auto_splits(const rfsn_fused_params* p) {
   return s;
 }
 
-template <int M, bool RVQ, int KS, int NHG>
+template <int M, bool RVQ, int KS, int NHG, bool LUT>
 int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   const int splits = auto_splits(p);
   const int tiles = total_tiles_host(p);
   const int tps = (tiles + splits - 1) / splits;
   const int blocks = p->batch * p->kv_heads * splits;
-  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG>;  // 160 KB of static LDS
+  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG, LUT>;  // 160 KB of static LDS
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(BlockShape<NHG>::T), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
   if (st) return st;
@@ -920,8 +1137,11 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
 template <int M, bool RVQ, int KS>
 int dispatch_nhg(const rfsn_fused_params* p, hipStream_t s) {
   const int G = p->q_heads / p->kv_heads;
-  if (G <= 4) return launch_fused<M, RVQ, KS, 1>(p, s);
-  return launch_fused<M, RVQ, KS, 2>(p, s);
+  if constexpr (M == 16 && RVQ) {
+    if (p->k_layout == 1) return launch_fused<M, RVQ, KS, 1, true>(p, s);
+  }
+  if (G <= 4) return launch_fused<M, RVQ, KS, 1, false>(p, s);
+  return launch_fused<M, RVQ, KS, 2, false>(p, s);
 }
 
 template <int M, bool RVQ>
@@ -982,6 +1202,9 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
     RFSN_REQUIRE(!p->merge || p->part_base + splits == p->part_slots,
                  "fused: the merging call must fill the last slots (part_base + splits == part_slots)");
   }
+  RFSN_REQUIRE(p->k_layout == 0 || p->k_layout == 1, "fused: k_layout must be 0 or 1");
+  RFSN_REQUIRE(p->k_layout == 0 || (f.pq_subspaces == 16 && f.rvq_subspaces == 16 && p->q_heads / p->kv_heads <= 4),
+               "fused: k_layout 1 needs 16 PQ and 16 RVQ subspaces and at most 4 query heads per KV head");
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;

@@ -179,10 +179,12 @@ def decode(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional
 
 
 def sparse_fold(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Optional[torch.Tensor],
-                rvq_cb: Optional[torch.Tensor], sparse_idx: torch.Tensor, sparse_val: torch.Tensor) -> torch.Tensor:
+                rvq_cb: Optional[torch.Tensor], sparse_idx: torch.Tensor, sparse_val: torch.Tensor,
+                delta: bool = False) -> torch.Tensor:
     """Corrected coordinates fp16(K[idx] + val) of the sparse stage, [N, k] fp16:
     the sparse values the fused kernel's layout carries (a store per entry
-    instead of a read-modify-write)."""
+    instead of a read-modify-write).  ``delta``: the score deltas
+    fp16(corrected - (base[idx] + rvq[idx])) of the score-table K layout."""
     _dev(pq, "sparse_fold")
     pq = _contig(pq)
     n = pq.shape[0]
@@ -193,8 +195,9 @@ def sparse_fold(fmt: WarmFormat, pq: torch.Tensor, pq_cb: torch.Tensor, rvq: Opt
     sidx, sval = _contig(sparse_idx), _contig(sparse_val)
     codes = L.Codes(pq.data_ptr(), L.ptr(rvq), sidx.data_ptr(), sval.data_ptr())
     f = fmt.c()
-    L.call("rfsn_sparse_fold", C.byref(f), C.byref(codes), n, _contig(pq_cb).data_ptr(),
-           L.ptr(None if rvq_cb is None else _contig(rvq_cb)), out.data_ptr(), _stream(pq))
+    L.call("rfsn_sparse_delta" if delta else "rfsn_sparse_fold", C.byref(f), C.byref(codes), n,
+           _contig(pq_cb).data_ptr(), L.ptr(None if rvq_cb is None else _contig(rvq_cb)), out.data_ptr(),
+           _stream(pq))
     return out
 
 
@@ -261,6 +264,71 @@ def pack_codes(src: torch.Tensor, dst: torch.Tensor, t_base: int) -> None:
     H, T, M = src.shape
     src = _contig(src)
     L.call("rfsn_pack_codes", src.data_ptr(), T * M, T, M, H, dst.data_ptr(), dst.stride(0), t_base, _stream(src))
+
+
+def score_layout_ok(fmt: WarmFormat, q_heads: int, kv_heads: int) -> bool:
+    """Whether the fused kernel can score K codes through q . centroid tables:
+    16 PQ and 16 RVQ subspaces, at most 4 query heads per KV head."""
+    return (fmt.pq_subspaces == 16 and fmt.rvq_subspaces == 16 and fmt.head_dim == 64
+            and kv_heads > 0 and q_heads % kv_heads == 0 and q_heads // kv_heads <= 4)
+
+
+def pack_score_codes(pq: torch.Tensor, rvq: torch.Tensor, sidx: Optional[torch.Tensor], sval: Optional[torch.Tensor],
+                     dst: Dict[str, Optional[torch.Tensor]], t_base: int) -> None:
+    """Plain codes pq, rvq [H, T, 16] and sparse entries sidx, sval [H, T, k]
+    (sval: score deltas) into the score-table K layout of ``dst`` (``pq``,
+    ``rvq`` [H, cap*16]; ``sparse_idx``, ``sparse_val`` [H, cap, k]) at tokens
+    t_base..: token t = 32 tau + 16 u + r has code byte 4g + b at
+    512 tau + 32 r + 8 g + 4 u + b holding subspace 4g + (b ^ ((r >> 2) & 3)),
+    odd tokens with the two stages swapped, and sparse entry e at
+    32 k tau + 2 k r + 2 e + u."""
+    _dev(pq, "pack_score_codes")
+    H, T, M = pq.shape
+    if M != 16 or tuple(rvq.shape) != (H, T, 16):
+        raise ValueError("pack_score_codes: PQ and RVQ codes must be [H, T, 16]")
+    k = 0 if sidx is None else int(sidx.shape[2])
+    cap = dst["pq"].shape[1] // 16
+    pq, rvq = _contig(pq), _contig(rvq)
+    si = None if sidx is None else _contig(sidx)
+    sv = None if sval is None else _contig(sval)
+    L.call("rfsn_pack_score_codes", pq.data_ptr(), rvq.data_ptr(), L.ptr(si), L.ptr(sv), k, T, H,
+           dst["pq"].data_ptr(), dst["rvq"].data_ptr(), L.ptr(dst.get("sparse_idx") if k else None),
+           L.ptr(dst.get("sparse_val") if k else None), cap, t_base, _stream(pq))
+
+
+def _score_positions(T: int, t0: int, k: int, device):
+    """(code byte offsets [T, 16], code subspace of each byte [T, 16], sparse
+    entry offsets [T, k]) of tokens t0 .. t0+T-1 in the score-table K layout."""
+    t = torch.arange(t0, t0 + T, device=device)
+    j = torch.arange(16, device=device)
+    tau, u, r = t >> 5, (t >> 4) & 1, t & 15
+    pos = (512 * tau + 32 * r + 4 * u)[:, None] + (8 * (j >> 2) + (j & 3))[None, :]
+    sub = (j & 12)[None, :] | ((j & 3)[None, :] ^ ((r >> 2) & 3)[:, None])
+    e = torch.arange(k, device=device)
+    spos = (32 * k * tau + 2 * k * r + u)[:, None] + 2 * e[None, :]
+    return pos, sub, spos
+
+
+def unpack_score_codes(dst: Dict[str, Optional[torch.Tensor]], T: int, t0: int = 0):
+    """Inverse of ``pack_score_codes`` for tokens t0 .. t0+T-1: plain
+    (pq, rvq [H, T, 16], sparse_idx, sparse_val [H, T, k] or None)."""
+    p, r_ = dst["pq"], dst["rvq"]
+    H = p.shape[0]
+    k = 0 if dst.get("sparse_idx") is None else int(dst["sparse_idx"].shape[2])
+    pos, sub, spos = _score_positions(T, t0, k, p.device)
+    inv = torch.empty_like(sub)
+    inv.scatter_(1, sub, torch.arange(16, device=p.device)[None, :].expand(T, 16).contiguous())
+    bytes_at = pos.gather(1, inv)                                   # [T, 16]: byte of subspace s
+    gp = p[:, bytes_at.reshape(-1)].reshape(H, T, 16)
+    gr = r_[:, bytes_at.reshape(-1)].reshape(H, T, 16)
+    odd = ((torch.arange(t0, t0 + T, device=p.device) & 1) == 1)[None, :, None]
+    pq, rvq = torch.where(odd, gr, gp), torch.where(odd, gp, gr)
+    if not k:
+        return pq, rvq, None, None
+    flat = spos.reshape(-1)
+    si = dst["sparse_idx"].reshape(H, -1)[:, flat].reshape(H, T, k)
+    sv = dst["sparse_val"].reshape(H, -1)[:, flat].reshape(H, T, k)
+    return pq, rvq, si, sv
 
 
 class SegmentTable:
@@ -338,8 +406,11 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
                     splits: int = 0, table: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
                     workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                     hot_cap: Optional[int] = None, launch: bool = True,
-                    part: Optional[Tuple[int, int, bool]] = None):
+                    part: Optional[Tuple[int, int, bool]] = None, k_layout: int = 0):
     """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
+
+    ``k_layout`` = 1 when every segment's K codes are ``pack_score_codes``
+    rows with ``sparse_fold(delta=True)`` values (``score_layout_ok``).
 
     hot_k/hot_v: [.., Hkv, hot_cap, D] fp16 (sequence stride ``hot_seq_stride``
     elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
@@ -379,6 +450,7 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
     p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
     p.max_tokens, p.splits = max_tokens, splits
+    p.k_layout = int(k_layout)
     if part is not None:
         if splits <= 0 or workspace is None:
             raise ValueError("partial calls need explicit splits and a shared workspace")

@@ -113,24 +113,15 @@ def cpu_baseline(w, cache, q, gpu_out, sample, repeats, threads=None):
     """Time the torch-CPU restatement of the path on a bounded sample, on
     every host core (or ``threads``)."""
     import torch
-    from apple_amd.batched import untile
     from oracle import cpu_baseline as cb
 
     cores = threads or len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    f = cache.fmt
     total, n, max_err = 0.0, 0, 0.0
     for b in range(min(sample, w.batch)):
         nw, nh = cache.num_warm[b], cache.num_hot[b]
-        codes = {}
-        for kv in ("k", "v"):
-            c = cache.codes[kv]
-            codes[kv] = {"pq": untile(c["pq"][b], f.pq_subspaces, nw).cpu()}
-            if f.rvq_subspaces:
-                codes[kv]["rvq"] = untile(c["rvq"][b], f.rvq_subspaces, nw).cpu()
-            if f.sparse_k:
-                codes[kv]["sparse_idx"] = c["sparse_idx"][b, :, :nw].cpu()
-                codes[kv]["sparse_val"] = c["sparse_val"][b, :, :nw].cpu()
+        codes = {kv: {k: t.cpu() for k, t in cache.plain_codes(kv, b).items() if t is not None}
+                 for kv in ("k", "v")}
         cbs = {k: v[b].cpu() for k, v in cache.cb.items()}
         hk, hv = cache.hot_k[b, :, :nh].cpu(), cache.hot_v[b, :, :nh].cpu()
         qb = q[b:b + 1].cpu()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 2
+#define RFSN_ABI_VERSION 3
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -120,6 +120,15 @@ int rfsn_decode(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
 int rfsn_sparse_fold(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
                      const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, void* stream);
 
+/* Score deltas of the sparse stage: out[v][j] = fp16(c - (float(base[idx]) +
+ * float(rvq[idx]))) in fp32 arithmetic, c = the corrected coordinate of
+ * rfsn_sparse_fold.  A kernel that scores codes through q . centroid tables
+ * (which sum base + rvq unrounded) adds q[idx] * out[v][j] to reach q . K of
+ * the decoded key.  out is [N][k] fp16.  No reference symbol (see
+ * rfsn_sparse_fold). */
+int rfsn_sparse_delta(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
+                      const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, void* stream);
+
 /* Reference-format hybrid decode (quantization.py:310-319): base =
  * C_pq[pq_codes]; corr = fp16(sum_l C_l[rvq_codes[a][l]]) scattered to rows
  * offsets[a]; out = fp16(base + corr) (corr = +0 for inactive rows). */
@@ -154,6 +163,22 @@ int rfsn_blockwise_attention(const void* q_dev, int32_t B, int32_t Hq, int32_t D
 int rfsn_pack_codes(const uint8_t* src_dev, int64_t src_head_stride, int64_t T, int32_t M, int32_t heads,
                     uint8_t* dst_dev, int64_t dst_head_stride, int64_t t_base, void* stream);
 
+/* K layout of k_layout = 1 (16 PQ + 16 RVQ subspaces, k <= 16 sparse
+ * entries).  Token t = 32*tau + 16*u + r of a head: code byte j = 4*g + b of
+ * its row (in each code array) sits at byte 512*tau + 32*r + 8*g + 4*u + b of
+ * the head's block and holds subspace 4*g + (b ^ ((r >> 2) & 3)); odd tokens
+ * keep their RVQ codes in the PQ array and their PQ codes in the RVQ array.
+ * Sparse entry e of the token sits at entry 32*k*tau + 2*k*r + 2*e + u of the
+ * head's block in both sparse arrays.  Converts plain rows [heads][T][16]
+ * (codes) and [heads][T][k] (sparse index / value) into tokens
+ * t_base .. t_base+T-1 of blocks of dst_tokens tokens (a multiple of 32) per
+ * head.  No reference symbol: lays codes out for the fused kernel's score
+ * tables (the warm append of cache.py:122-132). */
+int rfsn_pack_score_codes(const uint8_t* pq_src_dev, const uint8_t* rvq_src_dev, const uint8_t* sparse_idx_dev,
+                          const uint16_t* sparse_val_dev, int32_t k, int64_t T, int32_t heads,
+                          uint8_t* pq_dst_dev, uint8_t* rvq_dst_dev, uint8_t* sparse_idx_dst_dev,
+                          uint16_t* sparse_val_dst_dev, int64_t dst_tokens, int64_t t_base, void* stream);
+
 /* Fused warm-tier dequant + exact decode attention over [hot | segments] (or
  * [segments | hot]).  Replaces RFSNv10KVCacheMLX.attention_forward
  * (cache.py:395-428) = materialize_window (cache.py:344-393) +
@@ -161,10 +186,13 @@ int rfsn_pack_codes(const uint8_t* src_dev, int64_t src_head_stride, int64_t T, 
  *
  * A segment is a run of encoded tokens of one sequence for all KV heads.
  * PQ and RVQ codes are in the tiled layout (head h at byte h*head_stride*M
- * resp. h*head_stride*M_r); sparse arrays are plain rows, (head h, token t)
- * at row h*head_stride + t.  head_stride is a multiple of 32.  The sparse
- * values of a segment are the corrected coordinates of rfsn_sparse_fold
- * (fp16(K[idx] + residual)), not the residuals.
+ * resp. h*head_stride*M_r; K codes and sparse entries in the
+ * rfsn_pack_score_codes layout when k_layout = 1);
+ * sparse arrays are plain rows, (head h, token t) at row h*head_stride + t.
+ * head_stride is a multiple of 32.  The sparse values of a segment are the
+ * corrected coordinates of rfsn_sparse_fold (fp16(K[idx] + residual)), or
+ * for K with k_layout = 1 the score deltas of rfsn_sparse_delta, not the
+ * residuals.
  * Segment window positions are pos0 .. pos0+len-1 (used by causal masking;
  * tokens at negative positions are skipped). */
 typedef struct rfsn_segment {
@@ -221,6 +249,15 @@ typedef struct rfsn_fused_params {
   int32_t part_base;
   int32_t part_slots;
   int32_t merge;
+  /* Layout of the K streams of every segment:
+   * 0: PQ/RVQ codes tiled (rfsn_pack_codes), sparse values the corrected
+   *    coordinates of rfsn_sparse_fold;
+   * 1: PQ/RVQ codes and sparse entries in the rfsn_pack_score_codes
+   *    layout, sparse values the score deltas of rfsn_sparse_delta.  Needs M = M_r = 16 and at most 4 query heads per
+   *    KV head: the kernel then scores codes through a per-call table of
+   *    q . centroid (fp16) instead of reconstructing K.
+   * V streams are always layout 0. */
+  int32_t k_layout;
 } rfsn_fused_params;
 
 /* Token splits the call would use (p->splits, or the automatic choice when 0);

@@ -257,6 +257,24 @@ def ext_decode(pq_codes, pq_cb, rvq_codes=None, rvq_cb=None, sparse_idx=None, sp
     return recon
 
 
+def score_delta(pq_codes, pq_cb, rvq_codes, rvq_cb, sparse_idx, sparse_val) -> np.ndarray:
+    """Sparse entries as score deltas: ``fp16(c - (fl32(base[idx]) + fl32(rvq[idx])))``
+    in fp32, c = the decoded (corrected) coordinate ``ext_decode`` leaves at idx.
+
+    A scorer that sums q . base + q . rvq unrounded adds q[idx] * delta to
+    reach q . K of the decoded key at the sparse coordinates.  The decoded
+    coordinate follows quantization.py:317-319 (fp16(base + rvq)) and the
+    sparse stage of ``apply_sparse``.
+    """
+    base = pq_decode(pq_codes, pq_cb)
+    corr = pq_decode(rvq_codes, rvq_cb) if rvq_codes is not None else np.zeros_like(base)
+    dec = ext_decode(pq_codes, pq_cb, rvq_codes, rvq_cb, sparse_idx, sparse_val)
+    ix = sparse_idx.astype(np.int64)
+    c = np.take_along_axis(dec, ix, axis=1).astype(F32)
+    exact = np.take_along_axis(base, ix, axis=1).astype(F32) + np.take_along_axis(corr, ix, axis=1).astype(F32)
+    return (c - exact).astype(F16)
+
+
 # --------------------------------------------------------------------------
 # compressed-tensor helpers (quantization.py:330-403), numpy containers
 # --------------------------------------------------------------------------

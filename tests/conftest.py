@@ -34,3 +34,28 @@ def randn16(g: np.random.Generator, *shape, scale=1.0) -> np.ndarray:
 def rand_codebooks(g: np.random.Generator, M: int, C: int, d: int) -> np.ndarray:
     """quantization.py:108-115: N(0,1) * sqrt(2/d) in fp16."""
     return (g.standard_normal((M, C, d), dtype=np.float32) * np.float32((2.0 / d) ** 0.5)).astype(np.float16)
+
+
+def score_layout(pq, rvq, sidx, sval, t_base, cap):
+    """The score-table K layout of one head, restated: token t = 32 tau + 16 u + r
+    puts code byte j = 4g + b of its row (subspace 4g + (b ^ ((r >> 2) & 3)),
+    odd tokens with the two stages swapped) at byte 512 tau + 32 r + 8 g + 4 u + b
+    of each code array, and sparse entry e at 32 k tau + 2 k r + 2 e + u."""
+    T = pq.shape[0]
+    k = 0 if sidx is None else sidx.shape[1]
+    out_p = np.zeros(cap * 16, np.uint8)
+    out_r = np.zeros_like(out_p)
+    out_i = np.zeros(cap * k, np.uint8)
+    out_v = np.zeros(cap * k, np.float16)
+    for i in range(T):
+        t = t_base + i
+        tau, u, r = t >> 5, (t >> 4) & 1, t & 15
+        for j in range(16):
+            m = (j & 12) | ((j & 3) ^ ((r >> 2) & 3))
+            a, c = pq[i, m], rvq[i, m]
+            pos = 512 * tau + 32 * r + 8 * (j >> 2) + 4 * u + (j & 3)
+            out_p[pos], out_r[pos] = (c, a) if t & 1 else (a, c)
+        for e in range(k):
+            pos = 32 * k * tau + 2 * k * r + 2 * e + u
+            out_i[pos], out_v[pos] = sidx[i, e], sval[i, e]
+    return out_p, out_r, out_i, out_v

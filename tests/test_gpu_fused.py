@@ -102,6 +102,45 @@ def test_fused_cache_attention(device, case):
         assert err <= TOL, (causal, qp, err)
 
 
+def test_fused_codebook_k_path(device, monkeypatch):
+    """With the K codes tiled (score tables turned off), the kernel rebuilds
+    K^ from the codebooks for a format the score tables would serve: the
+    same parity."""
+    from apple_amd import kernels as K
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    monkeypatch.setattr(K, "score_layout_ok", lambda *a: False)
+    seed, Hq, Hkv, M, Mr, k, nw, nh = 2, 32, 8, 16, 16, 4, 2000, 96
+    g, cfg, keys, values, cbs, kq, vq = _setup(seed, Hq, Hkv, M, Mr, k, nw, nh)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._fused_ok() and cache._k_layout == 0 and not cache._warm_tiled[0].score_rows
+    wk, wv = _oracle_window(keys, values, cbs, Mr, k, nw)
+    q = randn16(g, 2, Hq, 64)
+    for causal in (True, False):
+        out = cache.attention_forward(T(q, device), causal=causal)
+        ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, causal, None)
+        assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
+def test_fused_score_tables_in_use(device):
+    """The Llama-3.2-1B layer format (16 + 16 subspaces, 4 query heads per
+    KV head) streams its K codes as score-table rows."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    g, cfg, keys, values, cbs, kq, vq = _setup(2, 32, 8, 16, 16, 4, 300, 40)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._k_layout == 1 and cache._warm_tiled[0].score_rows and not cache._warm_tiled[1].score_rows
+    # 8 query heads per KV head: no score tables, the materialized path serves it
+    q = randn16(g, 1, 64, 64)
+    assert not cache._fused_ok(64)
+    wk, wv = _oracle_window(keys, values, cbs, 16, 4, 300)
+    out = cache.attention_forward(T(q, device), causal=False)
+    ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, False, None)
+    assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
 @pytest.mark.parametrize("cw", [1, 31, 100, 1500])
 def test_fused_context_window(device, cw):
     from apple_amd.cache import RFSNv10KVCacheMLX

@@ -152,6 +152,55 @@ def test_sparse_fold_bit_exact(device, M, Mr):
     assert np.array_equal(H(got).view(np.uint16), want.view(np.uint16))
 
 
+@pytest.mark.parametrize("Mr", [16, 0])
+def test_sparse_delta_bit_exact(device, Mr):
+    """Score deltas fp16(c - (base[idx] + rvq[idx])) equal the oracle's."""
+    from apple_amd import kernels as K
+
+    g = rng(230 + Mr)
+    n, D, k, M = 611, 64, 4, 16
+    x = randn16(g, n, D)
+    pq_cb = rand_codebooks(g, M, 256, D // M)
+    rvq_cb = rand_codebooks(g, Mr, 256, D // Mr) * np.float16(0.3) if Mr else None
+    fmt = K.WarmFormat(D, M, 256, Mr, 256 if Mr else 0, k)
+    ref = nx.ext_encode(x, pq_cb, rvq_cb, k)
+    want = nx.score_delta(ref["pq_codes"], pq_cb, ref.get("rvq_codes"), rvq_cb, ref["sparse_idx"],
+                          ref["sparse_val"])
+    got = K.sparse_fold(fmt, T(ref["pq_codes"], device), T(pq_cb, device),
+                        T(ref["rvq_codes"], device) if Mr else None, T(rvq_cb, device) if Mr else None,
+                        T(ref["sparse_idx"], device), T(ref["sparse_val"], device), delta=True)
+    assert np.array_equal(H(got).view(np.uint16), want.view(np.uint16))
+
+
+def test_pack_score_codes_bit_exact(device):
+    """pack_score_codes writes the score-table K layout (appends at any token
+    base) and unpack_score_codes inverts it."""
+    from apple_amd import kernels as K
+    from tests.conftest import score_layout
+
+    g = rng(19)
+    Hh, Tt, k = 3, 133, 4
+    pq = g.integers(0, 256, (Hh, Tt, 16)).astype(np.uint8)
+    rv = g.integers(0, 256, (Hh, Tt, 16)).astype(np.uint8)
+    si = g.integers(0, 64, (Hh, Tt, k)).astype(np.uint8)
+    sv = randn16(g, Hh, Tt, k)
+    cap = K.round_up(Tt + 40, 32)
+    dst = {"pq": torch.zeros((Hh, cap * 16), dtype=torch.uint8, device=device),
+           "sparse_idx": torch.zeros((Hh, cap, k), dtype=torch.uint8, device=device),
+           "sparse_val": torch.zeros((Hh, cap, k), dtype=torch.float16, device=device)}
+    dst["rvq"] = torch.zeros_like(dst["pq"])
+    for a, b in ((0, 50), (50, Tt)):
+        K.pack_score_codes(T(pq[:, a:b], device), T(rv[:, a:b], device), T(si[:, a:b], device), T(sv[:, a:b], device),
+                           dst, a)
+    for h in range(Hh):
+        wp, wr, wi, wv = score_layout(pq[h], rv[h], si[h], sv[h], 0, cap)
+        assert np.array_equal(H(dst["pq"][h]), wp) and np.array_equal(H(dst["rvq"][h]), wr)
+        assert np.array_equal(H(dst["sparse_idx"][h]).reshape(-1), wi)
+        assert np.array_equal(H(dst["sparse_val"][h]).reshape(-1).view(np.uint16), wv.view(np.uint16))
+    up, ur, ui, uv = K.unpack_score_codes(dst, Tt)
+    assert np.array_equal(H(up), pq) and np.array_equal(H(ur), rv) and np.array_equal(H(ui), si)
+
+
 @pytest.mark.parametrize("thr", [0.25, 5.0, float("inf"), 0.0])
 def test_rvq_full_bit_exact(device, thr):
     from apple_amd import kernels as K

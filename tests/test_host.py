@@ -119,6 +119,75 @@ def test_tiled_layout_is_a_bijection(M):
         assert plain[tpi * i + j, m] == lane * ipt + i
 
 
+def test_score_layout_roundtrip():
+    """unpack_score_codes inverts the score-table K layout at any token base."""
+    from apple_amd import kernels as K
+    from tests.conftest import score_layout
+
+    g = np.random.default_rng(3)
+    for t_base in (0, 5, 32):
+        T, k = 70, 4
+        cap = (t_base + T + 31) // 32 * 32
+        pq = g.integers(0, 256, (T, 16)).astype(np.uint8)
+        rv = g.integers(0, 256, (T, 16)).astype(np.uint8)
+        si = g.integers(0, 64, (T, k)).astype(np.uint8)
+        sv = g.standard_normal((T, k)).astype(np.float16)
+        p, r, i, v = score_layout(pq, rv, si, sv, t_base, cap)
+        dst = {"pq": torch.from_numpy(p[None]), "rvq": torch.from_numpy(r[None]),
+               "sparse_idx": torch.from_numpy(i.reshape(1, cap, k)), "sparse_val": torch.from_numpy(v.reshape(1, cap, k))}
+        up, ur, ui, uv = K.unpack_score_codes(dst, T, t0=t_base)
+        assert np.array_equal(up[0].numpy(), pq) and np.array_equal(ur[0].numpy(), rv)
+        assert np.array_equal(ui[0].numpy(), si) and np.array_equal(uv[0].numpy().view(np.uint16), sv.view(np.uint16))
+
+
+def test_score_table_lanes_cover_slots_without_bank_conflicts():
+    """The fused kernel's score-table reads, restated from its lane
+    constants: lane (n, g) = (lane & 15, lane >> 4) handles token row
+    tokr = 4(n & 3) + (n >> 2) of both halves and code block beta; it loads 8
+    bytes at 32 tokr + 8 beta of each code array (u = 0 in the low word),
+    gather k reads byte k of half u's word at the slot offsets lca / lcb, and
+    it loads sparse entry g of both tokens at entry 8 tokr + 2 g.  Every
+    (token, slot) is read exactly once, each slot offset is the slot that
+    byte holds, every sparse entry is read once, and in every 32-lane LDS
+    pass of a gather the lanes read 32 distinct slots (the 256-byte table
+    entry spans all 64 banks)."""
+    from tests.conftest import score_layout
+
+    g0 = np.random.default_rng(4)
+    pq = g0.integers(0, 256, (32, 16)).astype(np.uint8)
+    rv = g0.integers(0, 256, (32, 16)).astype(np.uint8)
+    si = np.arange(128, dtype=np.uint8).reshape(32, 4)
+    sv = np.zeros((32, 4), np.float16)
+    p, r, sidx, _ = score_layout(pq, rv, si, sv, 0, 32)
+    seen, seen_sparse = set(), set()
+    for u in range(2):
+        for k in range(4):
+            for arr_i, arr in enumerate((p, r)):
+                slots = []
+                for lane in range(64):
+                    n, gg = lane & 15, lane >> 4
+                    tokr = 4 * (n & 3) + (n >> 2)
+                    beta = (gg + 2 * (n >> 3)) & 3
+                    todd = (n >> 2) & 1
+                    off = 32 * beta + 8 * (k ^ (n & 3)) + (128 if todd ^ arr_i else 0)
+                    slot = off // 8  # 0..15 PQ subspace, 16..31 RVQ subspace
+                    t = 16 * u + tokr
+                    code = arr[32 * tokr + 8 * beta + 4 * u + k]
+                    assert code == (pq if slot < 16 else rv)[t, slot % 16], (u, k, lane)
+                    assert (t, slot) not in seen
+                    seen.add((t, slot))
+                    slots.append(slot)
+                for p0 in (0, 32):
+                    assert len(set(slots[p0:p0 + 32])) == 32, (u, k, arr_i, p0)
+        for lane in range(64):
+            n, gg = lane & 15, lane >> 4
+            tokr = 4 * (n & 3) + (n >> 2)
+            e = int(sidx[8 * tokr + 2 * gg + u])
+            assert e == si[16 * u + tokr, gg]
+            seen_sparse.add(e)
+    assert len(seen) == 32 * 32 and len(seen_sparse) == 128
+
+
 def test_workload_bytes_known_answers():
     from apple_amd.workloads import WORKLOADS
 

@@ -94,6 +94,23 @@ def check_attention(fn, g):
     return bool(np.abs(out - ref).max() <= 2e-3)
 
 
+def check_score_delta(fn, g):
+    """Score deltas put the decoded coordinate back on top of the unrounded
+    base + rvq sum: dec[idx] = base[idx] + rvq[idx] + delta up to the fp16
+    rounding of delta (and fp32 rounding of the sum), for every sparse entry."""
+    pq = rand_codebooks(g, 16, 256, 4)
+    rv = (rand_codebooks(g, 16, 256, 4).astype(F32) * 0.35).astype(np.float16)
+    x = randn16(g, 300, 64)
+    e = nx.ext_encode(x, pq, rv, 4)
+    delta = fn(e["pq_codes"], pq, e["rvq_codes"], rv, e["sparse_idx"], e["sparse_val"]).astype(np.float64)
+    dec = nx.ext_decode(e["pq_codes"], pq, e["rvq_codes"], rv, e["sparse_idx"], e["sparse_val"])
+    ix = e["sparse_idx"].astype(np.int64)
+    take = lambda a: np.take_along_axis(a.astype(np.float64), ix, axis=1)
+    b, r, c = take(nx.pq_decode(e["pq_codes"], pq)), take(nx.pq_decode(e["rvq_codes"], rv)), take(dec)
+    bound = np.abs(delta) * 2 ** -11 + (np.abs(b) + np.abs(r) + np.abs(c)) * 2 ** -23 + 2 ** -40
+    return bool(np.all(np.abs(c - (b + r + delta)) <= bound))
+
+
 # ---------------------------------------------------------------- distances, PQ
 
 def test_sqdist_float64_bound():
@@ -243,6 +260,21 @@ def test_apply_sparse_elementwise():
         for j in range(4):
             want[i, idx[i, j]] = np.float16(float(rec[i, idx[i, j]]) + float(val[i, j]))
     assert np.array_equal(out.view(np.uint16), want.view(np.uint16))
+
+
+def test_score_delta_restores_decoded_coordinates():
+    assert check_score_delta(nx.score_delta, rng(12))
+    # the deltas of a token without an RVQ stage are the same identity on base alone
+    g = rng(14)
+    pq = rand_codebooks(g, 16, 256, 4)
+    x = randn16(g, 50, 64)
+    e = nx.ext_encode(x, pq, None, 4)
+    d = nx.score_delta(e["pq_codes"], pq, None, None, e["sparse_idx"], e["sparse_val"])
+    ix = e["sparse_idx"].astype(np.int64)
+    dec = nx.ext_decode(e["pq_codes"], pq, None, None, e["sparse_idx"], e["sparse_val"])
+    want = (np.take_along_axis(dec, ix, 1).astype(F32)
+            - np.take_along_axis(nx.pq_decode(e["pq_codes"], pq), ix, 1).astype(F32)).astype(np.float16)
+    assert np.array_equal(d.view(np.uint16), want.view(np.uint16))
 
 
 def test_ext_format_roundtrip():
@@ -530,6 +562,20 @@ def test_planted_mistakes():
 
     assert not check_attention(attn_causal_off_by_one, rng(13))
     assert check_attention(nx.blockwise_attention, rng(13))
+
+    def delta_sign(*a):  # (base + rvq) - c
+        return (-nx.score_delta(*a).astype(F32)).astype(np.float16)
+
+    def delta_no_rvq(pq_codes, pq_cb, rvq_codes, rvq_cb, sidx, sval):  # the RVQ term dropped
+        ix = sidx.astype(np.int64)
+        c = np.take_along_axis(nx.ext_decode(pq_codes, pq_cb, rvq_codes, rvq_cb, sidx, sval), ix, 1)
+        return (c.astype(F32) - np.take_along_axis(nx.pq_decode(pq_codes, pq_cb), ix, 1).astype(F32)).astype(np.float16)
+
+    def delta_residual(pq_codes, pq_cb, rvq_codes, rvq_cb, sidx, sval):  # the stored residual itself
+        return sval
+
+    for bad in (delta_sign, delta_no_rvq, delta_residual):
+        assert not check_score_delta(bad, rng(12)), bad.__name__
 
 
 def test_cpu_baseline_matches_oracle():
