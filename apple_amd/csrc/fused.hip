@@ -41,13 +41,14 @@
 // Score tables (k_layout 1: 16 PQ + 16 RVQ subspaces, at most 4 query heads
 // per KV head): the block first writes T[code][slot][head] = fp16(q_head .
 // centroid) over the 32 slots (PQ subspaces, then RVQ) into the K table's
-// place, same 256-byte entries.  K codes then arrive as plain rows and a
-// lane (row r, k-group kg) gathers 8 table entries of one token (4 slots x
-// both stages), which are directly a 16x16x32 A operand with k = (slot,
-// head); B selects head = k % 4 into the replicated score columns, so four
-// MFMAs per half tile sum the 32 slots in fp32 and K^ is never built.  The
-// sparse stage adds fp16(q[idx] * delta) through a fifth MFMA, q[idx] taken
-// from other lanes' registers by ds_bpermute.
+// place, same 256-byte entries.  K codes then arrive in the
+// rfsn_pack_score_codes layout and a lane (row r, k-group kg) gathers 8 table
+// entries of one token (4 slots x both stages), which are directly two
+// 16x16x32 A operands with k = (slot, head); B selects head = k % 4 into the
+// replicated score columns, so four MFMAs per half tile sum the 32 slots in
+// fp32 and K^ is never built.  The sparse stage adds fp16(q[idx] * delta)
+// through a 16x16x16 MFMA, q[idx] taken from other lanes' registers by
+// ds_bpermute.
 // Split partials (m, l, acc) are merged by merge_partials_kernel.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
@@ -875,13 +876,17 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
       for (int r = 0; r < 8; ++r) arg[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias_m[hg]);
       mask(arg);
-      const float amax = fmaxf(fmaxf(fmaxf(arg[0], arg[1]), fmaxf(arg[2], arg[3])),
-                               fmaxf(fmaxf(arg[4], arg[5]), fmaxf(arg[6], arg[7])));
       // The running max only moves when some score exceeds it by more than
       // the fp16 headroom of P (any max gives the same softmax, the running
       // one only keeps exp2 in range); most tiles skip the cross-lane
-      // reduction and the rescale.
-      if (__builtin_amdgcn_ballot_w64(amax > kPScaleLog2 + kSlackLog2)) {
+      // reduction and the rescale.  The test takes a signed-integer max of
+      // the float bits: values above the (positive) threshold keep their
+      // order, negative ones compare below it, and no float max (which
+      // quiets NaN inputs first) is needed.
+      int ibits = (int)fbits(arg[0]);
+#pragma unroll
+      for (int r = 1; r < 8; ++r) ibits = max(ibits, (int)fbits(arg[r]));
+      if (__builtin_amdgcn_ballot_w64(ibits > (int)fbits(kPScaleLog2 + kSlackLog2))) {
         float sv[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) sv[r] = fmaf(sc[hg][r >> 2][r & 3], scale_log2, bias[hg]);

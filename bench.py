@@ -35,7 +35,10 @@ def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # the GPU raises its clocks over the first tens of milliseconds of work:
+    # 400 warm-up steps (about 70 ms on the default workload) reach the
+    # steady state before the timed region starts
+    ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--workload", default="batched_32x32k")
     ap.add_argument("--splits", type=int, default=0, help="token splits per (sequence, KV head); 0 = auto")
     ap.add_argument("--cpu-sample", type=int, default=4, help="sequences timed on the CPU baseline")
