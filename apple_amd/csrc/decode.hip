@@ -9,6 +9,8 @@
 // out = fp16(base + corr).
 #include "rfsn_common.h"
 
+#include <algorithm>
+
 namespace rfsn {
 namespace {
 
@@ -140,6 +142,85 @@ __global__ void kmeans_finish_kernel(int M, int C, int d, const double* __restri
   cb[gid] = f2h((float)(sums[gid] / (double)cnt));
 }
 
+// k-means member sums in two levels.  Each block accumulates the (subspace,
+// centroid) sums of its range of vectors in LDS, then writes them to its own
+// slice of the workspace; kmeans_reduce_kernel adds the slices in block order
+// in float64.  No global atomics: the single-level kernel above contends on
+// the hot centroids' addresses.  A centroid's slot holds its d sums and its
+// member count (fp32, exact below 2^24), d + 1 floats: with d = 4 the odd
+// stride spreads 64 random centroids over all 64 banks.
+constexpr int kKmeansMaxParts = 256;
+
+template <int W>  // LDS words of the table, M * C * (d + 1) <= W
+__global__ void __launch_bounds__(1024)
+kmeans_partial_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx, const uint8_t* __restrict__ codes,
+                      int M, int C, int64_t per_block, float* __restrict__ parts) {
+  __shared__ float sm[W];
+  const int d = D / M, e = d + 1;
+  const int S = M * C * e;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) sm[i] = 0.f;
+  __syncthreads();
+  const int64_t v0 = (int64_t)blockIdx.x * per_block;
+  const int64_t v1 = min(n, v0 + per_block);
+  const int64_t end = v1 * M;
+  int64_t idx = v0 * M + threadIdx.x;
+  if (d == 4 && (ldx & 3) == 0 && ((uintptr_t)x & 7) == 0) {
+    // 8 (vector, subspace) pairs per thread per step: every load of the step
+    // is issued before its atomics, so the memory latency is paid once per step
+    constexpr int U = 8;
+    const int64_t stride = (int64_t)blockDim.x;
+    for (; idx + (U - 1) * stride < end; idx += U * stride) {
+      int c[U];
+      uint2 xv[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int64_t id = idx + k * stride;
+        const int64_t v = id / M;
+        c[k] = codes[id];
+        xv[k] = *reinterpret_cast<const uint2*>(x + v * ldx + (id - v * M) * 4);
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int m = (int)((idx + k * stride) % M);
+        float* sp = sm + (m * C + min(c[k], C - 1)) * 5;  // codes come from an encode against these C rows
+        atomicAdd(sp + 0, h2f((uint16_t)(xv[k].x & 0xFFFFu)));
+        atomicAdd(sp + 1, h2f((uint16_t)(xv[k].x >> 16)));
+        atomicAdd(sp + 2, h2f((uint16_t)(xv[k].y & 0xFFFFu)));
+        atomicAdd(sp + 3, h2f((uint16_t)(xv[k].y >> 16)));
+        atomicAdd(sp + 4, 1.f);
+      }
+    }
+  }
+  for (; idx < end; idx += blockDim.x) {
+    const int64_t v = idx / M;
+    const int m = (int)(idx - v * M);
+    const int c = min((int)codes[idx], C - 1);
+    const uint16_t* xr = x + v * ldx + m * d;
+    float* sp = sm + (m * C + c) * e;
+    for (int u = 0; u < d; ++u) atomicAdd(sp + u, h2f(xr[u]));
+    atomicAdd(sp + d, 1.f);
+  }
+  __syncthreads();
+  float* ps = parts + (int64_t)blockIdx.x * S;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) ps[i] = sm[i];
+}
+
+__global__ void kmeans_reduce_kernel(int M, int C, int d, int nparts, const float* __restrict__ parts,
+                                     uint16_t* __restrict__ cb) {
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int e = d + 1, S = M * C * e;
+  if (gid >= M * C * d) return;
+  const int mc = gid / d, u = gid - mc * d;
+  double cnt = 0.0, sum = 0.0;
+#pragma unroll 8
+  for (int p = 0; p < nparts; ++p) {
+    cnt += (double)parts[(int64_t)p * S + mc * e + d];
+    sum += (double)parts[(int64_t)p * S + mc * e + u];
+  }
+  if (cnt == 0.0) return;  // empty cluster keeps its row
+  cb[gid] = f2h((float)(sum / cnt));
+}
+
 __global__ void zero_kernel(uint32_t* __restrict__ p, int64_t words) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < words) p[i] = 0u;
@@ -217,7 +298,9 @@ extern "C" int rfsn_decode_ref(const uint8_t* pq, int64_t n, int32_t D, int32_t 
 }
 
 extern "C" size_t rfsn_kmeans_workspace_bytes(int32_t M, int32_t C, int32_t d) {
-  return (size_t)M * C * d * sizeof(double) + (size_t)M * C * sizeof(unsigned int) + 256;
+  const size_t single = (size_t)M * C * d * sizeof(double) + (size_t)M * C * sizeof(unsigned int) + 256;
+  const size_t parts = (size_t)kKmeansMaxParts * (size_t)M * C * (d + 1) * 4 + 256;
+  return (size_t)M * C * (d + 1) <= 40 * 1024 ? parts : single;
 }
 
 extern "C" int rfsn_kmeans_update(const void* x, int64_t n, int32_t D, int64_t ldx, const uint8_t* codes, int32_t M,
@@ -226,6 +309,23 @@ extern "C" int rfsn_kmeans_update(const void* x, int64_t n, int32_t D, int64_t l
   const int d = D / M;
   RFSN_REQUIRE(ws_bytes >= rfsn_kmeans_workspace_bytes(M, C, d), "kmeans_update: workspace too small");
   hipStream_t s = (hipStream_t)stream;
+  const int64_t table_words = (int64_t)M * C * (d + 1);
+  if (table_words <= 40 * 1024) {
+    if (n == 0) return RFSN_OK;  // every cluster empty: the codebooks stay
+    // at least about 1,024 vectors per block, at most kKmeansMaxParts blocks
+    const int parts = (int)std::min<int64_t>(kKmeansMaxParts, std::max<int64_t>(1, ceil_div(n, 1024)));
+    const int64_t per_block = ceil_div(n, parts);
+    float* psums = (float*)ws;
+    if (table_words <= 20 * 1024)  // 80 KB: two blocks per CU
+      hipLaunchKernelGGL(kmeans_partial_kernel<20 * 1024>, dim3((unsigned)parts), dim3(1024), 0, s,
+                         (const uint16_t*)x, n, D, ldx, codes, M, C, per_block, psums);
+    else
+      hipLaunchKernelGGL(kmeans_partial_kernel<40 * 1024>, dim3((unsigned)parts), dim3(1024), 0, s,
+                         (const uint16_t*)x, n, D, ldx, codes, M, C, per_block, psums);
+    hipLaunchKernelGGL(kmeans_reduce_kernel, dim3((unsigned)ceil_div((int64_t)M * C * d, 256)), dim3(256), 0, s, M, C,
+                       d, parts, psums, (uint16_t*)cb);
+    return check_launch("kmeans_update");
+  }
   double* sums = (double*)ws;
   unsigned int* counts = (unsigned int*)(sums + (size_t)M * C * d);
   const int64_t words = ((int64_t)M * C * d * 2 + (int64_t)M * C);
