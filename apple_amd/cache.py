@@ -92,6 +92,7 @@ class TiledCodes:
         self.t: Dict[str, Optional[torch.Tensor]] = {}
         self._backing = backing
         self._carved = 0
+        self._segs: Dict[Tuple[int, int], tuple] = {}  # (head, tile_skip) -> seg() result
         self._alloc(cap)
 
     @staticmethod
@@ -140,6 +141,7 @@ class TiledCodes:
         if self.t and self.cap:
             self._move_live(self.t, new)
         self.t, self.cap, self.head = new, cap, 0
+        self._segs = {}
 
     def _live_tiles(self) -> int:
         return (self.len + K.TILE - 1) // K.TILE
@@ -200,14 +202,20 @@ class TiledCodes:
     def seg(self, tile_skip: int = 0):
         """(rfsn_codes addresses from live tile ``tile_skip``, the arrays to
         keep alive, tokens available from there): a segment without building
-        tensor views."""
+        tensor views.  The result depends only on the arrays, ``head`` and
+        ``tile_skip``, so it is kept until the arrays are reallocated."""
+        hit = self._segs.get((self.head, tile_skip))
+        if hit is not None:
+            return hit
         f = self.fmt
         o = (self.head + tile_skip) * K.TILE
         t = self.t
         ptr = lambda key, scale: None if t[key] is None else t[key].data_ptr() + o * scale
         codes = L.Codes(ptr("pq", f.pq_subspaces), ptr("rvq", f.rvq_subspaces),
                           ptr("sparse_idx", f.sparse_k), ptr("sparse_val", 2 * f.sparse_k))
-        return codes, [x for x in t.values() if x is not None], self.cap - o
+        hit = (codes, [x for x in t.values() if x is not None], self.cap - o)
+        self._segs[(self.head, tile_skip)] = hit
+        return hit
 
     def codes(self, tile_skip: int = 0) -> Dict[str, Optional[torch.Tensor]]:
         """Per-array views starting at live tile ``tile_skip`` (head stride unchanged)."""
@@ -390,6 +398,7 @@ class RFSNv10KVCacheMLX:
         self.cold_chunk_paths_by_id: Dict[int, Path] = {}
         self.cold_chunk_metadata: List[dict] = []
         self._cold_pinned: Dict[int, dict] = {}
+        self._cold_ids: Tuple[int, int, List[int]] = (0, 0, [])  # (id of the source dict, its size, sorted ids)
         self._cold_slots: "OrderedDict[int, dict]" = OrderedDict()  # chunk id -> device slot, LRU first
         self._cold_arena: Dict[int, torch.Tensor] = {}
         self._slot_buf: Optional[torch.Tensor] = None
@@ -775,6 +784,15 @@ class RFSNv10KVCacheMLX:
             host_buf.copy_(dev_buf)
             entry["tiled_buf"] = host_buf
         return entry
+
+    def cold_chunk_ids(self) -> List[int]:
+        """Ids of the cold chunks this cache holds, ascending (chunks are only
+        ever added or replaced in place, so the list is rebuilt when the
+        count changes)."""
+        src = self._cold_pinned if self.config.cold_medium == "pinned" else self.cold_chunk_paths_by_id
+        if self._cold_ids[0] != id(src) or self._cold_ids[1] != len(src):
+            self._cold_ids = (id(src), len(src), sorted(src))
+        return self._cold_ids[2]
 
     def has_cold_chunk(self, chunk_id: int) -> bool:
         if self.config.cold_medium == "pinned":

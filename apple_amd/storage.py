@@ -14,6 +14,7 @@ storage.py:113-140, or "pinned" host memory).
 from __future__ import annotations
 
 import asyncio
+import bisect
 import logging
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -281,7 +282,11 @@ class AsyncHierarchicalRouterMLX:
         cs = self._chunk_size()
         start_chunk = max(0, (current_position - context_window) // cs)
         end_chunk = max(start_chunk, (current_position + context_window) // cs)
-        cands = [cid for cid in range(start_chunk, end_chunk + 1) if self._exists(cid)]
+        if self._bound is not None:
+            ids = self._bound.cold_chunk_ids()
+            cands = ids[bisect.bisect_left(ids, start_chunk):bisect.bisect_right(ids, end_chunk)]
+        else:
+            cands = [cid for cid in range(start_chunk, end_chunk + 1) if self._exists(cid)]
         cands.sort(key=lambda cid: abs(cid * cs - current_position))
         return cands
 
