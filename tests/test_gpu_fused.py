@@ -72,6 +72,8 @@ CASES = [
     (4, 16, 8, 8, 8, 4, 333, 33),       # M=8 with RVQ and sparse, ragged
     (5, 8, 8, 16, 0, 4, 64, 0),         # no hot tier
     (6, 8, 4, 16, 16, 0, 0, 77),        # hot tier only
+    (7, 16, 4, 16, 16, 0, 333, 20),     # score tables without a sparse stage, ragged
+    (8, 8, 8, 16, 16, 4, 200, 16),      # score tables for one query head per KV head (3 padded columns)
 ]
 
 
