@@ -944,6 +944,14 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     }
   };
 
+  // The codes of the first encoded tiles are requested before the hot phase,
+  // so that their memory latency overlaps it.
+  const int seg_begin = max(t_begin, hot_tiles);
+  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
+#pragma unroll
+    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+  }
+
   // Phase 1: exact (hot) tiles, loaded synchronously (a few percent of tiles).
   const int hot_end = min(t_end, hot_tiles);
   for (int tt = t_begin + wave; tt < hot_end; tt += kWaves) {
@@ -976,10 +984,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // With 16 subspaces V^ goes from the gather registers into P.V (through
   // the buffer lane-major only for its sparse stage); with 8 its halves pass
   // through the buffer like K^.
-  const int seg_begin = max(t_begin, hot_tiles);
-  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
-#pragma unroll
-    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+  if (seg_begin < t_end) {
     RawHalf<M, RVQ> ra, rb;
     KHalf ka, kb;  // K halves of the score-table path (the codebook path gathers K into ra, rb)
     if constexpr (LUT) gather_k(kr[0], 0, ka);
