@@ -291,24 +291,28 @@ __device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const WarmBas
   }
 }
 
-// Copy rows [16u, 16u+16) of one exact (hot) tile into the wave's half-tile
-// buffer: rows [off, off+count) of hot[...][D]; rows past count -> 0.  Both
-// loads are issued before either is used (rows past count re-read the last
-// valid row and are zeroed after).
-__device__ __forceinline__ void build_hot_half(uint8_t* __restrict__ lds, int tbase, const TileSrc& src,
-                                               const uint16_t* __restrict__ hot, int lane, int u) {
-  uint4 v[2];
+// Rows [16u, 16u+16) of one exact (hot) tile, this lane's two 16-byte units:
+// rows [off, off+count) of hot[...][D] (rows past count re-read the last valid
+// row and are zeroed when stored).  A tile's four halves (K and V) are loaded
+// together, so that it waits for one memory round trip.
+__device__ __forceinline__ void load_hot_half(uint4 (&v)[2], const TileSrc& src, const uint16_t* __restrict__ hot,
+                                              int lane, int u) {
   const int u16 = lane & 7;  // 16-byte unit of the row
 #pragma unroll
   for (int k2 = 0; k2 < 2; ++k2) {
     const int row = min(16 * u + (lane >> 3) + 8 * k2, src.count - 1);
     v[k2] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + u16 * 8);
   }
+}
+// Store a loaded half into the wave's half-tile buffer (rows past count -> 0).
+__device__ __forceinline__ void store_hot_half(uint8_t* __restrict__ lds, int tbase, const TileSrc& src,
+                                               const uint4 (&v)[2], int lane, int u) {
+  const int u16 = lane & 7;
 #pragma unroll
   for (int k2 = 0; k2 < 2; ++k2) {
     const int r = (lane >> 3) + 8 * k2;  // buffer row
-    if (16 * u + r >= src.count) v[k2] = make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(lds + tbase + r * 128 + ((u16 ^ row_swz(r)) << 4)) = v[k2];
+    const uint4 w = 16 * u + r >= src.count ? make_uint4(0, 0, 0, 0) : v[k2];
+    *reinterpret_cast<uint4*>(lds + tbase + r * 128 + ((u16 ^ row_swz(r)) << 4)) = w;
   }
 }
 
@@ -960,16 +964,22 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     uint32_t pbl[NHG][8], pbh[NHG][8];
     half8_t a[2];
     half8_t av[2];
+    uint4 hk[2][2], hv[2][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      build_hot_half(lds, tbase, src, hotk, lane, u);
+      load_hot_half(hk[u], src, hotk, lane, u);
+      load_hot_half(hv[u], src, hotv, lane, u);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      store_hot_half(lds, tbase, src, hk[u], lane, u);
       score_operands(a);
       scores(a, sc, u);
     }
     softmax(src, sc, pbl, pbh);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      build_hot_half(lds, tbase, src, hotv, lane, u);
+      store_hot_half(lds, tbase, src, hv[u], lane, u);
       pv_operands(av);
       pv(av, pbl, pbh, u);
     }
