@@ -167,6 +167,7 @@ class TiledCodes:
             raise ValueError("pop_front_tiles: more tiles than held")
         self.head += n
         self.len -= n * K.TILE
+        self._segs = {}  # addresses of the old head are no longer asked for
 
     def append(self, pq: torch.Tensor, rvq: Optional[torch.Tensor], sidx: Optional[torch.Tensor],
                sval: Optional[torch.Tensor], pq_cb: Optional[torch.Tensor] = None,
@@ -185,6 +186,7 @@ class TiledCodes:
             if self._backing is None and self.head and 2 * K.round_up(need, K.TILE) <= self.cap:
                 self._move_live(self.t, self.t)  # the live tiles move to the front
                 self.head = 0
+                self._segs = {}
             else:
                 self._alloc(max(need, 2 * self.cap))
         t_base = self.head * K.TILE + self.len
@@ -204,7 +206,7 @@ class TiledCodes:
         keep alive, tokens available from there): a segment without building
         tensor views.  The result depends only on the arrays, ``head`` and
         ``tile_skip``, so it is kept until the arrays are reallocated."""
-        hit = self._segs.get((self.head, tile_skip))
+        hit = self._segs.get((self.head, tile_skip))  # cleared whenever the arrays or head move
         if hit is not None:
             return hit
         f = self.fmt
