@@ -49,7 +49,8 @@ class RFSNBatchedKVCache:
     def _alloc(self, fmt: K.WarmFormat) -> None:
         B, H, D, dev = self.batch, self.H, self.D, self.device
         self.fmt = fmt
-        self.k_layout = 1 if K.score_layout_ok(fmt, self.config.num_heads, H) else 0
+        tables = self.config.fused_score_tables and K.score_layout_ok(fmt, self.config.num_heads, H)
+        self.k_layout = 1 if tables else 0
         self.hot_k = torch.zeros((B, H, self.hot_cap, D), dtype=torch.float16, device=dev)
         self.hot_v = torch.zeros_like(self.hot_k)
         cap = self.warm_cap

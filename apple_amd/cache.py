@@ -488,9 +488,11 @@ class RFSNv10KVCacheMLX:
 
     @property
     def _k_layout(self) -> int:
-        """1 when K codes are score-table rows (subspace format, 16 + 16
-        subspaces, at most 4 query heads of the config per KV head)."""
-        return int(self._subspace and K.score_layout_ok(self._fmt(), self.config.num_heads, self.H))
+        """1 when K codes are score-table rows (``config.fused_score_tables``,
+        subspace format, 16 + 16 subspaces, at most 4 query heads of the
+        config per KV head)."""
+        return int(self._subspace and self.config.fused_score_tables
+                   and K.score_layout_ok(self._fmt(), self.config.num_heads, self.H))
 
     def _tiled_pair(self, **kw) -> Tuple["TiledCodes", "TiledCodes"]:
         """Empty (K, V) tiled code sets; K as score-table rows when the kernel scores K that way."""

@@ -8,7 +8,10 @@ configurations: ``num_kv_heads`` (GQA storage), ``rvq_subspaces`` (a
 subspace RVQ stage instead of the gated full-dimension one), ``sparse_topk``,
 ``tier_policy`` ("arrival" as in cache.py:103-118, or "recency": hot holds the
 newest tokens), ``cold_chunk_tokens`` and ``cold_medium`` ("npz" files as in
-storage.py:113-140, or "pinned" host memory).
+storage.py:113-140, or "pinned" host memory), and ``fused_score_tables``
+(the fused kernel may score K codes through fp16 q . centroid tables; False
+keeps the exact codebook path, whose scores are q . fp16(K^) as in the
+reference).
 """
 
 from __future__ import annotations
@@ -70,6 +73,11 @@ class RFSNConfig:
     tier_policy: str = "arrival"
     cold_chunk_tokens: Optional[int] = None
     cold_medium: str = "npz"
+    # score K through q . centroid tables where the format allows (16 + 16
+    # subspaces, <= 4 query heads per KV head): faster, but each table entry
+    # is rounded to fp16, so scores drift from q . fp16(K^) in proportion to
+    # |q|; False keeps the exact codebook path
+    fused_score_tables: bool = True
 
     def __post_init__(self) -> None:
         expected = self.num_subspaces * self.subspace_dim

@@ -199,7 +199,8 @@ def bench_encode(w, args, dev) -> dict:
                    "vectors_per_step": vectors,
                    "format": f"PQ M{w.pq_subspaces}x{w.pq_centroids}"
                              + (f" + RVQ M{w.rvq_subspaces}x{w.rvq_centroids}" if w.rvq_subspaces else "")
-                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else "")},
+                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else ""),
+                   "k_scoring": "fp16 q.centroid tables" if cache.k_layout == 1 else "codebook K^ rows"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_PEAK_TFLOPS, 5), "traffic": None, "kernel_ms": round(kernel_ms, 5),
                      "kernel_ms_percentiles": pct,
@@ -570,7 +571,8 @@ def main(argv=None) -> int:
                    "kv_heads": w.kv_heads, "head_dim": w.head_dim, "hot_tokens": w.hot, "warm_tokens": w.warm,
                    "format": f"PQ M{w.pq_subspaces}x{w.pq_centroids}"
                              + (f" + RVQ M{w.rvq_subspaces}x{w.rvq_centroids}" if w.rvq_subspaces else "")
-                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else "")},
+                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else ""),
+                   "k_scoring": "fp16 q.centroid tables" if cache.k_layout == 1 else "codebook K^ rows"},
         "hbm_gbs": round(achieved, 1),
         "bytes_per_step": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
