@@ -104,6 +104,39 @@ def test_fused_cache_attention(device, case):
         assert err <= TOL, (causal, qp, err)
 
 
+def test_fused_split_counts(device):
+    """One window of 8,064 tokens for 8 query heads on one KV head, attended
+    with 1, 3, 64 and 200 splits per (sequence, KV head) (at 200, splits
+    past the last tile hold no tokens): every split count gives the oracle's
+    result, repeated calls of one prepared launch give bit-identical outputs,
+    and so does a second launch prepared with the same split count."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    seed, Hq, Hkv, M, Mr, k, nw, nh = 11, 8, 1, 16, 16, 4, 8000, 64
+    g, cfg, keys, values, cbs, kq, vq = _setup(seed, Hq, Hkv, M, Mr, k, nw, nh)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._fused_ok()
+    wk, wv = _oracle_window(keys, values, cbs, Mr, k, nw)
+    q = randn16(g, 2, Hq, 64)
+    qd = T(q, device)
+    ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, False, None)
+    first = {}
+    for splits in (1, 3, 64, 200, 64):
+        out = torch.empty_like(qd)
+        launch = cache.prepare(qd, causal=False, splits=splits, out=out)
+        runs = [H(launch()).copy() for _ in range(3)]
+        torch.cuda.synchronize()
+        for r in runs[1:]:
+            assert np.array_equal(r.view(np.uint16), runs[0].view(np.uint16)), splits
+        err = np.abs(runs[0].astype(np.float32) - ref.astype(np.float32)).max()
+        assert err <= TOL, (splits, err)
+        if splits in first:  # a second prepared launch repeats the same bits
+            assert np.array_equal(runs[0].view(np.uint16), first[splits].view(np.uint16))
+        first[splits] = runs[0]
+    assert np.abs(first[200].astype(np.float32) - first[1].astype(np.float32)).max() <= 2e-3
+
+
 def test_fused_codebook_k_path(device):
     """With ``fused_score_tables=False`` the kernel rebuilds K^ from the
     codebooks for a format the score tables would serve: the same parity."""
