@@ -562,6 +562,16 @@ __device__ __forceinline__ void sparse_addrs(const TileRegs<M, RVQ, KS>& regs, u
   sa[1] = sbase ^ ((regs.sidx >> 7) & 0x7Eu);
 }
 
+// Wave issue priority 0..3 (s_setprio takes an immediate; p is wave-uniform).
+__device__ __forceinline__ void set_prio(int p) {
+  switch (p) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
 template <int M, bool RVQ, int KS, int NHG, bool LUT>
 __global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
 fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
@@ -999,10 +1009,20 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     KHalf ka, kb;  // K halves of the score-table path (the codebook path gathers K into ra, rb)
     if constexpr (LUT) gather_k(kr[0], 0, ka);
     else gather_k(kr[0], 0, ra);
+    // Issue priority falls as a wave works through its tiles.  With equal
+    // priorities a SIMD issues oldest-first: the block's youngest waves then
+    // finish about a third of the loop after its oldest (measured with
+    // per-wave timestamps at batch 32 x 32K), and the CU runs the tail with
+    // fewer waves.  A wave that is ahead yields to the ones behind it.
+    const int my_tiles = max((t_end - seg_begin - wave + kWaves - 1) / kWaves, 1);
+    int done = 0;
+    set_prio(3);
     for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
         if (srcs[s].kind >= 0) {
+          ++done;
+          set_prio(3 - min(3, (4 * done) / my_tiles));
           float4_t sc[NHG][2];
           uint32_t pbl[NHG][8], pbh[NHG][8];
           half8_t a[2];
@@ -1063,6 +1083,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     }
   }
 
+  set_prio(0);
   // ---- combine the waves of this block and write the split partial
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);  // [w][8] m, [w][8] l, [w][8][64] acc
