@@ -593,6 +593,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int b = vid / (splits * p.kv_heads);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  set_prio(3);  // lowered with the wave's progress through its encoded tiles
   const int G = p.q_heads / p.kv_heads;
   const int C = p.fmt.pq_centroids, Cr = RVQ ? p.fmt.rvq_centroids : 0;
   constexpr int d = kD / M;
@@ -1016,7 +1017,6 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     // fewer waves.  A wave that is ahead yields to the ones behind it.
     const int my_tiles = max((t_end - seg_begin - wave + kWaves - 1) / kWaves, 1);
     int done = 0;
-    set_prio(3);
     for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
