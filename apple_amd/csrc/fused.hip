@@ -600,7 +600,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 
   const int tbase = kTilesBase + wave * kBufBytes;  // this wave's half-tile buffer (LDS byte address)
   const cseg segs = (cseg)(p.segments + (int64_t)b * p.max_segments);
-  const int nseg = p.num_segments ? p.num_segments[b] : 0;
+  // a count beyond the table's row would read the next sequence's segments
+  const int nseg = p.num_segments ? min(max(p.num_segments[b], 0), p.max_segments) : 0;
 
   // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [table][e][PQ m | RVQ m][d]
   // (without an RVQ stage the upper slot half holds a second copy of the PQ table)

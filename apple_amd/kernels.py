@@ -428,6 +428,11 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     B, Hq, D = q.shape
     if out is None:
         out = torch.empty_like(q)
+    # the kernel sizes its splits from max_tokens: a row holding more tokens
+    # would lose its last tiles without an error
+    longest = hot_len + max((sum(int(s.len) for s in r) for r in segments.rows), default=0)
+    if longest > max_tokens:
+        raise ValueError(f"a sequence attends {longest} tokens, more than max_tokens = {max_tokens}")
     if table is None:
         table = segments.to_device(q.device)
     seg_t, nseg_t, maxs = table

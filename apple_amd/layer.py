@@ -182,10 +182,41 @@ class RFSNDecoderLayerMLX(torch.nn.Module):
         return hidden + ffn_out
 
 
-def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float = 500000.0) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Rotary tables [S, head_dim] (fp32): angle p * theta^(-2i/D), the two
-    halves repeated, as the rotary module the adapter calls returns them."""
-    inv = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64, device=positions.device) / head_dim)
+# Rotary frequency scaling of the Llama 3.1 / 3.2 checkpoints (their
+# config.json "rope_scaling"; Llama-3.2-1B: factor 32, low / high frequency
+# factors 1 / 4, original context 8192).
+LLAMA3_ROPE_SCALING = {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                       "original_max_position_embeddings": 8192}
+
+
+def rope_inv_freq(head_dim: int, theta: float = 500000.0, rope_scaling: Optional[Dict] = None,
+                  device=None) -> torch.Tensor:
+    """Rotary inverse frequencies [head_dim / 2] (float64): theta^(-2i/D),
+    then, for ``rope_scaling`` of type "llama3", Meta's published Llama 3.1
+    frequency scaling: components whose wavelength 2*pi/f is shorter than
+    original / high_freq_factor keep f, longer than original /
+    low_freq_factor become f / factor, and those between interpolate
+    linearly in original / wavelength between the two."""
+    inv = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64, device=device) / head_dim)
+    if not rope_scaling:
+        return inv
+    kind = rope_scaling.get("rope_type", rope_scaling.get("type"))
+    if kind != "llama3":
+        raise ValueError(f"unsupported rope_scaling type {kind!r} (only 'llama3')")
+    factor = float(rope_scaling["factor"])
+    lo, hi = float(rope_scaling["low_freq_factor"]), float(rope_scaling["high_freq_factor"])
+    orig = float(rope_scaling["original_max_position_embeddings"])
+    ratio = orig * inv / (2 * math.pi)           # periods of each component within the original context
+    smooth = ((ratio - lo) / (hi - lo)).clamp(0.0, 1.0)
+    return inv / factor * (1.0 - smooth) + inv * smooth
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float = 500000.0,
+                 rope_scaling: Optional[Dict] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Rotary tables [S, head_dim] (fp32): angle p * f_i (``rope_inv_freq``),
+    the two halves repeated, as the rotary module the adapter calls returns
+    them (llama32_adapter.py:528-553)."""
+    inv = rope_inv_freq(head_dim, theta, rope_scaling, positions.device)
     ang = positions.to(torch.float64)[:, None] * inv[None, :]
     ang = torch.cat([ang, ang], dim=-1)
     return ang.cos().float(), ang.sin().float()
@@ -203,14 +234,23 @@ class Llama32DecoderLayerMLX(torch.nn.Module):
     ``weights`` (optional) maps ``input_layernorm``, ``post_attention_layernorm``,
     ``q_proj``, ``k_proj``, ``v_proj``, ``o_proj``, ``gate_proj``, ``up_proj``,
     ``down_proj`` to tensors of the Hugging Face layer's shapes (a local state
-    dict); otherwise weights are drawn as an untrained layer's would be."""
+    dict); otherwise weights are drawn as an untrained layer's would be.
+
+    Rotary tables come, in this order, from the call's ``position_embeddings``
+    (cos, sin), from ``rotary_module`` (the reference's argument: called as
+    ``module(hidden, position_ids)``, else ``module(position_ids)``), or from
+    ``rope_cos_sin`` with ``rope_theta`` and ``rope_scaling`` (default: the
+    Llama-3.2 checkpoints' llama3 scaling).  Without ``position_ids`` a call's
+    positions continue after the cached tokens (the reference's adapter
+    defaults to 0 .. seq_len-1 and leaves positions to its caller)."""
 
     WEIGHTS = ("input_layernorm", "post_attention_layernorm", "q_proj", "k_proj", "v_proj", "o_proj",
                "gate_proj", "up_proj", "down_proj")
 
     def __init__(self, config: RFSNConfig, intermediate_size: int, layer_idx: int = 0, rms_norm_eps: float = 1e-5,
                  rope_theta: float = 500000.0, weights: Optional[Dict[str, torch.Tensor]] = None, device=None,
-                 generator: Optional[torch.Generator] = None, quantizer=None):
+                 generator: Optional[torch.Generator] = None, quantizer=None,
+                 rope_scaling: Optional[Dict] = LLAMA3_ROPE_SCALING, rotary_module=None):
         super().__init__()
         if device is None:
             if not torch.cuda.is_available():
@@ -227,6 +267,10 @@ class Llama32DecoderLayerMLX(torch.nn.Module):
         self.scale = config.head_dim ** -0.5
         self.rms_norm_eps = rms_norm_eps
         self.rope_theta = rope_theta
+        self.rope_scaling = dict(rope_scaling) if rope_scaling else None
+        if self.rope_scaling:
+            rope_inv_freq(config.head_dim, rope_theta, self.rope_scaling)  # rejects unsupported types now
+        self.rotary_module = rotary_module
         D, H, Hkv, I = config.hidden_dim, config.num_heads, self.num_kv_heads, intermediate_size
         shapes = {"input_layernorm": (D,), "post_attention_layernorm": (D,), "q_proj": (H * self.head_dim, D),
                   "k_proj": (Hkv * self.head_dim, D), "v_proj": (Hkv * self.head_dim, D),
@@ -264,8 +308,18 @@ class Llama32DecoderLayerMLX(torch.nn.Module):
         if position_ids is None:
             start = self.cache.total_tokens
             position_ids = torch.arange(start, start + seq_len, device=self.device)
-        return rope_cos_sin(torch.as_tensor(position_ids, device=self.device).reshape(-1), self.head_dim,
-                            self.rope_theta)
+        pid = torch.as_tensor(position_ids, device=self.device).reshape(-1)
+        if self.rotary_module is not None:
+            # llama32_adapter.py:535-553: HF rotary modules take (hidden, position_ids)
+            ids = pid.reshape(1, -1)
+            hidden = torch.zeros((1, seq_len, self.hidden_dim), dtype=torch.float32, device=self.device)
+            try:
+                cos, sin = self.rotary_module(hidden, ids)
+            except TypeError:
+                cos, sin = self.rotary_module(ids)
+            return tuple(torch.as_tensor(t, device=self.device).float().reshape(-1, self.head_dim)[-seq_len:]
+                         for t in (cos, sin))
+        return rope_cos_sin(pid, self.head_dim, self.rope_theta, self.rope_scaling)
 
     def _project_qkv(self, h16: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
         """llama32_adapter.py:570-580 without the KV repeat (the cache groups heads)."""

@@ -35,9 +35,10 @@ def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # the GPU raises its clocks over the first tens of milliseconds of work:
-    # 400 warm-up steps (about 70 ms on the default workload) reach the
-    # steady state before the timed region starts
+    # the GPU raises its clocks over the first tens of milliseconds of work;
+    # whatever --warmup asks for, warm-up also runs until WARMUP_FLOOR_MS of
+    # launches have completed (warm_up below), so that the timed region
+    # starts at the steady state
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--workload", default="batched_32x32k")
     ap.add_argument("--splits", type=int, default=0, help="token splits per (sequence, KV head); 0 = auto")
@@ -50,6 +51,32 @@ def parse_args(argv=None):
                     help="only run a plain device copy of MIB MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     return ap.parse_args(argv)
+
+
+# Measured on MI355X (one launch of the batch 32 x 32K decode step takes
+# 0.167 ms once the clocks are up): after 5 warm-up launches the next 40 took
+# 0.21 ms each, after 400 (about 70 ms) 0.167 ms.  The floor is well past that.
+WARMUP_FLOOR_MS = 300.0
+
+
+def warm_up(fn, steps: int, floor_ms: float = WARMUP_FLOOR_MS, batch: int = 64) -> dict:
+    """Run ``fn`` ``steps`` times, then more (in batches, synchronized) until
+    at least ``floor_ms`` of wall-clock time has passed since the first call.
+    Returns the steps actually run and the time they took."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    for _ in range(steps):
+        fn()
+        n += 1
+    torch.cuda.synchronize()
+    while (time.perf_counter() - t0) * 1e3 < floor_ms:
+        for _ in range(batch):
+            fn()
+        n += batch
+        torch.cuda.synchronize()
+    return {"steps_run": n, "ms": round((time.perf_counter() - t0) * 1e3, 1), "floor_ms": floor_ms}
 
 
 def copy_calibration(mib: int, reps: int = 5) -> dict:
@@ -168,9 +195,7 @@ def bench_encode(w, args, dev) -> dict:
         for (x, _), (pcb, rcb) in zip(xs, cbs):
             K.warm_encode(x, fmt, pcb, rcb)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm = warm_up(step, args.warmup)
     steps = max(args.steps, 256)  # one chunk is microseconds: time at least 256 back to back
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     log(f"timing {steps} encode steps")
@@ -191,7 +216,7 @@ def bench_encode(w, args, dev) -> dict:
         "metric": "warm-tier encode vectors/s (PQ+RVQ+top-k, MFMA nearest-centroid search), 1 GPU",
         "value": round(vectors / (kernel_ms * 1e-3), 1),
         "unit": "vectors/s",
-        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_run": warm,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded N(0,1) K/V with per-channel scale U(0.5,2); k-means codebooks)",
@@ -199,8 +224,7 @@ def bench_encode(w, args, dev) -> dict:
                    "vectors_per_step": vectors,
                    "format": f"PQ M{w.pq_subspaces}x{w.pq_centroids}"
                              + (f" + RVQ M{w.rvq_subspaces}x{w.rvq_centroids}" if w.rvq_subspaces else "")
-                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else ""),
-                   "k_scoring": "fp16 q.centroid tables" if cache.k_layout == 1 else "codebook K^ rows"},
+                             + (f" + top-{w.sparse_k} sparse" if w.sparse_k else "")},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_PEAK_TFLOPS, 5), "traffic": None, "kernel_ms": round(kernel_ms, 5),
                      "kernel_ms_percentiles": pct,
@@ -320,8 +344,7 @@ def bench_longctx(w, args, dev) -> dict:
     cache.prefetch_cold_chunks(ids)
     out = torch.empty_like(qd)
     launch = cache.prepare(qd, causal=True, cold_chunks=ids, splits=args.splits, out=out)
-    for _ in range(args.warmup):
-        launch()
+    warm = warm_up(launch, args.warmup)
     log(f"timing {args.steps} steps (cold chunks resident)")
     ms_per_step, kernel_ms = _timed(launch, args.steps)
     pct = step_percentiles(launch, args.steps)
@@ -386,7 +409,7 @@ def bench_longctx(w, args, dev) -> dict:
         "metric": "decode attn tokens/s + HBM GB/s (fused PQ+RVQ dequant-attn), 1 GPU",
         "value": round(w.batch / (ms_per_step * 1e-3), 1),
         "unit": "decode tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "warmup_run": warm,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded N(0,1) K/V with per-channel scale U(0.5,2); k-means codebooks on the warm span)",
@@ -532,9 +555,7 @@ def main(argv=None) -> int:
     cache, q = setup_decode(w, dev)
     out = torch.empty_like(q)
     launch = cache.prepare(q, splits=args.splits, out=out)
-    for _ in range(args.warmup):
-        launch()
-    torch.cuda.synchronize()
+    warm = warm_up(launch, args.warmup)
     # HIP events on the launch stream bracket the timed region; the kernel
     # time per step is their interval over the K back-to-back launches
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -561,6 +582,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_run": warm,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -111,7 +111,7 @@ def test_llama_layer_decode_matches_restatement(device, tmp_path):
     decode step against a float64 restatement around the oracle attention,
     and the prompt path (dense attention over repeated KV heads) against the
     same restatement."""
-    from apple_amd.layer import Llama32DecoderLayerMLX, rope_cos_sin
+    from apple_amd.layer import LLAMA3_ROPE_SCALING, Llama32DecoderLayerMLX, rope_cos_sin
 
     cfg = _ext_config(tmp_path)
     layer = Llama32DecoderLayerMLX(cfg, intermediate_size=1024, device=device, quantizer=_ext_quantizer(cfg, device, 8))
@@ -122,7 +122,8 @@ def test_llama_layer_decode_matches_restatement(device, tmp_path):
     layer.prefill_cache(torch.from_numpy(prompt).to(device))
 
     def rope(x, pos):                      # x [S, h, 64] fp16 -> fp16
-        cos, sin = (t.double().cpu().numpy() for t in rope_cos_sin(torch.tensor(pos), 64))
+        cos, sin = (t.double().cpu().numpy() for t in rope_cos_sin(torch.tensor(pos), 64, 500000.0,
+                                                                      LLAMA3_ROPE_SCALING))
         xf = x.astype(np.float64)
         rot = np.concatenate([-xf[..., 32:], xf[..., :32]], -1)
         return f16(xf * cos[:, None, :] + rot * sin[:, None, :])

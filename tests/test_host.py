@@ -302,3 +302,46 @@ def test_cold_slot_windows_avoid_busy_slots():
     assert w == [(16, nxt)]
     pool3 = list(range(100, 116)) + [-1] * 16      # the other half is free but its last reader still runs
     assert plan_slot_windows(pool3, list(range(16)), set(nxt), nxt, 64, frozenset(range(32))) == [(16, nxt)]
+
+
+def test_llama3_rope_frequencies_closed_form():
+    """Rotary inverse frequencies of the Llama-3.2 layer against closed forms
+    (head_dim 64, theta 500000, llama3 scaling factor 32, low / high
+    frequency factors 1 / 4, original context 8192):
+    * without scaling f_i = theta^(-2i/64) exactly;
+    * components with wavelength 2 pi / f below 8192 / 4 = 2048 tokens keep
+      f_i, those above 8192 tokens become f_i / 32 (for head_dim 64 and
+      theta 500000 the band edges fall between i = 14 | 15 and 17 | 18);
+    * between, the value lies strictly inside (f_i / 32, f_i) and the
+      interpolation weight is affine in 1 / wavelength: it reaches 0 and 1
+      where the bands begin;
+    * factor 1 is the identity; the tables are cos / sin of p * f."""
+    import math
+
+    from apple_amd.layer import LLAMA3_ROPE_SCALING, rope_cos_sin, rope_inv_freq
+
+    base = rope_inv_freq(64, 500000.0).numpy()
+    exact = np.array([500000.0 ** (-(2 * i) / 64) for i in range(32)])
+    assert np.array_equal(base, exact)
+    f = rope_inv_freq(64, 500000.0, LLAMA3_ROPE_SCALING).numpy()
+    wl = 2 * math.pi / base
+    high, low = wl < 2048, wl > 8192
+    assert list(np.nonzero(high)[0]) == list(range(15)) and list(np.nonzero(low)[0]) == list(range(18, 32))
+    assert np.array_equal(f[high], base[high])
+    assert np.allclose(f[low], base[low] / 32, rtol=1e-15, atol=0)
+    mid = ~(high | low)
+    assert mid.sum() == 3
+    assert np.all(f[mid] > base[mid] / 32) and np.all(f[mid] < base[mid])
+    w = (f[mid] - base[mid] / 32) / (base[mid] - base[mid] / 32)      # interpolation weight
+    x = 8192 / wl[mid]                                                  # periods in the original context
+    slope = np.diff(w) / np.diff(x)
+    assert np.allclose(slope, 1 / 3, rtol=1e-9) and np.isclose(w[0] - (x[0] - 1) / 3, 0, atol=1e-12)
+    ident = dict(LLAMA3_ROPE_SCALING, factor=1.0)
+    assert np.allclose(rope_inv_freq(64, 500000.0, ident).numpy(), base, rtol=1e-15, atol=0)
+    pos = torch.tensor([0, 1, 400, 131071])
+    cos, sin = rope_cos_sin(pos, 64, 500000.0, LLAMA3_ROPE_SCALING)
+    ang = pos.numpy()[:, None].astype(np.float64) * np.concatenate([f, f])[None, :]
+    assert np.allclose(cos.numpy(), np.cos(ang), atol=1e-6) and np.allclose(sin.numpy(), np.sin(ang), atol=1e-6)
+    assert np.all(cos.numpy()[0] == 1) and np.all(sin.numpy()[0] == 0)
+    with pytest.raises(ValueError):
+        rope_inv_freq(64, 500000.0, {"rope_type": "yarn", "factor": 4.0})
