@@ -82,6 +82,7 @@ SIGNATURES = {
     "rfsn_fused_splits": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_workspace_bytes": (sz, [C.POINTER(FusedParams)]),
     "rfsn_fused_decode_attention": (i32, [C.POINTER(FusedParams), vp]),
+    "rfsn_fused_decode_attention_noalloc": (i32, [C.POINTER(FusedParams), vp]),
     "rfsn_kmeans_workspace_bytes": (sz, [i32, i32, i32]),
     "rfsn_kmeans_update": (i32, [vp, i64, i32, i64, vp, i32, i32, vp, vp, sz, vp]),
     "rfsn_host_alloc": (i32, [sz, C.POINTER(vp)]),

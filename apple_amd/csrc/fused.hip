@@ -53,6 +53,7 @@
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace rfsn {
@@ -1253,4 +1254,58 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   const bool rvq = f.rvq_subspaces > 0;
   if (f.pq_subspaces == 16) return rvq ? dispatch_ks<16, true>(p, s) : dispatch_ks<16, false>(p, s);
   return rvq ? dispatch_ks<8, true>(p, s) : dispatch_ks<8, false>(p, s);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+// Split partials of rfsn_fused_decode_attention_noalloc live in this
+// file-scope device array instead of a caller workspace.  Each device that
+// runs the library holds its own copy (RFSN_FUSED_SCRATCH_BYTES) until the
+// process ends.  Host code never passes `scratch` itself to a kernel (in host
+// code the name is a host-side stand-in): the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[RFSN_FUSED_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(RFSN_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(RFSN_ERR_UNSUPPORTED, "fused_noalloc: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(RFSN_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return RFSN_OK;
+}
+}  // namespace
+
+extern "C" int rfsn_fused_decode_attention_noalloc(const rfsn_fused_params* p, void* stream) {
+  RFSN_REQUIRE(p != nullptr, "fused_noalloc: null params");
+  rfsn_fused_params q = *p;
+  q.workspace = nullptr;
+  q.workspace_bytes = 0;
+  const size_t need = rfsn_fused_workspace_bytes(&q);
+  if (need > (size_t)RFSN_FUSED_SCRATCH_BYTES)
+    return fail(RFSN_ERR_INVALID, "fused_noalloc: the call's split partials need " + std::to_string(need) +
+                                      " bytes, more than the " + std::to_string((size_t)RFSN_FUSED_SCRATCH_BYTES) +
+                                      "-byte scratch (fewer splits, query heads or sequences per call)");
+  if (need > 0) {
+    void* ptr = nullptr;
+    const int st = scratch_address(&ptr);
+    if (st) return st;
+    // every partial slot is written by the launch before the merge reads it:
+    // nothing in the scratch has to start at zero
+    q.workspace = ptr;
+    q.workspace_bytes = (size_t)RFSN_FUSED_SCRATCH_BYTES;
+  }
+  return rfsn_fused_decode_attention(&q, stream);
 }

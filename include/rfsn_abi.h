@@ -10,7 +10,8 @@
  *    (HBM) pointers; nothing here allocates device memory: scratch space is
  *    passed in as a workspace sized by the matching *_workspace_bytes().
  *  - Every kernel is asynchronous on the caller's hipStream_t (passed as
- *    void*; NULL = the legacy default stream).  No global mutable state.
+ *    void*; NULL = the legacy default stream).  No global mutable state,
+ *    except the per-GPU scratch array of rfsn_fused_decode_attention_noalloc.
  *  - fp16 tensors are passed as void* and hold IEEE binary16 bit patterns.
  *  - Shapes use the reference's names: N vectors, D = head_dim,
  *    M PQ subspaces of d = D/M dims with C centroids, M_r RVQ subspaces of
@@ -266,6 +267,20 @@ typedef struct rfsn_fused_params {
 int32_t rfsn_fused_splits(const rfsn_fused_params* p);
 size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);
 int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
+
+/* Allocation-free variant of rfsn_fused_decode_attention.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It ignores p->workspace / p->workspace_bytes and keeps the
+ * split partials in a library-owned device array of RFSN_FUSED_SCRATCH_BYTES
+ * per GPU (held until the process ends); it calls no hipMalloc or hipFree.
+ * A call whose partials (rfsn_fused_workspace_bytes with the same params)
+ * exceed that size returns RFSN_ERR_INVALID without launching.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race, and partial-mode calls of one window must
+ * not interleave with other calls of this entry point. */
+#define RFSN_FUSED_SCRATCH_BYTES (4u << 20)
+int rfsn_fused_decode_attention_noalloc(const rfsn_fused_params* p, void* stream);
 
 /* ---------------------------------------------------------------- k-means
  * One Lloyd update of PQ codebooks (rfsn_v10_mlx_ane_complete.py:197-207):

@@ -99,3 +99,21 @@ def test_version_and_validation_errors(lib):
     assert lib.rfsn_fused_workspace_bytes(None) == 0
     with pytest.raises(ValueError):
         _lib.check(-1, "probe")
+
+
+def test_noalloc_rejects_oversized_partials_on_the_host(lib):
+    """The allocation-free entry point refuses a call whose split partials
+    exceed its fixed scratch before touching the device (no launch, no
+    symbol lookup), and reports the size it would have needed."""
+    from apple_amd import _lib
+
+    p = _lib.FusedParams()
+    p.fmt = _lib.Format(64, 16, 256, 16, 256, 4)
+    p.batch, p.q_heads, p.kv_heads = 64, 32, 8
+    p.hot_len, p.max_tokens, p.max_segments, p.splits = 0, 1 << 20, 1, 100
+    need = lib.rfsn_fused_workspace_bytes(ctypes.byref(p))
+    assert need == 64 * 32 * 100 * 66 * 4 > (4 << 20)
+    assert lib.rfsn_fused_decode_attention_noalloc(ctypes.byref(p), None) == -1
+    msg = lib.rfsn_last_error()
+    assert str(need).encode() in msg and b"scratch" in msg
+    assert lib.rfsn_fused_decode_attention_noalloc(None, None) == -1
