@@ -604,6 +604,68 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // a count beyond the table's row would read the next sequence's segments
   const int nseg = p.num_segments ? min(max(p.num_segments[b], 0), p.max_segments) : 0;
 
+  const int g = lane >> 4;   // k-group of the 16x16 MFMA operands
+  const int n = lane & 15;   // column (B, D) / row (A)
+  // score-table lanes: row n holds token row tokr of each half (tokens
+  // t = 16u + tokr, so (t >> 2) & 3 = n & 3 and t & 1 = (n >> 2) & 1), k-group
+  // g the code block beta (4 subspaces of both stages), chosen so that the 8
+  // lanes of a block in one LDS pass differ in (n & 3, (n >> 2) & 1) and read
+  // 8 distinct slots
+  const int tokr = 4 * (n & 3) + (n >> 2);
+  const int beta = (g + 2 * (n >> 3)) & 3;
+  const uint32_t blk8 = 8u * (uint32_t)beta;
+
+  const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
+  WarmBase w0 = {};
+  if (nseg > 0) w0 = warm_base<M, RVQ, KS>(segs, h);
+  const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
+  int total_tiles = hot_tiles + seg0_tiles;
+  total_tiles += tail_tiles(segs, nseg);
+  const int t_begin = split * tiles_per_split;
+  const int t_end = min(total_tiles, t_begin + tiles_per_split);
+  const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
+  const uint16_t* hotv = (const uint16_t*)p.hot_v + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
+
+
+  using Regs = TileRegs<M, RVQ, KS>;
+  using KRegs = typename std::conditional<LUT, LutRegs, Regs>::type;
+  // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves.  Only
+  // encoded tiles go through slots (tt >= hot_tiles); a slot past the split
+  // is idle and re-reads the split's last tile, which is encoded.
+  TileSrc srcs[kDepth];
+  KRegs kr[kDepth];
+  Regs vr[kDepth];
+  auto load_k = [&](KRegs& rk, const WarmBase& w, int off, int count) __attribute__((always_inline)) {
+    if constexpr (LUT) load_tile_lut<KS>(rk, w, off, tokr, blk8, g);
+    else load_tile<M, RVQ, KS>(rk, w, 0, off, count, lane);
+  };
+  auto fetch = [&](TileSrc& s, KRegs& rk, Regs& rv, int tt) {
+    const int r = min(tt, t_end - 1) - hot_tiles;
+    if (r < seg0_tiles) {  // uniform; segment 0 from registers
+      s.kind = 1;
+      s.seg = 0;
+      s.off = r * kTile;
+      s.count = min(kTile, w0.len - s.off);
+      s.pos0 = w0.pos0 + s.off;
+      load_k(rk, w0, s.off, s.count);
+      load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
+    } else {
+      s = walk_segments(segs, nseg, r - seg0_tiles);
+      const WarmBase w = warm_base<M, RVQ, KS>(segs + s.seg, h);
+      load_k(rk, w, s.off, s.count);
+      load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
+    }
+    if (tt >= t_end) s.kind = -1;
+  };
+  // Every wave requests the codes of its first encoded tiles before the block
+  // stages its codebooks and builds its tables: HBM streams while the set-up
+  // runs.
+  const int seg_begin = max(t_begin, hot_tiles);
+  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
+#pragma unroll
+    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+  }
+
   // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [table][e][PQ m | RVQ m][d]
   // (without an RVQ stage the upper slot half holds a second copy of the PQ table)
   {
@@ -690,8 +752,6 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   }
 
   // ---- lane constants
-  const int g = lane >> 4;   // k-group of the 16x16 MFMA operands
-  const int n = lane & 15;   // column (B, D) / row (A)
   // gather lane (jg, mg) and its codebook slot; store offsets for the row
   // patterns of consecutive gathers
   const int jg = lane / M, mg = lane % M;
@@ -729,19 +789,21 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
     for (int c = 0; c < 2; ++c) raddr[c] = tbase + (4 * (n & 3) + (n >> 2)) * 128 + (((4 * c + g) ^ f) << 4);
   }
-  // B operand of P.V: the lane's fp16 probability at coordinate n & 3 of its k-group
+  // B operands of P.V: the probabilities X = (p_t0, p_t1) of a token pair,
+  // packed in one dword, go to coordinate ep = n & 3 of each token's half of
+  // the lane's k-group: dwords 0 (t0) and 2 (t1) for ep = 0, 1, dwords 1 and
+  // 3 for ep = 2, 3, in the low half for even ep and the high half for odd.
   const int ep = n & 3;
-  const uint32_t sel_lo = ep == 0 ? 0x0C0C0100u : (ep == 1 ? 0x01000C0Cu : 0x0C0C0C0Cu);
-  const uint32_t sel_hi = ep == 2 ? 0x0C0C0100u : (ep == 3 ? 0x01000C0Cu : 0x0C0C0C0Cu);
-  // score-table lanes: row n holds token row tokr of each half (tokens
-  // t = 16u + tokr, so (t >> 2) & 3 = n & 3 and t & 1 = (n >> 2) & 1), k-group
-  // g the code block beta (4 subspaces of both stages), chosen so that the 8
-  // lanes of a block in one LDS pass differ in (n & 3, (n >> 2) & 1) and read
-  // 8 distinct slots
-  const int tokr = 4 * (n & 3) + (n >> 2);
-  const int beta = (g + 2 * (n >> 3)) & 3;
+  uint32_t psel[4];
+  {
+    const uint32_t s0 = (ep & 1) ? 0x01000C0Cu : 0x0C0C0100u, s1 = (ep & 1) ? 0x03020C0Cu : 0x0C0C0302u;
+    const bool lo = ep < 2;
+    psel[0] = lo ? s0 : 0x0C0C0C0Cu;
+    psel[1] = lo ? 0x0C0C0C0Cu : s0;
+    psel[2] = lo ? s1 : 0x0C0C0C0Cu;
+    psel[3] = lo ? 0x0C0C0C0Cu : s1;
+  }
   const bool todd = ((n >> 2) & 1) != 0;
-  const uint32_t blk8 = 8u * (uint32_t)beta;
   uint32_t lca = 0, lcb = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -759,7 +821,8 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   half8_t qb[NHG][2];
   float bias[NHG], bias_m[NHG], m_run[NHG];
   int qpl[NHG];
-  float4_t acc[NHG], lsum[NHG];
+  float4_t acc[NHG];
+  float lsum[NHG];  // this lane's share of the softmax denominator (its tokens, its head)
 #pragma unroll
   for (int hg = 0; hg < NHG; ++hg) {
     const int hh = hg * 4 + (n >> 2);
@@ -775,7 +838,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     m_run[hg] = -__builtin_inff();
     qpl[hg] = (p.causal && p.qpos && valid) ? p.qpos[(int64_t)b * p.q_heads + h * G + hh] : 0x7fffffff;
     acc[hg] = float4_t{0.f, 0.f, 0.f, 0.f};
-    lsum[hg] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lsum[hg] = 0.f;
   }
   // smallest query position of this KV head's query heads (uniform)
   int qmin = 0x7fffffff;
@@ -794,52 +857,10 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     qc0 = qv[0] | (qv[1] << 16);
     qc1 = qv[2] | (qv[3] << 16);
   }
-  const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
-                        (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
-  const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
-  WarmBase w0 = {};
-  if (nseg > 0) w0 = warm_base<M, RVQ, KS>(segs, h);
-  const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
-  int total_tiles = hot_tiles + seg0_tiles;
-  total_tiles += tail_tiles(segs, nseg);
-  const int t_begin = split * tiles_per_split;
-  const int t_end = min(total_tiles, t_begin + tiles_per_split);
-  const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
-  const uint16_t* hotv = (const uint16_t*)p.hot_v + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
 
   __syncthreads();
 
-  using Regs = TileRegs<M, RVQ, KS>;
-  using KRegs = typename std::conditional<LUT, LutRegs, Regs>::type;
-  // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves.  Only
-  // encoded tiles go through slots (tt >= hot_tiles); a slot past the split
-  // is idle and re-reads the split's last tile, which is encoded.
-  TileSrc srcs[kDepth];
-  KRegs kr[kDepth];
-  Regs vr[kDepth];
-  auto load_k = [&](KRegs& rk, const WarmBase& w, int off, int count) __attribute__((always_inline)) {
-    if constexpr (LUT) load_tile_lut<KS>(rk, w, off, tokr, blk8, g);
-    else load_tile<M, RVQ, KS>(rk, w, 0, off, count, lane);
-  };
-  auto fetch = [&](TileSrc& s, KRegs& rk, Regs& rv, int tt) {
-    const int r = min(tt, t_end - 1) - hot_tiles;
-    if (r < seg0_tiles) {  // uniform; segment 0 from registers
-      s.kind = 1;
-      s.seg = 0;
-      s.off = r * kTile;
-      s.count = min(kTile, w0.len - s.off);
-      s.pos0 = w0.pos0 + s.off;
-      load_k(rk, w0, s.off, s.count);
-      load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
-    } else {
-      s = walk_segments(segs, nseg, r - seg0_tiles);
-      const WarmBase w = warm_base<M, RVQ, KS>(segs + s.seg, h);
-      load_k(rk, w, s.off, s.count);
-      load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
-    }
-    if (tt >= t_end) s.kind = -1;
-  };
   // score operands of the half in the buffer, then the scores: lane (g, n),
   // register i of half u = token 16u + 4i + g
   // Operand reads of data other lanes stored: a compiler barrier first, so
@@ -871,8 +892,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   };
   // online softmax in base 2; produces the B operands of P.V (probability at
   // coordinate n & 3 of the lane's k-group)
-  auto softmax = [&](const TileSrc& src, const float4_t (&sc)[NHG][2], uint32_t (&pbl)[NHG][8],
-                     uint32_t (&pbh)[NHG][8]) {
+  auto softmax = [&](const TileSrc& src, const float4_t (&sc)[NHG][2], uint32_t (&pb)[NHG][4][4]) {
     // uniform: nothing masked (a segment may start before the window, with
     // negative positions for the tokens to skip)
     const bool full = src.count == kTile && src.pos0 >= 0 && src.pos0 + kTile - 1 <= qmin;
@@ -925,12 +945,16 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
         for (int r = 0; r < 8; ++r) arg[r] = sv[r] + dm;
       }
+      // score registers 2q, 2q + 1 are the two tokens of P.V operand q; the
+      // denominator sums the same fp16 probabilities that P.V weights
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(arg[r]);
-        const uint32_t h16 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)pv);
-        pbl[hg][r] = __builtin_amdgcn_perm(0u, h16, sel_lo);
-        pbh[hg][r] = __builtin_amdgcn_perm(0u, h16, sel_hi);
+      for (int q = 0; q < 4; ++q) {
+        const half2_t ph = {(_Float16)__builtin_amdgcn_exp2f(arg[2 * q]),
+                            (_Float16)__builtin_amdgcn_exp2f(arg[2 * q + 1])};  // v_cvt_pk_f16_f32
+        const uint32_t x = __builtin_bit_cast(uint32_t, ph);
+        lsum[hg] = __builtin_amdgcn_fdot2(ph, half2_t{(_Float16)1.0f, (_Float16)1.0f}, lsum[hg], false);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pb[hg][q][k] = __builtin_amdgcn_perm(x, x, psel[k]);
       }
     }
   };
@@ -948,33 +972,24 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       av[j] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
     }
   };
-  auto pv = [&](const half8_t (&av)[2], const uint32_t (&pbl)[NHG][8], const uint32_t (&pbh)[NHG][8], int u) {
+  auto pv = [&](const half8_t (&av)[2], const uint32_t (&pb)[NHG][4][4], int u) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int hg = 0; hg < NHG; ++hg) {
-        const int r = 4 * u + 2 * j;
-        const half8_t bw = __builtin_bit_cast(half8_t, make_uint4(pbl[hg][r], pbh[hg][r], pbl[hg][r + 1], pbh[hg][r + 1]));
+        const uint32_t* b4 = pb[hg][2 * u + j];
+        const half8_t bw = __builtin_bit_cast(half8_t, make_uint4(b4[0], b4[1], b4[2], b4[3]));
         acc[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j], bw, acc[hg], 0, 0, 0);
-        lsum[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, bw, lsum[hg], 0, 0, 0);
       }
     }
   };
-
-  // The codes of the first encoded tiles are requested before the hot phase,
-  // so that their memory latency overlaps it.
-  const int seg_begin = max(t_begin, hot_tiles);
-  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
-#pragma unroll
-    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
-  }
 
   // Phase 1: exact (hot) tiles, loaded synchronously (a few percent of tiles).
   const int hot_end = min(t_end, hot_tiles);
   for (int tt = t_begin + wave; tt < hot_end; tt += kWaves) {
     const TileSrc src = hot_tile(p, tt);
     float4_t sc[NHG][2];
-    uint32_t pbl[NHG][8], pbh[NHG][8];
+    uint32_t pb[NHG][4][4];
     half8_t a[2];
     half8_t av[2];
     uint4 hk[2][2], hv[2][2];
@@ -989,12 +1004,12 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       score_operands(a);
       scores(a, sc, u);
     }
-    softmax(src, sc, pbl, pbh);
+    softmax(src, sc, pb);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       store_hot_half(lds, tbase, src, hv[u], lane, u);
       pv_operands(av);
-      pv(av, pbl, pbh, u);
+      pv(av, pb, u);
     }
   }
 
@@ -1017,16 +1032,23 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     // finish about a third of the loop after its oldest (measured with
     // per-wave timestamps at batch 32 x 32K), and the CU runs the tail with
     // fewer waves.  A wave that is ahead yields to the ones behind it.
+    // Priority 3 - stage, stage = floor(4 * done / my_tiles) capped at 3; it
+    // changes at most three times, so a tile only compares done with the
+    // count at which the next stage begins.
     const int my_tiles = max((t_end - seg_begin - wave + kWaves - 1) / kWaves, 1);
-    int done = 0;
+    int done = 0, stage = 0;
+    int next_at = (my_tiles + 3) >> 2;  // ceil(my_tiles / 4)
     for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
         if (srcs[s].kind >= 0) {
-          ++done;
-          set_prio(3 - min(3, (4 * done) / my_tiles));
+          if (++done >= next_at) {  // uniform
+            while (stage < 3 && 4 * done >= (stage + 1) * my_tiles) ++stage;
+            set_prio(3 - stage);
+            next_at = stage < 3 ? ((stage + 1) * my_tiles + 3) >> 2 : 0x7fffffff;
+          }
           float4_t sc[NHG][2];
-          uint32_t pbl[NHG][8], pbh[NHG][8];
+          uint32_t pb[NHG][4][4];
           half8_t a[2];
           half8_t av[2];
           uint32_t sav[2] = {0, 0};
@@ -1049,11 +1071,11 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
             gather_half<M, RVQ, KS>(lds, vr[s], 0, lc1_v, lc2_v, odd, ra);
             scores(a, sc, 1);
           }
-          softmax(srcs[s], sc, pbl, pbh);
+          softmax(srcs[s], sc, pb);
           if constexpr (M == 16 && KS == 0) {
             direct_half<RVQ>(ra, av);
             gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
-            pv(av, pbl, pbh, 0);
+            pv(av, pb, 0);
             direct_half<RVQ>(rb, av);
           } else if constexpr (M == 16) {
             uint32_t svl[2];
@@ -1063,7 +1085,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
             sparse_stage<M, RVQ, KS>(lds, vr[s], 0, svl, shalf);
             load_lanes(lds, tbase, lane, av);
             gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
-            pv(av, pbl, pbh, 0);
+            pv(av, pb, 0);
             direct_half<RVQ>(rb, av);
             store_lanes(lds, tbase, lane, av);
             sparse_stage<M, RVQ, KS>(lds, vr[s], 1, svl, shalf);
@@ -1072,13 +1094,13 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
             store_half<M, RVQ, KS>(lds, vr[s], ra, 0, waddr, sav, shalf);
             pv_operands(av);
             gather_half<M, RVQ, KS>(lds, vr[s], 1, lc1_v, lc2_v, odd, rb);
-            pv(av, pbl, pbh, 0);
+            pv(av, pb, 0);
             store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
             pv_operands(av);
           }
           if constexpr (LUT) gather_k(kr[(s + 1) % kDepth], 0, ka);  // next tile
           else gather_k(kr[(s + 1) % kDepth], 0, ra);
-          pv(av, pbl, pbh, 1);
+          pv(av, pb, 1);
         }
         fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
       }
@@ -1095,9 +1117,17 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
 #pragma unroll
   for (int hg = 0; hg < NHG; ++hg) {
     const int hh = hg * 4 + (n >> 2);
+    // the head's denominator: the lanes of its 4 k-groups (l, l ^ 16, l ^ 32, l ^ 48)
+    float ls = lsum[hg];
+    {
+      const auto r16 = __builtin_amdgcn_permlane16_swap(fbits(ls), fbits(ls), false, false);
+      ls = bitsf(r16[0]) + bitsf(r16[1]);
+      const auto r32 = __builtin_amdgcn_permlane32_swap(fbits(ls), fbits(ls), false, false);
+      ls = bitsf(r32[0]) + bitsf(r32[1]);
+    }
     if (g == 0 && ep == 0) {
       red_m[wave * 8 + hh] = m_run[hg];
-      red_l[wave * 8 + hh] = lsum[hg][0];
+      red_l[wave * 8 + hh] = ls;
     }
     // D rows 4g + r = subspace m, column n = (head, coordinate ep): dim 4m + ep
 #pragma unroll
