@@ -53,7 +53,8 @@ class FusedParams(C.Structure):
                 ("k_pq_cb", vp), ("k_rvq_cb", vp), ("v_pq_cb", vp), ("v_rvq_cb", vp),
                 ("pq_cb_stride", i64), ("rvq_cb_stride", i64),
                 ("max_tokens", i32), ("splits", i32), ("workspace", vp), ("workspace_bytes", sz),
-                ("part_base", i32), ("part_slots", i32), ("merge", i32), ("k_layout", i32)]
+                ("part_base", i32), ("part_slots", i32), ("merge", i32), ("k_layout", i32),
+                ("guard", vp), ("drift", vp), ("guard_tol", f32)]
 
 
 class Copy(C.Structure):
@@ -115,7 +116,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 3:
+    if lib.rfsn_abi_version() != 4:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

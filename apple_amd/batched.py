@@ -44,6 +44,9 @@ class RFSNBatchedKVCache:
         self.num_warm = [0] * batch
         self._table = None
         self._ws = None
+        self._guard: Optional[torch.Tensor] = None  # [B, 65] drift-guard rows (score tables)
+        self._vmax = [0.0] * batch                  # per sequence: max |V| of its values and V codebooks
+        self.last_drift: Optional[torch.Tensor] = None
         self.quantizers: List[Optional[Tuple[HybridQuantizerMLX, HybridQuantizerMLX]]] = [None] * batch
 
     def _alloc(self, fmt: K.WarmFormat) -> None:
@@ -51,6 +54,7 @@ class RFSNBatchedKVCache:
         self.fmt = fmt
         tables = self.config.fused_score_tables and K.score_layout_ok(fmt, self.config.num_heads, H)
         self.k_layout = 1 if tables else 0
+        self.guarded = bool(tables) and self.config.score_table_tolerance is not None
         self.hot_k = torch.zeros((B, H, self.hot_cap, D), dtype=torch.float16, device=dev)
         self.hot_v = torch.zeros_like(self.hot_k)
         cap = self.warm_cap
@@ -64,8 +68,15 @@ class RFSNBatchedKVCache:
             c["sparse_val"] = (torch.zeros((B, H, cap, fmt.sparse_k), dtype=torch.float16, device=dev)
                                if fmt.sparse_k else None)
             # corrected coordinates fp16(K[idx] + val): the sparse values the fused kernel streams
-            # (score deltas for K in the score-table layout, with the indices in that layout)
-            c["sparse_fold"] = torch.zeros_like(c["sparse_val"]) if fmt.sparse_k else None
+            # (score deltas for K in the score-table layout, with the indices in that layout; under
+            # the drift guard a second plane [B, 2, H, cap, k] holds the corrected coordinates in
+            # the same positions for the exact pass)
+            c["sparse_fold"], c["sparse_cc"] = None, None
+            if fmt.sparse_k and kv == "k" and self.guarded:
+                planes = torch.zeros((B, 2, H, cap, fmt.sparse_k), dtype=torch.float16, device=dev)
+                c["sparse_fold"], c["sparse_cc"] = planes[:, 0], planes[:, 1]
+            elif fmt.sparse_k:
+                c["sparse_fold"] = torch.zeros_like(c["sparse_val"])
             c["sparse_idx_s"] = (torch.zeros_like(c["sparse_idx"])
                                  if fmt.sparse_k and kv == "k" and self.k_layout == 1 else None)
             self.codes[kv] = c
@@ -122,6 +133,11 @@ class RFSNBatchedKVCache:
                        "sparse_idx": c["sparse_idx_s"][b] if fmt.sparse_k else None,
                        "sparse_val": c["sparse_fold"][b] if fmt.sparse_k else None}
                 K.pack_score_codes(view3(out["pq"]), view3(out["rvq"]), view3(out.get("sparse_idx")), fold, dst, 0)
+                if c["sparse_cc"] is not None:
+                    cc = K.sparse_fold(fmt, out["pq"], qz.pq.codebooks, out["rvq"], qz.rvq.codebooks,
+                                       out["sparse_idx"], out["sparse_val"]).view(self.H, nw, -1)
+                    K.pack_score_codes(view3(out["pq"]), view3(out["rvq"]), view3(out["sparse_idx"]), cc,
+                                       dict(dst, sparse_val=c["sparse_cc"][b]), 0)
             else:
                 K.pack_codes(view3(out["pq"]), c["pq"][b], 0)
                 if fmt.rvq_subspaces:
@@ -132,6 +148,11 @@ class RFSNBatchedKVCache:
         self.num_warm[b] = nw
         self.quantizers[b] = (key_quantizer, value_quantizer)
         self._table = None
+        if self.guarded:
+            vp, vr = value_quantizer.pq.codebooks.float(), value_quantizer.rvq.codebooks.float()
+            vcb = (vp.abs().amax(-2) + vr.abs().amax(-2)).amax()
+            self._vmax[b] = float(torch.maximum(values.abs().amax().float(), vcb))
+            self._guard = None
 
     def _segment_table(self):
         if self._table is None:
@@ -173,14 +194,22 @@ class RFSNBatchedKVCache:
                     qpos = qpos[:, None].expand(self.batch, q.shape[1]).contiguous()
         if self._ws is None:
             self._ws = torch.empty(4 << 20, dtype=torch.uint8, device=self.device)
-        return K.fused_attention(
+        guard = {}
+        if self.guarded:
+            if self._guard is None:
+                vmax = torch.tensor(self._vmax, dtype=torch.float32, device=self.device)
+                self._guard = K.score_guard(self.cb["k_pq"], self.cb["k_rvq"], vmax).contiguous()
+            guard = dict(guard=self._guard, guard_tol=float(self.config.score_table_tolerance))
+        fl = K.fused_attention(
             q, f, kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos, hot_k=self.hot_k,
             hot_v=self.hot_v, hot_len=self.num_hot[0], hot_pos0=self.num_warm[0],
             hot_seq_stride=self.H * self.hot_cap * self.D, segments=table, table=dev_table,
             k_pq_cb=self.cb["k_pq"], v_pq_cb=self.cb["v_pq"], k_rvq_cb=self.cb.get("k_rvq"),
             v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True,
             max_tokens=max(h + w for h, w in zip(self.num_hot, self.num_warm)), splits=splits,
-            workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=launch, k_layout=self.k_layout)
+            workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=False, k_layout=self.k_layout, **guard)
+        self.last_drift = fl.drift
+        return fl() if launch else fl
 
     def sequence_window(self, b: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Materialized (keys, values) [W, Hkv, D] of sequence b, warm then hot."""

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import ctypes as C
 import logging
+import math
 from collections import OrderedDict
 from pathlib import Path
 from typing import Any, Dict, List, Optional, Sequence, Tuple, Union
@@ -80,12 +81,17 @@ class TiledCodes:
     and ``sparse_val`` holds the score deltas."""
 
     def __init__(self, fmt: K.WarmFormat, heads: int, device, pinned: bool = False, cap: int = 0,
-                 backing: Optional[torch.Tensor] = None, score_rows: bool = False):
+                 backing: Optional[torch.Tensor] = None, score_rows: bool = False, exact_plane: bool = False):
         """``backing``: a uint8 buffer of at least ``nbytes(fmt, heads, cap)``
         that holds every array (fixed capacity), so that one copy moves the
-        whole set; otherwise each array is its own growable allocation."""
+        whole set; otherwise each array is its own growable allocation.
+        ``exact_plane`` (with ``score_rows``): the sparse values are two
+        planes [2, H, cap, k], the score deltas (``sparse_val``) and then the
+        corrected coordinates (``sparse_cc``) in the same positions, which the
+        fused kernel's exact pass reads when its drift guard fires."""
         self.fmt, self.heads, self.device, self.pinned = fmt, heads, device, pinned
         self.score_rows = score_rows
+        self.exact_plane = bool(exact_plane and score_rows and fmt.sparse_k)
         self.cap = 0
         self.len = 0
         self.head = 0  # tiles before the oldest live token (pop_front_tiles)
@@ -96,21 +102,22 @@ class TiledCodes:
         self._alloc(cap)
 
     @staticmethod
-    def _arrays(fmt: K.WarmFormat, heads: int, cap: int):
+    def _arrays(fmt: K.WarmFormat, heads: int, cap: int, plane: bool = False):
         f, H = fmt, heads
+        sv = (2, H, cap, f.sparse_k) if plane else (H, cap, f.sparse_k)
         return {"pq": ((H, cap * f.pq_subspaces), torch.uint8),
                 "rvq": ((H, cap * f.rvq_subspaces), torch.uint8) if f.rvq_subspaces else None,
                 "sparse_idx": ((H, cap, f.sparse_k), torch.uint8) if f.sparse_k else None,
-                "sparse_val": ((H, cap, f.sparse_k), torch.float16) if f.sparse_k else None}
+                "sparse_val": (sv, torch.float16) if f.sparse_k else None}
 
     @staticmethod
-    def nbytes(fmt: K.WarmFormat, heads: int, cap: int) -> int:
+    def nbytes(fmt: K.WarmFormat, heads: int, cap: int, plane: bool = False) -> int:
         """Bytes of one backing buffer: every array, each at a 256-byte boundary."""
         total = 0
-        for spec in TiledCodes._arrays(fmt, heads, K.round_up(max(cap, 0), K.TILE)).values():
+        for spec in TiledCodes._arrays(fmt, heads, K.round_up(max(cap, 0), K.TILE), plane).values():
             if spec is not None:
                 shape, dtype = spec
-                n = shape[0] * shape[1] * (shape[2] if len(shape) > 2 else 1) * (2 if dtype == torch.float16 else 1)
+                n = math.prod(shape) * (2 if dtype == torch.float16 else 1)
                 total += K.round_up(n, 256)
         return total
 
@@ -134,10 +141,13 @@ class TiledCodes:
         if self._backing is not None:
             if self.t:
                 raise ValueError("a TiledCodes set in one backing buffer has a fixed capacity")
-            if self._backing.numel() < TiledCodes.nbytes(self.fmt, self.heads, cap):
+            if self._backing.numel() < TiledCodes.nbytes(self.fmt, self.heads, cap, self.exact_plane):
                 raise ValueError("backing buffer too small for the tiled arrays")
         new = {key: (None if spec is None else self._new(*spec))
-               for key, spec in TiledCodes._arrays(self.fmt, self.heads, cap).items()}
+               for key, spec in TiledCodes._arrays(self.fmt, self.heads, cap, self.exact_plane).items()}
+        if self.exact_plane:
+            planes = new["sparse_val"]
+            new["sparse_val"], new["sparse_cc"] = planes[0], planes[1]
         if self.t and self.cap:
             self._move_live(self.t, new)
         self.t, self.cap, self.head = new, cap, 0
@@ -176,9 +186,12 @@ class TiledCodes:
         residuals ``sval`` are folded into corrected coordinates with the
         stream's codebooks."""
         H, T, _ = pq.shape
+        cc = None
         if self.fmt.sparse_k and T:
             f = self.fmt
             flat = lambda t: None if t is None else t.reshape(H * T, -1)
+            if self.exact_plane:
+                cc = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval)).view(H, T, -1)
             sval = K.sparse_fold(f, flat(pq), pq_cb, flat(rvq), rvq_cb, flat(sidx), flat(sval),
                                  delta=self.score_rows).view(H, T, -1)
         need = self.len + T
@@ -192,6 +205,8 @@ class TiledCodes:
         t_base = self.head * K.TILE + self.len
         if self.score_rows:
             K.pack_score_codes(pq, rvq, sidx, sval, self.t, t_base)
+            if cc is not None:
+                K.pack_score_codes(pq, rvq, sidx, cc, dict(self.t, sparse_val=self.t["sparse_cc"]), t_base)
         else:
             K.pack_codes(pq, self.t["pq"], t_base)
             if self.fmt.rvq_subspaces:
@@ -227,6 +242,8 @@ class TiledCodes:
         out["rvq"] = self.t["rvq"][:, o * f.rvq_subspaces:] if f.rvq_subspaces else None
         out["sparse_idx"] = self.t["sparse_idx"][:, o:] if f.sparse_k else None
         out["sparse_val"] = self.t["sparse_val"][:, o:] if f.sparse_k else None
+        if self.exact_plane:
+            out["sparse_cc"] = self.t["sparse_cc"][:, o:]
         return out
 
 
@@ -422,6 +439,12 @@ class RFSNv10KVCacheMLX:
         self.quantizer: Optional[QuantizerArg] = None
         self._kq: Optional[HybridQuantizerMLX] = None
         self._vq: Optional[HybridQuantizerMLX] = None
+        # drift guard of the score tables: running max |V| of the appended
+        # values, the guard's input row and the last call's estimates
+        self._vabs = torch.zeros((), dtype=torch.float32, device=self.device)
+        self._guard: Optional[torch.Tensor] = None
+        self._guard_key: Optional[Tuple[int, int]] = None
+        self.last_drift: Optional[torch.Tensor] = None
         self.last_access_stats = self._empty_access_stats()
 
     # ------------------------------------------------------------------ stats
@@ -494,11 +517,31 @@ class RFSNv10KVCacheMLX:
         return int(self._subspace and self.config.fused_score_tables
                    and K.score_layout_ok(self._fmt(), self.config.num_heads, self.H))
 
+    @property
+    def _guarded(self) -> bool:
+        """Score tables with the drift guard (``config.score_table_tolerance``):
+        K's sparse values then carry the corrected-coordinate plane."""
+        return bool(self._k_layout) and self.config.score_table_tolerance is not None
+
     def _tiled_pair(self, **kw) -> Tuple["TiledCodes", "TiledCodes"]:
         """Empty (K, V) tiled code sets; K as score-table rows when the kernel scores K that way."""
         fmt = self._fmt()
-        return (TiledCodes(fmt, self.H, self.device, score_rows=bool(self._k_layout), **kw),
+        return (TiledCodes(fmt, self.H, self.device, score_rows=bool(self._k_layout), exact_plane=self._guarded,
+                           **kw),
                 TiledCodes(fmt, self.H, self.device, **kw))
+
+    def _guard_tensor(self) -> torch.Tensor:
+        """The drift guard's [1, 65] input: the K codebooks' weights (built once
+        per quantizer pair) and the running bound on |V^| kept by ``update``."""
+        key = (id(self._kq), id(self._vq))
+        if self._guard_key != key:
+            g = torch.zeros((1, 65), dtype=torch.float32, device=self.device)
+            K.score_guard(self._kq.pq.codebooks, self._kq.rvq.codebooks, 0.0, out=g[0])
+            vp, vr = self._vq.pq.codebooks.float(), self._vq.rvq.codebooks.float()
+            vcb = (vp.abs().amax(-2) + vr.abs().amax(-2)).amax()
+            g[0, 64] = torch.maximum(vcb, self._vabs)
+            self._guard, self._guard_key = g, key
+        return self._guard
 
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Append [T, H, D] tokens to the hot tier.  The buffers hold up to
@@ -562,6 +605,10 @@ class RFSNv10KVCacheMLX:
         keys = new_keys.to(self.device, torch.float16)
         values = new_values.to(self.device, torch.float16)
         num_tokens = int(keys.shape[0])
+        if num_tokens and self._guarded:
+            torch.maximum(self._vabs, values.abs().amax().float(), out=self._vabs)
+            if self._guard is not None:
+                torch.maximum(self._guard[0, 64:], self._vabs.view(1), out=self._guard[0, 64:])
         if self._recency:
             self._update_recency(keys, values, disk_dir)
         else:
@@ -751,10 +798,16 @@ class RFSNv10KVCacheMLX:
     # consecutive chunks copied into consecutive slots is one hipMemcpyAsync.
     ARENA_CHUNKS = 64
 
+    def _chunk_split(self) -> Tuple[int, int]:
+        """Bytes of one chunk's tiled K codes and of its V codes (K first in
+        the chunk's pinned buffer and device slot)."""
+        chunk = K.round_up(self.config.chunk_tokens, K.TILE)
+        return (TiledCodes.nbytes(self._fmt(), self.H, chunk, self._guarded and self._fmt().sparse_k > 0),
+                TiledCodes.nbytes(self._fmt(), self.H, chunk))
+
     def _chunk_bytes(self) -> int:
         """Bytes of one chunk's tiled K and V codes (its pinned buffer and device slot)."""
-        chunk = K.round_up(self.config.chunk_tokens, K.TILE)
-        return 2 * TiledCodes.nbytes(self._fmt(), self.H, chunk)
+        return sum(self._chunk_split())
 
     def _arena_view(self, cid: int) -> torch.Tensor:
         nb = self._chunk_bytes()
@@ -774,15 +827,16 @@ class RFSNv10KVCacheMLX:
         if self._subspace:
             fmt = self._fmt()
             chunk = K.round_up(self.config.chunk_tokens, K.TILE)
-            half = self._chunk_bytes() // 2
-            dev_buf = torch.zeros(2 * half, dtype=torch.uint8, device=self.device)
+            kb, vb = self._chunk_split()
+            dev_buf = torch.zeros(kb + vb, dtype=torch.uint8, device=self.device)
             host_buf = self._arena_view(cid)
             for i, (name, store, qz) in enumerate((("key", ck, self._kq), ("value", cv, self._vq))):
-                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk, backing=dev_buf[i * half:(i + 1) * half],
-                                   score_rows=i == 0 and bool(self._k_layout))
+                o, n = (0, kb) if i == 0 else (kb, vb)
+                dev_t = TiledCodes(fmt, self.H, self.device, cap=chunk, backing=dev_buf[o:o + n],
+                                   score_rows=i == 0 and bool(self._k_layout), exact_plane=i == 0 and self._guarded)
                 dev_t.append(*_plain_head_major(store), qz.pq.codebooks, qz.rvq_codebooks)
-                host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk,
-                                    backing=host_buf[i * half:(i + 1) * half])
+                host_t = TiledCodes(fmt, self.H, None, pinned=True, cap=chunk, backing=host_buf[o:o + n],
+                                    score_rows=i == 0 and bool(self._k_layout), exact_plane=i == 0 and self._guarded)
                 host_t.len = dev_t.len
                 entry[f"{name}_tiled"] = host_t
             host_buf.copy_(dev_buf)
@@ -942,14 +996,14 @@ class RFSNv10KVCacheMLX:
     def _slot_entry(self, cid: int, slot: int) -> dict:
         """The slot's K and V views (built once per slot) holding chunk ``cid``."""
         if slot not in self._slot_views:
-            nb = self._chunk_bytes()
-            half = nb // 2
+            kb, vb = self._chunk_split()
+            nb = kb + vb
             pool = self._slot_pool()
             cap = K.round_up(self.config.chunk_tokens, K.TILE)
             self._slot_views[slot] = tuple(
-                TiledCodes(self._fmt(), self.H, self.device, cap=cap, backing=pool[o:o + half],
-                           score_rows=i == 0 and bool(self._k_layout))
-                for i, o in enumerate((slot * nb, slot * nb + half)))
+                TiledCodes(self._fmt(), self.H, self.device, cap=cap, backing=pool[o:o + n],
+                           score_rows=i == 0 and bool(self._k_layout), exact_plane=i == 0 and self._guarded)
+                for i, (o, n) in enumerate(((slot * nb, kb), (slot * nb + kb, vb))))
         e = self._cold_pinned[cid]
         kt, vt = self._slot_views[slot]
         kt.len, vt.len = e["key_tiled"].len, e["value_tiled"].len
@@ -1323,6 +1377,10 @@ class RFSNv10KVCacheMLX:
                       v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
                       cb_batch_stride=False, hot_cap=int(self._hot_k.shape[1]), out=out, launch=False,
                       k_layout=self._k_layout)
+        guard = None
+        if self._guarded:
+            guard = self._guard_tensor()
+            common.update(guard=guard, guard_tol=float(self.config.score_table_tolerance))
         has_resident = hot_len > 0 or not resident.empty
         if not fetched or not has_resident:
             # one launch; with chunks to copy it waits for them (nothing to overlap)
@@ -1331,12 +1389,15 @@ class RFSNv10KVCacheMLX:
                                    segments=table, max_tokens=max(res_tokens + in_tokens, 1), splits=splits,
                                    **common)
             step = K.PrefetchedStep(self._side_stream(), copies, [fl], wait_at=0) if copies else fl
+            self.last_drift = fl.drift
         else:
             # attend the resident part while the side stream copies the
             # missing chunks, then the copied chunks; partials merge at the end
             sa = K.fused_splits(B, Hq, self.H, hot_len, max(res_tokens, 1), resident.max_rows, splits)
             sb = K.fused_splits(B, Hq, self.H, 0, max(in_tokens, 1), incoming.max_rows, splits)
             ws = torch.empty(B * Hq * (sa + sb) * (D + 2) * 4, dtype=torch.uint8, device=self.device)
+            if guard is not None:
+                common["drift"] = torch.empty(B * Hq * (sa + sb), dtype=torch.float32, device=self.device)
             fa = K.fused_attention(qh, fmt, hot_k=hk, hot_v=hv, hot_len=hot_len, hot_pos0=hot_pos0,
                                    segments=resident, max_tokens=max(res_tokens, 1), splits=sa, workspace=ws,
                                    part=(0, sa + sb, False), **common)
@@ -1344,6 +1405,7 @@ class RFSNv10KVCacheMLX:
                                    max_tokens=max(in_tokens, 1), splits=sb, workspace=ws,
                                    part=(sa, sa + sb, True), **common)
             step = K.PrefetchedStep(self._side_stream(), copies, [fa, fb], wait_at=1)
+            self.last_drift = fb.drift
         if not launch:
             if copies:
                 # the staged slots count as resident from now on: fill them

@@ -82,13 +82,16 @@ struct BlockShape {
   static constexpr int T = W * 64;
   static constexpr size_t L = (size_t)kTilesBase + (size_t)W * kBufBytes;
   static_assert(L <= 160 * 1024, "LDS per CU");
-  static_assert((size_t)W * 16 * 4 + (size_t)W * 8 * kD * 4 <= L, "the wave combine reuses the codebook LDS");
+  static_assert((size_t)W * 24 * 4 + (size_t)W * 8 * kD * 4 + 8 * 4 <= L, "the wave combine reuses the codebook LDS");
 };
 constexpr float kPScaleLog2 = 14.0f;                // P is produced as p * 2^14
 // A score may exceed the running max by this much (log2 units) before the max
 // is moved: P then stays below 2^15.75 < 65504, the fp16 maximum.
 constexpr float kSlackLog2 = 1.75f;
 constexpr float kLog2e = 1.4426950408889634f;
+// Variance of a uniform rounding error of at most half an fp16 ulp, per unit
+// x^2: ulp(x) <= 2^-10 |x|, so ulp^2 / 12 <= 2^-20 x^2 / 12.
+constexpr float kDriftVar = 1.0f / (12.0f * 1048576.0f);
 
 __device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ float bitsf(uint32_t v) { return __builtin_bit_cast(float, v); }
@@ -159,10 +162,12 @@ struct WarmBase {
   gbytes sv[2];
   int len;
   int pos0;
+  uint32_t kplane;  // bytes from K's score deltas to its corrected-coordinate plane (exact pass over score rows)
 };
-template <int M, bool RVQ, int KS>
-__device__ __forceinline__ WarmBase warm_base(cseg sg, int h) {
+template <int M, bool RVQ, int KS, bool PLANE = false>
+__device__ __forceinline__ WarmBase warm_base(cseg sg, int h, int kv_heads = 0) {
   WarmBase w;
+  w.kplane = PLANE ? (uint32_t)((int64_t)kv_heads * sg->head_stride * KS * 2) : 0u;
   const int64_t row = (int64_t)h * sg->head_stride;  // first token row of head h
   const void* pq[2] = {sg->k.pq, sg->v.pq};
   const void* rvq[2] = {sg->k.rvq, sg->v.rvq};
@@ -386,6 +391,56 @@ __device__ __forceinline__ void load_tile_lut(LutRegs& r, const WarmBase& w, int
   }
 }
 
+// K codes of one tile for the exact pass over score-table rows: the registers
+// load_tile gives the codebook path (lane (j, m) = (lane / 16, lane % 16);
+// byte i of its 8 bytes per code array = subspace m of token 4i + j), read
+// from the rfsn_pack_score_codes rows.  Token 4i + j is row r = 4(i & 3) + j
+// of half u = i >> 2, and its subspace m sits at byte (m & 3) ^ (i & 3) of the
+// row's word 2(m >> 2) + u, so one 8-byte load per a = i & 3 brings the bytes
+// of tokens a and a + 4 (low and high word) and v_perm_b32 picks them: sel01
+// and sel23 take byte (m & 3) ^ a of words a = 0, 1 and 2, 3.  Odd tokens keep
+// their RVQ code in the PQ array, and an odd lane's first gather reads its
+// RVQ slot anyway, so the codes go to the gathers unswapped.  The sparse
+// entries 2 (lane >> 5), +1 of token lane & 31 (row r, half u) sit at
+// positions 8r + 4 (lane >> 5) + {u, 2 + u} of the tile's 128 (k = 4): the
+// index bytes come from the shared index array, the values from the
+// corrected-coordinate plane kplane bytes after the score deltas.
+template <int KS>
+__device__ __forceinline__ void load_tile_rows_exact(TileRegs<16, true, KS>& r, const WarmBase& w, int off,
+                                                     int count, int lane, uint32_t sel01, uint32_t sel23) {
+  const uint32_t co = (uint32_t)off * 16u + 32u * (uint32_t)(lane >> 4) + 8u * (uint32_t)((lane & 15) >> 2);
+  uint32_t a[2][4][2];  // [array][i & 3][word]
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint64_t x = gload<uint64_t>(w.pq[0], co + 128u * k), y = gload<uint64_t>(w.rvq[0], co + 128u * k);
+    a[0][k][0] = (uint32_t)x;
+    a[0][k][1] = (uint32_t)(x >> 32);
+    a[1][k][0] = (uint32_t)y;
+    a[1][k][1] = (uint32_t)(y >> 32);
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int wd = 0; wd < 2; ++wd) {
+      const uint32_t x01 = __builtin_amdgcn_perm(a[s][1][wd], a[s][0][wd], sel01);
+      const uint32_t x23 = __builtin_amdgcn_perm(a[s][3][wd], a[s][2][wd], sel23);
+      const uint32_t word = __builtin_amdgcn_perm(x23, x01, 0x05040100u);
+      if (s == 0) r.pq[wd] = word;
+      else r.rvq[wd] = word;
+    }
+  }
+  if constexpr (KS > 0) {
+    static_assert(KS == 4, "fused kernel carries 4 sparse entries");
+    const int t = min(lane & (kTile - 1), count - 1);
+    const uint32_t u = (uint32_t)t >> 4;
+    const uint32_t e = (uint32_t)off * KS + 8u * (uint32_t)(t & 15) + 4u * (uint32_t)(lane >> 5);
+    const uint32_t ib = gload<uint32_t>(w.si[0], e);
+    r.sidx = __builtin_amdgcn_perm(ib, ib, u ? 0x0C0C0301u : 0x0C0C0200u);
+    const uint64_t vb = gload<uint64_t>(w.sv[0], w.kplane + 2u * e);
+    r.sval = __builtin_amdgcn_perm((uint32_t)(vb >> 32), (uint32_t)vb, u ? 0x07060302u : 0x05040100u);
+  }
+}
+
 // Gather the 8 score-table entries of half u: for k = 0..3 the entries of
 // code byte k of the lane's PQ-array word and of its RVQ-array word.  The
 // row layout permutes and swaps the codes so that byte k of a word is the
@@ -573,15 +628,28 @@ __device__ __forceinline__ void set_prio(int p) {
   }
 }
 
-template <int M, bool RVQ, int KS, int NHG, bool LUT>
-__global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
-fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
-  static_assert(!LUT || (M == 16 && RVQ && NHG == 1), "score tables: 16 + 16 subspaces, <= 4 heads per KV head");
-  // static allocation: its base address is known at compile time, so LDS
-  // addresses built in registers need no base add
+// K paths of the kernel body.
+enum KMode : int {
+  kCodebook = 0,  // K^ rebuilt from the codebooks (k_layout 0)
+  kTables = 1,    // score tables (k_layout 1)
+  kExactRows = 2  // K^ rebuilt from the codebooks, codes read from the score-table rows (k_layout 1)
+};
+
+// One block's attention over its split: stage, stream the tiles, combine and
+// write the output (or the split partial).  With score tables and a drift
+// guard it returns true, without writing, when some head's drift estimate
+// exceeds the tolerance: the caller then runs the kExactRows body.  The
+// estimate needs sum_t p_t^2, which the table body accumulates beside the
+// softmax denominator.
+template <int M, bool RVQ, int KS, int NHG, int KM>
+__device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits, int tiles_per_split,
+                                          int blocks_total, uint8_t* __restrict__ lds) {
+  constexpr bool LUT = KM == kTables;
+  constexpr bool SX = KM == kExactRows;
+  static_assert(KM == kCodebook || (M == 16 && RVQ && NHG == 1),
+                "score-table rows: 16 + 16 subspaces, <= 4 heads per KV head");
   constexpr int kWaves = BlockShape<NHG>::W;
   constexpr int kThreads = BlockShape<NHG>::T;
-  __shared__ __align__(16) uint8_t lds[BlockShape<NHG>::L];
   // XCD-aware block mapping: consecutive hardware block ids go to different
   // XCDs; give each XCD a contiguous range of (sequence, head, split) units so
   // that one sequence's codebooks are fetched into one L2.
@@ -614,10 +682,15 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   const int tokr = 4 * (n & 3) + (n >> 2);
   const int beta = (g + 2 * (n >> 3)) & 3;
   const uint32_t blk8 = 8u * (uint32_t)beta;
+  // exact pass over score-table rows: v_perm_b32 selectors taking byte
+  // (m & 3) ^ a of words a = 0, 1 (sel01) and 2, 3 (sel23), m = lane % 16
+  const uint32_t m3 = (uint32_t)lane & 3u;
+  const uint32_t sel01 = 0x0C0C0000u | m3 | ((4u + (m3 ^ 1u)) << 8);
+  const uint32_t sel23 = 0x0C0C0000u | (m3 ^ 2u) | ((4u + (m3 ^ 3u)) << 8);
 
   const int hot_tiles = (p.hot_len + kTile - 1) / kTile;
   WarmBase w0 = {};
-  if (nseg > 0) w0 = warm_base<M, RVQ, KS>(segs, h);
+  if (nseg > 0) w0 = warm_base<M, RVQ, KS, SX>(segs, h, p.kv_heads);
   const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
   int total_tiles = hot_tiles + seg0_tiles;
   total_tiles += tail_tiles(segs, nseg);
@@ -637,6 +710,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   Regs vr[kDepth];
   auto load_k = [&](KRegs& rk, const WarmBase& w, int off, int count) __attribute__((always_inline)) {
     if constexpr (LUT) load_tile_lut<KS>(rk, w, off, tokr, blk8, g);
+    else if constexpr (SX) load_tile_rows_exact<KS>(rk, w, off, count, lane, sel01, sel23);
     else load_tile<M, RVQ, KS>(rk, w, 0, off, count, lane);
   };
   auto fetch = [&](TileSrc& s, KRegs& rk, Regs& rv, int tt) {
@@ -651,7 +725,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
     } else {
       s = walk_segments(segs, nseg, r - seg0_tiles);
-      const WarmBase w = warm_base<M, RVQ, KS>(segs + s.seg, h);
+      const WarmBase w = warm_base<M, RVQ, KS, SX>(segs + s.seg, h, p.kv_heads);
       load_k(rk, w, s.off, s.count);
       load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
     }
@@ -823,6 +897,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   int qpl[NHG];
   float4_t acc[NHG];
   float lsum[NHG];  // this lane's share of the softmax denominator (its tokens, its head)
+  float lsq[NHG];   // and of sum p^2 (score tables: the drift estimate)
 #pragma unroll
   for (int hg = 0; hg < NHG; ++hg) {
     const int hh = hg * 4 + (n >> 2);
@@ -839,6 +914,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
     qpl[hg] = (p.causal && p.qpos && valid) ? p.qpos[(int64_t)b * p.q_heads + h * G + hh] : 0x7fffffff;
     acc[hg] = float4_t{0.f, 0.f, 0.f, 0.f};
     lsum[hg] = 0.f;
+    lsq[hg] = 0.f;
   }
   // smallest query position of this KV head's query heads (uniform)
   int qmin = 0x7fffffff;
@@ -888,7 +964,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   // K half u of the tile in slot ks: score-table or codebook gathers
   auto gather_k = [&](const KRegs& rk, int u, KHalf& raw) __attribute__((always_inline)) {
     if constexpr (LUT) lut_gather(lds, rk, u, lca, lcb, raw);
-    else gather_half<M, RVQ, KS>(lds, rk, u, lc1_k, lc2_k, odd, raw);
+    else gather_half<M, RVQ, KS>(lds, rk, u, lc1_k, lc2_k, odd && !SX, raw);
   };
   // online softmax in base 2; produces the B operands of P.V (probability at
   // coordinate n & 3 of the lane's k-group)
@@ -938,6 +1014,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
         const float corr = none ? 1.f : __builtin_amdgcn_exp2f(m_run[hg] - mn);
         acc[hg] *= corr;
         lsum[hg] *= corr;
+        if constexpr (LUT) lsq[hg] *= corr * corr;
         m_run[hg] = mn;
         // exp2 argument = score - max + 14
         const float dm = none ? 0.f : kPScaleLog2 - mn;
@@ -953,6 +1030,7 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
                             (_Float16)__builtin_amdgcn_exp2f(arg[2 * q + 1])};  // v_cvt_pk_f16_f32
         const uint32_t x = __builtin_bit_cast(uint32_t, ph);
         lsum[hg] = __builtin_amdgcn_fdot2(ph, half2_t{(_Float16)1.0f, (_Float16)1.0f}, lsum[hg], false);
+        if constexpr (LUT) lsq[hg] = __builtin_amdgcn_fdot2(ph, ph, lsq[hg], false);
 #pragma unroll
         for (int k = 0; k < 4; ++k) pb[hg][q][k] = __builtin_amdgcn_perm(x, x, psel[k]);
       }
@@ -1110,10 +1188,13 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
   set_prio(0);
   // ---- combine the waves of this block and write the split partial
   __syncthreads();
-  float* red = reinterpret_cast<float*>(lds);  // [w][8] m, [w][8] l, [w][8][64] acc
+  // [w][8] m, [w][8] l, [w][8][64] acc, then (score tables) [w][8] sum p^2 and 8 drift estimates
+  float* red = reinterpret_cast<float*>(lds);
   float* red_m = red;
   float* red_l = red + kWaves * 8;
   float* red_a = red + kWaves * 16;
+  float* red_q = red_a + kWaves * 8 * kD;
+  float* est = red_q + kWaves * 8;
 #pragma unroll
   for (int hg = 0; hg < NHG; ++hg) {
     const int hh = hg * 4 + (n >> 2);
@@ -1125,15 +1206,60 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       const auto r32 = __builtin_amdgcn_permlane32_swap(fbits(ls), fbits(ls), false, false);
       ls = bitsf(r32[0]) + bitsf(r32[1]);
     }
+    float lq = lsq[hg];
+    if constexpr (LUT) {
+      const auto r16 = __builtin_amdgcn_permlane16_swap(fbits(lq), fbits(lq), false, false);
+      lq = bitsf(r16[0]) + bitsf(r16[1]);
+      const auto r32 = __builtin_amdgcn_permlane32_swap(fbits(lq), fbits(lq), false, false);
+      lq = bitsf(r32[0]) + bitsf(r32[1]);
+    }
     if (g == 0 && ep == 0) {
       red_m[wave * 8 + hh] = m_run[hg];
       red_l[wave * 8 + hh] = ls;
+      if constexpr (LUT) red_q[wave * 8 + hh] = lq;
     }
     // D rows 4g + r = subspace m, column n = (head, coordinate ep): dim 4m + ep
 #pragma unroll
     for (int r = 0; r < 4; ++r) red_a[(wave * 8 + hh) * kD + 4 * (4 * g + r) + ep] = acc[hg][r];
   }
   __syncthreads();
+  const int slots = p.part_slots ? p.part_slots : splits;
+  bool redo = false;
+  if constexpr (LUT) {
+    if (p.guard) {  // uniform
+      // drift estimate of head j = wave (< G <= 4): sigma^2 = scale^2 2^-20/12
+      // sum_i q_i^2 W_i (fp16 rounding of K^ and of the table entries, as
+      // uniform errors of at most 2^-10 |x| per ulp), times sqrt(sum p^2) / l
+      // (the first-order output change per unit logit noise) and 2 vmax
+      // (|v_t - out| <= 2 max |V^|)
+      const float* gw = p.guard + (p.pq_cb_stride ? (int64_t)b * 65 : 0);  // shared codebooks: one row
+      if (wave < G) {
+        const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + h * G + wave) * kD;
+        const float qv = h2f(qrow[lane]);
+        float s2 = qv * qv * gw[lane];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) s2 += __shfl_xor(s2, o, 64);
+        if (lane == 0) {
+          float Mx = -__builtin_inff();
+          for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, red_m[w * 8 + wave]);
+          float Ls = 0.f, Q = 0.f;
+          for (int w = 0; w < kWaves; ++w) {
+            const float mw = red_m[w * 8 + wave];
+            const float f = mw > -__builtin_inff() ? exp2f(mw - Mx) : 0.f;
+            Ls += red_l[w * 8 + wave] * f;
+            Q += red_q[w * 8 + wave] * f * f;
+          }
+          const float sigma = p.scale * sqrtf(kDriftVar * s2);
+          const float e = Ls > 0.f ? sigma * sqrtf(Q) / Ls * 2.f * gw[64] : 0.f;
+          est[wave] = e;
+          if (p.drift) p.drift[((int64_t)b * p.q_heads + h * G + wave) * slots + p.part_base + split] = e;
+        }
+      }
+      __syncthreads();
+      for (int j = 0; j < G; ++j) redo = redo || !(est[j] <= p.guard_tol);
+    }
+  }
+  if (redo) return true;  // uniform: the exact pass writes this block's output
   for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
     const int head = idx / kD, c = idx % kD;
     float Mx = -__builtin_inff();
@@ -1153,7 +1279,6 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       continue;
     }
     // partial slot: this call's split, after the slots of earlier calls in partial mode
-    const int slots = p.part_slots ? p.part_slots : splits;
     float* out = reinterpret_cast<float*>(p.workspace) +
                  (((int64_t)b * p.q_heads + h * G + head) * slots + p.part_base + split) * (kD + 2);
     if (c == 0) {
@@ -1161,6 +1286,30 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       out[1] = Ls;
     }
     out[2 + c] = A;
+  }
+  return false;
+}
+
+// The exact pass out of line: its registers are allocated apart from the
+// table pass's loop, which it would otherwise crowd into spills.
+template <int M, bool RVQ, int KS, int NHG>
+__device__ __noinline__ void exact_rows_pass(const rfsn_fused_params p, int splits, int tiles_per_split,
+                                             int blocks_total, uint8_t* lds) {
+  attn_body<M, RVQ, KS, NHG, kExactRows>(p, splits, tiles_per_split, blocks_total, lds);
+}
+
+template <int M, bool RVQ, int KS, int NHG, int KM>
+__global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
+fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
+  // static allocation: its base address is known at compile time, so LDS
+  // addresses built in registers need no base add
+  __shared__ __align__(16) uint8_t lds[BlockShape<NHG>::L];
+  const bool redo = attn_body<M, RVQ, KS, NHG, KM>(p, splits, tiles_per_split, blocks_total, lds);
+  if constexpr (KM == kTables) {
+    if (redo) {  // uniform
+      __syncthreads();  // every wave has read the combine area the exact pass restages over
+      exact_rows_pass<M, RVQ, KS, NHG>(p, splits, tiles_per_split, blocks_total, lds);
+    }
   }
 }
 
@@ -1187,13 +1336,13 @@ int auto_splits(const rfsn_fused_params* p) {
   return s;
 }
 
-template <int M, bool RVQ, int KS, int NHG, bool LUT>
+template <int M, bool RVQ, int KS, int NHG, int KM>
 int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
   const int splits = auto_splits(p);
   const int tiles = total_tiles_host(p);
   const int tps = (tiles + splits - 1) / splits;
   const int blocks = p->batch * p->kv_heads * splits;
-  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG, LUT>;  // 160 KB of static LDS
+  auto kern = fused_decode_attn_kernel<M, RVQ, KS, NHG, KM>;  // 160 KB of static LDS
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(BlockShape<NHG>::T), 0, s, *p, splits, tps, blocks);
   int st = check_launch("fused_decode_attention");
   if (st) return st;
@@ -1211,10 +1360,10 @@ template <int M, bool RVQ, int KS>
 int dispatch_nhg(const rfsn_fused_params* p, hipStream_t s) {
   const int G = p->q_heads / p->kv_heads;
   if constexpr (M == 16 && RVQ) {
-    if (p->k_layout == 1) return launch_fused<M, RVQ, KS, 1, true>(p, s);
+    if (p->k_layout == 1) return launch_fused<M, RVQ, KS, 1, kTables>(p, s);
   }
-  if (G <= 4) return launch_fused<M, RVQ, KS, 1, false>(p, s);
-  return launch_fused<M, RVQ, KS, 2, false>(p, s);
+  if (G <= 4) return launch_fused<M, RVQ, KS, 1, kCodebook>(p, s);
+  return launch_fused<M, RVQ, KS, 2, kCodebook>(p, s);
 }
 
 template <int M, bool RVQ>
@@ -1278,6 +1427,9 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   RFSN_REQUIRE(p->k_layout == 0 || p->k_layout == 1, "fused: k_layout must be 0 or 1");
   RFSN_REQUIRE(p->k_layout == 0 || (f.pq_subspaces == 16 && f.rvq_subspaces == 16 && p->q_heads / p->kv_heads <= 4),
                "fused: k_layout 1 needs 16 PQ and 16 RVQ subspaces and at most 4 query heads per KV head");
+  RFSN_REQUIRE(p->guard == nullptr || p->k_layout == 1, "fused: the drift guard serves k_layout 1 only");
+  RFSN_REQUIRE(p->guard == nullptr || p->guard_tol >= 0.f, "fused: guard_tol must be >= 0");
+  RFSN_REQUIRE(p->drift == nullptr || p->guard != nullptr, "fused: drift estimates need the guard");
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;

@@ -273,6 +273,28 @@ def score_layout_ok(fmt: WarmFormat, q_heads: int, kv_heads: int) -> bool:
             and kv_heads > 0 and q_heads % kv_heads == 0 and q_heads // kv_heads <= 4)
 
 
+def score_guard(k_pq_cb: torch.Tensor, k_rvq_cb: torch.Tensor, vmax, out: Optional[torch.Tensor] = None
+                ) -> torch.Tensor:
+    """Per-sequence inputs of the score tables' drift guard, float32 [..., 65]:
+    W_i = mean_c PQ_c,i^2 + mean_c RVQ_c,i^2 + mean_c |PQ_c(s)|^2 +
+    mean_c |RVQ_c(s)|^2 for coordinate i of subspace s (the second moment of
+    K^_i, whose fp16 rounding the tables skip, and of the table entries'
+    centroids per unit query), then ``vmax`` (an upper bound on |V^|).
+    Codebooks [M, C, 4] or [B, M, C, 4] (16 + 16 subspaces of head_dim 64);
+    ``vmax`` a number or a [B] tensor.  ``out`` receives the result in place."""
+    p, r = k_pq_cb.float(), k_rvq_cb.float()
+    lead = p.shape[:-3]
+    k2 = (p * p).mean(-2) + (r * r).mean(-2)                        # [..., 16, 4]
+    cn = (p * p).sum(-1).mean(-1) + (r * r).sum(-1).mean(-1)        # [..., 16]
+    w = (k2 + cn[..., None]).reshape(*lead, 64)
+    v = torch.as_tensor(vmax, dtype=torch.float32, device=w.device).expand(lead).reshape(*lead, 1)
+    g = torch.cat([w, v], -1)
+    if out is None:
+        return g
+    out.copy_(g)
+    return out
+
+
 def pack_score_codes(pq: torch.Tensor, rvq: torch.Tensor, sidx: Optional[torch.Tensor], sval: Optional[torch.Tensor],
                      dst: Dict[str, Optional[torch.Tensor]], t_base: int) -> None:
     """Plain codes pq, rvq [H, T, 16] and sparse entries sidx, sval [H, T, k]
@@ -406,11 +428,21 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
                     splits: int = 0, table: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
                     workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                     hot_cap: Optional[int] = None, launch: bool = True,
-                    part: Optional[Tuple[int, int, bool]] = None, k_layout: int = 0):
+                    part: Optional[Tuple[int, int, bool]] = None, k_layout: int = 0,
+                    guard: Optional[torch.Tensor] = None, guard_tol: float = 2e-3,
+                    drift: Optional[torch.Tensor] = None):
     """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
 
     ``k_layout`` = 1 when every segment's K codes are ``pack_score_codes``
     rows with ``sparse_fold(delta=True)`` values (``score_layout_ok``).
+
+    ``guard`` (k_layout 1, float32 [B, 65] from ``score_guard``, [1, 65]
+    with shared codebooks): a block
+    whose estimated output drift exceeds ``guard_tol`` recomputes its output
+    exactly, reading the corrected coordinates of K's sparse entries from the
+    plane after the score deltas (``TiledCodes(exact_plane=True)``).  The
+    estimates land in ``drift`` (float32, at least B * Hq * slots; allocated
+    when None) as [B, Hq, slots], slots = the call's splits or part slots.
 
     hot_k/hot_v: [.., Hkv, hot_cap, D] fp16 (sequence stride ``hot_seq_stride``
     elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
@@ -461,13 +493,28 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
             raise ValueError("partial calls need explicit splits and a shared workspace")
         p.part_base, p.part_slots, p.merge = int(part[0]), int(part[1]), int(bool(part[2]))
     lib = L.load()
+    if guard is not None:
+        if not k_layout:
+            raise ValueError("the drift guard serves the score-table K layout (k_layout=1) only")
+        rows = B if cb_batch_stride else 1  # shared codebooks share one guard row
+        if guard.dtype != torch.float32 or not guard.is_contiguous() or guard.numel() < rows * 65 \
+                or guard.device != q.device:
+            raise ValueError(f"guard must be a contiguous float32 [{rows}, 65] tensor on the query's device")
+        slots = p.part_slots if part is not None else int(lib.rfsn_fused_splits(C.byref(p)))
+        if drift is None:
+            drift = torch.empty(B * Hq * slots, dtype=torch.float32, device=q.device)
+        elif drift.dtype != torch.float32 or not drift.is_contiguous() or drift.numel() < B * Hq * slots:
+            raise ValueError(f"drift must be a contiguous float32 tensor of at least {B * Hq * slots} values")
+        p.guard, p.drift, p.guard_tol = guard.data_ptr(), drift.data_ptr(), float(guard_tol)
+        drift = drift[:B * Hq * slots].view(B, Hq, slots)
     wsb = lib.rfsn_fused_workspace_bytes(C.byref(p))
     if workspace is None or workspace.numel() < wsb:
         if part is not None:
             raise ValueError(f"partial calls share a workspace of at least {wsb} bytes")
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
-    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments, *cbs], out, _stream(q))
+    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments, *cbs, guard, drift], out, _stream(q))
+    fl.drift = drift
     if not launch:
         return fl
     fl()
@@ -494,6 +541,7 @@ class FusedLaunch:
         self._keep = keep
         self.out = out
         self.stream = stream
+        self.drift: Optional[torch.Tensor] = None  # [B, Hq, slots] drift estimates of the guard, if any
         self._fn = L.load().rfsn_fused_decode_attention
         self._ref = C.byref(self.params)
 

@@ -78,6 +78,11 @@ class RFSNConfig:
     # is rounded to fp16, so scores drift from q . fp16(K^) in proportion to
     # |q|; False keeps the exact codebook path
     fused_score_tables: bool = True
+    # drift guard of the score tables: a block whose estimated output drift
+    # (from |q|, the codebook magnitudes, sum p^2 and max |V|) exceeds this
+    # tolerance recomputes its output on the exact codebook path; None: no
+    # guard (the K sparse entries then carry no corrected-coordinate plane)
+    score_table_tolerance: Optional[float] = 2e-3
 
     def __post_init__(self) -> None:
         expected = self.num_subspaces * self.subspace_dim
@@ -92,6 +97,8 @@ class RFSNConfig:
             raise ValueError("tier_policy must be 'arrival' or 'recency'")
         if self.cold_medium not in ("npz", "pinned"):
             raise ValueError("cold_medium must be 'npz' or 'pinned'")
+        if self.score_table_tolerance is not None and not self.score_table_tolerance >= 0:
+            raise ValueError("score_table_tolerance must be None or >= 0")
 
     @property
     def kv_heads(self) -> int:

@@ -47,6 +47,7 @@ def parse_args(argv=None):
     ap.add_argument("--stream-steps", type=int, default=600,
                     help="long-context workload: streaming appends timed after the decode line (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-exact", action="store_true", help="skip timing the exact codebook K path beside the tables")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -137,6 +138,40 @@ def setup_decode(w, dev):
             log(f"sequence {b + 1}/{w.batch} encoded ({time.time() - t0:.1f} s)")
     torch.cuda.synchronize()
     return cache, torch.stack(qs).to(dev)
+
+
+def exact_path(w, cache, q, gpu_out, steps: int, dev) -> dict:
+    """The exact codebook K path timed beside the score tables: the same
+    sequences and codebooks prefilled into a cache that rebuilds K^ from the
+    codebooks (``fused_score_tables=False``), its kernel time over ``steps``
+    launches (HIP events on the launch stream), and its largest output
+    difference from the tables' output."""
+    import dataclasses
+
+    import torch
+    from apple_amd.batched import RFSNBatchedKVCache
+    from apple_amd.workloads import make_sequence
+
+    cfg = dataclasses.replace(cache.config, fused_score_tables=False)
+    exact = RFSNBatchedKVCache(cfg, w.batch, device=dev)
+    for b in range(w.batch):
+        k, v, _, _ = make_sequence(w, b)
+        exact.prefill(b, k.to(dev), v.to(dev), *cache.quantizers[b])
+    out = torch.empty_like(q)
+    launch = exact.prepare(q, out=out)
+    warm_up(launch, 10)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    achieved = w.bytes_per_step() / (ms * 1e-3) / 1e9
+    return {"k_scoring": "codebook K^ rows (exact)", "kernel_ms": round(ms, 5),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "max_abs_vs_tables": float((out.float() - gpu_out.float()).abs().max())}
 
 
 def cpu_baseline(w, cache, q, gpu_out, sample, repeats, threads=None):
@@ -602,6 +637,16 @@ def main(argv=None) -> int:
                      "kernel_ms": round(kernel_ms, 5), "kernel_ms_percentiles": pct,
                      "device_copy_gbs": copy_gbs, "frac_of_device_copy": round(achieved / copy_gbs, 4)},
     }
+    if cache.last_drift is not None:
+        # drift [B, Hq, splits]; a block (sequence, KV head, split) recomputes when one of its heads fires
+        tol = cache.config.score_table_tolerance
+        d = cache.last_drift.float().view(w.batch, w.kv_heads, w.q_heads // w.kv_heads, -1)
+        result["score_table_guard"] = {"tolerance": tol, "drift_max": float(d.max()),
+                                       "blocks_recomputed": int((d.amax(2) > tol).sum()),
+                                       "blocks": int(d.amax(2).numel())}
+    if cache.k_layout == 1 and not args.no_exact:
+        log("exact codebook K path")
+        result["exact_k_path"] = exact_path(w, cache, q, out, args.steps, dev)
     if not args.no_cpu:
         log("CPU baseline")
         cpu, err = cpu_baseline(w, cache, q, out, args.cpu_sample, args.cpu_repeats)

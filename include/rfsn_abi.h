@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 3
+#define RFSN_ABI_VERSION 4
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -259,6 +259,28 @@ typedef struct rfsn_fused_params {
    *    q . centroid (fp16) instead of reconstructing K.
    * V streams are always layout 0. */
   int32_t k_layout;
+  /* Drift guard of the score tables (k_layout = 1 only; guard = NULL: off).
+   * The tables sum q . centroid per subspace without rounding K^ =
+   * fp16(base + rvq) to fp16 as the decode does, so their scores drift from
+   * q . K^ by about one fp16 rounding of K^ per coordinate.  Each block
+   * estimates the drift of its output per query head,
+   *   est = scale * sqrt(2^-20/12 * sum_i q_i^2 W_i) * sqrt(sum_t p_t^2) / sum_t p_t * 2 * vmax
+   * (the logit noise of uniform roundings of at most 2^-10 |x| per ulp,
+   * times the first-order output change per unit of it), from guard[b] =
+   * {W_0 .. W_63, vmax} (one row for all sequences when the codebooks are
+   * shared, pq_cb_stride = 0; W_i = the second moment of K^_i over the
+   * codebooks plus those of the PQ and RVQ centroids of coordinate i's
+   * subspace, vmax >= |V^|), and a block where some head's est exceeds
+   * guard_tol recomputes its
+   * output exactly (K^ rebuilt from the codebooks) before writing it.  That
+   * pass reads the corrected coordinates fp16(K[idx] + residual) of K's
+   * sparse entries from a second plane of each K sparse-value array, at
+   * kv_heads * head_stride * k values after the score deltas, in the same
+   * positions.  drift (may be NULL): est per (sequence, query head, split
+   * slot), [B][Hq][slots] with slots = part_slots or the call's splits. */
+  const float* guard;
+  float* drift;
+  float guard_tol;
 } rfsn_fused_params;
 
 /* Token splits the call would use (p->splits, or the automatic choice when 0);

@@ -156,29 +156,100 @@ def test_fused_codebook_k_path(device):
         assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
 
 
+def _guard_estimate(q, cbs, vmax, wk, wv, scale=64 ** -0.5):
+    """The drift guard's estimate per (query, head), restated in numpy over
+    the oracle's softmax: scale * sqrt(2^-20/12 * sum_i q_i^2 W_i) *
+    sqrt(sum_t p_t^2) / sum_t p_t * 2 * vmax, W_i the second moments of K^_i
+    and of its subspace's centroids over the K codebooks."""
+    p, r = cbs["kp"].astype(np.float64), cbs["kr"].astype(np.float64)
+    W = ((p * p).mean(1) + (r * r).mean(1)).reshape(64) + np.repeat((p * p).sum(2).mean(1) + (r * r).sum(2).mean(1), 4)
+    B, Hq, _ = q.shape
+    G = Hq // wk.shape[1]
+    est = np.zeros((B, Hq))
+    for b in range(B):
+        for h in range(Hq):
+            qv = q[b, h].astype(np.float64)
+            lg = wk[:, h // G].astype(np.float64) @ qv * scale
+            w = np.exp(lg - lg.max())
+            est[b, h] = scale * np.sqrt((qv * qv * W).sum() / 12 / 2 ** 20) * np.sqrt((w * w).sum()) / w.sum() * 2 * vmax
+    return est
+
+
 def test_fused_error_envelope_peaked_queries(device):
-    """Sharper attention (queries scaled up to 8x): the codebook K path stays
-    within 2e-3 of the oracle at every scale (scores q . fp16(K^) as in the
-    reference); the score tables, whose fp16 entries round q . centroid, are
-    held to 2e-3 at the benchmark's query scale.  Measured on one MI355X
-    (2,064-token window): score tables 2.4e-4 / 1.95e-3 / 3.9e-3 / 1.3e-2 at
-    scales 1 / 2 / 4 / 8, the codebook path 1.2e-4 .. 1.95e-3."""
+    """Sharper attention (queries scaled up to 8x, 2,064-token window): both
+    K paths stay within 2e-3 of the oracle at every scale.  The codebook path
+    scores q . fp16(K^) as the reference does.  The score tables sum q .
+    centroid per subspace without K^'s fp16 rounding, which moves their
+    output by up to 1.3e-2 at 8x (measured on one MI355X without the guard);
+    their drift guard estimates that per block and recomputes the blocks
+    over the tolerance exactly: it stays quiet at 1x, where the tables hold
+    2e-3 by themselves, and fires at 4x and 8x (one split per query and KV
+    head; with several, each split estimates over its own tokens, an upper
+    bound on its share of the window's estimate, so it fires at least as
+    often).  The kernel's estimates match the numpy restatement of the
+    formula over the oracle's softmax."""
     from apple_amd.cache import RFSNv10KVCacheMLX
 
+    fired = {}
     for tables in (False, True):
         g, cfg, keys, values, cbs, kq, vq = _setup(11, 32, 8, 16, 16, 4, 2000, 64)
         cfg.fused_score_tables = tables
         cache = RFSNv10KVCacheMLX(cfg, device=device)
         cache.update(T(keys, device), T(values, device), (kq, vq))
-        assert cache._k_layout == int(tables)
+        assert cache._k_layout == int(tables) and cache._guarded == tables
         wk, wv = _oracle_window(keys, values, cbs, 16, 4, 2000)
+        vmax = max(float(np.abs(values.astype(np.float32)).max()),
+                   float((np.abs(cbs["vp"].astype(np.float32)).max(1) + np.abs(cbs["vr"].astype(np.float32)).max(1)).max()))
         q0 = randn16(g, 4, 32, 64).astype(np.float32)
-        for scale in ((1,) if tables else (1, 2, 4, 8)):
+        for scale in (1, 2, 4, 8):
             q = (q0 * scale).astype(np.float16)
             out = cache.attention_forward(T(q, device), causal=False)
             ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, False, None)
             err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
             assert err <= TOL, (tables, scale, err)
+            if tables:
+                # one split per (query, KV head): the block's estimate is the whole window's
+                one = torch.empty_like(T(q, device))
+                cache.prepare(T(q, device), causal=False, splits=1, out=one)()
+                assert np.abs(H(one).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+                drift = H(cache.last_drift)[:, :, 0]
+                est = _guard_estimate(q, cbs, vmax, wk, wv)
+                np.testing.assert_allclose(drift, est, rtol=0.05, atol=1e-7)
+                fired[scale] = bool((drift > cfg.score_table_tolerance).any())
+    assert not fired[1] and fired[4] and fired[8], fired
+
+
+def test_fused_exact_pass_matches_codebook_path(device):
+    """With the guard's tolerance at 0 every block of the score-table kernel
+    recomputes its output on the exact pass, which rebuilds K^ from the
+    codebooks while reading the score-table rows and the corrected-coordinate
+    plane: the outputs are bit-identical to the codebook path's over the
+    codebook layout, for one split and for several (split partials merged),
+    per-sequence cache and batched cache alike."""
+    from apple_amd.batched import RFSNBatchedKVCache
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    outs = {}
+    for mode in ("exact", "codebook"):
+        g, cfg, keys, values, cbs, kq, vq = _setup(21, 32, 8, 16, 16, 4, 3000, 80)
+        cfg.fused_score_tables = mode == "exact"
+        cfg.score_table_tolerance = 0.0
+        cache = RFSNv10KVCacheMLX(cfg, device=device)
+        cache.update(T(keys, device), T(values, device), (kq, vq))
+        q = T(randn16(g, 2, 32, 64), device)
+        for splits in (1, 5):
+            out = torch.empty_like(q)
+            cache.prepare(q, causal=True, splits=splits, out=out)()
+            outs[(mode, splits)] = H(out).copy()
+        if mode == "exact":
+            assert (H(cache.last_drift) > 0).all()
+        bc = RFSNBatchedKVCache(cfg, 2, device=device)
+        for b in range(2):
+            bc.prefill(b, T(keys, device), T(values, device), kq, vq)
+        assert bc.k_layout == int(mode == "exact")
+        outs[(mode, "batched")] = H(bc.attention_forward(q)).copy()
+    for key in (1, 5, "batched"):
+        assert np.array_equal(outs[("exact", key)].view(np.uint16), outs[("codebook", key)].view(np.uint16)), key
 
 
 def test_fused_score_tables_in_use(device):

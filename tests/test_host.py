@@ -345,3 +345,30 @@ def test_llama3_rope_frequencies_closed_form():
     assert np.all(cos.numpy()[0] == 1) and np.all(sin.numpy()[0] == 0)
     with pytest.raises(ValueError):
         rope_inv_freq(64, 500000.0, {"rope_type": "yarn", "factor": 4.0})
+
+
+def test_score_guard_weights():
+    """The drift guard's per-sequence row: W_i = mean_c PQ_c,i^2 + mean_c
+    RVQ_c,i^2 + mean_c |PQ_c(s)|^2 + mean_c |RVQ_c(s)|^2 (s = i // 4), then
+    the V bound; closed form on constant codebooks, and per-sequence rows of
+    stacked codebooks equal the rows of each."""
+    from apple_amd import kernels as K
+
+    p = torch.full((16, 256, 4), 0.5, dtype=torch.float16)
+    r = torch.full((16, 256, 4), -0.25, dtype=torch.float16)
+    g = K.score_guard(p, r, 3.0)
+    # 0.25 + 0.0625 per coordinate, 4 * that per subspace norm
+    assert torch.allclose(g[:64], torch.full((64,), 0.3125 * 5))
+    assert float(g[64]) == 3.0
+    gen = torch.Generator().manual_seed(3)
+    ps = torch.randn((3, 16, 256, 4), generator=gen).half()
+    rs = (torch.randn((3, 16, 256, 4), generator=gen) * 0.3).half()
+    rows = K.score_guard(ps, rs, torch.tensor([1.0, 2.0, 4.0]))
+    assert rows.shape == (3, 65)
+    for b in range(3):
+        one = K.score_guard(ps[b], rs[b], float(2 ** b))
+        assert torch.allclose(rows[b], one)
+        pf, rf = ps[b].double().numpy(), rs[b].double().numpy()
+        W = ((pf * pf).mean(1) + (rf * rf).mean(1)).reshape(64) \
+            + np.repeat((pf * pf).sum(2).mean(1) + (rf * rf).sum(2).mean(1), 4)
+        np.testing.assert_allclose(one[:64].numpy(), W, rtol=1e-5)
