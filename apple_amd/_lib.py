@@ -57,6 +57,10 @@ class FusedParams(C.Structure):
                 ("guard", vp), ("drift", vp), ("guard_tol", f32)]
 
 
+class EncodeJob(C.Structure):
+    _fields_ = [("x", vp), ("n", i64), ("ldx", i64), ("pq_cb", vp), ("rvq_cb", vp), ("out", Codes)]
+
+
 class Copy(C.Structure):
     _fields_ = [("dst_dev", vp), ("src_host", vp), ("bytes", sz)]
 
@@ -68,6 +72,7 @@ SIGNATURES = {
     "rfsn_pq_encode": (i32, [vp, i64, i32, i64, i64, vp, i32, i32, i64, vp, i64, i64, vp, i64, i64, i32, vp]),
     "rfsn_warm_encode_workspace_bytes": (sz, [C.POINTER(Format), i64]),
     "rfsn_warm_encode": (i32, [C.POINTER(Format), vp, i64, i64, vp, vp, Codes, vp, sz, vp]),
+    "rfsn_warm_encode_batch": (i32, [C.POINTER(Format), C.POINTER(EncodeJob), i32, vp]),
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),

@@ -623,6 +623,447 @@ sparse_topk64_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, con
   }
 }
 
+// ---------------------------------------------------------------- fused warm encode
+// One launch encodes up to kMaxJobs vector sets (a chunk's K and V): PQ, the
+// subspace RVQ stage on the register-resident fp16 PQ residual, then the
+// top-k |r2|, head_dim 64.  A block (16 waves) holds 256 vectors of one job
+// and first writes the augmented centroid rows of every (stage, subspace)
+// into LDS: coordinates in 8-byte groups, then (R/2 hi, R/2 lo, 1, 1), with
+// R the canonical fl32(S c*c); rows past the codebook get R/2 = +inf.  A wave
+// takes 16 vectors through every subspace: v_mfma_f32_16x16x16_f16 with
+// A = 16 centroid rows (lane l: row l % 16, k-group l / 16) and B = the 16
+// vectors (-x in the coordinate groups, (1, 1, L/2 hi, L/2 lo) in the next)
+// gives dist/2 of centroid 16t + 4(l / 16) + i and vector l % 16 in
+// accumulator i, so the four lanes of a vector screen 64 centroids each with
+// the keys and certificate of pq_encode_mfma_kernel, merge their top three,
+// and settle uncertain cases with the canonical float64 chain.  The residual
+// never leaves registers; each lane folds its share of the vector's r2 into a
+// running top-k, and the codes are written once per vector at the end.
+constexpr int kMaxJobs = 4;
+constexpr int kFeWaves = 16;
+constexpr int kFeThreads = kFeWaves * 64;
+constexpr int kFeVecs = kFeWaves * 16;  // vectors per block
+
+struct EncodeJob {
+  const uint16_t* x;
+  int64_t n;
+  int64_t ldx;
+  const uint16_t* pq_cb;
+  const uint16_t* rvq_cb;
+  uint8_t* pq;
+  uint8_t* rvq;
+  uint8_t* sidx;
+  uint16_t* sval;
+  int32_t block0;  // first block of the job in the grid
+};
+struct EncodeJobs {
+  EncodeJob j[kMaxJobs];
+  int32_t count;
+  int32_t C;   // PQ centroids
+  int32_t Cr;  // RVQ centroids
+};
+
+typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
+typedef float ff4 __attribute__((ext_vector_type(4)));
+
+// Insert key k into the sorted pair m1 <= m2 in two VALU ops.
+__device__ __forceinline__ void key_insert2(int& m1, int& m2, int k) {
+  asm("v_med3_i32 %1, %0, %1, %2\n\t"
+      "v_min_i32_e32 %0, %0, %2"
+      : "+v"(m1), "+v"(m2)
+      : "v"(k));
+}
+// Insert key k into the sorted triple m1 <= m2 <= m3 in three VALU ops.
+// Written out because the compiler, knowing m1 <= m2, turns the middle
+// median into a min / max pair.  k must be an ordinary VALU result, never an
+// MFMA destination read directly: the compiler pads MFMA -> VALU read hazards
+// only for reads it can see.
+__device__ __forceinline__ void key_insert3(int& m1, int& m2, int& m3, int k) {
+  asm("v_med3_i32 %2, %1, %2, %3\n\t"
+      "v_med3_i32 %1, %0, %1, %3\n\t"
+      "v_min_i32_e32 %0, %0, %3"
+      : "+v"(m1), "+v"(m2), "+v"(m3)
+      : "v"(k));
+}
+// The value of lane l ^ 16: ds_swizzle in bit-mask mode (and 0x1F, xor 0x10)
+// within each half of the wave; of lane l ^ 32: ds_bpermute from byte address
+// xor32_addr = 4 (l ^ 32).  Both run on the LDS crossbar, not the VALU.
+__device__ __forceinline__ int lane_xor16(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+__device__ __forceinline__ int lane_xor32(int v, int xor32_addr) { return __builtin_amdgcn_ds_bpermute(xor32_addr, v); }
+
+template <int DS, bool RVQ, int KS>
+__global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const EncodeJobs jobs) {
+  constexpr int M = 64 / DS;
+  constexpr int S = RVQ ? 2 : 1;       // stages
+  constexpr int CG = DS / 4;           // coordinate k-groups of a row
+  constexpr int RB = (CG + 1) * 8;     // row bytes: coordinate groups, then the R/2 group
+  constexpr int TB = 256 * RB;         // one (stage, subspace) table
+  __shared__ __align__(16) uint8_t tab[S * M * TB];
+  __shared__ uint32_t rmax_s[S * M];
+  // the block's job (uniform)
+  int ji = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxJobs; ++i)
+    if (i < jobs.count && (int)blockIdx.x >= jobs.j[i].block0) ji = i;
+  const EncodeJob& job = jobs.j[ji];
+  const int C = jobs.C, Cr = jobs.Cr;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- tables: row r of (stage s, subspace m) at tab + (s*M + m)*TB + r*RB
+  for (int i = tid; i < S * M; i += kFeThreads) rmax_s[i] = 0u;
+  __syncthreads();
+  for (int i = tid; i < S * M * 256; i += kFeThreads) {
+    const int r = i & 255, sm = i >> 8, s = sm / M, m = sm % M;
+    const int nc = s == 0 ? C : Cr;
+    const uint16_t* cb = (s == 0 ? job.pq_cb : job.rvq_cb) + ((size_t)m * nc + (r < nc ? r : 0)) * DS;
+    uint2 cw[CG];  // the centroid's coordinates, 4 fp16 per group
+#pragma unroll
+    for (int gq = 0; gq < CG; ++gq) cw[gq] = r < nc ? reinterpret_cast<const uint2*>(cb)[gq] : make_uint2(0u, 0u);
+    // R for the screening rows and the certificate's rmax: a float sum, whose
+    // error (< 2^-21 R) the certificate's 2^-17 R margin covers; the exact
+    // distances form the canonical float64 R themselves
+    float R = 0.0f;
+#pragma unroll
+    for (int gq = 0; gq < CG; ++gq) {
+      const fh4 c4 = __builtin_bit_cast(fh4, cw[gq]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) R = __builtin_fmaf((float)c4[u], (float)c4[u], R);
+    }
+    uint8_t* row = tab + (size_t)sm * TB + r * RB;
+#pragma unroll
+    for (int gq = 0; gq < CG; ++gq) *reinterpret_cast<uint2*>(row + 8 * gq) = cw[gq];
+    _Float16 rh, rl;
+    if (r < nc) {
+      const float half_r = 0.5f * R;
+      rh = (_Float16)half_r;
+      rl = (_Float16)(half_r - (float)rh);
+    } else {  // past the codebook: never the minimum
+      rh = (_Float16)__builtin_inff();
+      rl = (_Float16)0.0f;
+    }
+    const fh4 aug = {rh, rl, (_Float16)1.0f, (_Float16)1.0f};
+    *reinterpret_cast<fh4*>(row + 8 * CG) = aug;
+    // largest R of the table: a wave's 64 rows share (s, m)
+    uint32_t rb = r < nc ? (__builtin_bit_cast(uint32_t, R) & 0x7FFFFFFFu) : 0u;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) rb = max(rb, (uint32_t)__shfl_xor((int)rb, o, 64));
+    if (lane == 0) atomicMax(&rmax_s[sm], rb);
+  }
+  __syncthreads();
+
+  const int vi = lane & 15, g = lane >> 4;
+  const int64_t v = (int64_t)((int)blockIdx.x - job.block0) * kFeVecs + wave * 16 + vi;
+  const bool live = v < job.n;
+  const uint16_t* xv = job.x + (live ? v : 0) * job.ldx;
+
+  uint64_t codes[S][M / 8];  // the vector's code bytes, packed (byte m % 8 of word m / 8)
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int w = 0; w < M / 8; ++w) codes[s][w] = 0u;
+  // add code c of subspace m (m uniform: a shift, never a register index by m)
+  auto put_code = [&](int s, int m, int c) {
+    const uint64_t bits = (uint64_t)c << (8 * (m & 7));
+    if (M == 8 || m < 8) codes[s][0] |= bits;
+    else codes[s][M / 8 - 1] |= bits;
+  };
+  uint64_t top[KS > 0 ? KS : 1];
+#pragma unroll
+  for (int j = 0; j < (KS > 0 ? KS : 1); ++j) top[j] = 0;
+
+  // fl32(a - b) of two fp16 halves (v_fma_mix: a * 1 - b rounded once)
+  auto sub_h = [](_Float16 a, _Float16 b) { return __builtin_fmaf((float)a, 1.0f, -(float)b); };
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  auto pair = [](uint32_t w) { return __builtin_bit_cast(h2, w); };
+  auto pack = [](float lo, float hi) { return __builtin_bit_cast(uint32_t, h2{(_Float16)lo, (_Float16)hi}); };
+
+  // one nearest-centroid search of stage s, subspace m for the lane's vector
+  // slice xw (DS fp16 values, packed in pairs); returns the code
+  auto search = [&](int s, int m, const uint32_t (&xw)[DS / 2]) -> int {
+    const int nc = s == 0 ? C : Cr;
+    const uint8_t* tb = tab + (size_t)(s * M + m) * TB;
+    // screening L: a float sum (its error sits far inside the certificate's
+    // 2^-17 L); the canonical float64 chain is formed only for exact distances
+    float Ls = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DS / 2; ++k) {
+      const h2 x2 = pair(xw[k]);
+      Ls = __builtin_fmaf((float)x2[0], (float)x2[0], Ls);
+      Ls = __builtin_fmaf((float)x2[1], (float)x2[1], Ls);
+    }
+    const float half_l = 0.5f * Ls;
+    const _Float16 lh = (_Float16)half_l;
+    const _Float16 ll = (_Float16)(half_l - (float)lh);
+    uint2 bw = make_uint2(0u, 0u);  // B: -x of k-group g, or (1, 1, L/2 hi, L/2 lo)
+    if (g < CG) {
+      uint32_t b0 = xw[0], b1 = xw[1];
+      if constexpr (CG == 2) {
+        b0 = g ? xw[2] : b0;
+        b1 = g ? xw[3] : b1;
+      }
+      bw = make_uint2(b0 ^ 0x80008000u, b1 ^ 0x80008000u);  // exact: fp16 negation
+    } else if (g == CG) {
+      bw = make_uint2(0x3C003C00u, __builtin_bit_cast(uint32_t, h2{lh, ll}));
+    }
+    const fh4 b = __builtin_bit_cast(fh4, bw);
+    int maskv;  // 0xFFFFFF00 in a VGPR (the key build's other operand is the SGPR index)
+    asm("v_mov_b32 %0, 0xffffff00" : "=v"(maskv));
+    // k-groups past the R/2 group have B = 0: those lanes read the (finite)
+    // coordinate group instead, so that every lane loads and nothing branches
+    const uint8_t* arow = tb + vi * RB + 8 * (g <= CG ? g : 0);
+    // the lane's keys of chunk t, computed again by the exact rescreen below
+    auto screen = [&](auto&& insert) {
+      fh4 a[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) a[t] = *reinterpret_cast<const fh4*>(arow + 16 * t * RB);
+      ff4 acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a[0], b, ff4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {  // MFMA t + 1 issued before the keys of t
+        ff4 next = acc;
+        if (t + 1 < 16) next = __builtin_amdgcn_mfma_f32_16x16x16f16(a[t + 1], b, ff4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // centroid 16t + i (+ 4g below)
+          // the index as an opaque SGPR and the mask in a VGPR: one v_and_or_b32
+          int sidx;
+          asm("s_mov_b32 %0, %1" : "=s"(sidx) : "n"(16 * t + i));
+          const float z = acc[i];
+          insert(i, (__builtin_bit_cast(int, z) & maskv) | sidx);
+        }
+        acc = next;
+      }
+    };
+    const int x32 = 4 * (lane ^ 32);
+    // screening: the two smallest keys (two lists for independent chains)
+    int m1 = kNoKey, m2 = kNoKey, n1 = kNoKey, n2 = kNoKey;
+    screen([&](int i, int key) {
+      if (i & 1) key_insert2(n1, n2, key);
+      else key_insert2(m1, m2, key);
+    });
+    key_insert2(m1, m2, n1);
+    key_insert2(m1, m2, n2);
+    if (m1 != kNoKey) m1 |= 4 * g;
+    if (m2 != kNoKey) m2 |= 4 * g;
+    {  // the vector's four lanes l, l ^ 16, l ^ 32, l ^ 48
+      int o1 = lane_xor16(m1), o2 = lane_xor16(m2);
+      key_insert2(m1, m2, o1);
+      key_insert2(m1, m2, o2);
+      o1 = lane_xor32(m1, x32);
+      o2 = lane_xor32(m2, x32);
+      key_insert2(m1, m2, o1);
+      key_insert2(m1, m2, o2);
+    }
+    const float rmax = __builtin_bit_cast(float, rmax_s[s * M + m]);
+    const float v1 = key_value(m1), v2 = key_value(m2);
+    const float E = 0x1p-17f * (Ls + rmax) + 0x1p-22f;
+    const bool safe = rmax < 120000.0f;  // R / 2 representable in fp16 for every centroid
+    const bool unique = safe && v2 - v1 > 2.0f * E + 0x1p-14f * (fabsf(v1) + fabsf(v2));
+    if (__builtin_amdgcn_ballot_w64(!unique) == 0) return m1 & 0xFF;  // uniform: every vector settled
+    // some vector of the wave is uncertain: its three smallest keys, then
+    // the canonical float64 distances (x and L as float64 chains)
+    int p3 = kNoKey, p1 = kNoKey, p2 = kNoKey;
+    screen([&](int, int key) { key_insert3(p1, p2, p3, key); });
+    if (p1 != kNoKey) p1 |= 4 * g;
+    if (p2 != kNoKey) p2 |= 4 * g;
+    if (p3 != kNoKey) p3 |= 4 * g;
+    {
+      int o1 = lane_xor16(p1), o2 = lane_xor16(p2), o3 = lane_xor16(p3);
+      key_insert3(p1, p2, p3, o1);
+      key_insert3(p1, p2, p3, o2);
+      key_insert3(p1, p2, p3, o3);
+      o1 = lane_xor32(p1, x32);
+      o2 = lane_xor32(p2, x32);
+      o3 = lane_xor32(p3, x32);
+      key_insert3(p1, p2, p3, o1);
+      key_insert3(p1, p2, p3, o2);
+      key_insert3(p1, p2, p3, o3);
+    }
+    if (unique) return m1 & 0xFF;
+    double xs[DS];
+    double lacc = 0.0;
+#pragma unroll
+    for (int k = 0; k < DS / 2; ++k) {
+      const h2 x2 = pair(xw[k]);
+      xs[2 * k] = (double)(float)x2[0];
+      xs[2 * k + 1] = (double)(float)x2[1];
+      lacc = __builtin_fma(xs[2 * k], xs[2 * k], lacc);
+      lacc = __builtin_fma(xs[2 * k + 1], xs[2 * k + 1], lacc);
+    }
+    const float L = (float)lacc;
+    const float w1 = key_value(p1), w3 = key_value(p3);
+    const bool pair3 = safe && w3 - w1 > 2.0f * E + 0x1p-14f * (fabsf(w1) + fabsf(w3));
+    // canonical distance of centroid j: fl32(fl32(L - 2X) + R), X and R float64 chains
+    auto exact = [&](int j) {
+      const uint8_t* row = tb + j * RB;
+      double xa = 0.0, ra = 0.0;
+#pragma unroll
+      for (int u = 0; u < DS; ++u) {
+        const double c = (double)h2f(reinterpret_cast<const uint16_t*>(row)[u]);
+        xa = __builtin_fma(xs[u], c, xa);
+        ra = __builtin_fma(c, c, ra);
+      }
+      return __fadd_rn(__fsub_rn(L, 2.0f * (float)xa), (float)ra);
+    };
+    int code;
+    if (pair3) {
+      const int ja = min(p1 & 0xFF, p2 & 0xFF), jb = max(p1 & 0xFF, p2 & 0xFF);
+      const float da = exact(ja), db = exact(jb);
+      code = db < da ? jb : ja;  // first min: ties keep the lower index
+    } else {
+      float best = __builtin_inff();
+      code = 0;
+      for (int j = 0; j < nc; ++j) {
+        const float dj = exact(j);
+        if (dj < best) {
+          best = dj;
+          code = j;
+        }
+      }
+    }
+    return code;
+  };
+
+  // the vector's subspace slices, fp16 pairs, loaded one subspace ahead
+  auto load_x = [&](int m, uint32_t (&w)[DS / 2]) {
+    if constexpr (DS == 8) {
+      const uint4 v4 = *reinterpret_cast<const uint4*>(xv + m * DS);
+      w[0] = v4.x;
+      w[1] = v4.y;
+      w[2] = v4.z;
+      w[3] = v4.w;
+    } else {
+      const uint2 v2 = *reinterpret_cast<const uint2*>(xv + m * DS);
+      w[0] = v2.x;
+      w[1] = v2.y;
+    }
+  };
+  uint32_t xnext[DS / 2];
+  load_x(0, xnext);
+#pragma unroll 1
+  for (int m = 0; m < M; ++m) {
+    uint32_t xw[DS / 2];
+#pragma unroll
+    for (int k = 0; k < DS / 2; ++k) xw[k] = xnext[k];
+    if (m + 1 < M) load_x(m + 1, xnext);  // uniform
+    const int c0 = search(0, m, xw);
+    put_code(0, m, c0);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(tab + (size_t)m * TB + c0 * RB);
+    uint32_t rec[DS / 2];  // fp16(base + rvq) pairs
+#pragma unroll
+    for (int k = 0; k < DS / 2; ++k) rec[k] = base[k];
+    if constexpr (RVQ) {
+      uint32_t r1[DS / 2];  // PQ residual fp16(fl32(x) - fl32(c))
+#pragma unroll
+      for (int k = 0; k < DS / 2; ++k) {
+        const h2 x2 = pair(xw[k]), c2 = pair(rec[k]);
+        r1[k] = pack(sub_h(x2[0], c2[0]), sub_h(x2[1], c2[1]));
+      }
+      const int c1 = search(1, m, r1);
+      put_code(1, m, c1);
+      const uint32_t* cr = reinterpret_cast<const uint32_t*>(tab + (size_t)(M + m) * TB + c1 * RB);
+#pragma unroll
+      for (int k = 0; k < DS / 2; ++k) {  // fp16(fl32(base) + fl32(rvq))
+        const h2 a2 = pair(rec[k]), c2 = pair(cr[k]);
+        rec[k] = pack(__builtin_fmaf((float)a2[0], 1.0f, (float)c2[0]), __builtin_fmaf((float)a2[1], 1.0f, (float)c2[1]));
+      }
+    }
+    if constexpr (KS > 0) {
+      // this lane's share of the subspace: coordinates g * DS/4 + e, e < DS/4
+      // (pair word g for DS = 8, a half of word g >> 1 for DS = 4), selected
+      // without indexing registers by lane
+      uint32_t xs2 = xw[0], rs2 = rec[0];
+#pragma unroll
+      for (int k = 1; k < DS / 2; ++k) {
+        const bool sel = DS == 8 ? g == k : (g >> 1) == k;
+        xs2 = sel ? xw[k] : xs2;
+        rs2 = sel ? rec[k] : rs2;
+      }
+#pragma unroll
+      for (int e = 0; e < DS / 4; ++e) {
+        const int hsel = DS == 8 ? e : (g & 1);
+        const h2 x2 = pair(xs2), q2 = pair(rs2);
+        const float r2 = hsel ? sub_h(x2[1], q2[1]) : sub_h(x2[0], q2[0]);
+        const uint32_t mb = __builtin_bit_cast(uint32_t, r2) & 0x7FFFFFFFu;
+        if (mb <= 0x7F800000u) {  // NaN never enters
+          const int i = m * DS + g * (DS / 4) + e;
+          topk_insert(top, ((uint64_t)mb << 32) | ((uint64_t)(64 - i) << 16) | f2h(r2));
+        }
+      }
+    }
+  }
+  if constexpr (KS > 0) {
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+      uint64_t ot[KS];
+#pragma unroll
+      for (int j = 0; j < KS; ++j) ot[j] = __shfl_xor(top[j], o, 64);
+#pragma unroll
+      for (int j = 0; j < KS; ++j) topk_insert(top, ot[j]);
+    }
+  }
+  if (!live || g != 0) return;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    uint8_t* dst = (s == 0 ? job.pq : job.rvq) + v * M;
+    const uint64_t lo = codes[s][0];
+    if constexpr (M == 8) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)lo, (uint32_t)(lo >> 32));
+    } else {
+      const uint64_t hi = codes[s][M / 8 - 1];
+      *reinterpret_cast<uint4*>(dst) =
+          make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+    }
+  }
+  if constexpr (KS > 0) {
+    uint32_t iw = 0;
+    uint16_t vals[KS];
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const bool real = top[j] != 0;
+      iw |= (uint32_t)(real ? (uint8_t)(64 - (int)((top[j] >> 16) & 0xFFFF)) : 0u) << (8 * j);
+      vals[j] = real ? (uint16_t)(top[j] & 0xFFFF) : (uint16_t)0;
+    }
+    *reinterpret_cast<uint32_t*>(job.sidx + v * KS) = iw;
+    *reinterpret_cast<uint2*>(job.sval + v * KS) =
+        make_uint2(vals[0] | ((uint32_t)vals[1] << 16), vals[2] | ((uint32_t)vals[3] << 16));
+  }
+}
+
+// The fused encode serves head_dim 64, 4- or 8-dim subspaces, an RVQ stage of
+// the same split or none, k in {0, 4}, and aligned rows (16-byte x rows,
+// code and sparse rows at their natural alignment).
+bool fused_encode_ok(const rfsn_format* f, const EncodeJob& j) {
+  const int d = f->head_dim / f->pq_subspaces;
+  const auto al = [](const void* p, uintptr_t a) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % a == 0; };
+  return f->head_dim == 64 && (d == 4 || d == 8) && (f->rvq_subspaces == 0 || f->rvq_subspaces == f->pq_subspaces) &&
+         (f->sparse_k == 0 || f->sparse_k == 4) && j.ldx % 8 == 0 && al(j.x, 16) && al(j.pq_cb, 8) &&
+         al(j.rvq_cb, 8) && al(j.pq, f->pq_subspaces) && al(j.rvq, f->pq_subspaces) && al(j.sidx, 4) &&
+         al(j.sval, 8);
+}
+
+int launch_warm_encode_fused(const rfsn_format* f, EncodeJobs& jobs, hipStream_t s) {
+  int blocks = 0;
+  for (int i = 0; i < jobs.count; ++i) {
+    jobs.j[i].block0 = blocks;
+    blocks += (int)ceil_div(jobs.j[i].n, kFeVecs);
+  }
+  if (blocks == 0) return RFSN_OK;
+  jobs.C = f->pq_centroids;
+  jobs.Cr = f->rvq_subspaces ? f->rvq_centroids : 1;
+  const int d = f->head_dim / f->pq_subspaces;
+  const bool rvq = f->rvq_subspaces > 0;
+  const bool ks = f->sparse_k > 0;
+#define RFSN_FE(DS, R, K) hipLaunchKernelGGL((warm_encode_fused_kernel<DS, R, K>), dim3(blocks), dim3(kFeThreads), 0, s, jobs)
+  if (d == 8) {
+    if (rvq) { if (ks) RFSN_FE(8, true, 4); else RFSN_FE(8, true, 0); }
+    else { if (ks) RFSN_FE(8, false, 4); else RFSN_FE(8, false, 0); }
+  } else {
+    if (rvq) { if (ks) RFSN_FE(4, true, 4); else RFSN_FE(4, true, 0); }
+    else { if (ks) RFSN_FE(4, false, 4); else RFSN_FE(4, false, 0); }
+  }
+#undef RFSN_FE
+  return check_launch("warm_encode_fused");
+}
+
 template <int DSUB>
 int launch_pq(const void* x, int64_t n, int64_t ldx, int64_t xg, const void* cb, int M, int C, int d, int64_t cbg,
               uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg, int groups,
@@ -739,24 +1180,60 @@ extern "C" int rfsn_warm_encode(const rfsn_format* f, const void* x, int64_t n, 
   RFSN_REQUIRE(x && pq_cb && out.pq, "warm_encode: null pointer");
   RFSN_REQUIRE(ldx >= f->head_dim, "warm_encode: bad leading dimension");
   if (n == 0) return RFSN_OK;
+  RFSN_REQUIRE(f->rvq_subspaces == 0 || (rvq_cb && out.rvq), "warm_encode: RVQ stage needs codebooks and an output");
+  RFSN_REQUIRE(f->sparse_k == 0 || (out.sparse_idx && out.sparse_val), "warm_encode: sparse stage needs outputs");
+  hipStream_t s = (hipStream_t)stream;
+  EncodeJobs jobs = {};
+  jobs.count = 1;
+  jobs.j[0] = EncodeJob{(const uint16_t*)x, n, ldx, (const uint16_t*)pq_cb, (const uint16_t*)rvq_cb, out.pq, out.rvq,
+                        out.sparse_idx, (uint16_t*)out.sparse_val, 0};
+  if (fused_encode_ok(f, jobs.j[0])) return launch_warm_encode_fused(f, jobs, s);
+  // other formats: PQ, RVQ and top-k as separate launches, the PQ residual in the workspace
   const size_t need = rfsn_warm_encode_workspace_bytes(f, n);
   RFSN_REQUIRE(ws != nullptr && ws_bytes >= need, "warm_encode: workspace too small");
   const int D = f->head_dim;
-  hipStream_t s = (hipStream_t)stream;
   uint16_t* r1 = (uint16_t*)ws;  // [n][D] PQ residual
   st = pq_encode_impl(x, n, D, ldx, 0, pq_cb, f->pq_subspaces, f->pq_centroids, 0, out.pq, f->pq_subspaces, 0, r1,
                       D, 0, 1, s);
   if (st) return st;
   if (f->rvq_subspaces > 0) {
-    RFSN_REQUIRE(rvq_cb && out.rvq, "warm_encode: RVQ stage needs codebooks and an output");
     st = pq_encode_impl(r1, n, D, D, 0, rvq_cb, f->rvq_subspaces, f->rvq_centroids, 0, out.rvq, f->rvq_subspaces, 0,
                         nullptr, D, 0, 1, s);
     if (st) return st;
   }
   if (f->sparse_k > 0) {
-    RFSN_REQUIRE(out.sparse_idx && out.sparse_val, "warm_encode: sparse stage needs outputs");
     st = sparse_topk_impl(x, n, D, ldx, out.pq, f->pq_subspaces, f->pq_centroids, pq_cb, out.rvq, f->rvq_subspaces,
                           f->rvq_centroids, rvq_cb, f->sparse_k, out.sparse_idx, out.sparse_val, s);
+    if (st) return st;
+  }
+  return RFSN_OK;
+}
+
+extern "C" int rfsn_warm_encode_batch(const rfsn_format* f, const rfsn_encode_job* jobs, int32_t count,
+                                      void* stream) {
+  int st = validate_format(f);
+  if (st) return st;
+  RFSN_REQUIRE(count >= 0 && (count == 0 || jobs != nullptr), "warm_encode_batch: bad job list");
+  hipStream_t s = (hipStream_t)stream;
+  for (int i0 = 0; i0 < count; i0 += kMaxJobs) {
+    EncodeJobs batch = {};
+    for (int i = i0; i < count && i < i0 + kMaxJobs; ++i) {
+      const rfsn_encode_job& j = jobs[i];
+      RFSN_REQUIRE(j.n >= 0 && j.ldx >= f->head_dim, "warm_encode_batch: bad job");
+      if (j.n == 0) continue;  // an empty set launches nothing
+      RFSN_REQUIRE(j.x && j.pq_cb && j.out.pq, "warm_encode_batch: null pointer");
+      RFSN_REQUIRE(f->rvq_subspaces == 0 || (j.rvq_cb && j.out.rvq),
+                   "warm_encode_batch: RVQ stage needs codebooks and an output");
+      RFSN_REQUIRE(f->sparse_k == 0 || (j.out.sparse_idx && j.out.sparse_val),
+                   "warm_encode_batch: sparse stage needs outputs");
+      EncodeJob& e = batch.j[batch.count++];
+      e = EncodeJob{(const uint16_t*)j.x, j.n, j.ldx, (const uint16_t*)j.pq_cb, (const uint16_t*)j.rvq_cb, j.out.pq,
+                    j.out.rvq, j.out.sparse_idx, (uint16_t*)j.out.sparse_val, 0};
+      if (!fused_encode_ok(f, e))
+        return fail(RFSN_ERR_UNSUPPORTED, "warm_encode_batch: the one-launch encode serves head_dim 64, 4- or 8-dim "
+                                          "subspaces, an RVQ stage of the same split or none, k in {0, 4} and aligned rows");
+    }
+    st = launch_warm_encode_fused(f, batch, s);
     if (st) return st;
   }
   return RFSN_OK;

@@ -106,7 +106,7 @@ def warm_encode(x: torch.Tensor, fmt: WarmFormat, pq_cb: torch.Tensor,
                 rvq_cb: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
     """PQ + optional subspace RVQ + optional top-k sparse residual of x [N, D]."""
     _dev(x, "warm_encode")
-    if x.dim() != 2 or x.stride(1) != 1 or x.dtype != torch.float16:
+    if x.dim() != 2 or (x.shape[0] and x.stride(1) != 1) or x.dtype != torch.float16:
         raise ValueError("warm_encode expects fp16 [N, D] rows")
     n = x.shape[0]
     dev = x.device
@@ -116,6 +116,8 @@ def warm_encode(x: torch.Tensor, fmt: WarmFormat, pq_cb: torch.Tensor,
     if fmt.sparse_k:
         out["sparse_idx"] = torch.empty((n, fmt.sparse_k), dtype=torch.uint8, device=dev)
         out["sparse_val"] = torch.empty((n, fmt.sparse_k), dtype=torch.float16, device=dev)
+    if n == 0:
+        return out
     f = fmt.c()
     ws_bytes = L.load().rfsn_warm_encode_workspace_bytes(C.byref(f), n)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -124,6 +126,37 @@ def warm_encode(x: torch.Tensor, fmt: WarmFormat, pq_cb: torch.Tensor,
     L.call("rfsn_warm_encode", C.byref(f), x.data_ptr(), n, x.stride(0), _contig(pq_cb).data_ptr(),
            L.ptr(None if rvq_cb is None else _contig(rvq_cb)), codes, ws.data_ptr(), ws_bytes, _stream(x))
     return out
+
+
+def warm_encode_batch(items: Sequence[Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]],
+                      fmt: WarmFormat) -> List[Dict[str, torch.Tensor]]:
+    """``warm_encode`` of several (x, pq_cb, rvq_cb) sets of one format in one
+    launch (a chunk's K and V); the formats ``rfsn_warm_encode_batch`` serves."""
+    if not items:
+        return []
+    outs, keep = [], []
+    jobs = (L.EncodeJob * len(items))()
+    for i, (x, pq_cb, rvq_cb) in enumerate(items):
+        _dev(x, "warm_encode_batch")
+        if x.dim() != 2 or (x.shape[0] and x.stride(1) != 1) or x.dtype != torch.float16:
+            raise ValueError("warm_encode_batch expects fp16 [N, D] rows")
+        n, dev = x.shape[0], x.device
+        out = {"pq": torch.empty((n, fmt.pq_subspaces), dtype=torch.uint8, device=dev)}
+        if fmt.rvq_subspaces:
+            out["rvq"] = torch.empty((n, fmt.rvq_subspaces), dtype=torch.uint8, device=dev)
+        if fmt.sparse_k:
+            out["sparse_idx"] = torch.empty((n, fmt.sparse_k), dtype=torch.uint8, device=dev)
+            out["sparse_val"] = torch.empty((n, fmt.sparse_k), dtype=torch.float16, device=dev)
+        pcb = _contig(pq_cb)
+        rcb = None if rvq_cb is None else _contig(rvq_cb)
+        keep += [x, pcb, rcb]
+        jobs[i] = L.EncodeJob(x.data_ptr(), n, x.stride(0) if n else x.shape[1], pcb.data_ptr(), L.ptr(rcb),
+                              L.Codes(out["pq"].data_ptr(), L.ptr(out.get("rvq")), L.ptr(out.get("sparse_idx")),
+                                      L.ptr(out.get("sparse_val"))))
+        outs.append(out)
+    f = fmt.c()
+    L.call("rfsn_warm_encode_batch", C.byref(f), jobs, len(items), _stream(items[0][0]))
+    return outs
 
 
 def rvq_encode_full(resid: torch.Tensor, codebooks: torch.Tensor, threshold: float

@@ -88,6 +88,24 @@ int rfsn_warm_encode(const rfsn_format* fmt, const void* x_dev, int64_t n, int64
                      const void* pq_cb_dev, const void* rvq_cb_dev, rfsn_codes out,
                      void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* Several vector sets of one format in one launch (a chunk's K and V, as
+ * the warm append of cache.py:122-132 encodes them): each job is
+ * rfsn_warm_encode's x / n / ldx / codebooks / out.  Needs head_dim 64, 4- or
+ * 8-dim subspaces, an RVQ stage of the same split or none, sparse_k 0 or 4,
+ * 16-byte aligned x rows and naturally aligned code and sparse rows, and no
+ * workspace: the PQ residual stays in registers (RFSN_ERR_UNSUPPORTED for
+ * other formats; rfsn_warm_encode serves every format).  The same codes as
+ * rfsn_warm_encode, bit for bit. */
+typedef struct rfsn_encode_job {
+  const void* x;
+  int64_t n;
+  int64_t ldx;
+  const void* pq_cb;
+  const void* rvq_cb;
+  rfsn_codes out;
+} rfsn_encode_job;
+int rfsn_warm_encode_batch(const rfsn_format* fmt, const rfsn_encode_job* jobs, int32_t count, void* stream);
+
 /* Reference-mode RVQ (quantization.py:206-252), three steps:
  * (1) gate: mask[i] = fl32(sqrt(fl32(sum r^2))) > threshold (u8 0/1);
  * (2) compaction: offsets[0..A) = ascending indices with mask set,

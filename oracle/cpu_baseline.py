@@ -1,6 +1,12 @@
-"""Timed CPU baseline of the warm-tier decode path (test infrastructure only;
-``bench.py`` times it beside the GPU kernel, it is never the thing measured
-on the GPU).
+"""Timed CPU baselines of the warm-tier decode and encode paths (test
+infrastructure only; ``bench.py`` times them beside the GPU kernels, they are
+never the thing measured on the GPU).
+
+Encode: the reference's PyTorch form of the nearest-centroid search
+(rfsn_v10_unified_mac_launcher.py:358-373), fp32 ``torch.cdist ** 2`` and
+``argmin`` per subspace, applied to both stages and followed by the top-k.
+
+Decode:
 
 Restates the reference's PyTorch form (rfsn_v10_unified_mac_launcher.py:
 217-273): per-subspace ``F.embedding`` decode of the PQ codes, the same for
@@ -87,3 +93,41 @@ def decode_step(q: torch.Tensor, hot_k: torch.Tensor, hot_v: torch.Tensor, warm_
     keys = torch.cat([parts_k[0], hot_k.permute(1, 0, 2)], 0)
     values = torch.cat([parts_v[0], hot_v.permute(1, 0, 2)], 0)
     return blockwise_attention(q, keys, values, scale, block)
+
+
+def pq_encode_cdist(x: torch.Tensor, codebooks: torch.Tensor):
+    """Nearest centroid per subspace the way the reference's PyTorch backend
+    does it (rfsn_v10_unified_mac_launcher.py:358-373): fp32
+    ``torch.cdist(sub, centroids) ** 2`` and ``argmin``; returns the codes
+    [N, M] and the fp16 residual fp16(x - c)."""
+    M, C, d = codebooks.shape
+    codes = torch.empty((x.shape[0], M), dtype=torch.uint8)
+    resid = torch.empty_like(x)
+    xf = x.float()
+    for m in range(M):
+        sub = xf[:, m * d:(m + 1) * d]
+        cents = codebooks[m].float()
+        idx = (torch.cdist(sub, cents) ** 2).argmin(dim=1)
+        codes[:, m] = idx.to(torch.uint8)
+        resid[:, m * d:(m + 1) * d] = (sub - F.embedding(idx, cents)).half()
+    return codes, resid
+
+
+def warm_encode(x: torch.Tensor, pq_cb: torch.Tensor, rvq_cb: Optional[torch.Tensor], k: int) -> dict:
+    """Warm-format encode of fp16 vectors [N, D] in torch-CPU: PQ by cdist^2 +
+    argmin, the subspace RVQ stage on the fp16 PQ residual, then the top-k
+    |x - fp16(base + rvq)| coordinates (values fp16)."""
+    pq, r1 = pq_encode_cdist(x, pq_cb)
+    out = {"pq": pq}
+    recon = decode_codes(pq, pq_cb)
+    if rvq_cb is not None:
+        rvq, _ = pq_encode_cdist(r1, rvq_cb)
+        recon = (recon.float() + decode_codes(rvq, rvq_cb).float()).half()
+        out["rvq"] = rvq
+    if k:
+        r2 = x.float() - recon.float()
+        # |r2| descending, ties to the lower coordinate (a stable sort keeps index order)
+        idx = torch.sort(r2.abs(), dim=1, descending=True, stable=True).indices[:, :k]
+        out["sparse_idx"] = idx.to(torch.uint8)
+        out["sparse_val"] = torch.gather(r2, 1, idx).half()
+    return out

@@ -131,6 +131,79 @@ def test_warm_encode_bit_exact(device, M, Mr, k):
     assert np.array_equal(H(dec).view(np.uint16), rdec.view(np.uint16))
 
 
+@pytest.mark.parametrize("d", [4, 8])
+@pytest.mark.parametrize("C", [1, 16, 100, 256])
+def test_warm_encode_screening_paths(device, d, C):
+    """The one-launch warm encode (PQ, RVQ on the register-resident residual,
+    top-4) through each decision of its search, in both stages: duplicated,
+    triplicated and exactly equidistant centroids, vectors near them, |x|^2/2
+    beyond fp16, codebooks shorter than 256 and |c|^2/2 beyond fp16; codes
+    and sparse entries bit-exact against the oracle."""
+    from apple_amd import kernels as K
+
+    g = rng(700 + 7 * d + C)
+    D = 64
+    M = D // d
+    cb = rand_codebooks(g, M, C, d)
+    rcb = rand_codebooks(g, M, C, d) * np.float16(0.3)
+    rows = [randn16(g, 200, D)]
+    if C >= 16:
+        for c in (cb, rcb):
+            c[:, 5] = c[:, 2]
+            c[:, 9] = c[:, 2]
+            c[:, C - 1] = c[:, 7]
+        rows.append(np.concatenate([cb[m][[2, 7, 9, 5, 0, C - 1]] for m in range(M)], axis=1))
+        base = randn16(g, 1, d)[0]
+        for m in range(M):
+            cb[m, 11] = base
+            cb[m, 12] = base
+            cb[m, 11, 0] = base[0] + np.float16(0.25)
+            cb[m, 12, 0] = base[0] - np.float16(0.25)
+        rows.append(np.tile(base, (3, M)))
+        near = np.tile(base, (8, M)).view(np.uint16)
+        near[np.arange(8), np.arange(8) % D] ^= 1
+        rows.append(near.view(np.float16))
+    rows.append((randn16(g, 16, D).astype(np.float32) * 300.0).astype(np.float16))  # L / 2 > 65504
+    x = np.concatenate(rows, 0)
+    for pq_cb in (cb, None):
+        if pq_cb is None:  # R / 2 beyond fp16 for centroid 0 of every subspace
+            pq_cb = cb.copy()
+            pq_cb[:, 0] = (pq_cb[:, 0].astype(np.float32) * 200.0).astype(np.float16)
+        fmt = K.WarmFormat(D, M, C, M, C, 4)
+        out = K.warm_encode(T(x, device), fmt, T(pq_cb, device), T(rcb, device))
+        ref = nx.ext_encode(x, pq_cb, rcb, 4)
+        assert np.array_equal(H(out["pq"]), ref["pq_codes"])
+        assert np.array_equal(H(out["rvq"]), ref["rvq_codes"])
+        assert np.array_equal(H(out["sparse_idx"]), ref["sparse_idx"])
+        assert np.array_equal(H(out["sparse_val"]).view(np.uint16), ref["sparse_val"].view(np.uint16))
+
+
+def test_warm_encode_batch_one_launch(device):
+    """A chunk's K and V (and a third set, and an empty one) in one launch:
+    the same codes, bit for bit, as separate warm_encode calls and the oracle;
+    a format the one-launch encode does not serve is refused."""
+    from apple_amd import kernels as K
+
+    g = rng(811)
+    fmt = K.WarmFormat(64, 16, 256, 16, 256, 4)
+    sets = []
+    for n in (1000, 777, 33, 0):
+        x = (randn16(g, n, 64).astype(np.float32) * np.linspace(0.5, 2.0, 64, dtype=np.float32)).astype(np.float16)
+        sets.append((x, rand_codebooks(g, 16, 256, 4), rand_codebooks(g, 16, 256, 4) * np.float16(0.3)))
+    outs = K.warm_encode_batch([(T(x, device), T(p, device), T(r, device)) for x, p, r in sets], fmt)
+    for (x, p, r), out in zip(sets, outs):
+        one = K.warm_encode(T(x, device), fmt, T(p, device), T(r, device))
+        for key in ("pq", "rvq", "sparse_idx", "sparse_val"):
+            assert np.array_equal(H(out[key]).view(np.uint8), H(one[key]).view(np.uint8)), key
+        if len(x):
+            ref = nx.ext_encode(x, p, r, 4)
+            assert np.array_equal(H(out["pq"]), ref["pq_codes"]) and np.array_equal(H(out["rvq"]), ref["rvq_codes"])
+            assert np.array_equal(H(out["sparse_val"]).view(np.uint16), ref["sparse_val"].view(np.uint16))
+    with pytest.raises(RuntimeError, match="one-launch encode"):
+        K.warm_encode_batch([(T(sets[0][0], device), T(rand_codebooks(g, 4, 256, 16), device), None)],
+                            K.WarmFormat(64, 4, 256, 0, 0, 0))
+
+
 @pytest.mark.parametrize("M,Mr", [(16, 16), (8, 8), (16, 0)])
 def test_sparse_fold_bit_exact(device, M, Mr):
     """Corrected coordinates fp16(K[idx] + val) equal the warm decode's value

@@ -600,3 +600,23 @@ def test_cpu_baseline_matches_oracle():
     b = nx.blockwise_attention(q, k, v, 0.125, 32)
     assert np.abs(a.astype(np.float32) - b.astype(np.float32)).max() <= 1e-3
     assert math.isfinite(float(a.astype(np.float32).sum()))
+
+
+def test_cpu_baseline_encode_matches_oracle():
+    """The timed torch-CPU encode (cdist^2 + argmin per subspace, both stages,
+    top-4) gives the oracle's codes and sparse entries on data without
+    near-ties (its fp32 distances carry no canonical rounding chain)."""
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    g = np.random.default_rng(5)
+    x = (g.standard_normal((512, 64)) * np.linspace(0.5, 2.0, 64)).astype(np.float16)
+    p = (g.standard_normal((8, 256, 8)) * 0.5).astype(np.float16)
+    r = (g.standard_normal((8, 256, 8)) * 0.2).astype(np.float16)
+    out = cb.warm_encode(torch.from_numpy(x), torch.from_numpy(p), torch.from_numpy(r), 4)
+    ref = nx.ext_encode(x, p, r, 4)
+    assert np.array_equal(out["pq"].numpy(), ref["pq_codes"])
+    assert np.array_equal(out["rvq"].numpy(), ref["rvq_codes"])
+    assert np.array_equal(out["sparse_idx"].numpy(), ref["sparse_idx"])
+    assert np.array_equal(out["sparse_val"].numpy().view(np.uint16), ref["sparse_val"].view(np.uint16))
