@@ -73,6 +73,7 @@ SIGNATURES = {
     "rfsn_warm_encode_workspace_bytes": (sz, [C.POINTER(Format), i64]),
     "rfsn_warm_encode": (i32, [C.POINTER(Format), vp, i64, i64, vp, vp, Codes, vp, sz, vp]),
     "rfsn_warm_encode_batch": (i32, [C.POINTER(Format), C.POINTER(EncodeJob), i32, vp]),
+    "rfsn_hot_append": (i32, [vp, vp, i64, i32, i32, i32, vp, vp, i64, i64, vp, vp]),
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),

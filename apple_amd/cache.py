@@ -441,8 +441,8 @@ class RFSNv10KVCacheMLX:
         self._vq: Optional[HybridQuantizerMLX] = None
         # drift guard of the score tables: running max |V| of the appended
         # values, the guard's input row and the last call's estimates
-        self._vabs = torch.zeros((), dtype=torch.float32, device=self.device)
-        self._guard: Optional[torch.Tensor] = None
+        self._guard = torch.zeros((1, 65), dtype=torch.float32, device=self.device)
+        self._vabs = self._guard[0, 64:]  # the row's V bound, updated by every append
         self._guard_key: Optional[Tuple[int, int]] = None
         self.last_drift: Optional[torch.Tensor] = None
         self.last_access_stats = self._empty_access_stats()
@@ -532,15 +532,14 @@ class RFSNv10KVCacheMLX:
 
     def _guard_tensor(self) -> torch.Tensor:
         """The drift guard's [1, 65] input: the K codebooks' weights (built once
-        per quantizer pair) and the running bound on |V^| kept by ``update``."""
+        per quantizer pair) and the running bound on |V^| kept by the appends."""
         key = (id(self._kq), id(self._vq))
         if self._guard_key != key:
-            g = torch.zeros((1, 65), dtype=torch.float32, device=self.device)
-            K.score_guard(self._kq.pq.codebooks, self._kq.rvq.codebooks, 0.0, out=g[0])
+            self._guard[0, :64] = K.score_guard(self._kq.pq.codebooks, self._kq.rvq.codebooks, 0.0)[:64]
             vp, vr = self._vq.pq.codebooks.float(), self._vq.rvq.codebooks.float()
             vcb = (vp.abs().amax(-2) + vr.abs().amax(-2)).amax()
-            g[0, 64] = torch.maximum(vcb, self._vabs)
-            self._guard, self._guard_key = g, key
+            torch.maximum(self._vabs, vcb.view(1), out=self._vabs)
+            self._guard_key = key
         return self._guard
 
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -567,6 +566,38 @@ class RFSNv10KVCacheMLX:
         self._hot_k[:, h + self.num_hot:h + need] = k.permute(1, 0, 2).to(self.device, torch.float16)
         self._hot_v[:, h + self.num_hot:h + need] = v.permute(1, 0, 2).to(self.device, torch.float16)
         self.num_hot = need
+
+    def _try_hot_append(self, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """The decode loop's common append (recency tiers): new tokens [T, H, D]
+        that the hot tier holds without demoting any (num_hot + T <=
+        hot_capacity) and its buffers hold at the current head.  One
+        ``rfsn_hot_append`` launch, which also folds |v| into the drift
+        guard's V bound.  Returns False, with the cache untouched, otherwise."""
+        T = int(k.shape[0])
+        if not self._recency or not T or self.num_hot + T > self.hot_capacity:
+            return False
+        t0 = self._hot_head + self.num_hot
+        cap = int(self._hot_k.shape[1])
+        if t0 + T > cap:
+            return False
+        if k.device != self.device or k.dtype != torch.float16 or not k.is_contiguous():
+            k = k.to(self.device, torch.float16).contiguous()
+        if v.device != self.device or v.dtype != torch.float16 or not v.is_contiguous():
+            v = v.to(self.device, torch.float16).contiguous()
+        if tuple(k.shape) != (T, self.H, self.D) or tuple(v.shape) != (T, self.H, self.D):
+            raise ValueError(f"new_keys and new_values must be [T, {self.H}, {self.D}]")
+        L.call("rfsn_hot_append", k.data_ptr(), v.data_ptr(), self.H * self.D, T, self.H, self.D,
+               self._hot_k.data_ptr(), self._hot_v.data_ptr(), cap, t0,
+               self._vabs.data_ptr() if self._guarded else None, K._stream(k))
+        self.num_hot += T
+        self.total_tokens += T
+        return True
+
+    def decode_session(self, q: torch.Tensor, quantizer: QuantizerArg,
+                       router: Optional[AsyncHierarchicalRouterMLX] = None, cold_attended: int = 0,
+                       out: Optional[torch.Tensor] = None) -> "DecodeSession":
+        """A prepared decode loop over this cache (``DecodeSession``)."""
+        return DecodeSession(self, q, quantizer, router, cold_attended, out)
 
     def _hot_pop_oldest(self, n: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Remove and return the n oldest hot tokens as [n, H, D]."""
@@ -606,9 +637,7 @@ class RFSNv10KVCacheMLX:
         values = new_values.to(self.device, torch.float16)
         num_tokens = int(keys.shape[0])
         if num_tokens and self._guarded:
-            torch.maximum(self._vabs, values.abs().amax().float(), out=self._vabs)
-            if self._guard is not None:
-                torch.maximum(self._guard[0, 64:], self._vabs.view(1), out=self._guard[0, 64:])
+            torch.maximum(self._vabs, values.abs().amax().float().view(1), out=self._vabs)
         if self._recency:
             self._update_recency(keys, values, disk_dir)
         else:
@@ -1437,6 +1466,77 @@ class RFSNv10KVCacheMLX:
             warm_rvq_bytes = rows * self.config.num_rvq_layers * 2
         return {"hot_bytes": hot_bytes, "warm_pq_bytes": warm_pq_bytes, "warm_rvq_bytes": warm_rvq_bytes,
                 "cold_chunks": len(self.cold_chunk_metadata), "cold_tokens": self.num_cold}
+
+
+class DecodeSession:
+    """The decode loop of rfsn_v10_mlx_ane_complete.py:138-158 over one cache:
+    each ``step(k, v)`` appends the new token(s) and attends the window with
+    the query buffer ``q`` (read at launch time, so the caller refills it in
+    place), writing ``out``.
+
+    While a step only adds hot tokens (``_try_hot_append``) and the router's
+    chunk set stays, the step re-issues one prepared fused launch with its hot
+    length grown in place: two launches and no host-side rebuilding.  Any
+    other step (a demotion into warm, a migration to cold, another chunk set)
+    goes through the cache's general ``update`` and rebuilds the launch.  The
+    query is the newest token, so every window token is allowed and the launch
+    carries no query positions (cache.py:395-428 with causal masking at the
+    newest position).  The split count is pinned at each rebuild, so the
+    launch's workspace stays valid as the window grows.  ``router`` ranks the
+    cold chunks (storage.py:203-234); ``cold_attended`` of them are attended,
+    made resident in device slots at each rebuild."""
+
+    def __init__(self, cache: RFSNv10KVCacheMLX, q: torch.Tensor, quantizer: QuantizerArg,
+                 router: Optional[AsyncHierarchicalRouterMLX] = None, cold_attended: int = 0,
+                 out: Optional[torch.Tensor] = None):
+        if not cache._recency:
+            raise ValueError("a decode session needs tier_policy='recency' (the newest tokens stay hot)")
+        self.cache = cache
+        self.q = q
+        self.quantizer = quantizer
+        self.router = router
+        self.cold_attended = int(cold_attended)
+        self.out = torch.empty_like(q) if out is None else out
+        self._launch: Optional[K.FusedLaunch] = None
+        self._ids: Optional[List[int]] = None
+        self.rebuilds = 0
+
+    def _chunk_set(self) -> Optional[List[int]]:
+        """The router's nearest ``cold_attended`` chunks, or None (the cache's
+        own choice: every cold chunk of the window) without a router."""
+        if self.router is None or not self.cold_attended:
+            return None
+        total = self.cache.total_tokens
+        return self.router.rank(total - 1, total)[:self.cold_attended]
+
+    def step(self, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        c = self.cache
+        T = int(k.shape[0])
+        fast = self._launch is not None and c._try_hot_append(k, v)
+        if not fast:
+            c.update(k, v, self.quantizer)
+        ids = self._chunk_set()
+        if fast and ids == self._ids:
+            p = self._launch.params
+            p.hot_len += T
+            p.max_tokens += T
+            return self._launch()
+        self._rebuild(ids)
+        return self.out
+
+    def _rebuild(self, ids: Optional[List[int]]) -> None:
+        c = self.cache
+        self.rebuilds += 1
+        if ids:
+            c.prefetch_cold_chunks(ids, wait=True)  # resident: the step is one launch
+        step = c.prepare(self.q, causal=False, cold_chunks=ids, out=self.out)
+        if isinstance(step, K.FusedLaunch):
+            p = step.params
+            p.splits = int(L.load().rfsn_fused_splits(C.byref(p)))  # pinned as the window grows
+            self._launch, self._ids = step, ids
+        else:  # chunks still copying in: no prepared launch to grow until they are resident
+            self._launch, self._ids = None, None
+        step()
 
 
 def _to_host_store(s: CompressedTensorMLX) -> CompressedTensorMLX:

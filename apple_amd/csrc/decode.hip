@@ -338,3 +338,58 @@ extern "C" int rfsn_kmeans_update(const void* x, int64_t n, int32_t D, int64_t l
                      sums, counts, (uint16_t*)cb);
   return check_launch("kmeans_update");
 }
+
+// ---------------------------------------------------------------- hot-tier append
+namespace rfsn {
+namespace {
+
+// One thread per 8 fp16 (16 bytes) of a (token, head) row of K or V:
+// hot[h][t0 + t][:] = src[t][h][:]; the V rows also fold max |v| into *vabs
+// (float bits compared as integers: |v| >= 0; NaN bits order above +inf).
+__global__ void __launch_bounds__(256)
+hot_append_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t ld_t, int T, int H, int D,
+                  uint16_t* __restrict__ hot_k, uint16_t* __restrict__ hot_v, int64_t hot_cap, int64_t t0,
+                  uint32_t* __restrict__ vabs) {
+  const int units = D / 8;
+  const int64_t per = (int64_t)T * H * units;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * per) return;
+  const bool is_v = i >= per;
+  const int64_t j = is_v ? i - per : i;
+  const int u = (int)(j % units), h = (int)((j / units) % H);
+  const int64_t t = j / ((int64_t)units * H);
+  const uint16_t* src = (is_v ? v : k) + t * ld_t + (int64_t)h * D + 8 * u;
+  uint16_t* dst = (is_v ? hot_v : hot_k) + ((int64_t)h * hot_cap + t0 + t) * D + 8 * u;
+  const uint4 w = *reinterpret_cast<const uint4*>(src);
+  *reinterpret_cast<uint4*>(dst) = w;
+  if (is_v && vabs != nullptr) {
+    uint32_t m = 0;
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m = max(m, (uint32_t)__builtin_bit_cast(uint32_t, fabsf(h2f((uint16_t)(ww[e] & 0xFFFFu)))));
+      m = max(m, (uint32_t)__builtin_bit_cast(uint32_t, fabsf(h2f((uint16_t)(ww[e] >> 16)))));
+    }
+    atomicMax(vabs, m);
+  }
+}
+
+}  // namespace
+}  // namespace rfsn
+
+extern "C" int rfsn_hot_append(const void* k, const void* v, int64_t ld_t, int32_t T, int32_t heads, int32_t D,
+                               void* hot_k, void* hot_v, int64_t hot_cap, int64_t t0, float* vabs, void* stream) {
+  RFSN_REQUIRE(T >= 0 && heads > 0 && D > 0 && D % 8 == 0, "hot_append: head_dim must be a multiple of 8");
+  RFSN_REQUIRE(T == 0 || (k && v && hot_k && hot_v), "hot_append: null pointer");
+  RFSN_REQUIRE(ld_t >= (int64_t)heads * D && ld_t % 8 == 0, "hot_append: bad token stride");
+  RFSN_REQUIRE(t0 >= 0 && t0 + T <= hot_cap, "hot_append: tokens past the hot buffers' capacity");
+  RFSN_REQUIRE(reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(hot_k) % 16 == 0 && reinterpret_cast<uintptr_t>(hot_v) % 16 == 0,
+               "hot_append: rows must be 16-byte aligned");
+  if (T == 0) return RFSN_OK;
+  const int64_t work = 2 * (int64_t)T * heads * (D / 8);
+  hipLaunchKernelGGL(hot_append_kernel, dim3((unsigned)ceil_div(work, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)k, (const uint16_t*)v, ld_t, (int)T, (int)heads, (int)D, (uint16_t*)hot_k,
+                     (uint16_t*)hot_v, hot_cap, t0, reinterpret_cast<uint32_t*>(vabs));
+  return check_launch("hot_append");
+}

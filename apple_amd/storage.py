@@ -278,6 +278,7 @@ class AsyncHierarchicalRouterMLX:
         self._max_cache_size = 16
         self._pending_prefetch: set = set()
         self._bound = None
+        self._rank_memo = None  # (key, last chunk start, order) of the bound cache's last ranking
 
     def bind(self, cache) -> "AsyncHierarchicalRouterMLX":
         self._bound = cache
@@ -299,10 +300,21 @@ class AsyncHierarchicalRouterMLX:
         end_chunk = max(start_chunk, (current_position + context_window) // cs)
         if self._bound is not None:
             ids = self._bound.cold_chunk_ids()
+            # a decode loop asks again every token: while the bound cache's id
+            # list and the candidate range stay, and every candidate starts at
+            # or before the position (distance = position - start, so the
+            # order is descending id whatever the position), the last order holds
+            key = (id(ids), len(ids), start_chunk, end_chunk)
+            memo = self._rank_memo
+            if memo is not None and memo[0] == key and current_position >= memo[1]:
+                return list(memo[2])
             cands = ids[bisect.bisect_left(ids, start_chunk):bisect.bisect_right(ids, end_chunk)]
         else:
             cands = [cid for cid in range(start_chunk, end_chunk + 1) if self._exists(cid)]
         cands.sort(key=lambda cid: abs(cid * cs - current_position))
+        if self._bound is not None:
+            last = max(cands) * cs if cands else 0
+            self._rank_memo = (key, last, tuple(cands)) if current_position >= last else None
         return cands
 
     async def predict_and_prefetch(self, current_position: int, context_window: int, top_k: int = 2) -> List[int]:

@@ -510,7 +510,7 @@ def bench_stream(w, cache, router, quantizers, q, steps, dev) -> dict:
     import torch
     from apple_amd.workloads import make_sequence
 
-    kn, vn, _, _ = make_sequence(w, 1, tokens=2 * steps)
+    kn, vn, _, _ = make_sequence(w, 1, tokens=3 * steps)
     kn, vn = kn.to(dev), vn.to(dev)
     chunks0, tok0 = len(cache.cold_chunk_metadata), cache.total_tokens
     log(f"streaming {steps} appends")
@@ -531,8 +531,25 @@ def bench_stream(w, cache, router, quantizers, q, steps, dev) -> dict:
         cache.attention_forward(q, causal=True, cold_chunks=ids)
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # the same loop through a decode session: one prepared launch grown in
+    # place while a step only adds a hot token and the chunk set stays
+    sess = cache.decode_session(q, quantizers, router=router, cold_attended=w.cold_attended)
+    sess.step(kn[2 * steps:2 * steps + 1], vn[2 * steps:2 * steps + 1])
+    r0 = sess.rebuilds
+    log(f"streaming {steps - 1} decode-session steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(2 * steps + 1, 3 * steps):
+        sess.step(kn[i:i + 1], vn[i:i + 1])
+    torch.cuda.synchronize()
+    session_ms = (time.perf_counter() - t0) * 1e3 / (steps - 1)
+    pos = cache.total_tokens - 1
+    ref = cache.attention_forward(q, causal=True, cold_chunks=router.rank(pos, cache.total_tokens)[:w.cold_attended])
     return {"append_ms_per_token": round(append_ms, 4), "decode_step_ms": round(step_ms, 4),
             "decode_tokens_per_s": round(1e3 / step_ms, 1), "steps": steps,
+            "session_step_ms": round(session_ms, 4), "session_tokens_per_s": round(1e3 / session_ms, 1),
+            "session_rebuilds": sess.rebuilds - r0,
+            "session_max_abs_vs_attention_forward": float((sess.out.float() - ref.float()).abs().max()),
             "tokens_appended": cache.total_tokens - tok0,
             "chunks_moved_to_cold": len(cache.cold_chunk_metadata) - chunks0,
             "chunks_moved_during_appends": chunks1 - chunks0,

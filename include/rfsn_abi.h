@@ -198,6 +198,15 @@ int rfsn_pack_score_codes(const uint8_t* pq_src_dev, const uint8_t* rvq_src_dev,
                           uint8_t* pq_dst_dev, uint8_t* rvq_dst_dev, uint8_t* sparse_idx_dst_dev,
                           uint16_t* sparse_val_dst_dev, int64_t dst_tokens, int64_t t_base, void* stream);
 
+/* Hot-tier append: hot_k[h][t0 + t][:] = k[t][h][:] (and the same for V) for
+ * t < T, with the hot tier as [heads][hot_cap][D] fp16 and the new tokens as
+ * rows of stride ld_t elements; vabs (may be NULL) receives max(|vabs|, |v|)
+ * over the new values (the score tables' drift guard bounds |V| by it).  One
+ * launch.  Replaces the hot-tier write of the decode step's append
+ * (cache.py:89-120: mx.concatenate of the new tokens onto the hot arrays). */
+int rfsn_hot_append(const void* k_dev, const void* v_dev, int64_t ld_t, int32_t T, int32_t heads, int32_t D,
+                    void* hot_k_dev, void* hot_v_dev, int64_t hot_cap, int64_t t0, float* vabs_dev, void* stream);
+
 /* Fused warm-tier dequant + exact decode attention over [hot | segments] (or
  * [segments | hot]).  Replaces RFSNv10KVCacheMLX.attention_forward
  * (cache.py:395-428) = materialize_window (cache.py:344-393) +

@@ -567,6 +567,60 @@ def test_prefetch_ahead_decode_loop(device):
         assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL, step
 
 
+def test_decode_session_streaming(device):
+    """A decode loop through ``DecodeSession``: 90 one-token steps on a cache
+    with pinned cold chunks (64 hot tokens, so a 32-token block is demoted
+    every 32 steps, and warm overflow migrates whole 64-token chunks), the
+    router's 4 nearest chunks attended.  Every step is within 2e-3 of the
+    oracle over the step's window; the hot tier holds the newest tokens bit
+    for bit; the launch is rebuilt only when a step demotes, migrates or
+    changes the chunk set."""
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import AsyncHierarchicalRouterMLX, RFSNConfig
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    total0, steps, nh, nw, chunk, Hq, Hkv, D, M = 1500, 90, 64, 256, 64, 8, 4, 64, 16
+    g = rng(97)
+    keys, values = _kv(g, total0 + steps, Hkv, D)
+    cbs = {n: rand_codebooks(g, M, 256, D // M) for n in ("kp", "vp")}
+    cbs.update({n: rand_codebooks(g, M, 256, D // M) * np.float16(0.35) for n in ("kr", "vr")})
+    cfg = RFSNConfig(num_heads=Hq, head_dim=D, num_subspaces=M, subspace_dim=D // M, num_rvq_layers=1,
+                     rvq_codebook_size=256, hot_capacity=nh, warm_capacity=nw, block_size_seq=128,
+                     num_kv_heads=Hkv, rvq_subspaces=M, sparse_topk=4, tier_policy="recency",
+                     cold_medium="pinned", cold_chunk_tokens=chunk)
+    kq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["kp"]), rvq_codebooks=torch.from_numpy(cbs["kr"]))
+    vq = HybridQuantizerMLX(cfg, pq_codebooks=torch.from_numpy(cbs["vp"]), rvq_codebooks=torch.from_numpy(cbs["vr"]))
+    cache = RFSNv10KVCacheMLX(cfg, device=device, cold_slots=16)
+    cache.update(T(keys[:total0], device), T(values[:total0], device), (kq, vq))
+    dec = []
+    for x, p, r in ((keys, cbs["kp"], cbs["kr"]), (values, cbs["vp"], cbs["vr"])):
+        enc = nx.ext_encode(x.reshape(-1, D), p, r, 4)
+        dec.append(nx.ext_decode(enc["pq_codes"], p, enc["rvq_codes"], r, enc["sparse_idx"],
+                                 enc["sparse_val"]).reshape(-1, Hkv, D))
+    router = AsyncHierarchicalRouterMLX(cfg).bind(cache)
+    q = randn16(g, 1, Hq, D)
+    qd = T(q, device)
+    sess = cache.decode_session(qd, (kq, vq), router=router, cold_attended=4)
+    changes = 0
+    prev = None
+    for i in range(steps):
+        t = total0 + i
+        before = (cache.num_warm, cache.num_cold)
+        out = sess.step(T(keys[t:t + 1], device), T(values[t:t + 1], device))
+        ids = router.rank(t, t + 1)[:4]
+        changes += (cache.num_warm, cache.num_cold) != before or ids != prev
+        prev = ids
+        pos, wk, wv = _cold_window(ids, chunk, cache.num_cold, t + 1, cache.num_hot, keys, values, dec)
+        ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, False, None)
+        err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
+        assert err <= TOL, (i, err)
+    total = total0 + steps
+    assert cache.total_tokens == total and cache.num_hot + cache.num_warm + cache.num_cold == total
+    for tier, src in ((cache.hot_keys, keys), (cache.hot_values, values)):  # [T_hot, H, D], oldest first
+        assert np.array_equal(H(tier.contiguous()).view(np.uint16), src[total - cache.num_hot:total].view(np.uint16))
+    assert sess.rebuilds <= changes + 1 and sess.rebuilds < steps // 4, (sess.rebuilds, changes)
+
+
 def test_cold_chunks_npz_roundtrip(device, tmp_path):
     """The pinned cold tier written as the reference's chunk files
     (layer{L}_chunk{id}.npz, its key names) and read back into an empty cache:

@@ -372,3 +372,31 @@ def test_score_guard_weights():
         W = ((pf * pf).mean(1) + (rf * rf).mean(1)).reshape(64) \
             + np.repeat((pf * pf).sum(2).mean(1) + (rf * rf).sum(2).mean(1), 4)
         np.testing.assert_allclose(one[:64].numpy(), W, rtol=1e-5)
+
+
+def test_router_rank_memo_matches_fresh_ranking():
+    """The bound router's memoized ranking (reused while the cache's chunk
+    ids and the candidate range stay, and every candidate starts at or before
+    the position) equals a fresh ranking at every position, including when
+    the position falls back before the last chunk and when chunks are added."""
+    from apple_amd.storage import AsyncHierarchicalRouterMLX, RFSNConfig
+
+    cfg = RFSNConfig(num_heads=4, head_dim=64, num_subspaces=16, subspace_dim=4, cold_chunk_tokens=64,
+                     tier_policy="recency", cold_medium="pinned")
+
+    class Ids:  # the bound cache's side of the ranking: its config and sorted chunk ids
+        config = cfg
+
+        def __init__(self):
+            self.ids = list(range(0, 40, 2))
+
+        def cold_chunk_ids(self):
+            return self.ids
+
+    src = Ids()
+    memo = AsyncHierarchicalRouterMLX(cfg).bind(src)
+    for pos in [2600, 2601, 2700, 1000, 2601, 5000, 5001]:
+        for window in (pos + 1, 700):
+            fresh = AsyncHierarchicalRouterMLX(cfg).bind(src).rank(pos, window)
+            assert memo.rank(pos, window) == fresh, (pos, window)
+        src.ids = src.ids + [src.ids[-1] + 1]  # a new list object: chunks added
