@@ -57,6 +57,25 @@ class FusedParams(C.Structure):
                 ("guard", vp), ("drift", vp), ("guard_tol", f32)]
 
 
+class RefStoreCodes(C.Structure):
+    _fields_ = [("pq", vp), ("rvq", vp), ("active", vp)]
+
+
+class RefSegment(C.Structure):
+    _fields_ = [("k", RefStoreCodes), ("v", RefStoreCodes), ("exact_k", vp), ("exact_v", vp),
+                ("exact_token_stride", i64), ("exact_head_stride", i64), ("token0", i64), ("len", i32),
+                ("pos0", i32)]
+
+
+class RefParams(C.Structure):
+    _fields_ = [("head_dim", i32), ("pq_subspaces", i32), ("pq_centroids", i32), ("rvq_layers", i32),
+                ("rvq_centroids", i32), ("batch", i32), ("q_heads", i32), ("kv_heads", i32),
+                ("q", vp), ("out", vp), ("scale", f32), ("causal", i32), ("qpos", vp),
+                ("segments", vp), ("num_segments", i32), ("total_tokens", i32),
+                ("k_pq_cb", vp), ("v_pq_cb", vp), ("k_rvq_cb", vp), ("v_rvq_cb", vp),
+                ("splits", i32), ("workspace", vp), ("workspace_bytes", sz)]
+
+
 class EncodeJob(C.Structure):
     _fields_ = [("x", vp), ("n", i64), ("ldx", i64), ("pq_cb", vp), ("rvq_cb", vp), ("out", Codes)]
 
@@ -74,6 +93,8 @@ SIGNATURES = {
     "rfsn_warm_encode": (i32, [C.POINTER(Format), vp, i64, i64, vp, vp, Codes, vp, sz, vp]),
     "rfsn_warm_encode_batch": (i32, [C.POINTER(Format), C.POINTER(EncodeJob), i32, vp]),
     "rfsn_hot_append": (i32, [vp, vp, i64, i32, i32, i32, vp, vp, i64, i64, vp, vp]),
+    "rfsn_ref_attention_workspace_bytes": (sz, [C.POINTER(RefParams)]),
+    "rfsn_ref_attention": (i32, [C.POINTER(RefParams), vp]),
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),

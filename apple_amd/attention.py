@@ -76,8 +76,45 @@ class RFSNHybridAttentionMLX:
                  query_positions: Positions = None) -> torch.Tensor:
         if key_store.num_tokens != value_store.num_tokens:
             raise ValueError("Key/value stores must have the same token count")
+        if self._fused_ok(q, key_store, quantizer):
+            return self._fused(q, key_store, value_store, quantizer, causal, query_positions)
         decoded_keys = _decode_compressed_tensor(key_store, quantizer)
         decoded_values = _decode_compressed_tensor(value_store, quantizer)
         return _blockwise_exact_attention(q=q, keys=decoded_keys, values=decoded_values, scale=self.scale,
                                           block_size=self.block_size, causal=causal,
                                           query_positions=query_positions)
+
+    def _fused_ok(self, q: torch.Tensor, key_store: CompressedTensorMLX, quantizer: HybridQuantizerMLX) -> bool:
+        if quantizer.subspace or q.dim() != 3 or key_store.num_heads <= 0:
+            return False
+        M, C, _ = quantizer.pq.codebooks.shape
+        return (q.shape[-1] == quantizer.config.head_dim and q.shape[1] % key_store.num_heads == 0
+                and K.ref_attention_ok(int(q.shape[-1]), int(M), int(C), int(q.shape[1]), key_store.num_heads,
+                                       True))
+
+    def _fused(self, q, key_store, value_store, quantizer, causal, query_positions) -> torch.Tensor:
+        """Decode-and-attend in one kernel: each K/V vector is rebuilt in
+        registers with the reference's rounding (quantization.py:310-319) and
+        never written to HBM (rfsn_ref_attention)."""
+        B, Hq, _ = q.shape
+        T = key_store.num_tokens
+        if T == 0:
+            return torch.zeros_like(q)
+        dev = quantizer.device
+        kst = _on(key_store, dev)
+        vst = _on(value_store, dev)
+        pos = _normalize_query_positions(query_positions, B, Hq, T - 1, dev) if causal else None
+        cb, rcb = quantizer.pq.codebooks, quantizer.rvq.codebooks
+        out = K.ref_attention(q.to(device=dev, dtype=torch.float16), kv_heads=key_store.num_heads,
+                              scale=self.scale, causal=causal, qpos=pos,
+                              segments=[K.ref_store_segment(kst, vst, 0, T, 0)], k_pq_cb=cb, v_pq_cb=cb,
+                              k_rvq_cb=rcb, v_rvq_cb=rcb)
+        return out.to(q.dtype)
+
+
+def _on(store: CompressedTensorMLX, device) -> CompressedTensorMLX:
+    if store.pq_codes.device == torch.device(device):
+        return store
+    d = lambda t: None if t is None else t.to(device)
+    return CompressedTensorMLX(d(store.pq_codes), d(store.rvq_codes), d(store.rvq_mask), d(store.rvq_offsets),
+                               store.num_heads, d(store.sparse_idx), d(store.sparse_val))

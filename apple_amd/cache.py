@@ -1309,6 +1309,9 @@ class RFSNv10KVCacheMLX:
         if q.shape[-1] != self.D or q.dim() != 3 or q.shape[1] % self.H:
             raise ValueError("q must be [B, Hq, D] with Hq a multiple of the cache's KV heads")
         if not self._fused_ok(int(q.shape[1])):
+            if self._ref_ok(int(q.shape[1])):
+                return self._ref_forward(q, causal, query_positions, router, current_position, context_window,
+                                         cold_chunks)
             keys, values, adjusted = self.materialize_window(query_positions, context_window, router,
                                                              current_position, cold_chunks)
             self.last_access_stats["query_tokens"] = int(q.shape[0])
@@ -1318,6 +1321,67 @@ class RFSNv10KVCacheMLX:
                                               block_size=self.config.block_size_seq, causal=causal,
                                               query_positions=adjusted)
         return self._fused_forward(q, causal, query_positions, router, current_position, context_window, cold_chunks)
+
+    def _ref_ok(self, q_heads: int) -> bool:
+        """The reference-format kernel (PQ + gated full-dimension RVQ decoded
+        on the fly) serves this cache's codebooks and head grouping."""
+        if self._kq is None or self._subspace:
+            return False
+        kq, vq = self._kq, self._vq
+        M, C, _ = kq.pq.codebooks.shape
+        if tuple(vq.pq.codebooks.shape) != tuple(kq.pq.codebooks.shape):
+            return False
+        if tuple(kq.rvq.codebooks.shape) != tuple(vq.rvq.codebooks.shape):
+            return False
+        shared = kq.pq.codebooks.data_ptr() == vq.pq.codebooks.data_ptr()
+        return K.ref_attention_ok(self.D, int(M), int(C), q_heads, self.H, shared)
+
+    def _ref_forward(self, q, causal, query_positions, router, current_position, context_window, cold_chunks):
+        """attention_forward over reference-format tiers without decoding the
+        window into HBM: the plan of materialize_window (cache.py:344-393)
+        becomes a segment table in window order -- the hot tier as exact rows
+        of its ring, warm and cold stores as their codes -- and one launch
+        attends it, rebuilding each K/V vector in registers with the
+        reference's rounding (quantization.py:310-319)."""
+        start, end, adjusted = self._window_bounds(query_positions, context_window, current_position)
+        stats = self._empty_access_stats()
+        stats["window_start"], stats["window_end"] = start, end
+        stats["window_tokens"] = max(0, end - start)
+        stats["context_window"] = -1 if context_window is None else context_window
+        stats["used_router"] = int(router is not None)
+        plan = self._plan(start, end, stats, router, current_position, context_window, cold_chunks)
+        spans = self._tier_spans()
+        segs, pos = [], 0
+        for kind, x in plan:
+            if kind == "hot":
+                a, b = x[0] - spans["hot"][0], x[1] - spans["hot"][0]
+                hk, hv = self._hot_k, self._hot_v
+                segs.append(K.ref_exact_segment(hk, hv, hk.stride(1), hk.stride(0), self._hot_head + a, b - a, pos))
+            elif kind == "warm":
+                a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
+                segs.append(K.ref_store_segment(self.warm_keys, self.warm_values, a, b - a, pos))
+            else:
+                meta, ov, got = x
+                if got is None or self.config.cold_medium == "pinned":
+                    loaded = self.load_cold_chunk(meta["chunk_id"])
+                else:
+                    loaded = got
+                a, b = ov[0] - meta["start_token"], ov[1] - meta["start_token"]
+                kst = _to_device_store(self._chunk_store(loaded, "key"), self.device)
+                vst = _to_device_store(self._chunk_store(loaded, "value"), self.device)
+                segs.append(K.ref_store_segment(kst, vst, a, b - a, pos))
+            pos += segs[-1]["len"]
+        stats["query_tokens"] = int(q.shape[0])
+        self.last_access_stats = dict(stats)
+        if pos == 0:
+            return torch.zeros_like(q)
+        B, Hq = int(q.shape[0]), int(q.shape[1])
+        qpos = _normalize_query_positions(adjusted, B, Hq, pos - 1, self.device) if causal else None
+        kq, vq = self._kq, self._vq
+        out = K.ref_attention(q.to(torch.float16), kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos,
+                              segments=segs, k_pq_cb=kq.pq.codebooks, v_pq_cb=vq.pq.codebooks,
+                              k_rvq_cb=kq.rvq.codebooks, v_rvq_cb=vq.rvq.codebooks)
+        return out.to(q.dtype)
 
     def prepare(self, q: torch.Tensor, causal: bool = True, query_positions=None,
                 router: Optional[AsyncHierarchicalRouterMLX] = None, current_position: Optional[int] = None,

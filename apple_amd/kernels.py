@@ -8,6 +8,7 @@ library itself never allocates device memory) and raises on failure.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -551,6 +552,117 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     if not launch:
         return fl
     fl()
+    return out
+
+
+# --------------------------------------------------------------------------
+# reference-format attention (PQ + gated full-dimension RVQ, decoded on the fly)
+# --------------------------------------------------------------------------
+
+_ACTIVE_MAPS: Dict[int, tuple] = {}  # id(offsets) -> (weakref, rows, map)
+
+
+def active_map(offsets: torch.Tensor, rows: int) -> torch.Tensor:
+    """int32 [rows]: row r's index into the store's RVQ codes, or -1 -- the
+    scatter of the reference's decode (quantization.py:273-274: correction row
+    offsets[a] = codes row a); memoized per offsets tensor."""
+    key = id(offsets)
+    hit = _ACTIVE_MAPS.get(key)
+    if hit is not None and hit[0]() is offsets and hit[1] == rows:
+        return hit[2]
+    out = torch.full((rows,), -1, dtype=torch.int32, device=offsets.device)
+    a = int(offsets.shape[0])
+    if a:
+        out[offsets.long()] = torch.arange(a, dtype=torch.int32, device=offsets.device)
+    _ACTIVE_MAPS[key] = (weakref.ref(offsets, lambda _r, k=key: _ACTIVE_MAPS.pop(k, None)), rows, out)
+    return out
+
+
+def ref_store_segment(key_store, value_store, token0: int, length: int, pos0: int) -> dict:
+    """A coded segment of tokens token0 .. token0+length-1 of reference-format
+    stores (pq_codes [T, H, M] u8, rvq_codes [A, L] u16 placed by rvq_offsets
+    [A] over the T*H rows)."""
+    seg = {"len": int(length), "pos0": int(pos0), "token0": int(token0), "exact": None}
+    if token0 < 0 or length < 0 or token0 + length > min(key_store.num_tokens, value_store.num_tokens):
+        raise ValueError("segment tokens outside the stores")
+    for name, st in (("k", key_store), ("v", value_store)):
+        pq = _contig(st.pq_codes)
+        a = int(st.rvq_codes.shape[0]) if st.rvq_codes.dim() == 2 else 0
+        rows = int(pq.shape[0]) * int(pq.shape[1])
+        seg[name] = (pq, _contig(st.rvq_codes) if a else None, active_map(st.rvq_offsets, rows) if a else None)
+    return seg
+
+
+def ref_exact_segment(k: torch.Tensor, v: torch.Tensor, token_stride: int, head_stride: int, token0: int,
+                      length: int, pos0: int) -> dict:
+    """An exact segment of [heads, ..., D] fp16 buffers: (t, h, d) at base +
+    t * token_stride + h * head_stride + d (elements)."""
+    for t in (k, v):
+        if t.dtype != torch.float16 or t.stride(-1) != 1:
+            raise ValueError("exact rows must be fp16 with unit stride over head_dim")
+        hi = (token0 + length - 1) * token_stride + (t.shape[0] - 1) * head_stride + t.shape[-1] if length else 0
+        if token0 < 0 or length < 0 or hi > t.numel():
+            raise ValueError("exact segment outside its buffer")
+    return {"len": int(length), "pos0": int(pos0), "token0": int(token0),
+            "exact": (k, v, int(token_stride), int(head_stride)), "k": None, "v": None}
+
+
+def ref_attention_ok(head_dim: int, M: int, C: int, q_heads: int, kv_heads: int, shared_cb: bool) -> bool:
+    """Whether ``rfsn_ref_attention`` serves the shape."""
+    tab = head_dim * C * 2 * (1 if shared_cb else 2)
+    return (head_dim in (64, 128, 256) and M in (4, 8, 16, 32) and head_dim % M == 0 and 1 <= C <= 256
+            and kv_heads > 0 and q_heads % kv_heads == 0 and q_heads // kv_heads <= 8 and tab <= 160 * 1024)
+
+
+def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, qpos: Optional[torch.Tensor],
+                  segments: Sequence[dict], k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor,
+                  k_rvq_cb: Optional[torch.Tensor], v_rvq_cb: Optional[torch.Tensor],
+                  out: Optional[torch.Tensor] = None, splits: int = 0) -> torch.Tensor:
+    """Attention of q [B, Hq, D] over the window of ``segments`` (window
+    order; ``ref_store_segment`` / ``ref_exact_segment``), decoding the coded
+    ones on the fly (``rfsn_ref_attention``)."""
+    _dev(q, "ref_attention")
+    q = _contig(q)
+    B, Hq, D = q.shape
+    out = torch.empty_like(q) if out is None else out
+    total = sum(s["len"] for s in segments)
+    if total == 0:
+        return out.zero_()
+    keep = [q, out]
+    arr = (L.RefSegment * len(segments))()
+    for i, sd in enumerate(segments):
+        seg = arr[i]
+        seg.token0, seg.len, seg.pos0 = sd["token0"], sd["len"], sd["pos0"]
+        if sd["exact"] is not None:
+            ek, ev, ts, hs = sd["exact"]
+            seg.exact_k, seg.exact_v = ek.data_ptr(), ev.data_ptr()
+            seg.exact_token_stride, seg.exact_head_stride = ts, hs
+            keep += [ek, ev]
+        else:
+            for name, codes in (("k", seg.k), ("v", seg.v)):
+                pq, rvq, act = sd[name]
+                codes.pq, codes.rvq, codes.active = pq.data_ptr(), L.ptr(rvq), L.ptr(act)
+                keep += [pq, rvq, act]
+    raw = torch.frombuffer(bytearray(C.string_at(C.addressof(arr), C.sizeof(arr))), dtype=torch.uint8)
+    dev_segs = raw.to(q.device, non_blocking=False)
+    M, Cn, _ = k_pq_cb.shape
+    p = L.RefParams()
+    p.head_dim, p.pq_subspaces, p.pq_centroids = D, M, Cn
+    p.rvq_layers = 0 if k_rvq_cb is None else int(k_rvq_cb.shape[0])
+    p.rvq_centroids = 0 if k_rvq_cb is None else int(k_rvq_cb.shape[1])
+    p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
+    p.q, p.out, p.scale, p.causal = q.data_ptr(), out.data_ptr(), float(scale), int(causal)
+    qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)
+    p.qpos = L.ptr(qp)
+    p.segments, p.num_segments, p.total_tokens = dev_segs.data_ptr(), len(segments), total
+    cbs = [_contig(t) if t is not None else None for t in (k_pq_cb, v_pq_cb, k_rvq_cb, v_rvq_cb)]
+    p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
+    p.splits = splits
+    wsb = L.load().rfsn_ref_attention_workspace_bytes(C.byref(p))
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    L.call("rfsn_ref_attention", C.byref(p), _stream(q))
+    keep += [dev_segs, qp, ws, *cbs]  # alive until the launch is queued (the stream orders the reads)
     return out
 
 

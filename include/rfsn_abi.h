@@ -331,6 +331,67 @@ int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
 #define RFSN_FUSED_SCRATCH_BYTES (4u << 20)
 int rfsn_fused_decode_attention_noalloc(const rfsn_fused_params* p, void* stream);
 
+/* ---------------------------------------------------------------- reference-format attention
+ * Fused decode attention over reference-format compressed stores: PQ codes
+ * [T][heads][M] u8 with the gated full-dimension RVQ correction (codes
+ * [A][L] u16 of the active rows), decoded on the fly as quantization.py:
+ * 310-319 does (corr = fp16(sum_l fl32(C_l[code_l])), K = fp16(fl32(base) +
+ * fl32(corr)), corr = 0 for inactive rows), and exact segments (the hot
+ * tier).  Replaces RFSNHybridAttentionMLX.__call__ (attention.py:150-171)
+ * and attention_forward over reference-format tiers (cache.py:395-428,
+ * materialize_window + _blockwise_exact_attention) without writing the
+ * decoded window to HBM.  head_dim 64, 128 or 256; M in {4, 8, 16, 32}
+ * dividing head_dim, C <= 256 PQ centroids (the PQ codebooks of K and V must
+ * fit 160 KB of LDS together, or one when K and V share it); L RVQ layers of
+ * C_r <= 65536 codewords; at most 8 query heads per KV head.  B queries share
+ * the segments; segments are in window order. */
+typedef struct rfsn_ref_store_codes {
+  const uint8_t* pq;     /* [T][heads][M] u8 (4-byte aligned); NULL: an exact segment */
+  const uint16_t* rvq;   /* [A][L] u16 codes of the active rows                         */
+  const int32_t* active; /* [T][heads]: the row's index into rvq, or -1; NULL: none     */
+} rfsn_ref_store_codes;
+
+typedef struct rfsn_ref_segment {
+  rfsn_ref_store_codes k;
+  rfsn_ref_store_codes v;
+  const void* exact_k;         /* exact segments: fp16 (t, h, d) at exact + t*token_stride + h*head_stride + d */
+  const void* exact_v;
+  int64_t exact_token_stride;  /* elements */
+  int64_t exact_head_stride;   /* elements */
+  int64_t token0;              /* the segment's first window token is token token0 of its store */
+  int32_t len;                 /* tokens */
+  int32_t pos0;                /* window position of the segment's first token */
+} rfsn_ref_segment;
+
+typedef struct rfsn_ref_params {
+  int32_t head_dim;
+  int32_t pq_subspaces;
+  int32_t pq_centroids;
+  int32_t rvq_layers;     /* L, 0 = no RVQ */
+  int32_t rvq_centroids;  /* C_r */
+  int32_t batch;          /* B queries */
+  int32_t q_heads;
+  int32_t kv_heads;
+  const void* q;          /* [B][Hq][D] fp16 */
+  void* out;              /* [B][Hq][D] fp16 */
+  float scale;
+  int32_t causal;
+  const int32_t* qpos;    /* [B][Hq] window positions, or NULL */
+  const rfsn_ref_segment* segments;  /* device array, window order */
+  int32_t num_segments;
+  int32_t total_tokens;   /* sum of the segments' lengths (> 0) */
+  const void* k_pq_cb;    /* [M][C][d] fp16 */
+  const void* v_pq_cb;
+  const void* k_rvq_cb;   /* [L][C_r][D] fp16 */
+  const void* v_rvq_cb;
+  int32_t splits;         /* token splits per (query, KV head); 0 = auto */
+  void* workspace;        /* split partials: rfsn_ref_attention_workspace_bytes */
+  size_t workspace_bytes;
+} rfsn_ref_params;
+
+size_t rfsn_ref_attention_workspace_bytes(const rfsn_ref_params* p);
+int rfsn_ref_attention(const rfsn_ref_params* p, void* stream);
+
 /* ---------------------------------------------------------------- k-means
  * One Lloyd update of PQ codebooks (rfsn_v10_mlx_ane_complete.py:197-207):
  * every centroid with members becomes fp16(fp32 mean of its members); empty

@@ -62,6 +62,9 @@ def test_struct_layout_matches_c(tmp_path):
         "rfsn_segment": ["k", "v", "head_stride", "len", "pos0"],
         "rfsn_fused_params": [f for f, _ in _lib.FusedParams._fields_],
         "rfsn_copy": ["dst_dev", "src_host", "bytes"],
+        "rfsn_ref_store_codes": [f for f, _ in _lib.RefStoreCodes._fields_],
+        "rfsn_ref_segment": [f for f, _ in _lib.RefSegment._fields_],
+        "rfsn_ref_params": [f for f, _ in _lib.RefParams._fields_],
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "rfsn_abi.h"', "int main(void) {"]
     for s, fs in fields.items():
@@ -75,7 +78,8 @@ def test_struct_layout_matches_c(tmp_path):
     got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
                                                   check=True).stdout.splitlines())
     py = {"rfsn_format": _lib.Format, "rfsn_codes": _lib.Codes, "rfsn_segment": _lib.Segment,
-          "rfsn_fused_params": _lib.FusedParams, "rfsn_copy": _lib.Copy}
+          "rfsn_fused_params": _lib.FusedParams, "rfsn_copy": _lib.Copy, "rfsn_ref_store_codes": _lib.RefStoreCodes,
+          "rfsn_ref_segment": _lib.RefSegment, "rfsn_ref_params": _lib.RefParams}
     for s, cls in py.items():
         assert int(got[s]) == ctypes.sizeof(cls), s
         for f in fields[s]:
@@ -117,3 +121,33 @@ def test_noalloc_rejects_oversized_partials_on_the_host(lib):
     msg = lib.rfsn_last_error()
     assert str(need).encode() in msg and b"scratch" in msg
     assert lib.rfsn_fused_decode_attention_noalloc(None, None) == -1
+
+
+def test_ref_attention_validation(lib):
+    """rfsn_ref_attention rejects shapes outside its kernels on the host."""
+    from apple_amd import _lib
+
+    assert lib.rfsn_ref_attention(None, None) == -1
+    p = _lib.RefParams()
+    p.head_dim, p.pq_subspaces, p.pq_centroids = 96, 8, 256
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"head_dim" in lib.rfsn_last_error()
+    p.head_dim, p.pq_subspaces = 128, 2
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"num_subspaces" in lib.rfsn_last_error()
+    p.pq_subspaces, p.batch, p.q_heads, p.kv_heads = 8, 1, 12, 1
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"at most 8" in lib.rfsn_last_error()
+    p.q_heads, p.kv_heads = 4, 4
+    p.q = p.out = p.k_pq_cb = p.v_pq_cb = 16
+    p.head_dim, p.pq_centroids = 256, 256  # 2 x 128 KB of PQ tables (K and V differ)
+    p.v_pq_cb = 32
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"LDS" in lib.rfsn_last_error()
+    p.head_dim, p.total_tokens = 128, 0
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"empty window" in lib.rfsn_last_error()
+    p.total_tokens, p.num_segments, p.segments = 4096, 1, 64
+    assert lib.rfsn_ref_attention_workspace_bytes(ctypes.byref(p)) > 0  # 4 units: split
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"workspace" in lib.rfsn_last_error()
