@@ -58,7 +58,7 @@ class FusedParams(C.Structure):
 
 
 class RefStoreCodes(C.Structure):
-    _fields_ = [("pq", vp), ("rvq", vp), ("active", vp)]
+    _fields_ = [("pq", vp), ("rvq", vp), ("active", vp), ("rvq_sub", vp), ("sparse_idx", vp), ("sparse_val", vp)]
 
 
 class RefSegment(C.Structure):
@@ -69,7 +69,7 @@ class RefSegment(C.Structure):
 
 class RefParams(C.Structure):
     _fields_ = [("head_dim", i32), ("pq_subspaces", i32), ("pq_centroids", i32), ("rvq_layers", i32),
-                ("rvq_centroids", i32), ("batch", i32), ("q_heads", i32), ("kv_heads", i32),
+                ("rvq_centroids", i32), ("rvq_subspaces", i32), ("sparse_k", i32), ("batch", i32), ("q_heads", i32), ("kv_heads", i32),
                 ("q", vp), ("out", vp), ("scale", f32), ("causal", i32), ("qpos", vp),
                 ("segments", vp), ("num_segments", i32), ("total_tokens", i32),
                 ("k_pq_cb", vp), ("v_pq_cb", vp), ("k_rvq_cb", vp), ("v_rvq_cb", vp),

@@ -85,12 +85,14 @@ class RFSNHybridAttentionMLX:
                                           query_positions=query_positions)
 
     def _fused_ok(self, q: torch.Tensor, key_store: CompressedTensorMLX, quantizer: HybridQuantizerMLX) -> bool:
-        if quantizer.subspace or q.dim() != 3 or key_store.num_heads <= 0:
+        if q.dim() != 3 or key_store.num_heads <= 0 or key_store.subspace != quantizer.subspace:
             return False
         M, C, _ = quantizer.pq.codebooks.shape
+        f = quantizer.warm_format()
+        sub = (f.rvq_subspaces, f.rvq_centroids, f.sparse_k) if quantizer.subspace else (0, 0, 0)
         return (q.shape[-1] == quantizer.config.head_dim and q.shape[1] % key_store.num_heads == 0
                 and K.ref_attention_ok(int(q.shape[-1]), int(M), int(C), int(q.shape[1]), key_store.num_heads,
-                                       True))
+                                       True, *sub))
 
     def _fused(self, q, key_store, value_store, quantizer, causal, query_positions) -> torch.Tensor:
         """Decode-and-attend in one kernel: each K/V vector is rebuilt in
@@ -104,11 +106,13 @@ class RFSNHybridAttentionMLX:
         kst = _on(key_store, dev)
         vst = _on(value_store, dev)
         pos = _normalize_query_positions(query_positions, B, Hq, T - 1, dev) if causal else None
-        cb, rcb = quantizer.pq.codebooks, quantizer.rvq.codebooks
+        cb, rcb = quantizer.pq.codebooks, quantizer.rvq_codebooks
+        f = quantizer.warm_format()
         out = K.ref_attention(q.to(device=dev, dtype=torch.float16), kv_heads=key_store.num_heads,
                               scale=self.scale, causal=causal, qpos=pos,
                               segments=[K.ref_store_segment(kst, vst, 0, T, 0)], k_pq_cb=cb, v_pq_cb=cb,
-                              k_rvq_cb=rcb, v_rvq_cb=rcb)
+                              k_rvq_cb=rcb, v_rvq_cb=rcb, rvq_subspaces=f.rvq_subspaces if quantizer.subspace else 0,
+                              sparse_k=f.sparse_k if quantizer.subspace else 0)
         return out.to(q.dtype)
 
 

@@ -853,7 +853,7 @@ class RFSNv10KVCacheMLX:
         and NPZ export) and, for the subspace format, the tiled layout that
         prefetch copies into device slots (K then V in one buffer)."""
         entry = {"key": _to_host_store(ck), "value": _to_host_store(cv)}
-        if self._subspace:
+        if self._subspace and self._fmt().fused_ok:
             fmt = self._fmt()
             chunk = K.round_up(self.config.chunk_tokens, K.TILE)
             kb, vb = self._chunk_split()
@@ -1325,24 +1325,33 @@ class RFSNv10KVCacheMLX:
     def _ref_ok(self, q_heads: int) -> bool:
         """The reference-format kernel (PQ + gated full-dimension RVQ decoded
         on the fly) serves this cache's codebooks and head grouping."""
-        if self._kq is None or self._subspace:
+        if self._kq is None:
             return False
         kq, vq = self._kq, self._vq
         M, C, _ = kq.pq.codebooks.shape
         if tuple(vq.pq.codebooks.shape) != tuple(kq.pq.codebooks.shape):
             return False
-        if tuple(kq.rvq.codebooks.shape) != tuple(vq.rvq.codebooks.shape):
+        kr, vr = kq.rvq_codebooks, vq.rvq_codebooks
+        if (kr is None) != (vr is None) or (kr is not None and tuple(kr.shape) != tuple(vr.shape)):
+            return False
+        if self._subspace and kq.warm_format() != vq.warm_format():
             return False
         shared = kq.pq.codebooks.data_ptr() == vq.pq.codebooks.data_ptr()
-        return K.ref_attention_ok(self.D, int(M), int(C), q_heads, self.H, shared)
+        if not self._subspace:
+            return K.ref_attention_ok(self.D, int(M), int(C), q_heads, self.H, shared)
+        f = self._fmt()
+        return K.ref_attention_ok(self.D, int(M), int(C), q_heads, self.H, shared, f.rvq_subspaces,
+                                  f.rvq_centroids, f.sparse_k)
 
     def _ref_forward(self, q, causal, query_positions, router, current_position, context_window, cold_chunks):
-        """attention_forward over reference-format tiers without decoding the
-        window into HBM: the plan of materialize_window (cache.py:344-393)
+        """attention_forward over tiers the tiled fused kernel does not serve
+        (the reference format with active RVQ rows or cold chunks, formats
+        outside the tiled kernel's head_dim 64 / M 8 or 16) without decoding
+        the window into HBM: the plan of materialize_window (cache.py:344-393)
         becomes a segment table in window order -- the hot tier as exact rows
         of its ring, warm and cold stores as their codes -- and one launch
-        attends it, rebuilding each K/V vector in registers with the
-        reference's rounding (quantization.py:310-319)."""
+        attends it, rebuilding each K/V vector in registers with the decode's
+        rounding (quantization.py:310-319)."""
         start, end, adjusted = self._window_bounds(query_positions, context_window, current_position)
         stats = self._empty_access_stats()
         stats["window_start"], stats["window_end"] = start, end
@@ -1378,9 +1387,11 @@ class RFSNv10KVCacheMLX:
         B, Hq = int(q.shape[0]), int(q.shape[1])
         qpos = _normalize_query_positions(adjusted, B, Hq, pos - 1, self.device) if causal else None
         kq, vq = self._kq, self._vq
+        sub = self._fmt() if self._subspace else None
         out = K.ref_attention(q.to(torch.float16), kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos,
                               segments=segs, k_pq_cb=kq.pq.codebooks, v_pq_cb=vq.pq.codebooks,
-                              k_rvq_cb=kq.rvq.codebooks, v_rvq_cb=vq.rvq.codebooks)
+                              k_rvq_cb=kq.rvq_codebooks, v_rvq_cb=vq.rvq_codebooks,
+                              rvq_subspaces=sub.rvq_subspaces if sub else 0, sparse_k=sub.sparse_k if sub else 0)
         return out.to(q.dtype)
 
     def prepare(self, q: torch.Tensor, causal: bool = True, query_positions=None,

@@ -1,24 +1,29 @@
-// Fused decode attention over reference-format compressed stores for gfx950:
-// PQ codes with the gated full-dimension RVQ correction
-// (quantization.py:99-319), any head_dim that is a multiple of 64 up to 256.
+// Fused decode attention over compressed stores in CompressedTensorMLX's
+// layout for gfx950: PQ codes with the gated full-dimension RVQ correction
+// (quantization.py:99-319), or with a subspace RVQ stage and top-k sparse
+// residuals (the long-context format), head_dim 64, 128 or 256.
 //
 // Replaces the decode-then-attend of RFSNHybridAttentionMLX.__call__
 // (attention.py:150-171) and of RFSNv10KVCacheMLX.attention_forward over
-// reference-format tiers (cache.py:395-428: materialize_window, then
+// tiers the tiled fused kernel does not serve (cache.py:395-428: materialize_window, then
 // _blockwise_exact_attention), without writing the decoded window to HBM.
 //
 // One block = (query b, KV head h, token split), 4 waves.  The PQ codebooks
 // of K and V sit in LDS (entry-major rows of d fp16 per subspace).  A wave
-// streams the split's tokens one at a time with the token's codes in scalar
-// registers (uniform loads); lane l owns coordinates DPL*l .. DPL*l+DPL-1, so
-// it gathers its slice of the token's PQ entry from LDS and, for an active
-// row, its slice of the L RVQ codewords from global memory (64 lanes read one
-// codeword row: coalesced), and rebuilds the reference's rounding chain:
+// streams the split's tokens one at a time; lane l owns coordinates
+// DPL*l .. DPL*l+DPL-1 (one PQ subspace), so it reads that subspace's code
+// byte (lanes of one subspace share the load) and gathers its slice of the
+// token's PQ entry from LDS.  For an active row of the reference format it
+// adds its slice of the L RVQ codewords from global memory (64 lanes read
+// one codeword row: coalesced) with the reference's rounding chain:
 // corr = fp16(sum_l fl32(C_l[code_l])) in stage order, K = fp16(fl32(base) +
-// fl32(corr)) (corr = 0 for inactive rows).  Scores are the wave's sum of
-// q . K partials in fp32; the online softmax runs on the wave (uniform), and
-// the lane accumulates p * V on its coordinates.  The 4 waves combine in LDS;
-// splits write (m, l, acc) partials that merge_partials_kernel combines.
+// fl32(corr)) (corr = 0 for inactive rows).  The long-context format reads
+// its subspace RVQ entries from global memory (L2-resident codebooks) and
+// adds the sparse residuals to the coordinates they name.  Scores are the
+// wave's sum of q . K partials in fp32; the online softmax runs on the wave
+// (uniform), and the lane accumulates p * V on its coordinates.  The 4 waves
+// combine in LDS; splits write (m, l, acc) partials that
+// merge_partials_kernel combines.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
 
@@ -37,58 +42,72 @@ __device__ __forceinline__ float wave_sum64(float v) {
   return v;
 }
 
-// code byte m (0 <= m < M <= 32) of a row whose M bytes are the uniform
-// words w[0 .. M/4)
-template <int MW>
-__device__ __forceinline__ int code_byte(const uint32_t (&w)[MW], int m) {
-  uint32_t x = w[0];
-#pragma unroll
-  for (int i = 1; i < MW; ++i) x = (m >> 2) == i ? w[i] : x;
-  return (int)((x >> (8 * (m & 3))) & 0xFFu);
-}
+struct RvqShape {
+  int L, Cr;   // gated full-dimension layers
+  int Mr, dr;  // subspace stage (Mr = 0: none)
+  int k;       // sparse residuals
+};
 
-// The lane's DPL coordinates of one stored vector (PQ base + gated RVQ
-// correction) or of an exact row.
-template <int DPL, int MW>
+// The lane's DPL coordinates of one stored vector or of an exact row:
+// PQ base, then the gated full-dimension correction (reference format) or
+// the subspace RVQ stage and the sparse residuals (long-context format).
+template <int DPL>
 __device__ __forceinline__ void rebuild(float (&out)[DPL], const rfsn_ref_store_codes& sc, const uint16_t* exact_row,
                                         int64_t row, const uint16_t* __restrict__ tab, int M, int C, int dsub,
-                                        const uint16_t* rvq_cb, int L, int Cr, int D, int lane) {
+                                        const uint16_t* rvq_cb, const RvqShape& r, int D, int lane) {
   if (exact_row != nullptr) {
 #pragma unroll
     for (int u = 0; u < DPL; ++u) out[u] = h2f(exact_row[DPL * lane + u]);
     return;
   }
-  uint32_t w[MW];
-#pragma unroll
-  for (int i = 0; i < MW; ++i) w[i] = reinterpret_cast<const uint32_t*>(sc.pq + row * M)[i];  // M = 4 MW bytes
-  const int a = sc.active ? sc.active[row] : -1;  // uniform
+  // M in {4, 8, 16, 32}: the lane's DPL coordinates sit in one PQ subspace
+  // (d = D/M is a multiple of DPL = D/64)
+  const int m = (DPL * lane) / dsub;
+  const int code = sc.pq[row * M + m];
+  const uint16_t* entry = tab + ((int64_t)m * C + code) * dsub + (DPL * lane - m * dsub);
   float corr[DPL];
 #pragma unroll
   for (int u = 0; u < DPL; ++u) corr[u] = 0.0f;
-  if (a >= 0) {
-    float tot[DPL];
+  if (sc.rvq_sub != nullptr) {
+    // subspace stage: the lane's coordinates span at most two subspaces
+    const uint8_t* codes = sc.rvq_sub + row * r.Mr;
 #pragma unroll
-    for (int u = 0; u < DPL; ++u) tot[u] = 0.0f;
-    for (int l = 0; l < L; ++l) {
-      const int c = sc.rvq[(int64_t)a * L + l];
-      const uint16_t* cw = rvq_cb + ((int64_t)l * Cr + c) * D + DPL * lane;
-#pragma unroll
-      for (int u = 0; u < DPL; ++u) tot[u] = __fadd_rn(tot[u], h2f(cw[u]));
+    for (int u = 0; u < DPL; ++u) {
+      const int dd = DPL * lane + u;
+      const int mr = dd / r.dr;
+      corr[u] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
     }
+  } else {
+    const int a = sc.active ? sc.active[row] : -1;  // uniform
+    if (a >= 0) {
+      float tot[DPL];
 #pragma unroll
-    for (int u = 0; u < DPL; ++u) corr[u] = h2f(f2h(tot[u]));
+      for (int u = 0; u < DPL; ++u) tot[u] = 0.0f;
+      for (int l = 0; l < r.L; ++l) {
+        const int c = sc.rvq[(int64_t)a * r.L + l];
+        const uint16_t* cw = rvq_cb + ((int64_t)l * r.Cr + c) * D + DPL * lane;
+#pragma unroll
+        for (int u = 0; u < DPL; ++u) tot[u] = __fadd_rn(tot[u], h2f(cw[u]));
+      }
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) corr[u] = h2f(f2h(tot[u]));
+    }
   }
 #pragma unroll
-  for (int u = 0; u < DPL; ++u) {
-    const int dd = DPL * lane + u;
-    const int m = dd / dsub;
-    const int code = code_byte<MW>(w, m);
-    const float base = h2f(tab[((int64_t)m * C + code) * dsub + (dd - m * dsub)]);
-    out[u] = h2f(f2h(__fadd_rn(base, corr[u])));  // fp16(fl32(base) + fl32(corr))
+  for (int u = 0; u < DPL; ++u) out[u] = h2f(f2h(__fadd_rn(h2f(entry[u]), corr[u])));  // fp16(fl32(base) + fl32(corr))
+  if (sc.sparse_idx != nullptr) {
+    // K[idx] = fp16(fl32(K[idx]) + fl32(val)); the indices of a row are distinct
+    for (int j = 0; j < r.k; ++j) {
+      const int idx = sc.sparse_idx[row * r.k + j];  // uniform
+      const float val = h2f(sc.sparse_val[row * r.k + j]);
+#pragma unroll
+      for (int u = 0; u < DPL; ++u)
+        if (idx == DPL * lane + u) out[u] = h2f(f2h(__fadd_rn(out[u], val)));
+    }
   }
 }
 
-template <int DPL, int MW>
+template <int DPL>
 __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
                                                                int kv_tab_shared) {
   extern __shared__ __align__(16) uint16_t tabs[];
@@ -125,6 +144,12 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
   }
   __syncthreads();
 
+  RvqShape rs;
+  rs.L = p.rvq_layers;
+  rs.Cr = p.rvq_centroids;
+  rs.Mr = p.rvq_subspaces;
+  rs.dr = p.rvq_subspaces > 0 ? D / p.rvq_subspaces : 0;
+  rs.k = p.sparse_k;
   const cref segs = (cref)p.segments;
   const int begin = split * tps, end = min(p.total_tokens, begin + tps);
   int seg_base = 0;
@@ -136,9 +161,15 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
       kc.pq = segs[s].k.pq;
       kc.rvq = segs[s].k.rvq;
       kc.active = segs[s].k.active;
+      kc.rvq_sub = segs[s].k.rvq_sub;
+      kc.sparse_idx = segs[s].k.sparse_idx;
+      kc.sparse_val = segs[s].k.sparse_val;
       vc.pq = segs[s].v.pq;
       vc.rvq = segs[s].v.rvq;
       vc.active = segs[s].v.active;
+      vc.rvq_sub = segs[s].v.rvq_sub;
+      vc.sparse_idx = segs[s].v.sparse_idx;
+      vc.sparse_val = segs[s].v.sparse_val;
       const int64_t tok0 = segs[s].token0;
       const int pos0 = segs[s].pos0;
       const uint16_t* ek = (const uint16_t*)segs[s].exact_k;
@@ -150,10 +181,10 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
         const int pos = pos0 + t;
         float kk[DPL], vv[DPL];
         const int64_t erow = (tok0 + t) * segs[s].exact_token_stride + (int64_t)h * segs[s].exact_head_stride;
-        rebuild<DPL, MW>(kk, kc, kc.pq ? nullptr : ek + erow, row, ktab, M, C, dsub,
-                         (const uint16_t*)p.k_rvq_cb, p.rvq_layers, p.rvq_centroids, D, lane);
-        rebuild<DPL, MW>(vv, vc, vc.pq ? nullptr : ev + erow, row, vtab, M, C, dsub,
-                         (const uint16_t*)p.v_rvq_cb, p.rvq_layers, p.rvq_centroids, D, lane);
+        rebuild<DPL>(kk, kc, kc.pq ? nullptr : ek + erow, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb,
+                         rs, D, lane);
+        rebuild<DPL>(vv, vc, vc.pq ? nullptr : ev + erow, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb,
+                         rs, D, lane);
 #pragma unroll
         for (int g = 0; g < kRefMaxG; ++g) {
           if (g >= G) continue;  // uniform
@@ -236,25 +267,15 @@ size_t ref_lds_bytes(const rfsn_ref_params* p, bool shared) {
 }
 
 template <int DPL>
-int launch_ref(const rfsn_ref_params* p, int mw, hipStream_t s) {
+int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
   const int splits = ref_splits(p);
   const int tps = (p->total_tokens + splits - 1) / splits;
   const bool shared = p->k_pq_cb == p->v_pq_cb;
   const size_t lds = ref_lds_bytes(p, shared);
   const int blocks = p->batch * p->kv_heads * splits;
-#define RFSN_REF(MW)                                                                                       \
-  do {                                                                                                     \
-    auto kern = ref_attn_kernel<DPL, MW>;                                                                  \
-    if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared); \
-  } while (0)
-  switch (mw) {
-    case 1: RFSN_REF(1); break;
-    case 2: RFSN_REF(2); break;
-    case 4: RFSN_REF(4); break;
-    default: RFSN_REF(8); break;
-  }
-#undef RFSN_REF
+  auto kern = ref_attn_kernel<DPL>;
+  if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared);
   int st = check_launch("ref_attention");
   if (st || splits == 1) return st;
   return launch_merge(reinterpret_cast<const float*>(p->workspace), (int64_t)p->batch * p->q_heads, splits,
@@ -282,11 +303,17 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
   RFSN_REQUIRE(p->pq_centroids >= 1 && p->pq_centroids <= 256, "ref_attention: PQ codebook size must be in [1, 256]");
   RFSN_REQUIRE(p->rvq_layers >= 0 && (p->rvq_layers == 0 || (p->rvq_centroids >= 1 && p->rvq_centroids <= 65536)),
                "ref_attention: bad RVQ shape");
+  RFSN_REQUIRE(p->rvq_subspaces >= 0 && (p->rvq_subspaces == 0 || p->rvq_layers == 0),
+               "ref_attention: gated RVQ layers and an RVQ subspace stage are exclusive");
+  RFSN_REQUIRE(p->rvq_subspaces == 0 || (D % p->rvq_subspaces == 0 && p->rvq_centroids >= 1 && p->rvq_centroids <= 256),
+               "ref_attention: rvq_subspaces must divide head_dim, with at most 256 centroids");
+  RFSN_REQUIRE(p->sparse_k >= 0 && p->sparse_k <= 8, "ref_attention: sparse_k must be in [0, 8]");
   RFSN_REQUIRE(p->batch > 0 && p->q_heads > 0 && p->kv_heads > 0 && p->q_heads % p->kv_heads == 0 &&
                    p->q_heads / p->kv_heads <= kRefMaxG,
                "ref_attention: query heads must be a multiple of KV heads, at most 8 per KV head");
   RFSN_REQUIRE(p->q && p->out && p->k_pq_cb && p->v_pq_cb, "ref_attention: null pointer");
-  RFSN_REQUIRE(p->rvq_layers == 0 || (p->k_rvq_cb && p->v_rvq_cb), "ref_attention: RVQ codebooks missing");
+  RFSN_REQUIRE((p->rvq_layers == 0 && p->rvq_subspaces == 0) || (p->k_rvq_cb && p->v_rvq_cb),
+               "ref_attention: RVQ codebooks missing");
   RFSN_REQUIRE(p->num_segments >= 0 && p->total_tokens >= 0 && (p->num_segments == 0 || p->segments),
                "ref_attention: bad segment table");
   const size_t shared_lds = ref_lds_bytes(p, p->k_pq_cb == p->v_pq_cb);
@@ -297,8 +324,8 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
   const size_t wsb = rfsn_ref_attention_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "ref_attention: workspace too small");
   switch (D) {
-    case 64: return launch_ref<1>(p, M / 4, s);
-    case 128: return launch_ref<2>(p, M / 4, s);
-    default: return launch_ref<4>(p, M / 4, s);
+    case 64: return launch_ref<1>(p, s);
+    case 128: return launch_ref<2>(p, s);
+    default: return launch_ref<4>(p, s);
   }
 }

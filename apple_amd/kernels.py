@@ -579,17 +579,27 @@ def active_map(offsets: torch.Tensor, rows: int) -> torch.Tensor:
 
 
 def ref_store_segment(key_store, value_store, token0: int, length: int, pos0: int) -> dict:
-    """A coded segment of tokens token0 .. token0+length-1 of reference-format
-    stores (pq_codes [T, H, M] u8, rvq_codes [A, L] u16 placed by rvq_offsets
-    [A] over the T*H rows)."""
+    """A coded segment of tokens token0 .. token0+length-1 of two stores in
+    CompressedTensorMLX's layout: reference format (pq_codes [T, H, M] u8,
+    rvq_codes [A, L] u16 placed by rvq_offsets [A] over the T*H rows) or the
+    long-context format (rvq_codes [T, H, M_r] u8, sparse_idx / sparse_val
+    [T, H, k])."""
     seg = {"len": int(length), "pos0": int(pos0), "token0": int(token0), "exact": None}
     if token0 < 0 or length < 0 or token0 + length > min(key_store.num_tokens, value_store.num_tokens):
         raise ValueError("segment tokens outside the stores")
     for name, st in (("k", key_store), ("v", value_store)):
         pq = _contig(st.pq_codes)
-        a = int(st.rvq_codes.shape[0]) if st.rvq_codes.dim() == 2 else 0
         rows = int(pq.shape[0]) * int(pq.shape[1])
-        seg[name] = (pq, _contig(st.rvq_codes) if a else None, active_map(st.rvq_offsets, rows) if a else None)
+        if st.rvq_codes.dim() == 3:
+            rsub = _contig(st.rvq_codes) if st.rvq_codes.shape[-1] else None
+            k = 0 if st.sparse_idx is None else int(st.sparse_idx.shape[-1])
+            sidx = _contig(st.sparse_idx) if k else None
+            sval = _contig(st.sparse_val) if k else None
+            seg[name] = (pq, None, None, rsub, sidx, sval)
+        else:
+            a = int(st.rvq_codes.shape[0])
+            seg[name] = (pq, _contig(st.rvq_codes) if a else None, active_map(st.rvq_offsets, rows) if a else None,
+                         None, None, None)
     return seg
 
 
@@ -607,20 +617,25 @@ def ref_exact_segment(k: torch.Tensor, v: torch.Tensor, token_stride: int, head_
             "exact": (k, v, int(token_stride), int(head_stride)), "k": None, "v": None}
 
 
-def ref_attention_ok(head_dim: int, M: int, C: int, q_heads: int, kv_heads: int, shared_cb: bool) -> bool:
+def ref_attention_ok(head_dim: int, M: int, C: int, q_heads: int, kv_heads: int, shared_cb: bool,
+                     rvq_subspaces: int = 0, rvq_centroids: int = 0, sparse_k: int = 0) -> bool:
     """Whether ``rfsn_ref_attention`` serves the shape."""
     tab = head_dim * C * 2 * (1 if shared_cb else 2)
+    sub_ok = rvq_subspaces == 0 or (head_dim % rvq_subspaces == 0 and 1 <= rvq_centroids <= 256)
     return (head_dim in (64, 128, 256) and M in (4, 8, 16, 32) and head_dim % M == 0 and 1 <= C <= 256
-            and kv_heads > 0 and q_heads % kv_heads == 0 and q_heads // kv_heads <= 8 and tab <= 160 * 1024)
+            and kv_heads > 0 and q_heads % kv_heads == 0 and q_heads // kv_heads <= 8 and tab <= 160 * 1024
+            and sub_ok and 0 <= sparse_k <= 8)
 
 
 def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, qpos: Optional[torch.Tensor],
                   segments: Sequence[dict], k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor,
                   k_rvq_cb: Optional[torch.Tensor], v_rvq_cb: Optional[torch.Tensor],
+                  rvq_subspaces: int = 0, sparse_k: int = 0,
                   out: Optional[torch.Tensor] = None, splits: int = 0) -> torch.Tensor:
     """Attention of q [B, Hq, D] over the window of ``segments`` (window
     order; ``ref_store_segment`` / ``ref_exact_segment``), decoding the coded
-    ones on the fly (``rfsn_ref_attention``)."""
+    ones on the fly (``rfsn_ref_attention``).  RVQ codebooks are [L, C_r, D]
+    (gated full-dimension layers) or, with ``rvq_subspaces``, [M_r, C_r, D/M_r]."""
     _dev(q, "ref_attention")
     q = _contig(q)
     B, Hq, D = q.shape
@@ -640,16 +655,24 @@ def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool,
             keep += [ek, ev]
         else:
             for name, codes in (("k", seg.k), ("v", seg.v)):
-                pq, rvq, act = sd[name]
+                pq, rvq, act, rsub, sidx, sval = sd[name]
+                gated_mismatch = rvq is not None and (k_rvq_cb is None or rvq_subspaces)
+                if ((0 if rsub is None else rsub.shape[-1]) != rvq_subspaces
+                        or (0 if sidx is None else sidx.shape[-1]) != sparse_k or gated_mismatch):
+                    raise ValueError("segment codes do not match the format's RVQ / sparse stages")
                 codes.pq, codes.rvq, codes.active = pq.data_ptr(), L.ptr(rvq), L.ptr(act)
-                keep += [pq, rvq, act]
+                codes.rvq_sub, codes.sparse_idx, codes.sparse_val = L.ptr(rsub), L.ptr(sidx), L.ptr(sval)
+                keep += [pq, rvq, act, rsub, sidx, sval]
     raw = torch.frombuffer(bytearray(C.string_at(C.addressof(arr), C.sizeof(arr))), dtype=torch.uint8)
     dev_segs = raw.to(q.device, non_blocking=False)
     M, Cn, _ = k_pq_cb.shape
     p = L.RefParams()
     p.head_dim, p.pq_subspaces, p.pq_centroids = D, M, Cn
-    p.rvq_layers = 0 if k_rvq_cb is None else int(k_rvq_cb.shape[0])
-    p.rvq_centroids = 0 if k_rvq_cb is None else int(k_rvq_cb.shape[1])
+    if k_rvq_cb is not None and rvq_subspaces:
+        p.rvq_subspaces, p.rvq_centroids = int(rvq_subspaces), int(k_rvq_cb.shape[1])
+    elif k_rvq_cb is not None:
+        p.rvq_layers, p.rvq_centroids = int(k_rvq_cb.shape[0]), int(k_rvq_cb.shape[1])
+    p.sparse_k = int(sparse_k)
     p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
     p.q, p.out, p.scale, p.causal = q.data_ptr(), out.data_ptr(), float(scale), int(causal)
     qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)

@@ -331,24 +331,35 @@ int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
 #define RFSN_FUSED_SCRATCH_BYTES (4u << 20)
 int rfsn_fused_decode_attention_noalloc(const rfsn_fused_params* p, void* stream);
 
-/* ---------------------------------------------------------------- reference-format attention
- * Fused decode attention over reference-format compressed stores: PQ codes
- * [T][heads][M] u8 with the gated full-dimension RVQ correction (codes
- * [A][L] u16 of the active rows), decoded on the fly as quantization.py:
- * 310-319 does (corr = fp16(sum_l fl32(C_l[code_l])), K = fp16(fl32(base) +
- * fl32(corr)), corr = 0 for inactive rows), and exact segments (the hot
- * tier).  Replaces RFSNHybridAttentionMLX.__call__ (attention.py:150-171)
- * and attention_forward over reference-format tiers (cache.py:395-428,
- * materialize_window + _blockwise_exact_attention) without writing the
- * decoded window to HBM.  head_dim 64, 128 or 256; M in {4, 8, 16, 32}
- * dividing head_dim, C <= 256 PQ centroids (the PQ codebooks of K and V must
- * fit 160 KB of LDS together, or one when K and V share it); L RVQ layers of
- * C_r <= 65536 codewords; at most 8 query heads per KV head.  B queries share
- * the segments; segments are in window order. */
+/* ---------------------------------------------------------------- reference-layout attention
+ * Fused decode attention over compressed stores in the layout
+ * CompressedTensorMLX holds them (storage.py:75-98, token-major rows of
+ * [T][heads]), decoding each K/V vector in registers, never to HBM:
+ *  - reference format: PQ codes [T][heads][M] u8 with the gated
+ *    full-dimension RVQ correction (codes [A][L] u16 of the active rows),
+ *    decoded as quantization.py:310-319 does (corr = fp16(sum_l
+ *    fl32(C_l[code_l])), K = fp16(fl32(base) + fl32(corr)), corr = 0 for
+ *    inactive rows);
+ *  - long-context format: PQ codes, then subspace RVQ codes [T][heads][M_r]
+ *    u8 (K = fp16(fl32(base) + fl32(rvq))), then k sparse residuals
+ *    (K[idx] = fp16(fl32(K[idx]) + fl32(val)));
+ *  - exact segments (the hot tier).
+ * Replaces RFSNHybridAttentionMLX.__call__ (attention.py:150-171) and
+ * attention_forward over tiers the tiled fused kernel does not serve
+ * (cache.py:395-428, materialize_window + _blockwise_exact_attention).
+ * head_dim 64, 128 or 256; M in {4, 8, 16, 32} dividing head_dim, C <= 256
+ * PQ centroids (the PQ codebooks of K and V must fit 160 KB of LDS together,
+ * or one when K and V share it); either L gated RVQ layers of C_r <= 65536
+ * codewords or M_r RVQ subspaces (dividing head_dim, C_r <= 256); k <= 8
+ * sparse residuals; at most 8 query heads per KV head.  B queries share the
+ * segments; segments are in window order. */
 typedef struct rfsn_ref_store_codes {
-  const uint8_t* pq;     /* [T][heads][M] u8 (4-byte aligned); NULL: an exact segment */
-  const uint16_t* rvq;   /* [A][L] u16 codes of the active rows                         */
-  const int32_t* active; /* [T][heads]: the row's index into rvq, or -1; NULL: none     */
+  const uint8_t* pq;          /* [T][heads][M] u8 (4-byte aligned); NULL: an exact segment  */
+  const uint16_t* rvq;        /* gated format: [A][L] u16 codes of the active rows          */
+  const int32_t* active;      /* gated format: [T][heads] index into rvq, or -1; NULL: none */
+  const uint8_t* rvq_sub;     /* long-context format: [T][heads][M_r] u8, or NULL            */
+  const uint8_t* sparse_idx;  /* long-context format: [T][heads][k] u8, or NULL              */
+  const uint16_t* sparse_val; /* long-context format: [T][heads][k] fp16 residuals           */
 } rfsn_ref_store_codes;
 
 typedef struct rfsn_ref_segment {
@@ -367,8 +378,10 @@ typedef struct rfsn_ref_params {
   int32_t head_dim;
   int32_t pq_subspaces;
   int32_t pq_centroids;
-  int32_t rvq_layers;     /* L, 0 = no RVQ */
-  int32_t rvq_centroids;  /* C_r */
+  int32_t rvq_layers;     /* L gated full-dimension layers, 0 = none */
+  int32_t rvq_centroids;  /* C_r (gated layers, or the subspace stage) */
+  int32_t rvq_subspaces;  /* M_r subspace-RVQ subspaces, 0 = none (exclusive with rvq_layers) */
+  int32_t sparse_k;       /* k sparse residuals per vector, 0 = none */
   int32_t batch;          /* B queries */
   int32_t q_heads;
   int32_t kv_heads;
@@ -382,7 +395,7 @@ typedef struct rfsn_ref_params {
   int32_t total_tokens;   /* sum of the segments' lengths (> 0) */
   const void* k_pq_cb;    /* [M][C][d] fp16 */
   const void* v_pq_cb;
-  const void* k_rvq_cb;   /* [L][C_r][D] fp16 */
+  const void* k_rvq_cb;   /* [L][C_r][D] fp16, or [M_r][C_r][D/M_r] for the subspace stage */
   const void* v_rvq_cb;
   int32_t splits;         /* token splits per (query, KV head); 0 = auto */
   void* workspace;        /* split partials: rfsn_ref_attention_workspace_bytes */

@@ -105,6 +105,71 @@ def test_segments_match_oracle(device, D, M, C, L, Cr, B, Hq, Hkv, causal, split
         assert not got[-1, -1].any()  # position -1 sees no key: zeros (attention.py:104-105)
 
 
+def _ext_store(g, n_tok, heads, M, C, Mr, Cr, k, D):
+    """Long-context-format store dict: PQ, subspace RVQ, k distinct sparse
+    coordinates per row with fp16 residuals."""
+    idx = np.argsort(g.random((n_tok * heads, D)), axis=1)[:, :k].astype(np.uint8).reshape(n_tok, heads, k)
+    return {"pq_codes": g.integers(0, C, (n_tok, heads, M), dtype=np.uint8),
+            "rvq_codes": g.integers(0, max(Cr, 1), (n_tok, heads, Mr), dtype=np.uint8),
+            "sparse_idx": idx, "sparse_val": randn16(g, n_tok, heads, k, scale=0.3)}
+
+
+def _ext_decode(st, pq_cb, rv_cb):
+    T_, H_, M = st["pq_codes"].shape
+    n = T_ * H_
+    Mr, k = st["rvq_codes"].shape[-1], st["sparse_idx"].shape[-1]
+    out = nx.ext_decode(st["pq_codes"].reshape(n, M), pq_cb, st["rvq_codes"].reshape(n, Mr) if Mr else None,
+                        rv_cb if Mr else None, st["sparse_idx"].reshape(n, k), st["sparse_val"].reshape(n, k))
+    return out.reshape(T_, H_, -1)
+
+
+def _ext_dev_store(st, dev):
+    from apple_amd.storage import CompressedTensorMLX
+
+    T_, H_ = st["pq_codes"].shape[:2]
+    return CompressedTensorMLX(pq_codes=T(st["pq_codes"], dev), rvq_codes=T(st["rvq_codes"], dev),
+                               rvq_mask=torch.ones((T_, H_), dtype=torch.bool, device=dev),
+                               rvq_offsets=torch.zeros((0,), dtype=torch.int32, device=dev), num_heads=H_,
+                               sparse_idx=T(st["sparse_idx"], dev), sparse_val=T(st["sparse_val"], dev))
+
+
+EXT_CASES = [
+    # D, M, C, Mr, Cr, k, B, Hq, Hkv
+    (128, 16, 256, 16, 256, 4, 1, 32, 4),   # head_dim 128 long-context format
+    (64, 8, 256, 4, 64, 3, 2, 8, 8),        # stage shapes the tiled kernel does not take
+    (256, 32, 256, 32, 256, 8, 1, 8, 2),
+    (128, 8, 128, 0, 0, 2, 2, 4, 4),        # PQ + sparse, no RVQ stage
+]
+
+
+@pytest.mark.parametrize("D,M,C,Mr,Cr,k,B,Hq,Hkv", EXT_CASES)
+def test_long_context_format_matches_oracle(device, D, M, C, Mr, Cr, k, B, Hq, Hkv):
+    from apple_amd import kernels as K
+
+    g = rng(2000 + D + M + Mr + k)
+    pq_cb = rand_codebooks(g, M, C, D // M)
+    rv_cb = rand_codebooks(g, max(Mr, 1), max(Cr, 1), D // max(Mr, 1))
+    sk, sv = _ext_store(g, 90, Hkv, M, C, Mr, Cr, k, D), _ext_store(g, 90, Hkv, M, C, Mr, Cr, k, D)
+    cap = 24
+    ring_k, ring_v = randn16(g, Hkv, cap, D), randn16(g, Hkv, cap, D)
+    keys = np.concatenate([_ext_decode(sk, pq_cb, rv_cb)[3:80], ring_k[:, :20].transpose(1, 0, 2)])
+    vals = np.concatenate([_ext_decode(sv, pq_cb, rv_cb)[3:80], ring_v[:, :20].transpose(1, 0, 2)])
+    W = keys.shape[0]
+    q = randn16(g, B, Hq, D, scale=2.0)
+    qp = g.integers(0, W, (B, Hq)).astype(np.int32)
+    qp.reshape(-1)[0] = W - 1
+    rk, rv = T(ring_k, device), T(ring_v, device)
+    segs = [K.ref_store_segment(_ext_dev_store(sk, device), _ext_dev_store(sv, device), 3, 77, 0),
+            K.ref_exact_segment(rk, rv, rk.stride(1), rk.stride(0), 0, 20, 77)]
+    rcb = T(rv_cb, device) if Mr else None
+    cb = T(pq_cb, device)  # one table for K and V: 256 x 256 x 2 B = 128 KB of LDS at head_dim 256
+    out = K.ref_attention(T(q, device), kv_heads=Hkv, scale=D ** -0.5, causal=True, qpos=T(qp, device),
+                          segments=segs, k_pq_cb=cb, v_pq_cb=cb, k_rvq_cb=rcb, v_rvq_cb=rcb, rvq_subspaces=Mr,
+                          sparse_k=k)
+    ref = nx.blockwise_attention(q, keys, vals, D ** -0.5, 16, True, qp)
+    assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
 def test_long_window_split_merge(device):
     """5000 coded tokens: the automatic split count (> 1) and the partial merge."""
     from apple_amd import kernels as K
@@ -243,3 +308,45 @@ def test_hybrid_attention_fused(device, tmp_path, monkeypatch):
     dk, dv = oq.decompress(oq.compress(k)), oq.decompress(oq.compress(v))
     ref = nx.blockwise_attention(q, dk, dv, 128 ** -0.5, 16, True, qp)
     assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+
+
+def test_head_dim_128_long_context_cache(device, tmp_path, monkeypatch):
+    """A head_dim-128 cache in the long-context format (PQ M16 + RVQ M16 +
+    top-4, recency tiers, pinned cold chunks): the tiled kernel does not
+    take it, and attention_forward attends it fused, within 2e-3 of the
+    oracle's blockwise attention over the materialized window."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    cfg = RFSNConfig(hidden_dim=1024, num_heads=8, head_dim=128, num_subspaces=16, subspace_dim=8,
+                     num_rvq_layers=1, rvq_codebook_size=256, rvq_sparsity_threshold=0.0, hot_capacity=64,
+                     warm_capacity=96, cold_capacity=512, block_size_seq=32, num_kv_heads=2, rvq_subspaces=16,
+                     sparse_topk=4, tier_policy="recency", cold_chunk_tokens=32, cold_medium="pinned",
+                     disk_cache_dir=str(tmp_path))
+    g = rng(31)
+    qz = HybridQuantizerMLX(cfg, device=device, pq_codebooks=T(rand_codebooks(g, 16, 256, 8), device),
+                            rvq_codebooks=T(rand_codebooks(g, 16, 256, 8), device))
+    c = RFSNv10KVCacheMLX(cfg, layer_idx=0, device=device)
+    k, v = randn16(g, 300, 2, 128), randn16(g, 300, 2, 128)
+    c.update(T(k[:250], device), T(v[:250], device), qz)
+    c.update(T(k[250:], device), T(v[250:], device), qz)
+    assert c.num_cold > 0 and c.num_warm > 0 and c.num_hot > 0
+    assert not c._fused_ok(8) and c._ref_ok(8)
+    q = randn16(g, 2, 8, 128)
+    qp = np.array([299, 180], np.int32)
+    for cw in (None, 200):
+        kw_, vw_, adj = c.materialize_window(query_positions=T(qp, device), context_window=cw)
+        with monkeypatch.context() as mp:
+            _no_decode(mp)
+            out = H(c.attention_forward(T(q, device), causal=True, query_positions=T(qp, device), context_window=cw))
+        mat = nx.blockwise_attention(q, H(kw_), H(vw_), 128 ** -0.5, 16, True, H(adj))
+        assert np.abs(out.astype(np.float32) - mat.astype(np.float32)).max() <= TOL
+    # the materialized window itself is the oracle's decode of the cache's codes
+    ks = c.warm_keys
+    n = ks.num_tokens * 2
+    dec = nx.ext_decode(H(ks.pq_codes).reshape(n, 16), H(qz.pq.codebooks), H(ks.rvq_codes).reshape(n, 16),
+                        H(qz.rvq.codebooks), H(ks.sparse_idx).reshape(n, 4), H(ks.sparse_val).reshape(n, 4))
+    kw_, _, _ = c.materialize_window(query_positions=T(np.array([299, 299], np.int32), device))
+    w0 = c.num_cold
+    assert np.array_equal(H(kw_)[w0:w0 + ks.num_tokens].view(np.uint16), dec.reshape(-1, 2, 128).view(np.uint16))
