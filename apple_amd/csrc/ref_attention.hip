@@ -30,16 +30,26 @@
 namespace rfsn {
 namespace {
 
-constexpr int kRefWaves = 4;
+constexpr int kRefWaves = 8;
 constexpr int kRefThreads = kRefWaves * 64;
 constexpr int kRefMaxG = 8;  // query heads per KV head
+constexpr int kRefMaxL = 8;  // gated RVQ layers
 
 typedef const rfsn_ref_segment __attribute__((address_space(4)))* cref;
 
+// Sum over the 64 lanes, returned to every lane: DPP adds within each row of
+// 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror
+// leave every lane holding its row's sum), then the four row sums.
 __device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  auto f = [](int x) { return __builtin_bit_cast(float, x); };
+  auto i = [](float x) { return __builtin_bit_cast(int, x); };
+  v += f(__builtin_amdgcn_mov_dpp(i(v), 0xB1, 0xF, 0xF, true));
+  v += f(__builtin_amdgcn_mov_dpp(i(v), 0x4E, 0xF, 0xF, true));
+  v += f(__builtin_amdgcn_mov_dpp(i(v), 0x141, 0xF, 0xF, true));
+  v += f(__builtin_amdgcn_mov_dpp(i(v), 0x140, 0xF, 0xF, true));
+  const float r0 = f(__builtin_amdgcn_readlane(i(v), 0)), r1 = f(__builtin_amdgcn_readlane(i(v), 16));
+  const float r2 = f(__builtin_amdgcn_readlane(i(v), 32)), r3 = f(__builtin_amdgcn_readlane(i(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 struct RvqShape {
@@ -48,66 +58,106 @@ struct RvqShape {
   int k;       // sparse residuals
 };
 
-// The lane's DPL coordinates of one stored vector or of an exact row:
+// The lane's DPL coordinates of U stored vectors (rows row[u] of a store):
 // PQ base, then the gated full-dimension correction (reference format) or
 // the subspace RVQ stage and the sparse residuals (long-context format).
-template <int DPL>
-__device__ __forceinline__ void rebuild(float (&out)[DPL], const rfsn_ref_store_codes& sc, const uint16_t* exact_row,
-                                        int64_t row, const uint16_t* __restrict__ tab, int M, int C, int dsub,
-                                        const uint16_t* rvq_cb, const RvqShape& r, int D, int lane) {
-  if (exact_row != nullptr) {
-#pragma unroll
-    for (int u = 0; u < DPL; ++u) out[u] = h2f(exact_row[DPL * lane + u]);
-    return;
-  }
+// Every load of the U vectors is issued before the first is consumed: the
+// PQ code bytes and row indices, then the gated codes of every layer, then
+// the codewords.
+template <int DPL, int U>
+__device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_store_codes& sc, const int64_t (&row)[U],
+                                        const uint16_t* __restrict__ tab, int M, int C, int dsub,
+                                        const uint16_t* __restrict__ rvq_cb, const RvqShape& r, int lane) {
+  constexpr int D = 64 * DPL;
   // M in {4, 8, 16, 32}: the lane's DPL coordinates sit in one PQ subspace
   // (d = D/M is a multiple of DPL = D/64)
   const int m = (DPL * lane) / dsub;
-  const int code = sc.pq[row * M + m];
-  const uint16_t* entry = tab + ((int64_t)m * C + code) * dsub + (DPL * lane - m * dsub);
-  float corr[DPL];
+  const int off = DPL * lane - m * dsub;
+  int code[U];
 #pragma unroll
-  for (int u = 0; u < DPL; ++u) corr[u] = 0.0f;
+  for (int u = 0; u < U; ++u) code[u] = sc.pq[row[u] * M + m];
+  float corr[U][DPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int v = 0; v < DPL; ++v) corr[u][v] = 0.0f;
   if (sc.rvq_sub != nullptr) {
     // subspace stage: the lane's coordinates span at most two subspaces
-    const uint8_t* codes = sc.rvq_sub + row * r.Mr;
 #pragma unroll
-    for (int u = 0; u < DPL; ++u) {
-      const int dd = DPL * lane + u;
-      const int mr = dd / r.dr;
-      corr[u] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
-    }
-  } else {
-    const int a = sc.active ? sc.active[row] : -1;  // uniform
-    if (a >= 0) {
-      float tot[DPL];
+    for (int u = 0; u < U; ++u) {
+      const uint8_t* codes = sc.rvq_sub + row[u] * r.Mr;
 #pragma unroll
-      for (int u = 0; u < DPL; ++u) tot[u] = 0.0f;
-      for (int l = 0; l < r.L; ++l) {
-        const int c = sc.rvq[(int64_t)a * r.L + l];
-        const uint16_t* cw = rvq_cb + ((int64_t)l * r.Cr + c) * D + DPL * lane;
-#pragma unroll
-        for (int u = 0; u < DPL; ++u) tot[u] = __fadd_rn(tot[u], h2f(cw[u]));
+      for (int v = 0; v < DPL; ++v) {
+        const int dd = DPL * lane + v;
+        const int mr = dd / r.dr;
+        corr[u][v] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
       }
-#pragma unroll
-      for (int u = 0; u < DPL; ++u) corr[u] = h2f(f2h(tot[u]));
     }
+  } else if (sc.active != nullptr) {
+    int a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] = sc.active[row[u]];  // uniform
+    int64_t base[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) base[u] = (int64_t)(a[u] < 0 ? 0 : a[u]) * r.L;  // the store holds >= 1 active row
+    float tot[U][DPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < DPL; ++v) tot[u][v] = 0.0f;
+    // layers four at a time: their codes, then their codewords of the U
+    // rows in flight together; summed in stage order
+    for (int l = 0; l < r.L; l += 4) {
+      const int nl = min(4, r.L - l);
+      int c[4][U];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) c[j][u] = (a[u] < 0 || j >= nl) ? 0 : (int)sc.rvq[base[u] + l + j];
+      uint16_t w[4][U][DPL];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint16_t* cw = rvq_cb + ((int64_t)(j < nl ? l + j : l) * r.Cr + c[j][u]) * D + DPL * lane;
+#pragma unroll
+          for (int v = 0; v < DPL; ++v) w[j][u][v] = cw[v];
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int v = 0; v < DPL; ++v)
+            if (j < nl) tot[u][v] = __fadd_rn(tot[u][v], h2f(w[j][u][v]));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < DPL; ++v) corr[u][v] = a[u] < 0 ? 0.0f : h2f(f2h(tot[u][v]));
   }
 #pragma unroll
-  for (int u = 0; u < DPL; ++u) out[u] = h2f(f2h(__fadd_rn(h2f(entry[u]), corr[u])));  // fp16(fl32(base) + fl32(corr))
+  for (int u = 0; u < U; ++u) {
+    const uint16_t* entry = tab + ((int64_t)m * C + code[u]) * dsub + off;
+#pragma unroll
+    for (int v = 0; v < DPL; ++v) out[u][v] = h2f(f2h(__fadd_rn(h2f(entry[v]), corr[u][v])));  // fp16(base + corr)
+  }
   if (sc.sparse_idx != nullptr) {
     // K[idx] = fp16(fl32(K[idx]) + fl32(val)); the indices of a row are distinct
-    for (int j = 0; j < r.k; ++j) {
-      const int idx = sc.sparse_idx[row * r.k + j];  // uniform
-      const float val = h2f(sc.sparse_val[row * r.k + j]);
 #pragma unroll
-      for (int u = 0; u < DPL; ++u)
-        if (idx == DPL * lane + u) out[u] = h2f(f2h(__fadd_rn(out[u], val)));
+    for (int u = 0; u < U; ++u) {
+      for (int j = 0; j < r.k; ++j) {
+        const int idx = sc.sparse_idx[row[u] * r.k + j];  // uniform
+        const float val = h2f(sc.sparse_val[row[u] * r.k + j]);
+#pragma unroll
+        for (int v = 0; v < DPL; ++v)
+          if (idx == DPL * lane + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
+      }
     }
   }
 }
 
-template <int DPL>
+template <int DPL, int U, int GMAX>
 __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
                                                                int kv_tab_shared) {
   extern __shared__ __align__(16) uint16_t tabs[];
@@ -117,7 +167,8 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
   const int split = blockIdx.x % splits;
   const int h = (blockIdx.x / splits) % p.kv_heads;
   const int b = blockIdx.x / (splits * p.kv_heads);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps token indices scalar
 
   // PQ tables: [M][C][dsub] for K, then V (unless they share one)
   const int tab_elems = M * C * dsub;
@@ -127,16 +178,16 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
   const uint16_t* ktab = tabs;
   const uint16_t* vtab = kv_tab_shared ? tabs : tabs + tab_elems;
 
-  float qv[kRefMaxG][DPL], acc[kRefMaxG][DPL], m_run[kRefMaxG], l_run[kRefMaxG];
-  int qpos[kRefMaxG];
+  float qv[GMAX][DPL], acc[GMAX][DPL], m_run[GMAX], l_run[GMAX];
+  int qpos[GMAX];
 #pragma unroll
-  for (int g = 0; g < kRefMaxG; ++g) {
+  for (int g = 0; g < GMAX; ++g) {
     const int hq = h * G + (g < G ? g : 0);
     const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + hq) * D;
 #pragma unroll
-    for (int u = 0; u < DPL; ++u) {
-      qv[g][u] = g < G ? h2f(qrow[DPL * lane + u]) : 0.0f;
-      acc[g][u] = 0.0f;
+    for (int v = 0; v < DPL; ++v) {
+      qv[g][v] = g < G ? h2f(qrow[DPL * lane + v]) * p.scale : 0.0f;
+      acc[g][v] = 0.0f;
     }
     m_run[g] = -__builtin_inff();
     l_run[g] = 0.0f;
@@ -174,31 +225,63 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
       const int pos0 = segs[s].pos0;
       const uint16_t* ek = (const uint16_t*)segs[s].exact_k;
       const uint16_t* ev = (const uint16_t*)segs[s].exact_v;
-      const int first = lo + (((wave - (lo - begin)) % kRefWaves) + kRefWaves) % kRefWaves;
-      for (int i = first; i < hi; i += kRefWaves) {
-        const int t = i - seg_base;
-        const int64_t row = (tok0 + t) * p.kv_heads + h;
-        const int pos = pos0 + t;
-        float kk[DPL], vv[DPL];
-        const int64_t erow = (tok0 + t) * segs[s].exact_token_stride + (int64_t)h * segs[s].exact_head_stride;
-        rebuild<DPL>(kk, kc, kc.pq ? nullptr : ek + erow, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb,
-                         rs, D, lane);
-        rebuild<DPL>(vv, vc, vc.pq ? nullptr : ev + erow, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb,
-                         rs, D, lane);
+      const int64_t ets = segs[s].exact_token_stride, ehs = segs[s].exact_head_stride;
+      // wave w takes groups of U consecutive tokens, every kRefWaves-th group
+      for (int g0 = lo + wave * U; g0 < hi; g0 += kRefWaves * U) {
+        bool valid[U];
+        int pos[U];
+        int64_t row[U], tk[U];
 #pragma unroll
-        for (int g = 0; g < kRefMaxG; ++g) {
+        for (int u = 0; u < U; ++u) {
+          valid[u] = g0 + u < hi;
+          const int t = (valid[u] ? g0 + u : g0) - seg_base;  // past the end: re-read the group's first token
+          tk[u] = tok0 + t;
+          row[u] = tk[u] * p.kv_heads + h;
+          pos[u] = pos0 + t;
+        }
+        float kk[U][DPL], vv[U][DPL];
+        if (kc.pq == nullptr) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int64_t e = tk[u] * ets + (int64_t)h * ehs + DPL * lane;
+#pragma unroll
+            for (int v = 0; v < DPL; ++v) {
+              kk[u][v] = h2f(ek[e + v]);
+              vv[u][v] = h2f(ev[e + v]);
+            }
+          }
+        } else {
+          rebuild<DPL, U>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, lane);
+          rebuild<DPL, U>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, lane);
+        }
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
           if (g >= G) continue;  // uniform
-          float part = 0.0f;
+          float sc[U];
+          float mx = -__builtin_inff();
 #pragma unroll
-          for (int u = 0; u < DPL; ++u) part = __builtin_fmaf(qv[g][u], kk[u], part);
-          const float sc = wave_sum64(part) * p.scale;
-          if (pos < 0 || pos > qpos[g]) continue;  // masked (uniform)
-          const float mn = fmaxf(m_run[g], sc);
+          for (int u = 0; u < U; ++u) {
+            float part = 0.0f;
+#pragma unroll
+            for (int v = 0; v < DPL; ++v) part = __builtin_fmaf(qv[g][v], kk[u][v], part);
+            sc[u] = wave_sum64(part);  // q was scaled on load
+            if (!valid[u] || pos[u] < 0 || pos[u] > qpos[g]) sc[u] = -__builtin_inff();  // masked (uniform)
+            mx = fmaxf(mx, sc[u]);
+          }
+          if (mx == -__builtin_inff()) continue;  // no allowed token in the group (uniform)
+          const float mn = fmaxf(m_run[g], mx);
           const float corr = __expf(m_run[g] - mn);
-          const float pr = __expf(sc - mn);
-          l_run[g] = l_run[g] * corr + pr;
+          float l = l_run[g] * corr;
 #pragma unroll
-          for (int u = 0; u < DPL; ++u) acc[g][u] = __builtin_fmaf(pr, vv[u], acc[g][u] * corr);
+          for (int v = 0; v < DPL; ++v) acc[g][v] *= corr;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const float pr = __expf(sc[u] - mn);
+            l += pr;
+#pragma unroll
+            for (int v = 0; v < DPL; ++v) acc[g][v] = __builtin_fmaf(pr, vv[u][v], acc[g][v]);
+          }
+          l_run[g] = l;
           m_run[g] = mn;
         }
       }
@@ -206,21 +289,21 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
     seg_base += len;
   }
 
-  // combine the 4 waves: [w][g] m, l, then [w][g][D] acc
+  // combine the waves: [w][g] m, l, then [w][g][D] acc
   __syncthreads();
   float* red = reinterpret_cast<float*>(tabs);
   float* red_m = red;
   float* red_l = red + kRefWaves * kRefMaxG;
   float* red_a = red + 2 * kRefWaves * kRefMaxG;
 #pragma unroll
-  for (int g = 0; g < kRefMaxG; ++g) {
+  for (int g = 0; g < GMAX; ++g) {
     if (g >= G) continue;
     if (lane == 0) {
       red_m[wave * kRefMaxG + g] = m_run[g];
       red_l[wave * kRefMaxG + g] = l_run[g];
     }
 #pragma unroll
-    for (int u = 0; u < DPL; ++u) red_a[(wave * kRefMaxG + g) * D + DPL * lane + u] = acc[g][u];
+    for (int v = 0; v < DPL; ++v) red_a[(wave * kRefMaxG + g) * D + DPL * lane + v] = acc[g][v];
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += kRefThreads) {
@@ -273,7 +356,12 @@ int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
   const bool shared = p->k_pq_cb == p->v_pq_cb;
   const size_t lds = ref_lds_bytes(p, shared);
   const int blocks = p->batch * p->kv_heads * splits;
-  auto kern = ref_attn_kernel<DPL>;
+  constexpr int U = DPL == 4 ? 2 : 4;
+  const int G = p->q_heads / p->kv_heads;
+  auto kern = G <= 1 ? ref_attn_kernel<DPL, U, 1>
+              : G <= 2 ? ref_attn_kernel<DPL, U, 2>
+              : G <= 4 ? ref_attn_kernel<DPL, U, 4>
+                       : ref_attn_kernel<DPL, U, 8>;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared);
   int st = check_launch("ref_attention");
@@ -301,8 +389,9 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
   RFSN_REQUIRE((M == 4 || M == 8 || M == 16 || M == 32) && D % M == 0,
                "ref_attention: num_subspaces must be 4, 8, 16 or 32 and divide head_dim");
   RFSN_REQUIRE(p->pq_centroids >= 1 && p->pq_centroids <= 256, "ref_attention: PQ codebook size must be in [1, 256]");
-  RFSN_REQUIRE(p->rvq_layers >= 0 && (p->rvq_layers == 0 || (p->rvq_centroids >= 1 && p->rvq_centroids <= 65536)),
-               "ref_attention: bad RVQ shape");
+  RFSN_REQUIRE(p->rvq_layers >= 0 && p->rvq_layers <= kRefMaxL &&
+                   (p->rvq_layers == 0 || (p->rvq_centroids >= 1 && p->rvq_centroids <= 65536)),
+               "ref_attention: at most 8 gated RVQ layers of at most 65536 codewords");
   RFSN_REQUIRE(p->rvq_subspaces >= 0 && (p->rvq_subspaces == 0 || p->rvq_layers == 0),
                "ref_attention: gated RVQ layers and an RVQ subspace stage are exclusive");
   RFSN_REQUIRE(p->rvq_subspaces == 0 || (D % p->rvq_subspaces == 0 && p->rvq_centroids >= 1 && p->rvq_centroids <= 256),

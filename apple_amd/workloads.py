@@ -107,3 +107,41 @@ def make_sequence(w: Workload, b: int, tokens: Optional[int] = None
     v = (torch.randn((T, H, D), generator=g, dtype=torch.float32) * scale).to(torch.float16)
     q = torch.randn((w.q_heads, D), generator=g, dtype=torch.float32).to(torch.float16)
     return k, v, q, g
+
+
+@dataclass(frozen=True)
+class RefWorkload:
+    """A decode step over reference-format tiers (arrival policy: hot then
+    warm), attended by the decode-in-register kernel."""
+    name: str
+    heads: int
+    head_dim: int
+    context: int
+    hot: int
+    pq_subspaces: int
+    pq_centroids: int
+    rvq_layers: int
+    rvq_centroids: int
+
+    @property
+    def warm(self) -> int:
+        return self.context - self.hot
+
+    def bytes_per_step(self) -> int:
+        """Algorithmic HBM bytes: exact hot K/V; per warm vector its PQ codes,
+        its L u16 RVQ codes and its 4-byte row index (every row active at the
+        reference's 0.005 gate on N(0,1) data); K and V codebooks once; the
+        query read and the output written."""
+        D, H = self.head_dim, self.heads
+        per_vec = self.pq_subspaces + 2 * self.rvq_layers + 4
+        cb = 2 * (self.pq_centroids * D + self.rvq_layers * self.rvq_centroids * D) * 2
+        return self.hot * H * 2 * D * 2 + self.warm * H * 2 * per_vec + cb + 2 * H * D * 2
+
+
+REF_WORKLOADS: Dict[str, RefWorkload] = {
+    # the reference's default RFSNConfig (storage.py:23-45): 32 heads, head_dim
+    # 128, PQ 8 x 256 (d 16), 4 gated RVQ layers x 4,096, hot 8,192; 32,768
+    # context, so 24,576 warm tokens
+    "refdefault_32k": RefWorkload("refdefault_32k", heads=32, head_dim=128, context=32768, hot=8192,
+                                  pq_subspaces=8, pq_centroids=256, rvq_layers=4, rvq_centroids=4096),
+}

@@ -6,7 +6,7 @@ Encode: the reference's PyTorch form of the nearest-centroid search
 (rfsn_v10_unified_mac_launcher.py:358-373), fp32 ``torch.cdist ** 2`` and
 ``argmin`` per subspace, applied to both stages and followed by the top-k.
 
-Decode:
+Decode (long-context format):
 
 Restates the reference's PyTorch form (rfsn_v10_unified_mac_launcher.py:
 217-273): per-subspace ``F.embedding`` decode of the PQ codes, the same for
@@ -14,6 +14,10 @@ the RVQ stage, ``fp16(base + rvq)`` (quantization.py:317-319), the sparse
 residual ``K[idx] = fp16(K[idx] + val)``, then the blockwise online-softmax
 recurrence of attention.py:53-105 in fp32 with ``block`` tokens per step.
 GQA: query head h reads KV head h // (Hq // Hkv).
+
+Decode (reference format): ``ref_decode`` / ``ref_decode_step``, the gated
+full-dimension correction of quantization.py:254-275 on the PQ base, then
+the same attention.
 """
 
 from __future__ import annotations
@@ -92,6 +96,35 @@ def decode_step(q: torch.Tensor, hot_k: torch.Tensor, hot_v: torch.Tensor, warm_
         parts.append(x.reshape(Hkv, T, D).permute(1, 0, 2))
     keys = torch.cat([parts_k[0], hot_k.permute(1, 0, 2)], 0)
     values = torch.cat([parts_v[0], hot_v.permute(1, 0, 2)], 0)
+    return blockwise_attention(q, keys, values, scale, block)
+
+
+def ref_decode(pq: torch.Tensor, pq_cb: torch.Tensor, rvq: torch.Tensor, offsets: torch.Tensor,
+               rvq_cb: torch.Tensor) -> torch.Tensor:
+    """Reference-format decode (quantization.py:254-275, 310-319): PQ base,
+    the gated correction fp16(sum_l fl32(C_l[code_l])) on the rows named by
+    ``offsets``, then fp16(base + corr).  pq [N, M]; rvq [A, L]."""
+    base = decode_codes(pq, pq_cb)
+    corr = torch.zeros_like(base)
+    if rvq.shape[0]:
+        tot = torch.zeros((rvq.shape[0], base.shape[1]), dtype=torch.float32)
+        for layer in range(rvq.shape[1]):
+            tot += F.embedding(rvq[:, layer].long(), rvq_cb[layer]).float()
+        corr[offsets.long()] = tot.half()
+    return (base.float() + corr.float()).half()
+
+
+def ref_decode_step(q: torch.Tensor, hot_k: torch.Tensor, hot_v: torch.Tensor, warm_k: dict, warm_v: dict,
+                    cbs: dict, scale: float, block: int) -> torch.Tensor:
+    """One reference-format decode step (cache.py:395-428 with arrival
+    tiers): decode the warm stores, concatenate [hot | warm] and attend.
+    hot_* [T_hot, H, D]; warm_* hold pq [T, H, M], rvq [A, L], offsets [A]."""
+    T, H, M = warm_k["pq"].shape
+    D = hot_k.shape[-1]
+    dec = [ref_decode(w["pq"].reshape(T * H, M), cbs["pq"], w["rvq"], w["offsets"], cbs["rvq"]).reshape(T, H, D)
+           for w in (warm_k, warm_v)]
+    keys = torch.cat([hot_k, dec[0]], 0)
+    values = torch.cat([hot_v, dec[1]], 0)
     return blockwise_attention(q, keys, values, scale, block)
 
 
