@@ -6,10 +6,13 @@ reference's ``attention.py`` (attention.py:16-171).
 reference, only changes fp32 rounding (the kernel's tile is fixed).  Keys and
 values may have fewer heads than the query (GQA): query head ``h`` reads KV
 head ``h // (Hq // Hkv)`` (llama32_adapter.py:384-386).
-``RFSNHybridAttentionMLX`` decodes both compressed stores with the decode
-kernel and attends, as attention.py:159-171 does; the fused
+``RFSNHybridAttentionMLX`` attends the two compressed stores in one launch
+of the decode-in-register kernel (``kernels.ref_attention``), which rebuilds
+each K/V vector in registers with the decode's rounding (attention.py:159-171
+decodes both stores, then attends); stores outside that kernel's shapes are
+decoded and attended as the reference does.  The tiled fused
 dequant-attention kernel is driven by the cache (``cache.py``), which owns the
-tiled code layout that kernel streams.
+code layout that kernel streams.
 """
 
 from __future__ import annotations
