@@ -1559,7 +1559,9 @@ class DecodeSession:
     newest position).  The split count is pinned at each rebuild, so the
     launch's workspace stays valid as the window grows.  ``router`` ranks the
     cold chunks (storage.py:203-234); ``cold_attended`` of them are attended,
-    made resident in device slots at each rebuild."""
+    made resident in device slots at each rebuild.  A cache whose format the
+    tiled kernel does not serve runs ``update`` + ``attention_forward`` (the
+    decode-in-register kernel) every step."""
 
     def __init__(self, cache: RFSNv10KVCacheMLX, q: torch.Tensor, quantizer: QuantizerArg,
                  router: Optional[AsyncHierarchicalRouterMLX] = None, cold_attended: int = 0,
@@ -1596,6 +1598,13 @@ class DecodeSession:
             p.hot_len += T
             p.max_tokens += T
             return self._launch()
+        if not c._fused_ok(int(self.q.shape[1])):
+            # a format the tiled kernel does not serve: one decode-in-register
+            # launch over the window per step, nothing to grow in place
+            self._launch, self._ids = None, None
+            self.rebuilds += 1
+            self.out.copy_(c.attention_forward(self.q, causal=False, cold_chunks=ids))
+            return self.out
         self._rebuild(ids)
         return self.out
 

@@ -350,3 +350,34 @@ def test_head_dim_128_long_context_cache(device, tmp_path, monkeypatch):
     kw_, _, _ = c.materialize_window(query_positions=T(np.array([299, 299], np.int32), device))
     w0 = c.num_cold
     assert np.array_equal(H(kw_)[w0:w0 + ks.num_tokens].view(np.uint16), dec.reshape(-1, 2, 128).view(np.uint16))
+
+
+def test_decode_session_head_dim_128(device, tmp_path):
+    """A decode session over a head_dim-128 long-context cache: each step is
+    update + the decode-in-register attention, equal to attention_forward at
+    the newest position."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    cfg = RFSNConfig(hidden_dim=1024, num_heads=8, head_dim=128, num_subspaces=16, subspace_dim=8,
+                     num_rvq_layers=1, rvq_codebook_size=256, rvq_sparsity_threshold=0.0, hot_capacity=64,
+                     warm_capacity=96, cold_capacity=512, block_size_seq=32, num_kv_heads=2, rvq_subspaces=16,
+                     sparse_topk=4, tier_policy="recency", cold_chunk_tokens=32, cold_medium="pinned",
+                     disk_cache_dir=str(tmp_path))
+    g = rng(41)
+    qz = HybridQuantizerMLX(cfg, device=device, pq_codebooks=T(rand_codebooks(g, 16, 256, 8), device),
+                            rvq_codebooks=T(rand_codebooks(g, 16, 256, 8), device))
+    c = RFSNv10KVCacheMLX(cfg, layer_idx=0, device=device)
+    k, v = randn16(g, 260, 2, 128), randn16(g, 260, 2, 128)
+    c.update(T(k[:200], device), T(v[:200], device), qz)
+    q = T(randn16(g, 1, 8, 128), device)
+    sess = c.decode_session(q, qz)
+    for t in range(200, 260):
+        out = sess.step(T(k[t:t + 1], device), T(v[t:t + 1], device))
+    ref = c.attention_forward(q, causal=True)
+    assert sess.rebuilds == 60 and c.total_tokens == 260
+    assert float((out.float() - ref.float()).abs().max()) == 0.0
+    kw_, vw_, _ = c.materialize_window()
+    mat = nx.blockwise_attention(H(q), H(kw_), H(vw_), 128 ** -0.5, 16, False, None)
+    assert np.abs(H(out).astype(np.float32) - mat.astype(np.float32)).max() <= TOL
