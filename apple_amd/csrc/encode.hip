@@ -666,12 +666,16 @@ struct EncodeJobs {
 typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
 typedef float ff4 __attribute__((ext_vector_type(4)));
 
-// Insert key k into the sorted pair m1 <= m2 in two VALU ops.
-__device__ __forceinline__ void key_insert2(int& m1, int& m2, int k) {
-  asm("v_med3_i32 %1, %0, %1, %2\n\t"
-      "v_min_i32_e32 %0, %0, %2"
-      : "+v"(m1), "+v"(m2)
-      : "v"(k));
+// Insert keys a, b into the sorted pair m1 <= m2 in three VALU ops: the new
+// second smallest is min(m2, med3(m1, a, b)) (m2 >= m1, so the second of
+// {m1, m2, a, b} is the smaller of m2 and the second of {m1, a, b}).
+__device__ __forceinline__ void key_insert2x2(int& m1, int& m2, int a, int b) {
+  int t;
+  asm("v_med3_i32 %2, %0, %3, %4\n\t"
+      "v_min3_i32 %0, %0, %3, %4\n\t"
+      "v_min_i32_e32 %1, %1, %2"
+      : "+v"(m1), "+v"(m2), "=&v"(t)
+      : "v"(a), "v"(b));
 }
 // Insert key k into the sorted triple m1 <= m2 <= m3 in three VALU ops.
 // Written out because the compiler, knowing m1 <= m2, turns the middle
@@ -709,29 +713,43 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
   const int C = jobs.C, Cr = jobs.Cr;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // ---- tables: row r of (stage s, subspace m) at tab + (s*M + m)*TB + r*RB
+  // ---- tables: row r of (stage s, subspace m) at tab + (s*M + m)*TB + r*RB.
+  // Thread tid builds rows i = tid + kFeThreads * it; every centroid load is
+  // issued before the first row is formed, so the set-up waits for one memory
+  // round trip.
+  constexpr int kRows = S * M * 256 / kFeThreads;
+  static_assert(S * M * 256 % kFeThreads == 0, "table rows per thread");
   for (int i = tid; i < S * M; i += kFeThreads) rmax_s[i] = 0u;
-  __syncthreads();
-  for (int i = tid; i < S * M * 256; i += kFeThreads) {
+  uint2 cw[kRows][CG];  // the centroids' coordinates, 4 fp16 per group
+#pragma unroll
+  for (int it = 0; it < kRows; ++it) {
+    const int i = tid + kFeThreads * it;
     const int r = i & 255, sm = i >> 8, s = sm / M, m = sm % M;
     const int nc = s == 0 ? C : Cr;
     const uint16_t* cb = (s == 0 ? job.pq_cb : job.rvq_cb) + ((size_t)m * nc + (r < nc ? r : 0)) * DS;
-    uint2 cw[CG];  // the centroid's coordinates, 4 fp16 per group
 #pragma unroll
-    for (int gq = 0; gq < CG; ++gq) cw[gq] = r < nc ? reinterpret_cast<const uint2*>(cb)[gq] : make_uint2(0u, 0u);
+    for (int gq = 0; gq < CG; ++gq)
+      cw[it][gq] = r < nc ? reinterpret_cast<const uint2*>(cb)[gq] : make_uint2(0u, 0u);
+  }
+  __syncthreads();  // rmax_s cleared
+#pragma unroll
+  for (int it = 0; it < kRows; ++it) {
+    const int i = tid + kFeThreads * it;
+    const int r = i & 255, sm = i >> 8, s = sm / M;
+    const int nc = s == 0 ? C : Cr;
     // R for the screening rows and the certificate's rmax: a float sum, whose
     // error (< 2^-21 R) the certificate's 2^-17 R margin covers; the exact
     // distances form the canonical float64 R themselves
     float R = 0.0f;
 #pragma unroll
     for (int gq = 0; gq < CG; ++gq) {
-      const fh4 c4 = __builtin_bit_cast(fh4, cw[gq]);
+      const fh4 c4 = __builtin_bit_cast(fh4, cw[it][gq]);
 #pragma unroll
       for (int u = 0; u < 4; ++u) R = __builtin_fmaf((float)c4[u], (float)c4[u], R);
     }
     uint8_t* row = tab + (size_t)sm * TB + r * RB;
 #pragma unroll
-    for (int gq = 0; gq < CG; ++gq) *reinterpret_cast<uint2*>(row + 8 * gq) = cw[gq];
+    for (int gq = 0; gq < CG; ++gq) *reinterpret_cast<uint2*>(row + 8 * gq) = cw[it][gq];
     _Float16 rh, rl;
     if (r < nc) {
       const float half_r = 0.5f * R;
@@ -743,11 +761,16 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
     }
     const fh4 aug = {rh, rl, (_Float16)1.0f, (_Float16)1.0f};
     *reinterpret_cast<fh4*>(row + 8 * CG) = aug;
-    // largest R of the table: a wave's 64 rows share (s, m)
+    // largest R of the table (a wave's 64 rows share (s, m)): the wave's max
+    // by DPP within rows of 16 lanes, then the four row maxima
     uint32_t rb = r < nc ? (__builtin_bit_cast(uint32_t, R) & 0x7FFFFFFFu) : 0u;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) rb = max(rb, (uint32_t)__shfl_xor((int)rb, o, 64));
-    if (lane == 0) atomicMax(&rmax_s[sm], rb);
+    rb = max(rb, (uint32_t)__builtin_amdgcn_mov_dpp((int)rb, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+    rb = max(rb, (uint32_t)__builtin_amdgcn_mov_dpp((int)rb, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+    rb = max(rb, (uint32_t)__builtin_amdgcn_mov_dpp((int)rb, 0x141, 0xF, 0xF, true));  // row_half_mirror
+    rb = max(rb, (uint32_t)__builtin_amdgcn_mov_dpp((int)rb, 0x140, 0xF, 0xF, true));  // row_mirror
+    const uint32_t w0 = (uint32_t)__builtin_amdgcn_readlane((int)rb, 0), w1 = (uint32_t)__builtin_amdgcn_readlane((int)rb, 16);
+    const uint32_t w2 = (uint32_t)__builtin_amdgcn_readlane((int)rb, 32), w3 = (uint32_t)__builtin_amdgcn_readlane((int)rb, 48);
+    if (lane == 0) atomicMax(&rmax_s[sm], max(max(w0, w1), max(w2, w3)));
   }
   __syncthreads();
 
@@ -821,36 +844,35 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
       for (int t = 0; t < 16; ++t) {  // MFMA t + 1 issued before the keys of t
         ff4 next = acc;
         if (t + 1 < 16) next = __builtin_amdgcn_mfma_f32_16x16x16f16(a[t + 1], b, ff4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        int key[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // centroid 16t + i (+ 4g below)
           // the index as an opaque SGPR and the mask in a VGPR: one v_and_or_b32
           int sidx;
           asm("s_mov_b32 %0, %1" : "=s"(sidx) : "n"(16 * t + i));
           const float z = acc[i];
-          insert(i, (__builtin_bit_cast(int, z) & maskv) | sidx);
+          key[i] = (__builtin_bit_cast(int, z) & maskv) | sidx;
         }
+        insert(key);
         acc = next;
       }
     };
     const int x32 = 4 * (lane ^ 32);
     // screening: the two smallest keys (two lists for independent chains)
     int m1 = kNoKey, m2 = kNoKey, n1 = kNoKey, n2 = kNoKey;
-    screen([&](int i, int key) {
-      if (i & 1) key_insert2(n1, n2, key);
-      else key_insert2(m1, m2, key);
+    screen([&](const int (&key)[4]) {
+      key_insert2x2(m1, m2, key[0], key[1]);
+      key_insert2x2(n1, n2, key[2], key[3]);
     });
-    key_insert2(m1, m2, n1);
-    key_insert2(m1, m2, n2);
+    key_insert2x2(m1, m2, n1, n2);
     if (m1 != kNoKey) m1 |= 4 * g;
     if (m2 != kNoKey) m2 |= 4 * g;
     {  // the vector's four lanes l, l ^ 16, l ^ 32, l ^ 48
       int o1 = lane_xor16(m1), o2 = lane_xor16(m2);
-      key_insert2(m1, m2, o1);
-      key_insert2(m1, m2, o2);
+      key_insert2x2(m1, m2, o1, o2);
       o1 = lane_xor32(m1, x32);
       o2 = lane_xor32(m2, x32);
-      key_insert2(m1, m2, o1);
-      key_insert2(m1, m2, o2);
+      key_insert2x2(m1, m2, o1, o2);
     }
     const float rmax = __builtin_bit_cast(float, rmax_s[s * M + m]);
     const float v1 = key_value(m1), v2 = key_value(m2);
@@ -861,7 +883,10 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
     // some vector of the wave is uncertain: its three smallest keys, then
     // the canonical float64 distances (x and L as float64 chains)
     int p3 = kNoKey, p1 = kNoKey, p2 = kNoKey;
-    screen([&](int, int key) { key_insert3(p1, p2, p3, key); });
+    screen([&](const int (&key)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) key_insert3(p1, p2, p3, key[i]);
+    });
     if (p1 != kNoKey) p1 |= 4 * g;
     if (p2 != kNoKey) p2 |= 4 * g;
     if (p3 != kNoKey) p3 |= 4 * g;
