@@ -95,6 +95,7 @@ SIGNATURES = {
     "rfsn_hot_append": (i32, [vp, vp, i64, i32, i32, i32, vp, vp, i64, i64, vp, vp]),
     "rfsn_ref_attention_workspace_bytes": (sz, [C.POINTER(RefParams)]),
     "rfsn_ref_attention": (i32, [C.POINTER(RefParams), vp]),
+    "rfsn_read_stream": (i32, [vp, i64, vp, i32, vp]),
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),

@@ -450,6 +450,32 @@ def device_copy_gbs(mib: int = 1024, reps: int = 10) -> float:
     return round(gbs, 1)
 
 
+def device_read_gbs(gib: int = 4, blocks: int = 65536, reps: int = 10) -> float:
+    """Measured read-only HBM stream (rfsn_read_stream over ``gib`` GiB), GB/s:
+    the ceiling a read-dominated kernel can reach on this device."""
+    import torch
+    from apple_amd import _lib as L
+
+    n = gib << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    out = torch.empty(blocks, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        L.call("rfsn_read_stream", src.data_ptr(), n, out.data_ptr(), blocks, s)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        L.call("rfsn_read_stream", src.data_ptr(), n, out.data_ptr(), blocks, s)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = n * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, out
+    torch.cuda.empty_cache()
+    return round(gbs, 1)
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -757,6 +783,7 @@ def main(argv=None) -> int:
     kernel_ms = start.elapsed_time(end) / args.steps
     pct = step_percentiles(launch, args.steps)
     copy_gbs = device_copy_gbs()
+    read_gbs = device_read_gbs()
     step_bytes = w.bytes_per_step()
     achieved = step_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = traffic_from_profiles(w.name)
@@ -785,7 +812,8 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel_ms": round(kernel_ms, 5), "kernel_ms_percentiles": pct,
-                     "device_copy_gbs": copy_gbs, "frac_of_device_copy": round(achieved / copy_gbs, 4)},
+                     "device_copy_gbs": copy_gbs, "frac_of_device_copy": round(achieved / copy_gbs, 4),
+                     "device_read_gbs": read_gbs, "frac_of_device_read": round(achieved / read_gbs, 4)},
     }
     if cache.last_drift is not None:
         # drift [B, Hq, splits]; a block (sequence, KV head, split) recomputes when one of its heads fires

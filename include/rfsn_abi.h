@@ -438,6 +438,13 @@ int rfsn_event_query(void* event);
 /* 1 when every operation queued on the stream has finished, 0 when not yet, <0 on error. */
 int rfsn_stream_query(void* stream);
 
+/* ---------------------------------------------------------------- measurement
+ * A read-only stream over `bytes` (a positive multiple of 16, 16-byte
+ * aligned) with `blocks` blocks of 256 threads; out_dev receives one word
+ * per block.  No counterpart in the reference: it measures the HBM read
+ * ceiling that the decode kernels' roofline fractions are compared with. */
+int rfsn_read_stream(const void* src_dev, int64_t bytes, uint32_t* out_dev, int32_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
