@@ -236,6 +236,22 @@ __device__ __forceinline__ TileSrc walk_segments(cseg segs, int nseg, int r) {
   return s;
 }
 
+// Encoded tile r of segments 1..nseg-1 from the host's tile map (uniform):
+// one scalar load, then the segment's fields.  Entries are clamped to the
+// table (a segment index past it reads the last segment; a tile past its
+// segment counts no tokens).
+typedef const uint32_t __attribute__((address_space(4)))* cmap;
+__device__ __forceinline__ TileSrc map_tile(cseg segs, int nseg, cmap row, int r) {
+  const uint32_t e = row[r];
+  TileSrc s;
+  s.kind = 1;
+  s.seg = min((int)(e >> 16), nseg - 1);
+  s.off = (int)(e & 0xFFFFu) * kTile;
+  s.count = max(0, min(kTile, segs[s.seg].len - s.off));
+  s.pos0 = segs[s.seg].pos0 + s.off;
+  return s;
+}
+
 // Tiles of segments 1..nseg-1, 8 independent reads per step.
 __device__ __forceinline__ int tail_tiles(cseg segs, int nseg) {
   int total = 0;
@@ -693,7 +709,8 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
   if (nseg > 0) w0 = warm_base<M, RVQ, KS, SX>(segs, h, p.kv_heads);
   const int seg0_tiles = nseg > 0 ? (w0.len + kTile - 1) / kTile : 0;
   int total_tiles = hot_tiles + seg0_tiles;
-  total_tiles += tail_tiles(segs, nseg);
+  const cmap tmap = p.tile_map ? (cmap)(p.tile_map + (int64_t)b * p.tile_map_stride) : nullptr;
+  total_tiles += tmap ? min(max(p.tile_map_count[b], 0), (int)p.tile_map_stride) : tail_tiles(segs, nseg);
   const int t_begin = split * tiles_per_split;
   const int t_end = min(total_tiles, t_begin + tiles_per_split);
   const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
@@ -724,7 +741,7 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
       load_k(rk, w0, s.off, s.count);
       load_tile<M, RVQ, KS>(rv, w0, 1, s.off, s.count, lane);
     } else {
-      s = walk_segments(segs, nseg, r - seg0_tiles);
+      s = tmap ? map_tile(segs, nseg, tmap, r - seg0_tiles) : walk_segments(segs, nseg, r - seg0_tiles);
       const WarmBase w = warm_base<M, RVQ, KS, SX>(segs + s.seg, h, p.kv_heads);
       load_k(rk, w, s.off, s.count);
       load_tile<M, RVQ, KS>(rv, w, 1, s.off, s.count, lane);
@@ -1430,6 +1447,8 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   RFSN_REQUIRE(p->guard == nullptr || p->k_layout == 1, "fused: the drift guard serves k_layout 1 only");
   RFSN_REQUIRE(p->guard == nullptr || p->guard_tol >= 0.f, "fused: guard_tol must be >= 0");
   RFSN_REQUIRE(p->drift == nullptr || p->guard != nullptr, "fused: drift estimates need the guard");
+  RFSN_REQUIRE(p->tile_map == nullptr || (p->tile_map_count && p->tile_map_stride > 0 && p->max_segments > 0),
+               "fused: a tile map needs its counts, a positive stride and a segment table");
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;

@@ -13,6 +13,7 @@ from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import _lib as L
@@ -388,11 +389,20 @@ def unpack_score_codes(dst: Dict[str, Optional[torch.Tensor]], T: int, t0: int =
     return pq, rvq, si, sv
 
 
+def _round256(n: int) -> int:
+    """n rounded up to a multiple of 256 (device sub-buffer alignment)."""
+    return (n + 255) // 256 * 256
+
+
+_TILE_MAPS: "OrderedDict[tuple, np.ndarray]" = OrderedDict()
+
+
 class SegmentTable:
     """Host builder of the device ``rfsn_segment`` table of the fused kernel."""
 
     def __init__(self, batch: int):
         self.rows: List[List[L.Segment]] = [[] for _ in range(batch)]
+        self.tiles: List[List[int]] = [[] for _ in range(batch)]  # 32-token tiles of each segment
         self.keep: List[torch.Tensor] = []
 
     def add(self, b: int, k: Dict[str, Optional[torch.Tensor]], v: Dict[str, Optional[torch.Tensor]],
@@ -417,6 +427,7 @@ class SegmentTable:
             return L.Codes(L.ptr(c.get("pq")), L.ptr(c.get("rvq")), L.ptr(c.get("sparse_idx")),
                            L.ptr(c.get("sparse_val")))
         self.rows[b].append(L.Segment(codes(k), codes(v), head_stride, length, pos0))
+        self.tiles[b].append((int(length) + 31) // 32)
 
     def add_codes(self, b: int, k: "L.Codes", v: "L.Codes", keep: Sequence[torch.Tensor], head_stride: int,
                   length: int, pos0: int, available: int) -> None:
@@ -426,6 +437,7 @@ class SegmentTable:
             raise ValueError(f"segment of {length} tokens exceeds its {available} available code rows")
         self.keep.extend(keep)
         self.rows[b].append(L.Segment(k, v, head_stride, length, pos0))
+        self.tiles[b].append((int(length) + 31) // 32)
 
     @property
     def max_rows(self) -> int:
@@ -436,10 +448,36 @@ class SegmentTable:
     def empty(self) -> bool:
         return all(not r for r in self.rows)
 
-    def to_device(self, device) -> Tuple[torch.Tensor, torch.Tensor, int]:
-        """(segment table, segment counts, max_segments) in device memory.
-        Table and counts travel in one asynchronous copy from pinned memory,
-        so building a launch never waits for the work already queued."""
+    def tile_map(self) -> Tuple[List["np.ndarray"], int]:
+        """Per row, (segment << 16) | tile within the segment of every encoded
+        tile of segments 1..n-1, in order (the kernel's tile -> segment map).
+        Rows with the same segment lengths share one map (memoized)."""
+        rows = []
+        for b, r in enumerate(self.rows):
+            key = tuple(self.tiles[b][1:]) if len(self.tiles[b]) == len(r) else \
+                tuple((int(seg.len) + 31) // 32 for seg in r[1:])
+            hit = _TILE_MAPS.get(key)
+            if hit is not None:
+                _TILE_MAPS.move_to_end(key)
+                rows.append(hit)
+                continue
+            tiles = np.array(key, dtype=np.int64)
+            if len(tiles) > 0xFFFF or (len(tiles) and tiles.max() > 0x10000):
+                raise ValueError("tile map: at most 65535 segments of at most 65536 tiles")
+            seg = np.repeat(np.arange(1, len(tiles) + 1, dtype=np.int64), tiles)
+            within = np.arange(seg.size, dtype=np.int64) - np.repeat(np.cumsum(tiles) - tiles, tiles)
+            m = ((seg << 16) | within).astype(np.uint32)
+            _TILE_MAPS[key] = m
+            while len(_TILE_MAPS) > 64:
+                _TILE_MAPS.popitem(last=False)
+            rows.append(m)
+        return rows, max(1, max(m.size for m in rows))
+
+    def to_device(self, device) -> Tuple[torch.Tensor, torch.Tensor, int, torch.Tensor, torch.Tensor, int]:
+        """(segment table, segment counts, max_segments, tile map, tile map
+        counts, tile map stride) in device memory.  Everything travels in one
+        asynchronous copy from pinned memory, so building a launch never
+        waits for the work already queued."""
         maxs = max(1, max(len(r) for r in self.rows))
         size = C.sizeof(L.Segment)
         nb = size * len(self.rows) * maxs
@@ -448,11 +486,22 @@ class SegmentTable:
             for s, seg in enumerate(r):
                 host[b * maxs + s] = seg
         counts = (C.c_int32 * len(self.rows))(*[len(r) for r in self.rows])
-        staged = torch.empty(nb + C.sizeof(counts), dtype=torch.uint8, pin_memory=True)
+        maps, stride = self.tile_map()
+        nrows = len(self.rows)
+        o_counts = nb
+        o_map = _round256(o_counts + 4 * nrows)
+        o_mcounts = o_map + 4 * nrows * stride
+        staged = torch.empty(o_mcounts + 4 * nrows, dtype=torch.uint8, pin_memory=True)  # map rows read up to their counts
         C.memmove(staged.data_ptr(), host, nb)
-        C.memmove(staged.data_ptr() + nb, counts, C.sizeof(counts))
+        C.memmove(staged.data_ptr() + o_counts, counts, C.sizeof(counts))
+        buf = staged.numpy()
+        flat = buf[o_map:o_mcounts].view(np.uint32).reshape(nrows, stride)
+        for b, m in enumerate(maps):
+            flat[b, :m.size] = m
+        buf[o_mcounts:].view(np.int32)[:] = [m.size for m in maps]
         dev = staged.to(device, non_blocking=True)
-        return dev[:nb], dev[nb:].view(torch.int32), maxs
+        return (dev[:nb], dev[o_counts:o_counts + 4 * nrows].view(torch.int32), maxs,
+                dev[o_map:o_mcounts].view(torch.int32), dev[o_mcounts:].view(torch.int32), stride)
 
 
 def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: float, causal: bool,
@@ -502,7 +551,7 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
         raise ValueError(f"a sequence attends {longest} tokens, more than max_tokens = {max_tokens}")
     if table is None:
         table = segments.to_device(q.device)
-    seg_t, nseg_t, maxs = table
+    seg_t, nseg_t, maxs, *tmap = table
     qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)
     if out.shape != q.shape or out.dtype != torch.float16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous fp16 tensor shaped like q")
@@ -519,6 +568,9 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     p.hot_k, p.hot_v = L.ptr(hot_k), L.ptr(hot_v)
     p.hot_cap, p.hot_seq_stride, p.hot_len, p.hot_pos0 = hot_cap, hot_seq_stride, hot_len, hot_pos0
     p.segments, p.num_segments, p.max_segments = seg_t.data_ptr(), nseg_t.data_ptr(), maxs
+    if tmap:
+        map_t, map_n, map_stride = tmap
+        p.tile_map, p.tile_map_count, p.tile_map_stride = map_t.data_ptr(), map_n.data_ptr(), map_stride
     p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
     p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
     p.max_tokens, p.splits = max_tokens, splits
@@ -548,7 +600,8 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
             raise ValueError(f"partial calls share a workspace of at least {wsb} bytes")
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
-    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, workspace, segments, *cbs, guard, drift], out, _stream(q))
+    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, *tmap[:2], workspace, segments, *cbs, guard, drift], out,
+                     _stream(q))
     fl.drift = drift
     if not launch:
         return fl

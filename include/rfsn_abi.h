@@ -308,6 +308,14 @@ typedef struct rfsn_fused_params {
   const float* guard;
   float* drift;
   float guard_tol;
+  /* Tile map (optional; NULL: the kernel walks the segment table to find a
+   * tile, one scalar-memory round trip per 8 segments).  For row b,
+   * tile_map[b * tile_map_stride + r] = (segment << 16) | tile within the
+   * segment, for the encoded tiles r = 0, 1, ... of segments 1..nseg-1 in
+   * order, and tile_map_count[b] = their number (<= tile_map_stride). */
+  const uint32_t* tile_map;
+  const int32_t* tile_map_count;
+  int64_t tile_map_stride;
 } rfsn_fused_params;
 
 /* Token splits the call would use (p->splits, or the automatic choice when 0);
