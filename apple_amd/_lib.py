@@ -55,7 +55,8 @@ class FusedParams(C.Structure):
                 ("max_tokens", i32), ("splits", i32), ("workspace", vp), ("workspace_bytes", sz),
                 ("part_base", i32), ("part_slots", i32), ("merge", i32), ("k_layout", i32),
                 ("guard", vp), ("drift", vp), ("guard_tol", f32),
-                ("tile_map", vp), ("tile_map_count", vp), ("tile_map_stride", i64)]
+                ("tile_map", vp), ("tile_map_count", vp), ("tile_map_stride", i64),
+                ("k_tab", vp), ("v_tab", vp), ("tab_stride", i64)]
 
 
 class RefStoreCodes(C.Structure):

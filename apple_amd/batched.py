@@ -165,6 +165,16 @@ class RFSNBatchedKVCache:
             self._table = (t, t.to_device(self.device))
         return self._table
 
+    def _entry_tables(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Per-sequence entry-major K and V tables ([B, 256, 128],
+        ``kernels.entry_tables``), rebuilt when a codebook tensor changes."""
+        cbs = [self.cb["k_pq"], self.cb.get("k_rvq"), self.cb["v_pq"], self.cb.get("v_rvq")]
+        key = tuple((t.data_ptr(), t._version) if t is not None else None for t in cbs)
+        if getattr(self, "_tables_key", None) != key:
+            self._tables = (K.entry_tables(cbs[0], cbs[1]), K.entry_tables(cbs[2], cbs[3]))
+            self._tables_key = key
+        return self._tables
+
     def prepare(self, q: torch.Tensor, causal: bool = False, query_positions=None, splits: int = 0,
                 out: Optional[torch.Tensor] = None) -> "K.FusedLaunch":
         """A reusable launch of ``attention_forward`` on these buffers (q is
@@ -205,7 +215,7 @@ class RFSNBatchedKVCache:
             hot_v=self.hot_v, hot_len=self.num_hot[0], hot_pos0=self.num_warm[0],
             hot_seq_stride=self.H * self.hot_cap * self.D, segments=table, table=dev_table,
             k_pq_cb=self.cb["k_pq"], v_pq_cb=self.cb["v_pq"], k_rvq_cb=self.cb.get("k_rvq"),
-            v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True,
+            v_rvq_cb=self.cb.get("v_rvq"), cb_batch_stride=True, tables=self._entry_tables(),
             max_tokens=max(h + w for h, w in zip(self.num_hot, self.num_warm)), splits=splits,
             workspace=self._ws, out=out, hot_cap=self.hot_cap, launch=False, k_layout=self.k_layout, **guard)
         self.last_drift = fl.drift

@@ -444,6 +444,8 @@ class RFSNv10KVCacheMLX:
         self._guard = torch.zeros((1, 65), dtype=torch.float32, device=self.device)
         self._vabs = self._guard[0, 64:]  # the row's V bound, updated by every append
         self._guard_key: Optional[Tuple[int, int]] = None
+        self._tables_key: Optional[tuple] = None
+        self._tables: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self.last_drift: Optional[torch.Tensor] = None
         self.last_access_stats = self._empty_access_stats()
 
@@ -541,6 +543,18 @@ class RFSNv10KVCacheMLX:
             torch.maximum(self._vabs, vcb.view(1), out=self._vabs)
             self._guard_key = key
         return self._guard
+
+    def _entry_tables(self, rvq: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The fused kernel's entry-major K and V tables (``kernels.entry_tables``),
+        built once per codebook set (keyed like the guard, by the quantizers
+        and their codebook tensors)."""
+        cbs = [self._kq.pq.codebooks, self._kq.rvq.codebooks if rvq else None,
+               self._vq.pq.codebooks, self._vq.rvq.codebooks if rvq else None]
+        key = (id(self._kq), id(self._vq), *[(t.data_ptr(), t._version) if t is not None else None for t in cbs])
+        if self._tables_key != key:
+            self._tables = (K.entry_tables(cbs[0], cbs[1]), K.entry_tables(cbs[2], cbs[3]))
+            self._tables_key = key
+        return self._tables
 
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Append [T, H, D] tokens to the hot tier.  The buffers hold up to
@@ -1480,7 +1494,7 @@ class RFSNv10KVCacheMLX:
                       k_rvq_cb=self._kq.rvq.codebooks if fmt.rvq_subspaces else None,
                       v_rvq_cb=self._vq.rvq.codebooks if fmt.rvq_subspaces else None,
                       cb_batch_stride=False, hot_cap=int(self._hot_k.shape[1]), out=out, launch=False,
-                      k_layout=self._k_layout)
+                      k_layout=self._k_layout, tables=self._entry_tables(bool(fmt.rvq_subspaces)))
         guard = None
         if self._guarded:
             guard = self._guard_tensor()

@@ -748,48 +748,79 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
     }
     if (tt >= t_end) s.kind = -1;
   };
-  // Every wave requests the codes of its first encoded tiles before the block
-  // stages its codebooks and builds its tables: HBM streams while the set-up
-  // runs.
   const int seg_begin = max(t_begin, hot_tiles);
-  if (seg_begin < t_end) {  // uniform: the split has encoded tiles
-#pragma unroll
-    for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
-  }
 
   // ---- stage this sequence's codebooks: HBM [m][e][d] -> LDS [table][e][PQ m | RVQ m][d]
   // (without an RVQ stage the upper slot half holds a second copy of the PQ table)
   {
     const uint16_t* kp = (const uint16_t*)p.k_pq_cb + (int64_t)b * p.pq_cb_stride;
     const uint16_t* vp = (const uint16_t*)p.v_pq_cb + (int64_t)b * p.pq_cb_stride;
-    const uint16_t* srcs[4] = {kp, vp, RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : kp,
-                               RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : vp};
+    const uint16_t* cbp[4] = {kp, vp, RVQ ? (const uint16_t*)p.k_rvq_cb + (int64_t)b * p.rvq_cb_stride : kp,
+                              RVQ ? (const uint16_t*)p.v_rvq_cb + (int64_t)b * p.rvq_cb_stride : vp};
     // every load of this thread is issued before its first LDS store, so the
     // block waits for one memory round trip rather than one per entry
     using Vec = typename std::conditional<d == 4, uint2, uint4>::type;
     constexpr int kIters = (M * 256 + kThreads - 1) / kThreads;
+    constexpr int kTabVecs = kTableBytes / 16;                      // uint4 units of one table
+    constexpr int kTabIters = (kTabVecs + kThreads - 1) / kThreads;
+    const bool pre = p.v_tab != nullptr;  // uniform: entry-major tables from the host
     Vec v[4][kIters];
+    uint4 tv[2][kTabIters];
+    if (pre) {
+      // contiguous copies of the K (codebook path) and V tables
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (LUT && (c & 1) == 0) continue;  // the K tables become score tables below
-      const int n = (c < 2 || !RVQ) ? C : Cr;
+      for (int c = 0; c < 2; ++c) {
+        if (LUT && c == 0) continue;  // the K tables become score tables below
+        const uint4* src = reinterpret_cast<const uint4*>((const uint8_t*)(c ? p.v_tab : p.k_tab) + (int64_t)b * p.tab_stride);
 #pragma unroll
-      for (int i = 0; i < kIters; ++i) {
-        const int idx = threadIdx.x + i * kThreads;
-        const int e = idx / M, m = idx % M;  // consecutive lanes store consecutive slots of one entry
-        v[c][i] = Vec{};
-        if (idx < M * 256 && e < n) v[c][i] = *reinterpret_cast<const Vec*>(srcs[c] + ((int64_t)m * n + e) * d);
+        for (int i = 0; i < kTabIters; ++i) {
+          const int idx = threadIdx.x + i * kThreads;
+          tv[c][i] = idx < kTabVecs ? src[idx] : make_uint4(0u, 0u, 0u, 0u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (LUT && (c & 1) == 0) continue;  // the K tables become score tables below
+        const int n = (c < 2 || !RVQ) ? C : Cr;
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+          const int idx = threadIdx.x + i * kThreads;
+          const int e = idx / M, m = idx % M;  // consecutive lanes store consecutive slots of one entry
+          v[c][i] = Vec{};
+          if (idx < M * 256 && e < n) v[c][i] = *reinterpret_cast<const Vec*>(cbp[c] + ((int64_t)m * n + e) * d);
+        }
       }
     }
+    // Every wave requests the codes of its first encoded tiles now, after the
+    // codebook loads: HBM streams while the set-up runs, and the stores below
+    // wait only for the (L2-resident) codebook loads issued before them.
+    if (seg_begin < t_end) {  // uniform: the split has encoded tiles
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (LUT && (c & 1) == 0) continue;
-      uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
+      for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+    }
+    if (pre) {
 #pragma unroll
-      for (int i = 0; i < kIters; ++i) {
-        const int idx = threadIdx.x + i * kThreads;
-        const int e = idx / M, m = idx % M;
-        if (idx < M * 256) *reinterpret_cast<Vec*>(dst + e * kEntryBytes + m * d * 2) = v[c][i];
+      for (int c = 0; c < 2; ++c) {
+        if (LUT && c == 0) continue;
+        uint4* dst = reinterpret_cast<uint4*>(lds + c * kTableBytes);
+#pragma unroll
+        for (int i = 0; i < kTabIters; ++i) {
+          const int idx = threadIdx.x + i * kThreads;
+          if (idx < kTabVecs) dst[idx] = tv[c][i];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (LUT && (c & 1) == 0) continue;
+        uint8_t* dst = lds + (c & 1) * kTableBytes + (c >> 1) * kRvqSlot;
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+          const int idx = threadIdx.x + i * kThreads;
+          const int e = idx / M, m = idx % M;
+          if (idx < M * 256) *reinterpret_cast<Vec*>(dst + e * kEntryBytes + m * d * 2) = v[c][i];
+        }
       }
     }
   }
@@ -813,10 +844,14 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
       qw[j] = j < G ? *reinterpret_cast<const uint2*>(qrow + 4 * m) : make_uint2(0, 0);
     }
     uint2 e[kPasses];
+    const uint8_t* ktab = p.k_tab ? (const uint8_t*)p.k_tab + (int64_t)b * p.tab_stride : nullptr;
 #pragma unroll
     for (int i = 0; i < kPasses; ++i) {
       const int c = (threadIdx.x >> 5) + kRows * i;
-      e[i] = c < nc ? *reinterpret_cast<const uint2*>(cb + ((int64_t)m * nc + c) * 4) : make_uint2(0, 0);
+      if (ktab)  // entry-major: consecutive lanes read consecutive slots of one entry
+        e[i] = *reinterpret_cast<const uint2*>(ktab + c * kEntryBytes + s * 8);
+      else
+        e[i] = c < nc ? *reinterpret_cast<const uint2*>(cb + ((int64_t)m * nc + c) * 4) : make_uint2(0, 0);
     }
     float qf[4][4];
 #pragma unroll
@@ -1449,6 +1484,11 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
   RFSN_REQUIRE(p->drift == nullptr || p->guard != nullptr, "fused: drift estimates need the guard");
   RFSN_REQUIRE(p->tile_map == nullptr || (p->tile_map_count && p->tile_map_stride > 0 && p->max_segments > 0),
                "fused: a tile map needs its counts, a positive stride and a segment table");
+  RFSN_REQUIRE((p->k_tab == nullptr) == (p->v_tab == nullptr) && p->tab_stride >= 0 &&
+                   (p->tab_stride == 0 || p->tab_stride >= 65536) &&
+                   reinterpret_cast<uintptr_t>(p->k_tab) % 16 == 0 && reinterpret_cast<uintptr_t>(p->v_tab) % 16 == 0 &&
+                   p->tab_stride % 16 == 0,
+               "fused: entry tables come as a 16-byte aligned K and V pair of 64 KB per sequence (stride 0 or >= 65536)");
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
   hipStream_t s = (hipStream_t)stream;

@@ -389,6 +389,23 @@ def unpack_score_codes(dst: Dict[str, Optional[torch.Tensor]], T: int, t0: int =
     return pq, rvq, si, sv
 
 
+def entry_tables(pq_cb: torch.Tensor, rvq_cb: Optional[torch.Tensor]) -> torch.Tensor:
+    """The fused kernel's entry-major table of one codebook pair: fp16
+    [..., 256, 128], entry e = [PQ entries e of the M subspaces | RVQ entries
+    e] (the PQ entries again without an RVQ stage), zeros past a codebook's
+    size.  pq_cb [..., M, C, d], rvq_cb [..., M, C_r, d] or None, M * d = 64."""
+    def arrange(cb: torch.Tensor) -> torch.Tensor:
+        *lead, M, C, d = cb.shape
+        if M * d != 64 or C > 256:
+            raise ValueError("entry tables: head_dim 64 and at most 256 centroids")
+        t = cb.to(torch.float16).movedim(-2, -3).reshape(*lead, C, M * d)
+        if C < 256:
+            t = torch.cat([t, t.new_zeros((*lead, 256 - C, M * d))], dim=-2)
+        return t
+    pq = arrange(pq_cb)
+    return torch.cat([pq, arrange(rvq_cb) if rvq_cb is not None else pq], dim=-1).contiguous()
+
+
 def _round256(n: int) -> int:
     """n rounded up to a multiple of 256 (device sub-buffer alignment)."""
     return (n + 255) // 256 * 256
@@ -514,7 +531,8 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
                     hot_cap: Optional[int] = None, launch: bool = True,
                     part: Optional[Tuple[int, int, bool]] = None, k_layout: int = 0,
                     guard: Optional[torch.Tensor] = None, guard_tol: float = 2e-3,
-                    drift: Optional[torch.Tensor] = None):
+                    drift: Optional[torch.Tensor] = None,
+                    tables: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
     """Fused dequant + decode attention; q [B, Hq, D] -> [B, Hq, D] fp16.
 
     ``k_layout`` = 1 when every segment's K codes are ``pack_score_codes``
@@ -532,6 +550,10 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     elements, 0 = shared).  Codebooks [B, M, C, d] when ``cb_batch_stride``
     else [M, C, d] shared.  With ``launch=False`` returns a ``FusedLaunch``
     that re-issues the same launch (same buffers) without rebuilding it.
+
+    ``tables`` = (K, V) ``entry_tables`` of the codebooks ([B, 256, 128]
+    with ``cb_batch_stride``, else [256, 128]): staged by the kernel with
+    contiguous loads instead of gathered from the codebooks.
 
     ``part = (base, slots, merge)`` attends one part of a window split over
     several calls on one stream: the call's split partials go to slots
@@ -575,6 +597,14 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     p.pq_cb_stride, p.rvq_cb_stride = pq_stride, rvq_stride
     p.max_tokens, p.splits = max_tokens, splits
     p.k_layout = int(k_layout)
+    if tables is not None:
+        kt, vt = tables
+        rows = B if cb_batch_stride else 1
+        for t in (kt, vt):
+            if t.dtype != torch.float16 or not t.is_contiguous() or t.numel() != rows * 256 * 128 \
+                    or t.device != q.device:
+                raise ValueError(f"entry tables must be contiguous fp16 [{rows}, 256, 128] on the query's device")
+        p.k_tab, p.v_tab, p.tab_stride = kt.data_ptr(), vt.data_ptr(), 65536 if cb_batch_stride else 0
     if part is not None:
         if splits <= 0 or workspace is None:
             raise ValueError("partial calls need explicit splits and a shared workspace")
@@ -600,8 +630,8 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
             raise ValueError(f"partial calls share a workspace of at least {wsb} bytes")
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = workspace.data_ptr(), workspace.numel()
-    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, *tmap[:2], workspace, segments, *cbs, guard, drift], out,
-                     _stream(q))
+    fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, *tmap[:2], workspace, segments, *cbs, guard, drift,
+                         *(tables or ())], out, _stream(q))
     fl.drift = drift
     if not launch:
         return fl

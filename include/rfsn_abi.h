@@ -316,6 +316,16 @@ typedef struct rfsn_fused_params {
   const uint32_t* tile_map;
   const int32_t* tile_map_count;
   int64_t tile_map_stride;
+  /* Entry-major codebook tables (optional; NULL: the kernel gathers its LDS
+   * tables from the [M][C][d] codebooks above).  256 entries of 256 bytes:
+   * entry e = [the PQ entries e of subspaces 0..M-1, d fp16 each | the RVQ
+   * entries e (the PQ entries again without an RVQ stage)], zeros past a
+   * codebook's size.  Sequence b's tables start tab_stride bytes after
+   * sequence b-1's (0: shared).  They must hold what the codebooks hold; the
+   * kernel then stages them with contiguous loads. */
+  const void* k_tab;
+  const void* v_tab;
+  int64_t tab_stride;
 } rfsn_fused_params;
 
 /* Token splits the call would use (p->splits, or the automatic choice when 0);
