@@ -170,11 +170,30 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps token indices scalar
 
-  // PQ tables: [M][C][dsub] for K, then V (unless they share one)
+  // PQ tables: [M][C][dsub] for K, then V (unless they share one), copied in
+  // 16-byte units (C * D * 2 bytes, a multiple of 16), up to 8 loads per
+  // thread in flight before their stores
   const int tab_elems = M * C * dsub;
-  for (int i = threadIdx.x; i < tab_elems; i += kRefThreads) tabs[i] = ((const uint16_t*)p.k_pq_cb)[i];
-  if (!kv_tab_shared)
-    for (int i = threadIdx.x; i < tab_elems; i += kRefThreads) tabs[tab_elems + i] = ((const uint16_t*)p.v_pq_cb)[i];
+  {
+    const int units = tab_elems / 8;
+    uint4* dst = reinterpret_cast<uint4*>(tabs);
+    for (int t = 0; t < (kv_tab_shared ? 1 : 2); ++t) {
+      const uint4* src = reinterpret_cast<const uint4*>(t ? p.v_pq_cb : p.k_pq_cb);
+      for (int i0 = threadIdx.x; i0 < units; i0 += 8 * kRefThreads) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * kRefThreads;
+          v[u] = i < units ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * kRefThreads;
+          if (i < units) dst[t * units + i] = v[u];
+        }
+      }
+    }
+  }
   const uint16_t* ktab = tabs;
   const uint16_t* vtab = kv_tab_shared ? tabs : tabs + tab_elems;
 
@@ -401,6 +420,8 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
                    p->q_heads / p->kv_heads <= kRefMaxG,
                "ref_attention: query heads must be a multiple of KV heads, at most 8 per KV head");
   RFSN_REQUIRE(p->q && p->out && p->k_pq_cb && p->v_pq_cb, "ref_attention: null pointer");
+  RFSN_REQUIRE(reinterpret_cast<uintptr_t>(p->k_pq_cb) % 16 == 0 && reinterpret_cast<uintptr_t>(p->v_pq_cb) % 16 == 0,
+               "ref_attention: PQ codebooks must be 16-byte aligned");
   RFSN_REQUIRE((p->rvq_layers == 0 && p->rvq_subspaces == 0) || (p->k_rvq_cb && p->v_rvq_cb),
                "ref_attention: RVQ codebooks missing");
   RFSN_REQUIRE(p->num_segments >= 0 && p->total_tokens >= 0 && (p->num_segments == 0 || p->segments),
