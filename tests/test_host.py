@@ -400,3 +400,81 @@ def test_router_rank_memo_matches_fresh_ranking():
             fresh = AsyncHierarchicalRouterMLX(cfg).bind(src).rank(pos, window)
             assert memo.rank(pos, window) == fresh, (pos, window)
         src.ids = src.ids + [src.ids[-1] + 1]  # a new list object: chunks added
+
+
+def test_tile_map_walks_segments_in_order():
+    """The fused kernel's tile map: for every encoded tile past segment 0, in
+    window order, (segment << 16) | tile within the segment -- checked
+    against a plain walk over the segment lengths, with empty and one-token
+    segments, and memoized rows identical to fresh ones."""
+    from apple_amd import _lib as L
+    from apple_amd import kernels as K
+
+    t = K.SegmentTable(3)
+    lens = [[100, 33, 0, 1, 64, 700], [15360] + [512] * 16, [5]]
+    for b, row in enumerate(lens):
+        for n in row:
+            t.add_codes(b, L.Codes(), L.Codes(), [], 0, n, 0, 1 << 24)
+    maps, stride = t.tile_map()
+    for b, row in enumerate(lens):
+        want = [(s << 16) | j for s in range(1, len(row)) for j in range((row[s] + 31) // 32)]
+        assert maps[b].tolist() == want
+    assert stride == max(len(m) for m in maps) == 256
+    again, _ = t.tile_map()  # memo hits give the same rows
+    assert all(np.array_equal(a, m) for a, m in zip(again, maps))
+    big = K.SegmentTable(1)
+    big.add_codes(0, L.Codes(), L.Codes(), [], 0, 32, 0, 1 << 24)
+    big.add_codes(0, L.Codes(), L.Codes(), [], 0, 32 * 0x10001, 0, 1 << 26)
+    with pytest.raises(ValueError):
+        big.tile_map()
+
+
+def test_entry_tables_layout():
+    """kernels.entry_tables: entry e = [PQ entries e of the subspaces | RVQ
+    entries e], zeros past a short codebook, the PQ half repeated without an
+    RVQ stage, per-sequence leading dimensions kept."""
+    from apple_amd import kernels as K
+
+    g = torch.Generator().manual_seed(5)
+    pq = torch.randn(16, 256, 4, generator=g).half()
+    rv = torch.randn(16, 200, 4, generator=g).half()
+    t = K.entry_tables(pq, rv)
+    assert t.shape == (256, 128) and t.dtype == torch.float16
+    for e in (0, 77, 199, 255):
+        assert torch.equal(t[e, :64].view(16, 4), pq[:, e])
+    for e in (0, 199):
+        assert torch.equal(t[e, 64:].view(16, 4), rv[:, e])
+    assert not t[200:, 64:].any()
+    pq8 = torch.randn(3, 8, 256, 8, generator=g).half()
+    t8 = K.entry_tables(pq8, None)
+    assert t8.shape == (3, 256, 128)
+    assert torch.equal(t8[2, 9, :64].view(8, 8), pq8[2, :, 9]) and torch.equal(t8[..., 64:], t8[..., :64])
+    with pytest.raises(ValueError):
+        K.entry_tables(torch.zeros(8, 256, 16).half(), None)  # head_dim 128: not a fused-kernel table
+
+
+def test_reference_active_map_and_segments():
+    """Row -> RVQ code row map of reference-format stores (the scatter of
+    quantization.py:273-274), its memo, and the segment bounds checks."""
+    from apple_amd import kernels as K
+
+    offs = torch.tensor([1, 4, 5, 9], dtype=torch.int32)
+    m = K.active_map(offs, 12)
+    assert m.tolist() == [-1, 0, -1, -1, 1, 2, -1, -1, -1, 3, -1, -1]
+    assert K.active_map(offs, 12) is m  # memoized per offsets tensor
+    assert K.active_map(offs, 16).shape == (16,)
+    T, H, M, L = 6, 2, 8, 3
+    st = CompressedTensorMLX(pq_codes=torch.zeros((T, H, M), dtype=torch.uint8),
+                             rvq_codes=torch.zeros((4, L), dtype=torch.uint16),
+                             rvq_mask=torch.zeros((T, H), dtype=torch.bool), rvq_offsets=offs, num_heads=H)
+    seg = K.ref_store_segment(st, st, 2, 4, 10)
+    assert seg["len"] == 4 and seg["token0"] == 2 and seg["pos0"] == 10 and seg["k"][2].tolist() == m.tolist()
+    with pytest.raises(ValueError):
+        K.ref_store_segment(st, st, 3, 4, 0)  # past the store
+    ring = torch.zeros((H, 8, 64), dtype=torch.float16)
+    K.ref_exact_segment(ring, ring, ring.stride(1), ring.stride(0), 2, 6, 0)
+    with pytest.raises(ValueError):
+        K.ref_exact_segment(ring, ring, ring.stride(1), ring.stride(0), 3, 6, 0)
+    assert K.ref_attention_ok(128, 8, 256, 4, 4, True) and not K.ref_attention_ok(96, 8, 256, 4, 4, True)
+    assert not K.ref_attention_ok(256, 16, 256, 8, 1, False)  # 2 x 128 KB of tables
+    assert K.ref_attention_ok(256, 16, 256, 8, 1, True, 16, 256, 4)
