@@ -662,6 +662,10 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
                                           int blocks_total, uint8_t* __restrict__ lds) {
   constexpr bool LUT = KM == kTables;
   constexpr bool SX = KM == kExactRows;
+  // codes in flight per wave: the exact pass reads K's codes from the
+  // score-table rows (4 loads per array for a tile) and keeps one tile ahead,
+  // which holds its loop within the registers a call leaves it
+  constexpr int kDep = SX ? 1 : kDepth;
   static_assert(KM == kCodebook || (M == 16 && RVQ && NHG == 1),
                 "score-table rows: 16 + 16 subspaces, <= 4 heads per KV head");
   constexpr int kWaves = BlockShape<NHG>::W;
@@ -722,9 +726,9 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
   // kDepth tiles in flight per wave: slot s holds tile tt + s*kWaves.  Only
   // encoded tiles go through slots (tt >= hot_tiles); a slot past the split
   // is idle and re-reads the split's last tile, which is encoded.
-  TileSrc srcs[kDepth];
-  KRegs kr[kDepth];
-  Regs vr[kDepth];
+  TileSrc srcs[kDep];
+  KRegs kr[kDep];
+  Regs vr[kDep];
   auto load_k = [&](KRegs& rk, const WarmBase& w, int off, int count) __attribute__((always_inline)) {
     if constexpr (LUT) load_tile_lut<KS>(rk, w, off, tokr, blk8, g);
     else if constexpr (SX) load_tile_rows_exact<KS>(rk, w, off, count, lane, sel01, sel23);
@@ -797,7 +801,7 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
     // wait only for the (L2-resident) codebook loads issued before them.
     if (seg_begin < t_end) {  // uniform: the split has encoded tiles
 #pragma unroll
-      for (int s = 0; s < kDepth; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
+      for (int s = 0; s < kDep; ++s) fetch(srcs[s], kr[s], vr[s], seg_begin + wave + s * kWaves);
     }
     if (pre) {
 #pragma unroll
@@ -1168,9 +1172,9 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
     const int my_tiles = max((t_end - seg_begin - wave + kWaves - 1) / kWaves, 1);
     int done = 0, stage = 0;
     int next_at = (my_tiles + 3) >> 2;  // ceil(my_tiles / 4)
-    for (int tt = seg_begin + wave; tt < t_end; tt += kDepth * kWaves) {
+    for (int tt = seg_begin + wave; tt < t_end; tt += kDep * kWaves) {
 #pragma unroll
-      for (int s = 0; s < kDepth; ++s) {
+      for (int s = 0; s < kDep; ++s) {
         if (srcs[s].kind >= 0) {
           if (++done >= next_at) {  // uniform
             while (stage < 3 && 4 * done >= (stage + 1) * my_tiles) ++stage;
@@ -1228,11 +1232,19 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
             store_half<M, RVQ, KS>(lds, vr[s], rb, 1, waddr, sav, shalf);
             pv_operands(av);
           }
-          if constexpr (LUT) gather_k(kr[(s + 1) % kDepth], 0, ka);  // next tile
-          else gather_k(kr[(s + 1) % kDepth], 0, ra);
+          if constexpr (kDep > 1) {  // the next tile's codes are in the other slot
+            if constexpr (LUT) gather_k(kr[(s + 1) % kDep], 0, ka);
+            else gather_k(kr[(s + 1) % kDep], 0, ra);
+          }
           pv(av, pb, 1);
         }
-        fetch(srcs[s], kr[s], vr[s], tt + (s + kDepth) * kWaves);
+        fetch(srcs[s], kr[s], vr[s], tt + (s + kDep) * kWaves);
+        if constexpr (kDep == 1) {  // one slot: the next tile's first gather follows its fetch
+          if (srcs[0].kind >= 0) {
+            if constexpr (LUT) gather_k(kr[0], 0, ka);
+            else gather_k(kr[0], 0, ra);
+          }
+        }
       }
     }
   }
