@@ -111,6 +111,7 @@ SIGNATURES = {
     "rfsn_pack_codes": (i32, [vp, i64, i64, i32, i32, vp, i64, i64, vp]),
     "rfsn_pack_score_codes": (i32, [vp, vp, vp, vp, i32, i64, i32, vp, vp, vp, vp, i64, i64, vp]),
     "rfsn_fused_splits": (i32, [C.POINTER(FusedParams)]),
+    "rfsn_fused_k_scoring": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_workspace_bytes": (sz, [C.POINTER(FusedParams)]),
     "rfsn_fused_decode_attention": (i32, [C.POINTER(FusedParams), vp]),
     "rfsn_fused_decode_attention_noalloc": (i32, [C.POINTER(FusedParams), vp]),

@@ -67,6 +67,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 constexpr int kTile = 32;                           // tokens per wave tile
 constexpr int kD = 64;                              // head_dim of the fused kernel
 constexpr int kDepth = 2;                           // tiles whose codes are in flight per wave
+constexpr int kTableMinTilesPerWave = 16;           // tiles per wave for which the score tables pay off
 constexpr int kEntryBytes = 256;                    // one codebook entry: PQ slots, then RVQ slots
 constexpr int kRvqSlot = 128;                       // byte offset of the RVQ slots in an entry
 constexpr int kTableBytes = 256 * kEntryBytes;      // one K or V table, 64 KB
@@ -651,6 +652,19 @@ enum KMode : int {
   kExactRows = 2  // K^ rebuilt from the codebooks, codes read from the score-table rows (k_layout 1)
 };
 
+// XCD-aware block mapping: consecutive hardware block ids go to different
+// XCDs; give each XCD a contiguous range of (sequence, head, split) units so
+// that one sequence's codebooks are fetched into one L2.
+__device__ __forceinline__ void block_unit(int blocks_total, int splits, int kv_heads, int& b, int& h, int& split) {
+  const int L = blockIdx.x;
+  const int per = blocks_total / 8, rem = blocks_total % 8;
+  const int xcd = L % 8, k = L / 8;
+  const int vid = xcd * per + min(xcd, rem) + k;
+  split = vid % splits;
+  h = (vid / splits) % kv_heads;
+  b = vid / (splits * kv_heads);
+}
+
 // One block's attention over its split: stage, stream the tiles, combine and
 // write the output (or the split partial).  With score tables and a drift
 // guard it returns true, without writing, when some head's drift estimate
@@ -670,16 +684,8 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
                 "score-table rows: 16 + 16 subspaces, <= 4 heads per KV head");
   constexpr int kWaves = BlockShape<NHG>::W;
   constexpr int kThreads = BlockShape<NHG>::T;
-  // XCD-aware block mapping: consecutive hardware block ids go to different
-  // XCDs; give each XCD a contiguous range of (sequence, head, split) units so
-  // that one sequence's codebooks are fetched into one L2.
-  const int L = blockIdx.x;
-  const int per = blocks_total / 8, rem = blocks_total % 8;
-  const int xcd = L % 8, k = L / 8;
-  const int vid = xcd * per + min(xcd, rem) + k;
-  const int split = vid % splits;
-  const int h = (vid / splits) % p.kv_heads;
-  const int b = vid / (splits * p.kv_heads);
+  int b, h, split;
+  block_unit(blocks_total, splits, p.kv_heads, b, h, split);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   set_prio(3);  // lowered with the wave's progress through its encoded tiles
@@ -1375,6 +1381,15 @@ fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_sp
       exact_rows_pass<M, RVQ, KS, NHG>(p, splits, tiles_per_split, blocks_total, lds);
     }
   }
+  if constexpr (KM == kExactRows) {
+    // launched instead of the table body: no table drift to report
+    if (p.drift && threadIdx.x < p.q_heads / p.kv_heads) {
+      int b, h, split;
+      block_unit(blocks_total, splits, p.kv_heads, b, h, split);
+      const int slots = p.part_slots ? p.part_slots : splits;
+      p.drift[((int64_t)b * p.q_heads + h * (p.q_heads / p.kv_heads) + threadIdx.x) * slots + p.part_base + split] = 0.f;
+    }
+  }
 }
 
 int waves_for(const rfsn_fused_params* p) {
@@ -1420,11 +1435,36 @@ int launch_fused(const rfsn_fused_params* p, hipStream_t s) {
                       (int64_t)p->batch * p->q_heads, splits, kD, p->out, s);
 }
 
+// How a call scores K: kCodebook (K^ rebuilt from the codebooks, k_layout
+// 0), kTables, or kExactRows (the drift guard's exact pass alone).
+//
+// The guard estimates a block's drift over its split, not over the
+// whole window: with S splits of similar weight the estimate is about
+// sqrt(S) times the window's, and a block that fires recomputes its
+// split after the table pass.  With the guard on, a launch of several
+// splits so short that a wave streams fewer than kTableMinTilesPerWave
+// tiles runs the exact pass alone (from the codebooks): measured on
+// one MI355X it is faster there (batch 4 x 32K, 8 splits: 0.032 ms
+// against 0.097 ms), while at 16 tiles per wave and more the tables win.
+int k_route(const rfsn_fused_params* p) {
+  if (p->k_layout != 1) return kCodebook;
+  if (p->guard) {
+    const int splits = auto_splits(p);
+    const int tps = (total_tiles_host(p) + splits - 1) / splits;
+    if (splits > 1 && tps < kTableMinTilesPerWave * BlockShape<1>::W) return kExactRows;
+  }
+  return kTables;
+}
+
 template <int M, bool RVQ, int KS>
 int dispatch_nhg(const rfsn_fused_params* p, hipStream_t s) {
   const int G = p->q_heads / p->kv_heads;
   if constexpr (M == 16 && RVQ) {
-    if (p->k_layout == 1) return launch_fused<M, RVQ, KS, 1, kTables>(p, s);
+    switch (k_route(p)) {
+      case kTables: return launch_fused<M, RVQ, KS, 1, kTables>(p, s);
+      case kExactRows: return launch_fused<M, RVQ, KS, 1, kExactRows>(p, s);
+      default: break;
+    }
   }
   if (G <= 4) return launch_fused<M, RVQ, KS, 1, kCodebook>(p, s);
   return launch_fused<M, RVQ, KS, 2, kCodebook>(p, s);
@@ -1447,6 +1487,11 @@ using namespace rfsn;
 extern "C" int32_t rfsn_fused_splits(const rfsn_fused_params* p) {
   if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0) return 0;
   return auto_splits(p);
+}
+
+extern "C" int32_t rfsn_fused_k_scoring(const rfsn_fused_params* p) {
+  if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0) return -1;
+  return k_route(p);
 }
 
 extern "C" size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p) {

@@ -823,6 +823,15 @@ class FusedLaunch:
             L.check(st, "rfsn_fused_decode_attention")
         return self.out
 
+    K_SCORING = {0: "codebook K^ rows", 1: "fp16 q.centroid tables", 2: "codebook K^ over score-table rows"}
+
+    @property
+    def k_scoring(self) -> str:
+        """How the launch scores K: the codebook rows (k_layout 0), the score
+        tables (drift guard recomputing where it fires), or the guard's exact
+        pass alone (a guarded launch of several short splits)."""
+        return self.K_SCORING[int(L.load().rfsn_fused_k_scoring(self._ref))]
+
 
 class PrefetchedStep:
     """A decode step whose window includes chunks still in pinned host memory.

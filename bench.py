@@ -806,7 +806,7 @@ def main(argv=None) -> int:
                    "format": f"PQ M{w.pq_subspaces}x{w.pq_centroids}"
                              + (f" + RVQ M{w.rvq_subspaces}x{w.rvq_centroids}" if w.rvq_subspaces else "")
                              + (f" + top-{w.sparse_k} sparse" if w.sparse_k else ""),
-                   "k_scoring": "fp16 q.centroid tables" if cache.k_layout == 1 else "codebook K^ rows"},
+                   "k_scoring": launch.k_scoring},
         "hbm_gbs": round(achieved, 1),
         "bytes_per_step": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -815,7 +815,7 @@ def main(argv=None) -> int:
                      "device_copy_gbs": copy_gbs, "frac_of_device_copy": round(achieved / copy_gbs, 4),
                      "device_read_gbs": read_gbs, "frac_of_device_read": round(achieved / read_gbs, 4)},
     }
-    if cache.last_drift is not None:
+    if cache.last_drift is not None and cache.k_layout == 1 and launch.k_scoring == "fp16 q.centroid tables":
         # drift [B, Hq, splits]; a block (sequence, KV head, split) recomputes when one of its heads fires
         tol = cache.config.score_table_tolerance
         d = cache.last_drift.float().view(w.batch, w.kv_heads, w.q_heads // w.kv_heads, -1)

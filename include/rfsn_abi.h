@@ -304,7 +304,10 @@ typedef struct rfsn_fused_params {
    * sparse entries from a second plane of each K sparse-value array, at
    * kv_heads * head_stride * k values after the score deltas, in the same
    * positions.  drift (may be NULL): est per (sequence, query head, split
-   * slot), [B][Hq][slots] with slots = part_slots or the call's splits. */
+   * slot), [B][Hq][slots] with slots = part_slots or the call's splits.
+   * A guarded call of several splits whose blocks hold fewer than 256
+   * tiles of 32 tokens (16 per wave) runs that exact pass alone, with no
+   * tables; its drift entries are 0. */
   const float* guard;
   float* drift;
   float guard_tol;
@@ -332,6 +335,12 @@ typedef struct rfsn_fused_params {
  * sizes partial-mode slots.  Part of the attention_forward replacement
  * (cache.py:395-428). */
 int32_t rfsn_fused_splits(const rfsn_fused_params* p);
+/* How the call would score K: 0 = K^ rebuilt from the codebooks (k_layout
+ * 0), 1 = score tables (with the drift guard's recompute where it fires),
+ * 2 = the guard's exact pass alone (see guard above); -1 for a malformed
+ * shape.  No counterpart in the reference, whose attention always
+ * materializes K (cache.py:395-428); for hosts that report the route. */
+int32_t rfsn_fused_k_scoring(const rfsn_fused_params* p);
 size_t rfsn_fused_workspace_bytes(const rfsn_fused_params* p);
 int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* stream);
 

@@ -123,6 +123,35 @@ def test_noalloc_rejects_oversized_partials_on_the_host(lib):
     assert lib.rfsn_fused_decode_attention_noalloc(None, None) == -1
 
 
+def test_fused_k_scoring_route(lib):
+    """The K route a fused call takes, decided on the host: the codebook rows
+    for k_layout 0, the score tables for k_layout 1, and with the drift guard
+    on the guard's exact pass alone when the call runs several splits of
+    fewer than 256 tiles (32 tokens each) per block."""
+    from apple_amd import _lib
+
+    def route(batch, hot, tokens, k_layout=1, guard=True, splits=0):
+        p = _lib.FusedParams()
+        p.fmt = _lib.Format(64, 16, 256, 16, 256, 4)
+        p.batch, p.q_heads, p.kv_heads = batch, 32, 8
+        p.hot_len, p.max_tokens, p.max_segments, p.splits = hot, tokens, 1, splits
+        p.k_layout = k_layout
+        if guard:
+            p.guard = 256  # never dereferenced on the host
+        return lib.rfsn_fused_k_scoring(ctypes.byref(p)), lib.rfsn_fused_splits(ctypes.byref(p))
+
+    # one sequence, 8,192 tokens: 257 tiles over 17 splits, 16 tiles per block
+    assert route(1, 512, 8192) == (2, 17)
+    assert route(1, 512, 8192, guard=False) == (1, 17)
+    assert route(1, 512, 8192, splits=1) == (1, 1)  # one split: the estimate covers the window
+    assert route(1, 512, 8192, k_layout=0) == (0, 17)
+    # 32,768 tokens: 1,025 tiles; batch 4 -> 8 splits of 129 tiles, batch 8 -> 4 of 257, batch 32 -> 1
+    assert route(4, 1024, 32768) == (2, 8)
+    assert route(8, 1024, 32768) == (1, 4)
+    assert route(32, 1024, 32768) == (1, 1)
+    assert lib.rfsn_fused_k_scoring(None) == -1
+
+
 def test_ref_attention_validation(lib):
     """rfsn_ref_attention rejects shapes outside its kernels on the host."""
     from apple_amd import _lib

@@ -225,31 +225,42 @@ def test_fused_exact_pass_matches_codebook_path(device):
     codebooks while reading the score-table rows and the corrected-coordinate
     plane: the outputs are bit-identical to the codebook path's over the
     codebook layout, for one split and for several (split partials merged),
-    per-sequence cache and batched cache alike."""
+    per-sequence cache and batched cache alike.  A guarded launch of several
+    splits with fewer than 256 tiles per block runs the exact pass alone
+    (3,080 tokens in 5 splits; its drift entries are 0); 2 splits of 16,580
+    tokens hold 260 tiles each and run the table pass first."""
     from apple_amd.batched import RFSNBatchedKVCache
     from apple_amd.cache import RFSNv10KVCacheMLX
 
     outs = {}
     for mode in ("exact", "codebook"):
-        g, cfg, keys, values, cbs, kq, vq = _setup(21, 32, 8, 16, 16, 4, 3000, 80)
-        cfg.fused_score_tables = mode == "exact"
-        cfg.score_table_tolerance = 0.0
-        cache = RFSNv10KVCacheMLX(cfg, device=device)
-        cache.update(T(keys, device), T(values, device), (kq, vq))
-        q = T(randn16(g, 2, 32, 64), device)
-        for splits in (1, 5):
-            out = torch.empty_like(q)
-            cache.prepare(q, causal=True, splits=splits, out=out)()
-            outs[(mode, splits)] = H(out).copy()
-        if mode == "exact":
-            assert (H(cache.last_drift) > 0).all()
-        bc = RFSNBatchedKVCache(cfg, 2, device=device)
-        for b in range(2):
-            bc.prefill(b, T(keys, device), T(values, device), kq, vq)
-        assert bc.k_layout == int(mode == "exact")
-        outs[(mode, "batched")] = H(bc.attention_forward(q)).copy()
-    for key in (1, 5, "batched"):
-        assert np.array_equal(outs[("exact", key)].view(np.uint16), outs[("codebook", key)].view(np.uint16)), key
+        for nw, split_counts in ((3000, (1, 5)), (16500, (2,))):
+            g, cfg, keys, values, cbs, kq, vq = _setup(21, 32, 8, 16, 16, 4, nw, 80)
+            cfg.fused_score_tables = mode == "exact"
+            cfg.score_table_tolerance = 0.0
+            cache = RFSNv10KVCacheMLX(cfg, device=device)
+            cache.update(T(keys, device), T(values, device), (kq, vq))
+            q = T(randn16(g, 2, 32, 64), device)
+            for splits in split_counts:
+                out = torch.empty_like(q)
+                cache.prepare(q, causal=True, splits=splits, out=out)()
+                outs[(mode, nw, splits)] = H(out).copy()
+                if mode == "exact":
+                    drift = H(cache.last_drift)
+                    assert drift.shape[-1] == splits
+                    if splits == 5:
+                        assert (drift == 0).all()  # exact pass alone
+                    else:
+                        assert (drift > 0).all()   # table pass, every block recomputed
+            if nw == 3000:
+                bc = RFSNBatchedKVCache(cfg, 2, device=device)
+                for b in range(2):
+                    bc.prefill(b, T(keys, device), T(values, device), kq, vq)
+                assert bc.k_layout == int(mode == "exact")
+                outs[(mode, "batched")] = H(bc.attention_forward(q)).copy()
+    for key in ((3000, 1), (3000, 5), (16500, 2), "batched"):
+        assert np.array_equal(outs[("exact",) + (key if isinstance(key, tuple) else (key,))].view(np.uint16),
+                              outs[("codebook",) + (key if isinstance(key, tuple) else (key,))].view(np.uint16)), key
 
 
 def test_fused_score_tables_in_use(device):
