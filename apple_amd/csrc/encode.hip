@@ -846,18 +846,20 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
         if (t + 1 < 16) next = __builtin_amdgcn_mfma_f32_16x16x16f16(a[t + 1], b, ff4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         int key[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // centroid 16t + i (+ 4g below)
-          // the index as an opaque SGPR and the mask in a VGPR: one v_and_or_b32
-          int sidx;
-          asm("s_mov_b32 %0, %1" : "=s"(sidx) : "n"(16 * t + i));
+        for (int i = 0; i < 4; ++i) {  // centroid 16t + 4g + i, keyed 4t + i
+          // 4t + i < 64 is an inline constant and the mask sits in a VGPR:
+          // one v_and_or_b32 per key (the index orders the lane's centroids
+          // as 16t + 4g + i does; widen restores the centroid)
           const float z = acc[i];
-          key[i] = (__builtin_bit_cast(int, z) & maskv) | sidx;
+          key[i] = (__builtin_bit_cast(int, z) & maskv) | (4 * t + i);
         }
         insert(key);
         acc = next;
       }
     };
     const int x32 = 4 * (lane ^ 32);
+    // a lane key's index 4t + i -> centroid 16t + 4g + i (kNoKey stays)
+    auto widen = [&](int k) { return k == kNoKey ? k : (k & ~0x3F) | ((k & 0x3C) << 2) | (4 * g) | (k & 3); };
     // screening: the two smallest keys (two lists for independent chains)
     int m1 = kNoKey, m2 = kNoKey, n1 = kNoKey, n2 = kNoKey;
     screen([&](const int (&key)[4]) {
@@ -865,8 +867,8 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
       key_insert2x2(n1, n2, key[2], key[3]);
     });
     key_insert2x2(m1, m2, n1, n2);
-    if (m1 != kNoKey) m1 |= 4 * g;
-    if (m2 != kNoKey) m2 |= 4 * g;
+    m1 = widen(m1);
+    m2 = widen(m2);
     {  // the vector's four lanes l, l ^ 16, l ^ 32, l ^ 48
       int o1 = lane_xor16(m1), o2 = lane_xor16(m2);
       key_insert2x2(m1, m2, o1, o2);
@@ -887,9 +889,9 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
 #pragma unroll
       for (int i = 0; i < 4; ++i) key_insert3(p1, p2, p3, key[i]);
     });
-    if (p1 != kNoKey) p1 |= 4 * g;
-    if (p2 != kNoKey) p2 |= 4 * g;
-    if (p3 != kNoKey) p3 |= 4 * g;
+    p1 = widen(p1);
+    p2 = widen(p2);
+    p3 = widen(p3);
     {
       int o1 = lane_xor16(p1), o2 = lane_xor16(p2), o3 = lane_xor16(p3);
       key_insert3(p1, p2, p3, o1);
