@@ -8,22 +8,22 @@
 // tiers the tiled fused kernel does not serve (cache.py:395-428: materialize_window, then
 // _blockwise_exact_attention), without writing the decoded window to HBM.
 //
-// One block = (query b, KV head h, token split), 4 waves.  The PQ codebooks
+// One block = (query b, KV head h, token split), 8 waves.  The PQ codebooks
 // of K and V sit in LDS (entry-major rows of d fp16 per subspace).  A wave
-// streams the split's tokens one at a time; lane l owns coordinates
-// DPL*l .. DPL*l+DPL-1 (one PQ subspace), so it reads that subspace's code
-// byte (lanes of one subspace share the load) and gathers its slice of the
-// token's PQ entry from LDS.  For an active row of the reference format it
-// adds its slice of the L RVQ codewords from global memory (64 lanes read
-// one codeword row: coalesced) with the reference's rounding chain:
-// corr = fp16(sum_l fl32(C_l[code_l])) in stage order, K = fp16(fl32(base) +
-// fl32(corr)) (corr = 0 for inactive rows).  The long-context format reads
-// its subspace RVQ entries from global memory (L2-resident codebooks) and
-// adds the sparse residuals to the coordinates they name.  Scores are the
-// wave's sum of q . K partials in fp32; the online softmax runs on the wave
-// (uniform), and the lane accumulates p * V on its coordinates.  The 4 waves
-// combine in LDS; splits write (m, l, acc) partials that
-// merge_partials_kernel combines.
+// holds P token groups (P = 4, 2, 1 at head_dim 64, 128, 256), and lane ll of
+// a group owns DPL = 4 coordinates (one PQ subspace), so one instruction
+// serves P tokens.  A lane reads its token's code byte for its subspace and
+// gathers its slice of the PQ entry from LDS.  For an active row of the
+// reference format it adds its slice of the L RVQ codewords from global
+// memory (a group's lanes read one codeword row: coalesced) with the
+// reference's rounding chain: corr = fp16(sum_l fl32(C_l[code_l])) in stage
+// order, K = fp16(fl32(base) + fl32(corr)) (corr = 0 for inactive rows).  The
+// long-context format reads its subspace RVQ entries from global memory
+// (L2-resident codebooks) and adds the sparse residuals to the coordinates
+// they name.  A token's score is its group's sum of q . K partials in fp32;
+// the online softmax runs on the wave (uniform), and the lane accumulates
+// p * V on its coordinates.  The groups, then the 8 waves, combine in LDS;
+// splits write (m, l, acc) partials that merge_partials_kernel combines.
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
 
@@ -37,10 +37,12 @@ constexpr int kRefMaxL = 8;  // gated RVQ layers
 
 typedef const rfsn_ref_segment __attribute__((address_space(4)))* cref;
 
-// Sum over the 64 lanes, returned to every lane: DPP adds within each row of
-// 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror
-// leave every lane holding its row's sum), then the four row sums.
-__device__ __forceinline__ float wave_sum64(float v) {
+// Sums over the P token groups of a wave (64 / P lanes each): DPP adds
+// within each row of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror leave every lane holding its row's sum), then
+// the row sums of each group, returned as uniform scalars s[0..P).
+template <int P>
+__device__ __forceinline__ void group_sums(float v, float (&s)[P]) {
   auto f = [](int x) { return __builtin_bit_cast(float, x); };
   auto i = [](float x) { return __builtin_bit_cast(int, x); };
   v += f(__builtin_amdgcn_mov_dpp(i(v), 0xB1, 0xF, 0xF, true));
@@ -49,7 +51,67 @@ __device__ __forceinline__ float wave_sum64(float v) {
   v += f(__builtin_amdgcn_mov_dpp(i(v), 0x140, 0xF, 0xF, true));
   const float r0 = f(__builtin_amdgcn_readlane(i(v), 0)), r1 = f(__builtin_amdgcn_readlane(i(v), 16));
   const float r2 = f(__builtin_amdgcn_readlane(i(v), 32)), r3 = f(__builtin_amdgcn_readlane(i(v), 48));
-  return (r0 + r1) + (r2 + r3);
+  if constexpr (P == 4) {
+    s[0] = r0;
+    s[1] = r1;
+    s[2] = r2;
+    s[3] = r3;
+  } else if constexpr (P == 2) {
+    s[0] = r0 + r1;
+    s[1] = r2 + r3;
+  } else {
+    s[0] = (r0 + r1) + (r2 + r3);
+  }
+}
+
+// The value of x for this lane's token group (tg < P), from uniform x[0..P).
+template <int P>
+__device__ __forceinline__ float pick(const float (&x)[P], int tg) {
+  float r = x[0];
+#pragma unroll
+  for (int p = 1; p < P; ++p) r = tg == p ? x[p] : r;
+  return r;
+}
+
+// Sum of v over the lanes that hold the same coordinates in the P token
+// groups (lanes l, l ^ 16, l ^ 32, l ^ 48 for P = 4; l, l ^ 32 for P = 2).
+template <int P>
+__device__ __forceinline__ float across_groups(float v) {
+  auto f = [](uint32_t x) { return __builtin_bit_cast(float, x); };
+  auto u = [](float x) { return __builtin_bit_cast(uint32_t, x); };
+  if constexpr (P == 4) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u(v), u(v), false, false);
+    v = f(r16[0]) + f(r16[1]);
+  }
+  if constexpr (P >= 2) {
+    const auto r32 = __builtin_amdgcn_permlane32_swap(u(v), u(v), false, false);
+    v = f(r32[0]) + f(r32[1]);
+  }
+  return v;
+}
+
+// DPL consecutive fp16 values at p (DPL * 2-byte aligned when vec).
+template <int DPL>
+__device__ __forceinline__ void load_h(const uint16_t* p, uint16_t (&w)[DPL], bool vec = true) {
+  if constexpr (DPL == 4) {
+    if (vec) {
+      const uint2 x = *reinterpret_cast<const uint2*>(p);
+      w[0] = (uint16_t)x.x;
+      w[1] = (uint16_t)(x.x >> 16);
+      w[2] = (uint16_t)x.y;
+      w[3] = (uint16_t)(x.y >> 16);
+      return;
+    }
+  } else if constexpr (DPL == 2) {
+    if (vec) {
+      const uint32_t x = *reinterpret_cast<const uint32_t*>(p);
+      w[0] = (uint16_t)x;
+      w[1] = (uint16_t)(x >> 16);
+      return;
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < DPL; ++v) w[v] = p[v];
 }
 
 struct RvqShape {
@@ -58,21 +120,20 @@ struct RvqShape {
   int k;       // sparse residuals
 };
 
-// The lane's DPL coordinates of U stored vectors (rows row[u] of a store):
+// The lane's DPL coordinates c0 .. c0 + DPL - 1 of U stored vectors (rows
+// row[u] of a store, one per lane: the lane's token group picks its token):
 // PQ base, then the gated full-dimension correction (reference format) or
 // the subspace RVQ stage and the sparse residuals (long-context format).
 // Every load of the U vectors is issued before the first is consumed: the
 // PQ code bytes and row indices, then the gated codes of every layer, then
 // the codewords.
-template <int DPL, int U>
+template <int D, int DPL, int U>
 __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_store_codes& sc, const int64_t (&row)[U],
                                         const uint16_t* __restrict__ tab, int M, int C, int dsub,
-                                        const uint16_t* __restrict__ rvq_cb, const RvqShape& r, int lane) {
-  constexpr int D = 64 * DPL;
-  // M in {4, 8, 16, 32}: the lane's DPL coordinates sit in one PQ subspace
-  // (d = D/M is a multiple of DPL = D/64)
-  const int m = (DPL * lane) / dsub;
-  const int off = DPL * lane - m * dsub;
+                                        const uint16_t* __restrict__ rvq_cb, const RvqShape& r, int c0) {
+  // the lane's DPL coordinates sit in one PQ subspace (dsub is a multiple of DPL)
+  const int m = c0 / dsub;
+  const int off = c0 - m * dsub;
   int code[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) code[u] = sc.pq[row[u] * M + m];
@@ -82,13 +143,13 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
 #pragma unroll
     for (int v = 0; v < DPL; ++v) corr[u][v] = 0.0f;
   if (sc.rvq_sub != nullptr) {
-    // subspace stage: the lane's coordinates span at most two subspaces
+    // subspace stage: the lane's coordinates may span several subspaces
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint8_t* codes = sc.rvq_sub + row[u] * r.Mr;
 #pragma unroll
       for (int v = 0; v < DPL; ++v) {
-        const int dd = DPL * lane + v;
+        const int dd = c0 + v;
         const int mr = dd / r.dr;
         corr[u][v] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
       }
@@ -96,7 +157,7 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
   } else if (sc.active != nullptr) {
     int a[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = sc.active[row[u]];  // uniform
+    for (int u = 0; u < U; ++u) a[u] = sc.active[row[u]];
     int64_t base[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) base[u] = (int64_t)(a[u] < 0 ? 0 : a[u]) * r.L;  // the store holds >= 1 active row
@@ -118,11 +179,8 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const uint16_t* cw = rvq_cb + ((int64_t)(j < nl ? l + j : l) * r.Cr + c[j][u]) * D + DPL * lane;
-#pragma unroll
-          for (int v = 0; v < DPL; ++v) w[j][u][v] = cw[v];
-        }
+        for (int u = 0; u < U; ++u)
+          load_h<DPL>(rvq_cb + ((int64_t)(j < nl ? l + j : l) * r.Cr + c[j][u]) * D + c0, w[j][u]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -138,30 +196,36 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint16_t* entry = tab + ((int64_t)m * C + code[u]) * dsub + off;
+    uint16_t e[DPL];
+    load_h<DPL>(tab + ((int64_t)m * C + code[u]) * dsub + off, e);
 #pragma unroll
-    for (int v = 0; v < DPL; ++v) out[u][v] = h2f(f2h(__fadd_rn(h2f(entry[v]), corr[u][v])));  // fp16(base + corr)
+    for (int v = 0; v < DPL; ++v) out[u][v] = h2f(f2h(__fadd_rn(h2f(e[v]), corr[u][v])));  // fp16(base + corr)
   }
   if (sc.sparse_idx != nullptr) {
     // K[idx] = fp16(fl32(K[idx]) + fl32(val)); the indices of a row are distinct
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       for (int j = 0; j < r.k; ++j) {
-        const int idx = sc.sparse_idx[row[u] * r.k + j];  // uniform
+        const int idx = sc.sparse_idx[row[u] * r.k + j];
         const float val = h2f(sc.sparse_val[row[u] * r.k + j]);
 #pragma unroll
         for (int v = 0; v < DPL; ++v)
-          if (idx == DPL * lane + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
+          if (idx == c0 + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
       }
     }
   }
 }
 
-template <int DPL, int U, int GMAX>
-__global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
+// Lane geometry: a wave holds P token groups of 64 / P lanes, and lane ll of
+// a group owns coordinates c0 = DPL * ll .. c0 + DPL - 1 (DPL = D * P / 64),
+// so one instruction serves P tokens.  A wave takes U * P consecutive tokens
+// per step.
+template <int D, int P, int U, int GMAX>
+__global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_eu(GMAX == 1 ? 4 : 1))) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
                                                                int kv_tab_shared) {
   extern __shared__ __align__(16) uint16_t tabs[];
-  constexpr int D = 64 * DPL;
+  constexpr int DPL = D * P / 64;
+  constexpr int LG = 64 / P;  // lanes per token group
   const int M = p.pq_subspaces, C = p.pq_centroids, dsub = D / M;
   const int G = p.q_heads / p.kv_heads;
   const int split = blockIdx.x % splits;
@@ -169,6 +233,8 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
   const int b = blockIdx.x / (splits * p.kv_heads);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps token indices scalar
+  const int tg = lane / LG;        // the lane's token group
+  const int c0 = DPL * (lane % LG);  // its first coordinate
 
   // PQ tables: [M][C][dsub] for K, then V (unless they share one), copied in
   // 16-byte units (C * D * 2 bytes, a multiple of 16), up to 8 loads per
@@ -205,7 +271,7 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
     const uint16_t* qrow = (const uint16_t*)p.q + ((int64_t)b * p.q_heads + hq) * D;
 #pragma unroll
     for (int v = 0; v < DPL; ++v) {
-      qv[g][v] = g < G ? h2f(qrow[DPL * lane + v]) * p.scale : 0.0f;
+      qv[g][v] = g < G ? h2f(qrow[c0 + v]) * p.scale : 0.0f;
       acc[g][v] = 0.0f;
     }
     m_run[g] = -__builtin_inff();
@@ -245,49 +311,57 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
       const uint16_t* ek = (const uint16_t*)segs[s].exact_k;
       const uint16_t* ev = (const uint16_t*)segs[s].exact_v;
       const int64_t ets = segs[s].exact_token_stride, ehs = segs[s].exact_head_stride;
-      // wave w takes groups of U consecutive tokens, every kRefWaves-th group
-      for (int g0 = lo + wave * U; g0 < hi; g0 += kRefWaves * U) {
-        bool valid[U];
-        int pos[U];
+      // exact rows: DPL-wide loads when the rows and strides allow them (uniform)
+      const bool evec = (((uintptr_t)ek | (uintptr_t)ev) % (2 * DPL) == 0) && ets % DPL == 0 && ehs % DPL == 0;
+      // wave w takes steps of U * P consecutive tokens, every kRefWaves-th step;
+      // token g0 + u * P + tg is slot u of the lane's group
+      for (int g0 = lo + wave * (U * P); g0 < hi; g0 += kRefWaves * U * P) {
         int64_t row[U], tk[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          valid[u] = g0 + u < hi;
-          const int t = (valid[u] ? g0 + u : g0) - seg_base;  // past the end: re-read the group's first token
+          const int tl = g0 + u * P + tg;
+          const int t = (tl < hi ? tl : g0) - seg_base;  // past the end: re-read the step's first token
           tk[u] = tok0 + t;
           row[u] = tk[u] * p.kv_heads + h;
-          pos[u] = pos0 + t;
         }
         float kk[U][DPL], vv[U][DPL];
         if (kc.pq == nullptr) {
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const int64_t e = tk[u] * ets + (int64_t)h * ehs + DPL * lane;
+            const int64_t e = tk[u] * ets + (int64_t)h * ehs + c0;
+            uint16_t wk[DPL], wv[DPL];
+            load_h<DPL>(ek + e, wk, evec);
+            load_h<DPL>(ev + e, wv, evec);
 #pragma unroll
             for (int v = 0; v < DPL; ++v) {
-              kk[u][v] = h2f(ek[e + v]);
-              vv[u][v] = h2f(ev[e + v]);
+              kk[u][v] = h2f(wk[v]);
+              vv[u][v] = h2f(wv[v]);
             }
           }
         } else {
-          rebuild<DPL, U>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, lane);
-          rebuild<DPL, U>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, lane);
+          rebuild<D, DPL, U>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, c0);
+          rebuild<D, DPL, U>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, c0);
         }
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
           if (g >= G) continue;  // uniform
-          float sc[U];
+          float sc[U][P];
           float mx = -__builtin_inff();
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             float part = 0.0f;
 #pragma unroll
             for (int v = 0; v < DPL; ++v) part = __builtin_fmaf(qv[g][v], kk[u][v], part);
-            sc[u] = wave_sum64(part);  // q was scaled on load
-            if (!valid[u] || pos[u] < 0 || pos[u] > qpos[g]) sc[u] = -__builtin_inff();  // masked (uniform)
-            mx = fmaxf(mx, sc[u]);
+            group_sums<P>(part, sc[u]);  // q was scaled on load
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+              const int tt = g0 + u * P + q;
+              const int pos = pos0 + (tt - seg_base);
+              if (tt >= hi || pos < 0 || pos > qpos[g]) sc[u][q] = -__builtin_inff();  // masked (uniform)
+              mx = fmaxf(mx, sc[u][q]);
+            }
           }
-          if (mx == -__builtin_inff()) continue;  // no allowed token in the group (uniform)
+          if (mx == -__builtin_inff()) continue;  // no allowed token in the step (uniform)
           const float mn = fmaxf(m_run[g], mx);
           const float corr = __expf(m_run[g] - mn);
           float l = l_run[g] * corr;
@@ -295,10 +369,15 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
           for (int v = 0; v < DPL; ++v) acc[g][v] *= corr;
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const float pr = __expf(sc[u] - mn);
-            l += pr;
+            float pr[P];
 #pragma unroll
-            for (int v = 0; v < DPL; ++v) acc[g][v] = __builtin_fmaf(pr, vv[u][v], acc[g][v]);
+            for (int q = 0; q < P; ++q) {
+              pr[q] = __expf(sc[u][q] - mn);
+              l += pr[q];
+            }
+            const float pl = pick<P>(pr, tg);
+#pragma unroll
+            for (int v = 0; v < DPL; ++v) acc[g][v] = __builtin_fmaf(pl, vv[u][v], acc[g][v]);
           }
           l_run[g] = l;
           m_run[g] = mn;
@@ -308,6 +387,11 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
     seg_base += len;
   }
 
+  // the token groups of a wave hold partial sums of the same coordinates
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+    for (int v = 0; v < DPL; ++v) acc[g][v] = across_groups<P>(acc[g][v]);
   // combine the waves: [w][g] m, l, then [w][g][D] acc
   __syncthreads();
   float* red = reinterpret_cast<float*>(tabs);
@@ -321,8 +405,9 @@ __global__ void __launch_bounds__(kRefThreads) ref_attn_kernel(const rfsn_ref_pa
       red_m[wave * kRefMaxG + g] = m_run[g];
       red_l[wave * kRefMaxG + g] = l_run[g];
     }
+    if (tg == 0)
 #pragma unroll
-    for (int v = 0; v < DPL; ++v) red_a[(wave * kRefMaxG + g) * D + DPL * lane + v] = acc[g][v];
+      for (int v = 0; v < DPL; ++v) red_a[(wave * kRefMaxG + g) * D + c0 + v] = acc[g][v];
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += kRefThreads) {
@@ -368,19 +453,21 @@ size_t ref_lds_bytes(const rfsn_ref_params* p, bool shared) {
   return t > combine ? t : combine;
 }
 
-template <int DPL>
+// P token groups per wave: 4 coordinates per lane where the PQ subspace
+// allows it (head_dim 64 with 32 subspaces of 2: 2 coordinates, P = 2)
+template <int D, int P>
 int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
   const int splits = ref_splits(p);
   const int tps = (p->total_tokens + splits - 1) / splits;
   const bool shared = p->k_pq_cb == p->v_pq_cb;
   const size_t lds = ref_lds_bytes(p, shared);
   const int blocks = p->batch * p->kv_heads * splits;
-  constexpr int U = DPL == 4 ? 2 : 4;
+  constexpr int U = 8 / (D * P / 64);  // 8 coordinates of K and of V per lane in flight
   const int G = p->q_heads / p->kv_heads;
-  auto kern = G <= 1 ? ref_attn_kernel<DPL, U, 1>
-              : G <= 2 ? ref_attn_kernel<DPL, U, 2>
-              : G <= 4 ? ref_attn_kernel<DPL, U, 4>
-                       : ref_attn_kernel<DPL, U, 8>;
+  auto kern = G <= 1 ? ref_attn_kernel<D, P, U, 1>
+              : G <= 2 ? ref_attn_kernel<D, P, U, 2>
+              : G <= 4 ? ref_attn_kernel<D, P, U, 4>
+                       : ref_attn_kernel<D, P, U, 8>;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared);
   int st = check_launch("ref_attention");
@@ -424,6 +511,9 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
                "ref_attention: PQ codebooks must be 16-byte aligned");
   RFSN_REQUIRE((p->rvq_layers == 0 && p->rvq_subspaces == 0) || (p->k_rvq_cb && p->v_rvq_cb),
                "ref_attention: RVQ codebooks missing");
+  RFSN_REQUIRE(p->rvq_layers == 0 ||
+                   (reinterpret_cast<uintptr_t>(p->k_rvq_cb) % 8 == 0 && reinterpret_cast<uintptr_t>(p->v_rvq_cb) % 8 == 0),
+               "ref_attention: gated RVQ codebooks must be 8-byte aligned");
   RFSN_REQUIRE(p->num_segments >= 0 && p->total_tokens >= 0 && (p->num_segments == 0 || p->segments),
                "ref_attention: bad segment table");
   const size_t shared_lds = ref_lds_bytes(p, p->k_pq_cb == p->v_pq_cb);
@@ -434,8 +524,8 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
   const size_t wsb = rfsn_ref_attention_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "ref_attention: workspace too small");
   switch (D) {
-    case 64: return launch_ref<1>(p, s);
-    case 128: return launch_ref<2>(p, s);
-    default: return launch_ref<4>(p, s);
+    case 64: return M == 32 ? launch_ref<64, 2>(p, s) : launch_ref<64, 4>(p, s);
+    case 128: return launch_ref<128, 2>(p, s);
+    default: return launch_ref<256, 1>(p, s);
   }
 }
