@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
     const int len = segs[s].len;
     const int lo = max(begin, seg_base), hi = min(end, seg_base + len);
     if (lo < hi) {
-      rfsn_ref_store_codes kc, vc;  // field by field: the table lives in the constant address space
+      rfsn_ref_store_codes kc{}, vc{};  // field by field: the table lives in the constant address space
       kc.pq = segs[s].k.pq;
       kc.rvq = segs[s].k.rvq;
       kc.active = segs[s].k.active;
