@@ -166,15 +166,30 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int v = 0; v < DPL; ++v) tot[u][v] = 0.0f;
+    // four layers' codes in one 8-byte load when every row's codes start
+    // 8-byte aligned (L a multiple of 4, an aligned code array; uniform)
+    const bool quad = r.L % 4 == 0 && reinterpret_cast<uintptr_t>(sc.rvq) % 8 == 0;
     // layers four at a time: their codes, then their codewords of the U
     // rows in flight together; summed in stage order
     for (int l = 0; l < r.L; l += 4) {
       const int nl = min(4, r.L - l);
       int c[4][U];
+      if (quad) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int u = 0; u < U; ++u) {
+          const uint2 w = *reinterpret_cast<const uint2*>(sc.rvq + base[u] + l);
+          const bool on = a[u] >= 0;
+          c[0][u] = on ? (int)(w.x & 0xFFFFu) : 0;
+          c[1][u] = on ? (int)(w.x >> 16) : 0;
+          c[2][u] = on ? (int)(w.y & 0xFFFFu) : 0;
+          c[3][u] = on ? (int)(w.y >> 16) : 0;
+        }
+      } else {
 #pragma unroll
-        for (int u = 0; u < U; ++u) c[j][u] = (a[u] < 0 || j >= nl) ? 0 : (int)sc.rvq[base[u] + l + j];
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int u = 0; u < U; ++u) c[j][u] = (a[u] < 0 || j >= nl) ? 0 : (int)sc.rvq[base[u] + l + j];
+      }
       uint16_t w[4][U][DPL];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
