@@ -127,7 +127,7 @@ struct RvqShape {
 // Every load of the U vectors is issued before the first is consumed: the
 // PQ code bytes and row indices, then the gated codes of every layer, then
 // the codewords.
-template <int D, int DPL, int U>
+template <int D, int DPL, int U, bool EXT>
 __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_store_codes& sc, const int64_t (&row)[U],
                                         const uint16_t* __restrict__ tab, int M, int C, int dsub,
                                         const uint16_t* __restrict__ rvq_cb, const RvqShape& r, int c0) {
@@ -142,19 +142,34 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int v = 0; v < DPL; ++v) corr[u][v] = 0.0f;
-  if (sc.rvq_sub != nullptr) {
-    // subspace stage: the lane's coordinates may span several subspaces
+  if (EXT && sc.rvq_sub != nullptr) {
+    if (r.dr % DPL == 0) {  // uniform: the lane's coordinates sit in one subspace, one code
+      const int mr = c0 / r.dr;
+      int cr[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint8_t* codes = sc.rvq_sub + row[u] * r.Mr;
+      for (int u = 0; u < U; ++u) cr[u] = sc.rvq_sub[row[u] * r.Mr + mr];
 #pragma unroll
-      for (int v = 0; v < DPL; ++v) {
-        const int dd = c0 + v;
-        const int mr = dd / r.dr;
-        corr[u][v] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
+      for (int u = 0; u < U; ++u) {
+        uint16_t e[DPL];
+        load_h<DPL>(rvq_cb + ((int64_t)mr * r.Cr + cr[u]) * r.dr + (c0 - mr * r.dr), e,
+                    reinterpret_cast<uintptr_t>(rvq_cb) % (2 * DPL) == 0);
+#pragma unroll
+        for (int v = 0; v < DPL; ++v) corr[u][v] = h2f(e[v]);
+      }
+    } else {
+      // the lane's coordinates span several subspaces
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint8_t* codes = sc.rvq_sub + row[u] * r.Mr;
+#pragma unroll
+        for (int v = 0; v < DPL; ++v) {
+          const int dd = c0 + v;
+          const int mr = dd / r.dr;
+          corr[u][v] = h2f(rvq_cb[((int64_t)mr * r.Cr + codes[mr]) * r.dr + (dd - mr * r.dr)]);
+        }
       }
     }
-  } else if (sc.active != nullptr) {
+  } else if (!EXT && sc.active != nullptr) {
     int a[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) a[u] = sc.active[row[u]];
@@ -216,16 +231,32 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
 #pragma unroll
     for (int v = 0; v < DPL; ++v) out[u][v] = h2f(f2h(__fadd_rn(h2f(e[v]), corr[u][v])));  // fp16(base + corr)
   }
-  if (sc.sparse_idx != nullptr) {
+  if (EXT && sc.sparse_idx != nullptr) {
     // K[idx] = fp16(fl32(K[idx]) + fl32(val)); the indices of a row are distinct
+    const bool quad = r.k == 4 && reinterpret_cast<uintptr_t>(sc.sparse_idx) % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(sc.sparse_val) % 8 == 0;  // uniform: one load per array
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      for (int j = 0; j < r.k; ++j) {
-        const int idx = sc.sparse_idx[row[u] * r.k + j];
-        const float val = h2f(sc.sparse_val[row[u] * r.k + j]);
+      if (quad) {
+        const uint32_t iw = *reinterpret_cast<const uint32_t*>(sc.sparse_idx + row[u] * 4);
+        const uint2 vw = *reinterpret_cast<const uint2*>(sc.sparse_val + row[u] * 4);
+        const uint32_t vh[4] = {vw.x & 0xFFFFu, vw.x >> 16, vw.y & 0xFFFFu, vw.y >> 16};
 #pragma unroll
-        for (int v = 0; v < DPL; ++v)
-          if (idx == c0 + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
+        for (int j = 0; j < 4; ++j) {
+          const int idx = (int)((iw >> (8 * j)) & 0xFFu);
+          const float val = h2f((uint16_t)vh[j]);
+#pragma unroll
+          for (int v = 0; v < DPL; ++v)
+            if (idx == c0 + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
+        }
+      } else {
+        for (int j = 0; j < r.k; ++j) {
+          const int idx = sc.sparse_idx[row[u] * r.k + j];
+          const float val = h2f(sc.sparse_val[row[u] * r.k + j]);
+#pragma unroll
+          for (int v = 0; v < DPL; ++v)
+            if (idx == c0 + v) out[u][v] = h2f(f2h(__fadd_rn(out[u][v], val)));
+        }
       }
     }
   }
@@ -234,8 +265,9 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
 // Lane geometry: a wave holds P token groups of 64 / P lanes, and lane ll of
 // a group owns coordinates c0 = DPL * ll .. c0 + DPL - 1 (DPL = D * P / 64),
 // so one instruction serves P tokens.  A wave takes U * P consecutive tokens
-// per step.
-template <int D, int P, int U, int GMAX>
+// per step.  EXT: the long-context format (subspace RVQ stage, sparse
+// residuals); otherwise the reference format (gated RVQ) or PQ only.
+template <int D, int P, int U, int GMAX, bool EXT>
 __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_eu(GMAX == 1 ? 4 : 1))) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
                                                                int kv_tab_shared) {
   extern __shared__ __align__(16) uint16_t tabs[];
@@ -354,8 +386,8 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
             }
           }
         } else {
-          rebuild<D, DPL, U>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, c0);
-          rebuild<D, DPL, U>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, c0);
+          rebuild<D, DPL, U, EXT>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, c0);
+          rebuild<D, DPL, U, EXT>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, c0);
         }
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
@@ -477,12 +509,19 @@ int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
   const bool shared = p->k_pq_cb == p->v_pq_cb;
   const size_t lds = ref_lds_bytes(p, shared);
   const int blocks = p->batch * p->kv_heads * splits;
-  constexpr int U = 8 / (D * P / 64);  // 8 coordinates of K and of V per lane in flight
+  // token slots per lane: 8 coordinates of K and of V in flight per lane,
+  // 12 for the gated format with 4 coordinates per lane (its kernel has the
+  // registers; measured best at the reference's default config)
+  constexpr int DPL = D * P / 64;
+  constexpr int U = 8 / DPL;
+  constexpr int UG = DPL == 4 ? 3 : U;
   const int G = p->q_heads / p->kv_heads;
-  auto kern = G <= 1 ? ref_attn_kernel<D, P, U, 1>
-              : G <= 2 ? ref_attn_kernel<D, P, U, 2>
-              : G <= 4 ? ref_attn_kernel<D, P, U, 4>
-                       : ref_attn_kernel<D, P, U, 8>;
+  const bool ext = p->rvq_subspaces > 0 || p->sparse_k > 0;
+  auto pick_g = [G](auto k1, auto k2, auto k4, auto k8) { return G <= 1 ? k1 : G <= 2 ? k2 : G <= 4 ? k4 : k8; };
+  auto kern = ext ? pick_g(ref_attn_kernel<D, P, U, 1, true>, ref_attn_kernel<D, P, U, 2, true>,
+                           ref_attn_kernel<D, P, U, 4, true>, ref_attn_kernel<D, P, U, 8, true>)
+                  : pick_g(ref_attn_kernel<D, P, UG, 1, false>, ref_attn_kernel<D, P, UG, 2, false>,
+                           ref_attn_kernel<D, P, UG, 4, false>, ref_attn_kernel<D, P, UG, 8, false>);
   if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared);
   int st = check_launch("ref_attention");
