@@ -57,6 +57,7 @@ CASES = [
     (128, 16, 256, 0, 0, 2, 4, 2, True, 3),       # pq-only stores (no RVQ stage)
     (128, 8, 256, 3, 256, 2, 16, 2, True, 7),     # 8 query heads per KV head
     (256, 16, 128, 1, 65536, 1, 2, 2, True, 0),   # 16-bit RVQ codes
+    (64, 32, 64, 2, 128, 1, 4, 4, True, 0),       # 2-wide PQ subspaces: 2 coordinates per lane, 2 token groups
 ]
 
 
@@ -139,6 +140,8 @@ EXT_CASES = [
     (64, 8, 256, 4, 64, 3, 2, 8, 8),        # stage shapes the tiled kernel does not take
     (256, 32, 256, 32, 256, 8, 1, 8, 2),
     (128, 8, 128, 0, 0, 2, 2, 4, 4),        # PQ + sparse, no RVQ stage
+    (64, 16, 256, 32, 64, 4, 1, 4, 2),      # 2-wide RVQ subspaces: a lane's 4 coordinates span two
+    (64, 32, 64, 16, 128, 4, 1, 4, 4),      # 2-wide PQ subspaces: 2 coordinates per lane, 2 token groups
 ]
 
 
