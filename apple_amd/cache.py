@@ -46,6 +46,8 @@ from .quantization import (
     _append_compressed_tensor,
     _compress_tensor_sequence,
     _decode_compressed_tensor,
+    _encode_pair_head_major,
+    _head_major_store,
     _slice_compressed_tensor,
 )
 from .storage import (
@@ -581,12 +583,22 @@ class RFSNv10KVCacheMLX:
         self._hot_v[:, h + self.num_hot:h + need] = v.permute(1, 0, 2).to(self.device, torch.float16)
         self.num_hot = need
 
-    def _try_hot_append(self, k: torch.Tensor, v: torch.Tensor) -> bool:
+    def _hot_append_args(self, stream: Optional[int] = None) -> Tuple[Optional[int], int]:
+        """(drift guard's V bound address or None, stream) of ``_try_hot_append``:
+        fixed while the quantizers stay, so a decode session computes them once
+        per rebuild."""
+        return (self._vabs.data_ptr() if self._guarded else None,
+                L.stream_handle(self.device) if stream is None else stream)
+
+    def _try_hot_append(self, k: torch.Tensor, v: torch.Tensor,
+                        args: Optional[Tuple[Optional[int], int]] = None) -> bool:
         """The decode loop's common append (recency tiers): new tokens [T, H, D]
         that the hot tier holds without demoting any (num_hot + T <=
         hot_capacity) and its buffers hold at the current head.  One
         ``rfsn_hot_append`` launch, which also folds |v| into the drift
-        guard's V bound.  Returns False, with the cache untouched, otherwise."""
+        guard's V bound, on the current stream (``args``: the
+        ``_hot_append_args`` to use instead).  Returns False, with the cache
+        untouched, otherwise."""
         T = int(k.shape[0])
         if not self._recency or not T or self.num_hot + T > self.hot_capacity:
             return False
@@ -600,9 +612,9 @@ class RFSNv10KVCacheMLX:
             v = v.to(self.device, torch.float16).contiguous()
         if tuple(k.shape) != (T, self.H, self.D) or tuple(v.shape) != (T, self.H, self.D):
             raise ValueError(f"new_keys and new_values must be [T, {self.H}, {self.D}]")
+        vabs, stream = self._hot_append_args(K._stream(k)) if args is None else args
         L.call("rfsn_hot_append", k.data_ptr(), v.data_ptr(), self.H * self.D, T, self.H, self.D,
-               self._hot_k.data_ptr(), self._hot_v.data_ptr(), cap, t0,
-               self._vabs.data_ptr() if self._guarded else None, K._stream(k))
+               self._hot_k.data_ptr(), self._hot_v.data_ptr(), cap, t0, vabs, stream)
         self.num_hot += T
         self.total_tokens += T
         return True
@@ -614,10 +626,11 @@ class RFSNv10KVCacheMLX:
         return DecodeSession(self, q, quantizer, router, cold_attended, out)
 
     def _hot_pop_oldest(self, n: int) -> Tuple[torch.Tensor, torch.Tensor]:
-        """Remove and return the n oldest hot tokens as [n, H, D]."""
+        """Remove and return the n oldest hot tokens as [n, H, D] (copies,
+        head-major in memory, as the warm encode reads them)."""
         h = self._hot_head
-        k = self._hot_k[:, h:h + n].permute(1, 0, 2).clone()
-        v = self._hot_v[:, h:h + n].permute(1, 0, 2).clone()
+        k = self._hot_k[:, h:h + n].clone().permute(1, 0, 2)
+        v = self._hot_v[:, h:h + n].clone().permute(1, 0, 2)
         self._hot_head += n
         self.num_hot -= n
         return k, v
@@ -719,16 +732,29 @@ class RFSNv10KVCacheMLX:
         self._hot_append(keys[direct:], values[direct:])
 
     def _add_to_warm(self, keys: torch.Tensor, values: torch.Tensor) -> None:
-        """cache.py:122-132."""
-        ck = _compress_tensor_sequence(keys, self._kq)
-        cv = _compress_tensor_sequence(values, self._vq)
+        """cache.py:122-132.  Under a subspace format that the one-launch
+        encode serves, K and V share one launch whose head-major codes feed
+        the tiled store as they are."""
+        hm = _encode_pair_head_major(keys, values, self._kq, self._vq) if self._subspace else None
+        if hm is None:
+            ck = _compress_tensor_sequence(keys, self._kq)
+            cv = _compress_tensor_sequence(values, self._vq)
+        else:
+            plain = not isinstance(self._wk, _RingStore)  # a plain store keeps contiguous codes
+            ck, cv = _head_major_store(hm[0], plain), _head_major_store(hm[1], plain)
         if isinstance(self._wk, _RingStore):
             self._wk.append(ck)
             self._wv.append(cv)
         else:
             self.warm_keys = _append_compressed_tensor(self.warm_keys, ck)
             self.warm_values = _append_compressed_tensor(self.warm_values, cv)
-        self._warm_tiled_append(ck, cv)
+        if hm is None:
+            self._warm_tiled_append(ck, cv)
+        elif self._fmt().fused_ok:
+            if self._warm_tiled is None:
+                self._warm_tiled = self._tiled_pair()
+            for tiled, codes, qz in zip(self._warm_tiled, hm, (self._kq, self._vq)):
+                tiled.append(*codes, qz.pq.codebooks, qz.rvq_codebooks)
         self.num_warm += int(keys.shape[0])
 
     def _warm_to_cold(self, n: int, disk_dir) -> None:
@@ -1571,7 +1597,8 @@ class DecodeSession:
     query is the newest token, so every window token is allowed and the launch
     carries no query positions (cache.py:395-428 with causal masking at the
     newest position).  The split count is pinned at each rebuild, so the
-    launch's workspace stays valid as the window grows.  ``router`` ranks the
+    launch's workspace stays valid as the window grows.  A fast step runs on
+    the stream that was current at the last rebuild.  ``router`` ranks the
     cold chunks (storage.py:203-234); ``cold_attended`` of them are attended,
     made resident in device slots at each rebuild.  A cache whose format the
     tiled kernel does not serve runs ``update`` + ``attention_forward`` (the
@@ -1590,6 +1617,7 @@ class DecodeSession:
         self.out = torch.empty_like(q) if out is None else out
         self._launch: Optional[K.FusedLaunch] = None
         self._ids: Optional[List[int]] = None
+        self._hot_args: Optional[Tuple[Optional[int], int]] = None  # the fast step's hot-append arguments
         self.rebuilds = 0
 
     def _chunk_set(self) -> Optional[List[int]]:
@@ -1603,7 +1631,7 @@ class DecodeSession:
     def step(self, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         c = self.cache
         T = int(k.shape[0])
-        fast = self._launch is not None and c._try_hot_append(k, v)
+        fast = self._launch is not None and c._try_hot_append(k, v, self._hot_args)
         if not fast:
             c.update(k, v, self.quantizer)
         ids = self._chunk_set()
@@ -1632,6 +1660,9 @@ class DecodeSession:
             p = step.params
             p.splits = int(L.load().rfsn_fused_splits(C.byref(p)))  # pinned as the window grows
             self._launch, self._ids = step, ids
+            # fast steps append on the launch's stream, so the append and the
+            # launch that reads it stay ordered
+            self._hot_args = c._hot_append_args(step.stream)
         else:  # chunks still copying in: no prepared launch to grow until they are resident
             self._launch, self._ids = None, None
         step()

@@ -131,6 +131,14 @@ def warm_encode(x: torch.Tensor, fmt: WarmFormat, pq_cb: torch.Tensor,
     return out
 
 
+def batch_encode_ok(fmt: WarmFormat) -> bool:
+    """Whether ``rfsn_warm_encode_batch`` serves the format: head_dim 64, 4-
+    or 8-dim PQ subspaces, an RVQ stage of the same split or none, top-k
+    sparse residuals with k 0 or 4 (rows from torch's aligned allocations)."""
+    return (fmt.head_dim == 64 and fmt.pq_subspaces in (8, 16)
+            and fmt.rvq_subspaces in (0, fmt.pq_subspaces) and fmt.sparse_k in (0, 4))
+
+
 def warm_encode_batch(items: Sequence[Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]],
                       fmt: WarmFormat) -> List[Dict[str, torch.Tensor]]:
     """``warm_encode`` of several (x, pq_cb, rvq_cb) sets of one format in one

@@ -239,6 +239,46 @@ def _compress_tensor_sequence(tensor: torch.Tensor, quantizer: HybridQuantizerML
     )
 
 
+def _encode_pair_head_major(keys: torch.Tensor, values: torch.Tensor, kq: HybridQuantizerMLX,
+                            vq: HybridQuantizerMLX):
+    """K and V [T, H, D] of one subspace format in one ``warm_encode_batch``
+    launch, with head-major codes: per tensor (pq, rvq, sparse_idx,
+    sparse_val), each [H, T, *] (None for a stage the format lacks).  The
+    codes are those of ``_compress_tensor_sequence`` (each vector is encoded
+    on its own), laid out for the tiled store.  None when that launch does
+    not serve the pair (the reference format, two formats, or one the
+    one-launch encode does not cover)."""
+    if not (kq.subspace and vq.subspace):
+        return None
+    fmt = kq.warm_format()
+    if fmt != vq.warm_format() or not K.batch_encode_ok(fmt):
+        return None
+    T, H, D = keys.shape
+    if T == 0:
+        return None
+    hm = [t.to(device=kq.device, dtype=torch.float16).permute(1, 0, 2).contiguous().view(H * T, D)
+          for t in (keys, values)]
+    outs = K.warm_encode_batch([(hm[0], kq.pq.codebooks, kq.rvq_codebooks),
+                                (hm[1], vq.pq.codebooks, vq.rvq_codebooks)], fmt)
+    shape = lambda t: None if t is None else t.view(H, T, -1)
+    return [tuple(shape(o.get(f)) for f in ("pq", "rvq", "sparse_idx", "sparse_val")) for o in outs]
+
+
+def _head_major_store(codes, contiguous: bool = False) -> CompressedTensorMLX:
+    """A token-major CompressedTensorMLX of head-major subspace codes (pq,
+    rvq, sparse_idx, sparse_val) [H, T, *]: views, or copies with
+    ``contiguous``."""
+    pq, rvq, sidx, sval = codes
+    H, T, _ = pq.shape
+    dev = pq.device
+    pm = (lambda t: t.permute(1, 0, 2).contiguous()) if contiguous else (lambda t: t.permute(1, 0, 2))
+    tm = lambda t, dt: pm(t) if t is not None else torch.zeros((T, H, 0), dtype=dt, device=dev)
+    return CompressedTensorMLX(pq_codes=pm(pq), rvq_codes=tm(rvq, torch.uint8),
+                               rvq_mask=torch.ones((T, H), dtype=torch.bool, device=dev),
+                               rvq_offsets=torch.zeros((0,), dtype=torch.int32, device=dev), num_heads=H,
+                               sparse_idx=tm(sidx, torch.uint8), sparse_val=tm(sval, torch.float16))
+
+
 def _append_compressed_tensor(base: CompressedTensorMLX, addition: CompressedTensorMLX) -> CompressedTensorMLX:
     """quantization.py:346-361."""
     if base.num_heads != addition.num_heads:
