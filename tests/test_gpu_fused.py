@@ -578,6 +578,33 @@ def test_prefetch_ahead_decode_loop(device):
         assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL, step
 
 
+@pytest.mark.parametrize("M, Mr, k", [(16, 16, 4), (8, 8, 0), (16, 0, 4), (8, 0, 0)])
+def test_paired_head_major_encode_matches_per_tensor(device, M, Mr, k):
+    """A demotion's K + V encode (one launch, head-major codes) gives the
+    per-tensor encode's codes bit for bit, from token-major inputs and from
+    head-major ones (the popped hot tokens); None where it does not apply."""
+    from apple_amd.quantization import _compress_tensor_sequence, _encode_pair_head_major, _head_major_store
+
+    g, cfg, keys, values, cbs, kq, vq = _setup(11, 8, 4, M, Mr, k, 37, 16)
+    kd, vd = T(keys, device), T(values, device)
+    if not (Mr or k):  # the reference format keeps its own encode
+        assert _encode_pair_head_major(kd, vd, kq, vq) is None
+        return
+    head_major = lambda x: x.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    for kin, vin in ((kd, vd), (head_major(kd), head_major(vd))):
+        hm = _encode_pair_head_major(kin, vin, kq, vq)
+        assert hm is not None
+        for codes, x, qz in zip(hm, (kin, vin), (kq, vq)):
+            ref = _compress_tensor_sequence(x, qz)
+            for plain in (False, True):
+                got = _head_major_store(codes, plain)
+                for f in ("pq_codes", "rvq_codes", "rvq_mask", "sparse_idx", "sparse_val"):
+                    a, b = getattr(got, f), getattr(ref, f)
+                    assert a.shape == b.shape and a.dtype == b.dtype and torch.equal(a.contiguous(), b), f
+                    assert not plain or a.is_contiguous(), f
+    assert _encode_pair_head_major(kd[:0], vd[:0], kq, vq) is None
+
+
 def test_decode_session_streaming(device):
     """A decode loop through ``DecodeSession``: 90 one-token steps on a cache
     with pinned cold chunks (64 hot tokens, so a 32-token block is demoted
