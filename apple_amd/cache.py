@@ -414,6 +414,7 @@ class RFSNv10KVCacheMLX:
             self._wk = CompressedTensorMLX.empty(config, self.H, self.device)
             self._wv = CompressedTensorMLX.empty(config, self.H, self.device)
         self._warm_tiled: Optional[Tuple[TiledCodes, TiledCodes]] = None
+        self._fmt_memo: Optional[Tuple[object, K.WarmFormat]] = None
 
         self.cold_chunk_paths: List[Path] = []
         self.cold_chunk_paths_by_id: Dict[int, Path] = {}
@@ -511,7 +512,12 @@ class RFSNv10KVCacheMLX:
         return self.config.ext_format
 
     def _fmt(self) -> K.WarmFormat:
-        return self._kq.warm_format()
+        """The K quantizer's warm format, kept per quantizer object (its
+        codebooks fix the format's shapes when it is built)."""
+        memo = self._fmt_memo
+        if memo is None or memo[0] is not self._kq:
+            memo = self._fmt_memo = (self._kq, self._kq.warm_format())
+        return memo[1]
 
     @property
     def _k_layout(self) -> int:
