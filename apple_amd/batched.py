@@ -264,7 +264,8 @@ def _kernel_view(c: Dict[str, Optional[torch.Tensor]]) -> Dict[str, Optional[tor
     """The arrays the fused kernel streams: tiled codes, sparse indices and
     the corrected coordinates as its sparse values."""
     si = c["sparse_idx_s"] if c.get("sparse_idx_s") is not None else c["sparse_idx"]
-    return {"pq": c["pq"], "rvq": c["rvq"], "sparse_idx": si, "sparse_val": c["sparse_fold"]}
+    return {"pq": c["pq"], "rvq": c["rvq"], "sparse_idx": si, "sparse_val": c["sparse_fold"],
+            "sparse_cc": c.get("sparse_cc")}
 
 
 def untile(tiled: torch.Tensor, M: int, T: int) -> torch.Tensor:

@@ -236,6 +236,12 @@ class TiledCodes:
         self._segs[(self.head, tile_skip)] = hit
         return hit
 
+    def plane_bytes(self) -> Optional[int]:
+        """Bytes from ``sparse_val`` to ``sparse_cc`` (the exact pass's plane), or None."""
+        if not self.exact_plane:
+            return None
+        return self.t["sparse_cc"].data_ptr() - self.t["sparse_val"].data_ptr()
+
     def codes(self, tile_skip: int = 0) -> Dict[str, Optional[torch.Tensor]]:
         """Per-array views starting at live tile ``tile_skip`` (head stride unchanged)."""
         f = self.fmt
@@ -385,6 +391,26 @@ def _plain_head_major(store: CompressedTensorMLX):
     return pm(store.pq_codes), pm(store.rvq_codes), pm(store.sparse_idx), pm(store.sparse_val)
 
 
+class _CodebookKey:
+    """Memo key of tables built from a quantizer pair's codebooks.  It holds
+    the objects themselves (compared by identity, so a freed tensor's address
+    or id reused by a new one cannot match) and the tensors' versions."""
+
+    __slots__ = ("objs", "versions")
+
+    def __init__(self, objs: tuple, versions: tuple):
+        self.objs, self.versions = objs, versions
+
+    def __eq__(self, other) -> bool:
+        return (isinstance(other, _CodebookKey) and self.versions == other.versions
+                and len(self.objs) == len(other.objs) and all(a is b for a, b in zip(self.objs, other.objs)))
+
+    def __ne__(self, other) -> bool:
+        return not self.__eq__(other)
+
+    __hash__ = None
+
+
 class RFSNv10KVCacheMLX:
     """Tiered KV cache with exact hot storage and compressed warm/cold storage."""
 
@@ -446,8 +472,8 @@ class RFSNv10KVCacheMLX:
         # values, the guard's input row and the last call's estimates
         self._guard = torch.zeros((1, 65), dtype=torch.float32, device=self.device)
         self._vabs = self._guard[0, 64:]  # the row's V bound, updated by every append
-        self._guard_key: Optional[Tuple[int, int]] = None
-        self._tables_key: Optional[tuple] = None
+        self._guard_key: Optional[_CodebookKey] = None
+        self._tables_key: Optional[_CodebookKey] = None
         self._tables: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self.last_drift: Optional[torch.Tensor] = None
         self.last_access_stats = self._empty_access_stats()
@@ -540,10 +566,19 @@ class RFSNv10KVCacheMLX:
                            **kw),
                 TiledCodes(fmt, self.H, self.device, **kw))
 
+    def _codebook_key(self, rvq: bool = True) -> "_CodebookKey":
+        """The quantizer pair and each codebook tensor with its version:
+        differs when a quantizer is swapped or its codebooks are replaced
+        (``calibrate_quantizer``) or written in place."""
+        cbs = (self._kq.pq.codebooks, self._kq.rvq.codebooks if rvq else None,
+               self._vq.pq.codebooks, self._vq.rvq.codebooks if rvq else None)
+        return _CodebookKey((self._kq, self._vq) + cbs, tuple(None if t is None else t._version for t in cbs))
+
     def _guard_tensor(self) -> torch.Tensor:
-        """The drift guard's [1, 65] input: the K codebooks' weights (built once
-        per quantizer pair) and the running bound on |V^| kept by the appends."""
-        key = (id(self._kq), id(self._vq))
+        """The drift guard's [1, 65] input: the K codebooks' weights (rebuilt
+        whenever a codebook changes) and the running bound on |V^| kept by the
+        appends and the V codebooks."""
+        key = self._codebook_key()
         if self._guard_key != key:
             self._guard[0, :64] = K.score_guard(self._kq.pq.codebooks, self._kq.rvq.codebooks, 0.0)[:64]
             vp, vr = self._vq.pq.codebooks.float(), self._vq.rvq.codebooks.float()
@@ -558,7 +593,7 @@ class RFSNv10KVCacheMLX:
         and their codebook tensors)."""
         cbs = [self._kq.pq.codebooks, self._kq.rvq.codebooks if rvq else None,
                self._vq.pq.codebooks, self._vq.rvq.codebooks if rvq else None]
-        key = (id(self._kq), id(self._vq), *[(t.data_ptr(), t._version) if t is not None else None for t in cbs])
+        key = self._codebook_key(rvq)
         if self._tables_key != key:
             self._tables = (K.entry_tables(cbs[0], cbs[1]), K.entry_tables(cbs[2], cbs[3]))
             self._tables_key = key
@@ -1498,7 +1533,7 @@ class RFSNv10KVCacheMLX:
                 (kc, kk, avail), (vc, vk, _) = kt.seg(skip), vt.seg(skip)
                 for bi in range(B):
                     resident.add_codes(bi, kc, vc, kk + vk, kt.cap, b - skip * K.TILE,
-                                       spans["warm"][0] + skip * K.TILE - start, avail)
+                                       spans["warm"][0] + skip * K.TILE - start, avail, kt.plane_bytes())
                 res_tokens += b - skip * K.TILE
             else:
                 meta, ov, _ = x
@@ -1509,7 +1544,7 @@ class RFSNv10KVCacheMLX:
                 (kc, kk, avail), (vc, vk, _) = dev["key"].seg(skip), dev["value"].seg(skip)
                 for bi in range(B):
                     table.add_codes(bi, kc, vc, kk + vk, dev["key"].cap, b - skip * K.TILE,
-                                    meta["start_token"] + skip * K.TILE - start, avail)
+                                    meta["start_token"] + skip * K.TILE - start, avail, dev["key"].plane_bytes())
                 if meta["chunk_id"] in fetched:
                     in_tokens += b - skip * K.TILE
                 else:
@@ -1604,7 +1639,8 @@ class DecodeSession:
     carries no query positions (cache.py:395-428 with causal masking at the
     newest position).  The split count is pinned at each rebuild, so the
     launch's workspace stays valid as the window grows.  A fast step runs on
-    the stream that was current at the last rebuild.  ``router`` ranks the
+    the stream that was current at the last rebuild; a step called with
+    another current stream rebuilds on that one.  ``router`` ranks the
     cold chunks (storage.py:203-234); ``cold_attended`` of them are attended,
     made resident in device slots at each rebuild.  A cache whose format the
     tiled kernel does not serve runs ``update`` + ``attention_forward`` (the
@@ -1637,7 +1673,11 @@ class DecodeSession:
     def step(self, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         c = self.cache
         T = int(k.shape[0])
-        fast = self._launch is not None and c._try_hot_append(k, v, self._hot_args)
+        # the fast step appends and launches on the stream pinned at the last
+        # rebuild; a caller that has switched streams since takes the rebuild
+        # path, so its conversions and the launches stay on one stream
+        fast = (self._launch is not None and L.stream_handle(c.device) == self._hot_args[1]
+                and c._try_hot_append(k, v, self._hot_args))
         if not fast:
             c.update(k, v, self.quantizer)
         ids = self._chunk_set()

@@ -1241,25 +1241,29 @@ extern "C" int rfsn_warm_encode_batch(const rfsn_format* f, const rfsn_encode_jo
   int st = validate_format(f);
   if (st) return st;
   RFSN_REQUIRE(count >= 0 && (count == 0 || jobs != nullptr), "warm_encode_batch: bad job list");
+  auto as_job = [](const rfsn_encode_job& j) {
+    return EncodeJob{(const uint16_t*)j.x, j.n, j.ldx, (const uint16_t*)j.pq_cb, (const uint16_t*)j.rvq_cb, j.out.pq,
+                     j.out.rvq, j.out.sparse_idx, (uint16_t*)j.out.sparse_val, 0};
+  };
+  // every job is checked before the first launch: a refused call writes no output
+  for (int i = 0; i < count; ++i) {
+    const rfsn_encode_job& j = jobs[i];
+    RFSN_REQUIRE(j.n >= 0 && j.ldx >= f->head_dim, "warm_encode_batch: bad job " + std::to_string(i));
+    if (j.n == 0) continue;  // an empty set launches nothing
+    RFSN_REQUIRE(j.x && j.pq_cb && j.out.pq, "warm_encode_batch: null pointer in job " + std::to_string(i));
+    RFSN_REQUIRE(f->rvq_subspaces == 0 || (j.rvq_cb && j.out.rvq),
+                 "warm_encode_batch: RVQ stage needs codebooks and an output");
+    RFSN_REQUIRE(f->sparse_k == 0 || (j.out.sparse_idx && j.out.sparse_val),
+                 "warm_encode_batch: sparse stage needs outputs");
+    if (!fused_encode_ok(f, as_job(j)))
+      return fail(RFSN_ERR_UNSUPPORTED, "warm_encode_batch: the one-launch encode serves head_dim 64, 4- or 8-dim "
+                                        "subspaces, an RVQ stage of the same split or none, k in {0, 4} and aligned rows");
+  }
   hipStream_t s = (hipStream_t)stream;
   for (int i0 = 0; i0 < count; i0 += kMaxJobs) {
     EncodeJobs batch = {};
-    for (int i = i0; i < count && i < i0 + kMaxJobs; ++i) {
-      const rfsn_encode_job& j = jobs[i];
-      RFSN_REQUIRE(j.n >= 0 && j.ldx >= f->head_dim, "warm_encode_batch: bad job");
-      if (j.n == 0) continue;  // an empty set launches nothing
-      RFSN_REQUIRE(j.x && j.pq_cb && j.out.pq, "warm_encode_batch: null pointer");
-      RFSN_REQUIRE(f->rvq_subspaces == 0 || (j.rvq_cb && j.out.rvq),
-                   "warm_encode_batch: RVQ stage needs codebooks and an output");
-      RFSN_REQUIRE(f->sparse_k == 0 || (j.out.sparse_idx && j.out.sparse_val),
-                   "warm_encode_batch: sparse stage needs outputs");
-      EncodeJob& e = batch.j[batch.count++];
-      e = EncodeJob{(const uint16_t*)j.x, j.n, j.ldx, (const uint16_t*)j.pq_cb, (const uint16_t*)j.rvq_cb, j.out.pq,
-                    j.out.rvq, j.out.sparse_idx, (uint16_t*)j.out.sparse_val, 0};
-      if (!fused_encode_ok(f, e))
-        return fail(RFSN_ERR_UNSUPPORTED, "warm_encode_batch: the one-launch encode serves head_dim 64, 4- or 8-dim "
-                                          "subspaces, an RVQ stage of the same split or none, k in {0, 4} and aligned rows");
-    }
+    for (int i = i0; i < count && i < i0 + kMaxJobs; ++i)
+      if (jobs[i].n > 0) batch.j[batch.count++] = as_job(jobs[i]);
     st = launch_warm_encode_fused(f, batch, s);
     if (st) return st;
   }

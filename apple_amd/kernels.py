@@ -429,9 +429,14 @@ class SegmentTable:
         self.rows: List[List[L.Segment]] = [[] for _ in range(batch)]
         self.tiles: List[List[int]] = [[] for _ in range(batch)]  # 32-token tiles of each segment
         self.keep: List[torch.Tensor] = []
+        # per segment: bytes from K's sparse values to their corrected-coordinate
+        # plane (the drift guard's exact pass reads it), None without such a plane
+        self.k_planes: List[List[Optional[int]]] = [[] for _ in range(batch)]
 
     def add(self, b: int, k: Dict[str, Optional[torch.Tensor]], v: Dict[str, Optional[torch.Tensor]],
             head_stride: int, length: int, pos0: int) -> None:
+        """``k`` may carry ``sparse_cc``, the corrected coordinates in the
+        plane after ``sparse_val`` (``TiledCodes(exact_plane=True)``)."""
         def codes(c):
             # the kernel reads whole 32-token tiles of the tiled code rows: the
             # segment must fit the views it is given
@@ -451,18 +456,42 @@ class SegmentTable:
                     self.keep.append(t)
             return L.Codes(L.ptr(c.get("pq")), L.ptr(c.get("rvq")), L.ptr(c.get("sparse_idx")),
                            L.ptr(c.get("sparse_val")))
+        sv, cc = k.get("sparse_val"), k.get("sparse_cc")
+        plane = None
+        if sv is not None and cc is not None:
+            if cc.dtype != sv.dtype or cc.shape != sv.shape or cc.stride() != sv.stride():
+                raise ValueError("sparse_cc must have the shape and strides of sparse_val")
+            plane = cc.data_ptr() - sv.data_ptr()
         self.rows[b].append(L.Segment(codes(k), codes(v), head_stride, length, pos0))
         self.tiles[b].append((int(length) + 31) // 32)
+        self.k_planes[b].append(plane)
 
     def add_codes(self, b: int, k: "L.Codes", v: "L.Codes", keep: Sequence[torch.Tensor], head_stride: int,
-                  length: int, pos0: int, available: int) -> None:
+                  length: int, pos0: int, available: int, k_plane: Optional[int] = None) -> None:
         """Like ``add`` from precomputed addresses (``TiledCodes.seg``);
-        ``available`` = tokens of the code rows from the segment's start."""
+        ``available`` = tokens of the code rows from the segment's start;
+        ``k_plane`` = bytes from K's sparse values to their corrected-coordinate
+        plane (``TiledCodes.plane_bytes``), None without one."""
         if length > 0 and (length + 31) // 32 * 32 > available:
             raise ValueError(f"segment of {length} tokens exceeds its {available} available code rows")
         self.keep.extend(keep)
         self.rows[b].append(L.Segment(k, v, head_stride, length, pos0))
         self.tiles[b].append((int(length) + 31) // 32)
+        self.k_planes[b].append(k_plane)
+
+    def check_exact_planes(self, kv_heads: int, sparse_k: int) -> None:
+        """The drift guard's exact pass reads K's corrected coordinates at
+        ``kv_heads * head_stride * sparse_k`` fp16 values past each K sparse
+        value pointer: refuse a table with a K segment lacking that plane."""
+        for b, row in enumerate(self.rows):
+            for s, seg in enumerate(row):
+                want = kv_heads * int(seg.head_stride) * sparse_k * 2
+                got = self.k_planes[b][s]
+                if seg.len > 0 and got != want:
+                    raise ValueError(
+                        f"drift guard: K segment {s} of sequence {b} has no corrected-coordinate plane "
+                        f"{want} bytes after its sparse values (got {got}); build its codes with "
+                        "TiledCodes(exact_plane=True) or pass sparse_cc")
 
     @property
     def max_rows(self) -> int:
@@ -630,6 +659,8 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
             drift = torch.empty(B * Hq * slots, dtype=torch.float32, device=q.device)
         elif drift.dtype != torch.float32 or not drift.is_contiguous() or drift.numel() < B * Hq * slots:
             raise ValueError(f"drift must be a contiguous float32 tensor of at least {B * Hq * slots} values")
+        if fmt.sparse_k:
+            segments.check_exact_planes(kv_heads, fmt.sparse_k)
         p.guard, p.drift, p.guard_tol = guard.data_ptr(), drift.data_ptr(), float(guard_tol)
         drift = drift[:B * Hq * slots].view(B, Hq, slots)
     wsb = lib.rfsn_fused_workspace_bytes(C.byref(p))

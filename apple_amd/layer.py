@@ -19,6 +19,7 @@ reference's initialisation or a local state dict; nothing is downloaded.
 
 from __future__ import annotations
 
+import itertools
 import math
 import shutil
 from pathlib import Path
@@ -311,8 +312,11 @@ class Llama32DecoderLayerMLX(torch.nn.Module):
         pid = torch.as_tensor(position_ids, device=self.device).reshape(-1)
         if self.rotary_module is not None:
             # llama32_adapter.py:535-553: HF rotary modules take (hidden, position_ids)
-            ids = pid.reshape(1, -1)
-            hidden = torch.zeros((1, seq_len, self.hidden_dim), dtype=torch.float32, device=self.device)
+            # on the device of their own buffers or parameters
+            first = next(itertools.chain(self.rotary_module.buffers(), self.rotary_module.parameters()), None)
+            rdev = self.device if first is None else first.device
+            ids = pid.reshape(1, -1).to(rdev)
+            hidden = torch.zeros((1, seq_len, self.hidden_dim), dtype=torch.float32, device=rdev)
             try:
                 cos, sin = self.rotary_module(hidden, ids)
             except TypeError:

@@ -219,6 +219,41 @@ def test_fused_error_envelope_peaked_queries(device):
     assert not fired[1] and fired[4] and fired[8], fired
 
 
+def test_guard_follows_recalibrated_codebooks(device):
+    """The drift guard's weights and the entry tables follow the K codebooks:
+    after calibrate_quantizer replaces them, and after an in-place write, the
+    next call's guard row is the new codebooks' weights."""
+    from apple_amd import kernels as K
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.calibrate import calibrate_quantizer
+
+    g, cfg, keys, values, cbs, kq, vq = _setup(12, 32, 8, 16, 16, 4, 600, 64)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._guarded
+    q = T(randn16(g, 1, 32, 64), device)
+
+    def row():
+        return H(cache._guard[0, :64]).copy()
+
+    def want():
+        return H(K.score_guard(kq.pq.codebooks, kq.rvq.codebooks, 0.0)[:64])
+
+    cache.attention_forward(q, causal=False)
+    first = row()
+    np.testing.assert_array_equal(first, want())
+    calibrate_quantizer(kq, T(keys.reshape(-1, 64), device), num_iterations=2,
+                        generator=torch.Generator().manual_seed(3))
+    cache.attention_forward(q, causal=False)
+    second = row()
+    assert not np.array_equal(first, second)
+    np.testing.assert_array_equal(second, want())
+    kq.rvq.codebooks.mul_(2.0)  # written in place: same tensor, new version
+    cache.attention_forward(q, causal=False)
+    np.testing.assert_array_equal(row(), want())
+    assert not np.array_equal(row(), second)
+
+
 def test_fused_exact_pass_matches_codebook_path(device):
     """With the guard's tolerance at 0 every block of the score-table kernel
     recomputes its output on the exact pass, which rebuilds K^ from the

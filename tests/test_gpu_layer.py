@@ -165,3 +165,39 @@ def test_llama_layer_decode_matches_restatement(device, tmp_path):
     hidden = f16(xs[0].astype(np.float64) + f16(f16(ctx).reshape(24, 512).astype(np.float64) @ W["o_proj"].T))
     ref = f16(hidden.astype(np.float64) + mlp(hidden))
     assert np.abs(dense[0] - ref.astype(np.float32)).max() <= 2e-2
+
+
+def test_llama_layer_cpu_rotary_module(device, tmp_path):
+    """A rotary module whose buffers live on the CPU is called on the CPU
+    (llama32_adapter.py:535-553 resolves the device from the module) and its
+    tables give the same decode step as the layer's own rope_cos_sin."""
+    from apple_amd.layer import LLAMA3_ROPE_SCALING, Llama32DecoderLayerMLX, rope_cos_sin
+
+    class CpuRotary(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.register_buffer("anchor", torch.zeros(1))
+            self.calls = 0
+
+        def forward(self, hidden, position_ids):
+            assert hidden.device.type == "cpu" and position_ids.device.type == "cpu"
+            self.calls += 1
+            cos, sin = rope_cos_sin(position_ids.reshape(-1), 64, 500000.0, LLAMA3_ROPE_SCALING)
+            return cos[None], sin[None]
+
+    cfg = _ext_config(tmp_path)
+    base = Llama32DecoderLayerMLX(cfg, intermediate_size=256, device=device, quantizer=_ext_quantizer(cfg, device, 8),
+                                  generator=torch.Generator().manual_seed(4))
+    weights = {n: getattr(base, n).detach().clone() for n in Llama32DecoderLayerMLX.WEIGHTS}
+    rot = CpuRotary()
+    other = Llama32DecoderLayerMLX(_ext_config(tmp_path / "b"), intermediate_size=256, device=device,
+                                   quantizer=_ext_quantizer(cfg, device, 8), weights=weights, rotary_module=rot)
+    g = rng(34)
+    prompt = torch.from_numpy(randn16(g, 1, 40, 512)).to(device)
+    x = torch.from_numpy(randn16(g, 1, 1, 512)).to(device)
+    outs = []
+    for layer in (base, other):
+        layer.prefill_cache(prompt)
+        outs.append(H(layer(x, use_cache=True)))
+    assert rot.calls >= 2
+    np.testing.assert_array_equal(outs[0], outs[1])

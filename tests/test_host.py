@@ -478,3 +478,42 @@ def test_reference_active_map_and_segments():
     assert K.ref_attention_ok(128, 8, 256, 4, 4, True) and not K.ref_attention_ok(96, 8, 256, 4, 4, True)
     assert not K.ref_attention_ok(256, 16, 256, 8, 1, False)  # 2 x 128 KB of tables
     assert K.ref_attention_ok(256, 16, 256, 8, 1, True, 16, 256, 4)
+
+
+def test_guard_refuses_k_segments_without_exact_plane():
+    """Under the drift guard the exact pass reads K's corrected coordinates
+    kv_heads * head_stride * k values past each K sparse-value pointer: the
+    host refuses a segment table in which some K segment lacks that plane
+    (codes built without TiledCodes(exact_plane=True) or a direct caller),
+    and accepts the plane both from precomputed addresses and from tensors."""
+    from apple_amd import _lib as L
+    from apple_amd import kernels as K
+    from apple_amd.cache import TiledCodes
+
+    H, cap, k = 2, 64, 4
+    plane = H * cap * k * 2
+    ok = K.SegmentTable(2)
+    for b in range(2):
+        ok.add_codes(b, L.Codes(), L.Codes(), [], cap, 40, 0, cap, k_plane=plane)
+    ok.check_exact_planes(H, k)
+    for bad_plane in (None, plane - 2, 2 * plane):
+        t = K.SegmentTable(2)
+        t.add_codes(0, L.Codes(), L.Codes(), [], cap, 40, 0, cap, k_plane=plane)
+        t.add_codes(1, L.Codes(), L.Codes(), [], cap, 40, 0, cap, k_plane=bad_plane)
+        with pytest.raises(ValueError, match="plane"):
+            t.check_exact_planes(H, k)
+    empty = K.SegmentTable(1)  # a zero-length segment reads nothing
+    empty.add_codes(0, L.Codes(), L.Codes(), [], cap, 0, 0, cap)
+    empty.check_exact_planes(H, k)
+
+    fmt = K.WarmFormat(64, 16, 256, 16, 256, k)
+    for exact in (True, False):
+        tc = TiledCodes(fmt, H, torch.device("cpu"), cap=cap, score_rows=True, exact_plane=exact)
+        assert tc.plane_bytes() == (plane if exact else None)
+        t = K.SegmentTable(1)
+        t.add(0, tc.codes(1), tc.codes(1), tc.cap, 20, 0)
+        if exact:
+            t.check_exact_planes(H, k)
+        else:
+            with pytest.raises(ValueError, match="plane"):
+                t.check_exact_planes(H, k)

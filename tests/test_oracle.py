@@ -620,3 +620,152 @@ def test_cpu_baseline_encode_matches_oracle():
     assert np.array_equal(out["rvq"].numpy(), ref["rvq_codes"])
     assert np.array_equal(out["sparse_idx"].numpy(), ref["sparse_idx"])
     assert np.array_equal(out["sparse_val"].numpy().view(np.uint16), ref["sparse_val"].view(np.uint16))
+
+
+# ---------------------------------------------------------------- timed CPU baselines, decode steps
+
+def _ref_store(g, T, H, pq, rv, thr):
+    """A reference-format warm store [T, H] encoded by the pinned oracle."""
+    x = randn16(g, T * H, pq.shape[0] * pq.shape[2])
+    pq_codes, rvq_codes, mask, offs = nx.hybrid_encode(x, pq, rv, thr)
+    return x, {"pq": pq_codes.reshape(T, H, -1), "rvq": rvq_codes, "mask": mask, "offsets": offs}
+
+
+def check_ref_decode(fn, g) -> bool:
+    """``fn`` (cpu_baseline.ref_decode's signature) equals the pinned
+    ``numerics.hybrid_decode`` bit for bit, active and inactive rows."""
+    import torch
+
+    pq = rand_codebooks(g, 8, 256, 16)
+    rv = _rvq_codebooks(g, 4, 512, 128)
+    ok = True
+    for thr in (0.25, 1.6, float("inf")):  # every row, about half the rows, no row gated
+        _, st = _ref_store(g, 24, 4, pq, rv, thr)
+        n = 24 * 4
+        want = nx.hybrid_decode(st["pq"].reshape(n, -1), st["rvq"], st["mask"], st["offsets"], pq, rv)
+        got = fn(torch.from_numpy(st["pq"].reshape(n, -1)), torch.from_numpy(pq),
+                 torch.from_numpy(st["rvq"].astype(np.int64)), torch.from_numpy(st["offsets"]),
+                 torch.from_numpy(rv)).numpy()
+        ok &= bool(np.array_equal(got.view(np.uint16), want.view(np.uint16)))
+    return ok
+
+
+def check_ref_decode_step(fn, g) -> bool:
+    """``fn`` (cpu_baseline.ref_decode_step's signature) is the textbook
+    float64 softmax attention over [hot | warm] decoded by the pinned oracle,
+    within 1e-3 on the fp16 output (fp32 blockwise recurrence), GQA 4:1."""
+    import torch
+
+    H, Hq, D, T, Th = 2, 8, 128, 40, 9
+    pq = rand_codebooks(g, 8, 256, 16)
+    rv = _rvq_codebooks(g, 4, 256, 128)
+    _, wk = _ref_store(g, T, H, pq, rv, 1.6)
+    _, wv = _ref_store(g, T, H, pq, rv, 1.6)
+    hot_k, hot_v = randn16(g, Th, H, D), randn16(g, Th, H, D)
+    q = randn16(g, 1, Hq, D, scale=2.0)
+    dec = [nx.hybrid_decode(w["pq"].reshape(T * H, -1), w["rvq"], w["mask"], w["offsets"], pq, rv).reshape(T, H, D)
+           for w in (wk, wv)]
+    want = nx.dense_attention_f64(q, np.concatenate([hot_k, dec[0]]), np.concatenate([hot_v, dec[1]]), D ** -0.5)
+    tw = {k: torch.from_numpy(v if k != "rvq" else v.astype(np.int64)) for k, v in wk.items()}
+    tv = {k: torch.from_numpy(v if k != "rvq" else v.astype(np.int64)) for k, v in wv.items()}
+    got = fn(torch.from_numpy(q), torch.from_numpy(hot_k), torch.from_numpy(hot_v), tw, tv,
+             {"pq": torch.from_numpy(pq), "rvq": torch.from_numpy(rv)}, D ** -0.5, 16).numpy()
+    return float(np.abs(got.astype(np.float64) - want).max()) <= 1e-3
+
+
+def check_decode_step(fn, g) -> bool:
+    """``fn`` (cpu_baseline.decode_step's signature) is the textbook float64
+    attention over [warm | hot] with the warm tier decoded by the pinned
+    ``numerics.ext_decode`` (separate K and V codebooks, PQ + RVQ + top-4),
+    within 1e-3 on the fp16 output, GQA 4:1."""
+    import torch
+
+    Hkv, Hq, D, T, Th = 2, 8, 64, 70, 11
+    cbs = {n: rand_codebooks(g, 16, 256, 4) for n in ("k_pq", "k_rvq", "v_pq", "v_rvq")}
+    for n in ("k_rvq", "v_rvq"):
+        cbs[n] = (cbs[n].astype(F32) * 0.35).astype(np.float16)
+    warm, dec = {}, {}
+    for s in ("k", "v"):
+        x = randn16(g, Hkv * T, D)
+        e = nx.ext_encode(x, cbs[s + "_pq"], cbs[s + "_rvq"], 4)
+        dec[s] = nx.ext_decode(e["pq_codes"], cbs[s + "_pq"], e["rvq_codes"], cbs[s + "_rvq"], e["sparse_idx"],
+                               e["sparse_val"]).reshape(Hkv, T, D).transpose(1, 0, 2)
+        warm[s] = {"pq": e["pq_codes"].reshape(Hkv, T, -1), "rvq": e["rvq_codes"].reshape(Hkv, T, -1),
+                   "sparse_idx": e["sparse_idx"].reshape(Hkv, T, -1), "sparse_val": e["sparse_val"].reshape(Hkv, T, -1)}
+    hot_k, hot_v = randn16(g, Hkv, Th, D), randn16(g, Hkv, Th, D)  # [Hkv, T_hot, D] as the bench holds them
+    q = randn16(g, 1, Hq, D, scale=2.0)
+    want = nx.dense_attention_f64(q, np.concatenate([dec["k"], hot_k.transpose(1, 0, 2)]),
+                                  np.concatenate([dec["v"], hot_v.transpose(1, 0, 2)]), 0.125)
+    tw = {s: {k: torch.from_numpy(v) for k, v in warm[s].items()} for s in ("k", "v")}
+    got = fn(torch.from_numpy(q), torch.from_numpy(hot_k), torch.from_numpy(hot_v), tw["k"], tw["v"],
+             {k: torch.from_numpy(v) for k, v in cbs.items()}, 0.125, 32).numpy()
+    return float(np.abs(got.astype(np.float64) - want).max()) <= 1e-3
+
+
+def test_cpu_baseline_decode_steps_pinned():
+    """The three timed decode baselines against the pinned oracle: the
+    reference-format decode bit for bit, both decode steps within fp32
+    rounding of textbook attention over the oracle-decoded window."""
+    from oracle import cpu_baseline as cb
+
+    assert check_ref_decode(cb.ref_decode, rng(31))
+    assert check_ref_decode_step(cb.ref_decode_step, rng(32))
+    assert check_decode_step(cb.decode_step, rng(33))
+
+
+def test_cpu_baseline_planted_mistakes():
+    """Each baseline pin rejects a plausible mistake planted in the baseline."""
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import cpu_baseline as cb
+
+    def ref_decode_shuffled(pq, pq_cb, rvq, offsets, rvq_cb):  # corrections scattered to the wrong rows
+        return cb.ref_decode(pq, pq_cb, rvq, torch.roll(offsets, 1), rvq_cb)
+
+    def ref_decode_f16_sum(pq, pq_cb, rvq, offsets, rvq_cb):  # stage sum rounded to fp16 at every stage
+        base = cb.decode_codes(pq, pq_cb)
+        corr = torch.zeros_like(base)
+        if rvq.shape[0]:
+            tot = torch.zeros((rvq.shape[0], base.shape[1]), dtype=torch.float16)
+            for layer in range(rvq.shape[1]):
+                tot = (tot.float() + F.embedding(rvq[:, layer].long(), rvq_cb[layer]).float()).half()
+            corr[offsets.long()] = tot
+        return (base.float() + corr.float()).half()
+
+    def ref_decode_no_base(pq, pq_cb, rvq, offsets, rvq_cb):  # the correction alone on active rows
+        out = cb.ref_decode(pq, pq_cb, rvq, offsets, rvq_cb)
+        out[offsets.long()] = (out[offsets.long()].float() - cb.decode_codes(pq, pq_cb)[offsets.long()].float()).half()
+        return out
+
+    for bad in (ref_decode_shuffled, ref_decode_f16_sum, ref_decode_no_base):
+        assert not check_ref_decode(bad, rng(31)), bad.__name__
+
+    def swapped_kv(q, hot_k, hot_v, warm_k, warm_v, cbs, scale, block):  # V decoded with K's codebooks
+        return cb.decode_step(q, hot_k, hot_v, warm_k, warm_v,
+                              dict(cbs, v_pq=cbs["k_pq"], v_rvq=cbs["k_rvq"], k_pq=cbs["v_pq"], k_rvq=cbs["v_rvq"]),
+                              scale, block)
+
+    def no_sparse(q, hot_k, hot_v, warm_k, warm_v, cbs, scale, block):  # sparse stage dropped
+        strip = lambda w: {k: v for k, v in w.items() if not k.startswith("sparse")}
+        return cb.decode_step(q, hot_k, hot_v, strip(warm_k), strip(warm_v), cbs, scale, block)
+
+    for bad in (swapped_kv, no_sparse):
+        assert not check_decode_step(bad, rng(33)), bad.__name__
+
+    def ref_step_values_as_keys(q, hot_k, hot_v, warm_k, warm_v, cbs, scale, block):
+        return cb.ref_decode_step(q, hot_k, hot_v, warm_k, warm_k, cbs, scale, block)
+
+    real_attn = cb.blockwise_attention
+
+    def interleaved_gqa(q, keys, values, scale, block):  # kv head h % Hkv instead of h // rep
+        rep = q.shape[1] // keys.shape[1]
+        return real_attn(q, keys.repeat(1, rep, 1), values.repeat(1, rep, 1), scale, block)
+
+    assert not check_ref_decode_step(ref_step_values_as_keys, rng(32))
+    try:
+        cb.blockwise_attention = interleaved_gqa
+        assert not check_ref_decode_step(cb.ref_decode_step, rng(32))
+        assert not check_decode_step(cb.decode_step, rng(33))
+    finally:
+        cb.blockwise_attention = real_attn
