@@ -101,7 +101,8 @@ SIGNATURES = {
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
     "rfsn_mask_compact": (i32, [vp, i64, vp, vp, vp, sz, vp]),
-    "rfsn_rvq_encode_full": (i32, [vp, i64, i32, vp, i64, vp, i32, i32, vp, vp]),
+    "rfsn_rvq_encode_full_workspace_bytes": (sz, [i64, i32, i32, i32]),
+    "rfsn_rvq_encode_full": (i32, [vp, i64, i32, vp, i64, vp, i32, i32, vp, vp, sz, vp]),
     "rfsn_decode": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, i64, i32, vp]),
     "rfsn_sparse_fold": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, vp]),
     "rfsn_sparse_delta": (i32, [C.POINTER(Format), C.POINTER(Codes), i64, vp, vp, vp, vp]),
@@ -147,7 +148,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 4:
+    if lib.rfsn_abi_version() != 5:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

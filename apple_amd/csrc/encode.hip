@@ -272,7 +272,7 @@ sparse_topk_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx
 }
 
 // ---------------------------------------------------------------------------
-// Nearest-centroid search on MFMA (subspace dims d = 4 and d = 8).
+// Nearest-centroid search on MFMA (subspace dims d = 4, 8 and 16).
 //
 // Half the squared distance is one MFMA dot product of augmented operands:
 //   centroid row  [ c_j (d) | rh_j  rl_j  1  1 | 0 ... ]   (A, 32 centroids)
@@ -320,8 +320,12 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
                       const uint16_t* __restrict__ cb, int M, int C, int64_t cb_gstride,
                       uint8_t* __restrict__ codes, int64_t ldc, int64_t codes_gstride,
                       uint16_t* __restrict__ resid, int64_t ldr, int64_t resid_gstride) {
-  constexpr int K = DS == 4 ? 8 : 16;  // MFMA depth: 32x32x8 (d = 4) or 32x32x16 (d = 8)
-  constexpr int KH = K / 2;            // operand halves per lane
+  // row depth: 32x32x8 (d = 4), one 32x32x16 (d = 8) or two (d = 16: the
+  // coordinates, then the augmented group)
+  constexpr int K = DS == 4 ? 8 : (DS == 8 ? 16 : 32);
+  constexpr int KH = DS == 16 ? 8 : K / 2;  // operand halves per lane and MFMA
+  constexpr int NSTEP = DS == 16 ? 2 : 1;
+  constexpr int AUG = DS == 16 ? 16 : KH;   // first element of the augmented group
   __shared__ __align__(16) _Float16 tab[256 * K];  // augmented centroid rows
   __shared__ float Rs[256];                        // canonical R_j
   __shared__ uint32_t rmax_s[kMfmaThreads / 64];
@@ -356,10 +360,10 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       const float half_r = 0.5f * R;
       const _Float16 rh = (_Float16)half_r;
       const _Float16 rl = (_Float16)(half_r - (float)rh);
-      row[KH] = rh;
-      row[KH + 1] = rl;
-      row[KH + 2] = (_Float16)1.0f;
-      row[KH + 3] = (_Float16)1.0f;
+      row[AUG] = rh;
+      row[AUG + 1] = rl;
+      row[AUG + 2] = (_Float16)1.0f;
+      row[AUG + 3] = (_Float16)1.0f;
       Rs[j] = R;
       rmax_t = max(rmax_t, __builtin_bit_cast(uint32_t, R) & 0x7FFFFFFFu);
     }
@@ -393,17 +397,29 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
   const float half_l = 0.5f * L;
   const _Float16 lh = (_Float16)half_l;
   const _Float16 ll = (_Float16)(half_l - (float)lh);
-  _Float16 bop[KH];
+  // B of MFMA step st: lane (col, hi) holds k = 16 st + KH hi .. + KH - 1
+  _Float16 bop[NSTEP][KH];
 #pragma unroll
-  for (int u = 0; u < KH; ++u) bop[u] = (_Float16)0.0f;
-  if (hi == 0) {
+  for (int st = 0; st < NSTEP; ++st)
 #pragma unroll
-    for (int u = 0; u < DS; ++u) bop[u] = (_Float16)(-(float)xs[u]);
+    for (int u = 0; u < KH; ++u) bop[st][u] = (_Float16)0.0f;
+  if constexpr (DS == 16) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) bop[0][u] = (_Float16)(-(float)xs[8 * hi + u]);
+    if (hi == 0) {
+      bop[1][0] = (_Float16)1.0f;
+      bop[1][1] = (_Float16)1.0f;
+      bop[1][2] = lh;
+      bop[1][3] = ll;
+    }
+  } else if (hi == 0) {
+#pragma unroll
+    for (int u = 0; u < DS; ++u) bop[0][u] = (_Float16)(-(float)xs[u]);
   } else {
-    bop[0] = (_Float16)1.0f;
-    bop[1] = (_Float16)1.0f;
-    bop[2] = lh;
-    bop[3] = ll;
+    bop[0][0] = (_Float16)1.0f;
+    bop[0][1] = (_Float16)1.0f;
+    bop[0][2] = lh;
+    bop[0][3] = ll;
   }
 
   // residual rows take one DS*2-byte store when the output is aligned for it
@@ -422,17 +438,20 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         a[u] = arow[u];
-        b[u] = bop[u];
+        b[u] = bop[0][u];
       }
       acc = __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, acc, 0, 0, 0);
     } else {
-      mh8 a, b;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        a[u] = arow[u];
-        b[u] = bop[u];
+      for (int st = 0; st < NSTEP; ++st) {
+        mh8 a, b;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          a[u] = arow[16 * st + u];
+          b[u] = bop[st][u];
+        }
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
       }
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -465,7 +484,9 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
     top3_insert(m1, m2, m3, o3);
   }
   const float v1 = key_value(m1), v2 = key_value(m2), v3 = key_value(m3);
-  const float E = 0x1p-17f * (L + rmax) + 0x1p-22f;
+  // (d + 6) 2^-23 (L + R) covers the accumulation, split and canonical errors;
+  // E keeps at least a 4x margin over it (d = 16: 2^-16)
+  const float E = (DS == 16 ? 0x1p-16f : 0x1p-17f) * (L + rmax) + 0x1p-22f;
   const bool unique = v2 - v1 > 2.0f * E + 0x1p-14f * (fabsf(v1) + fabsf(v2));
   const bool pair = v3 - v1 > 2.0f * E + 0x1p-14f * (fabsf(v1) + fabsf(v3));
   const bool safe = rmax < 120000.0f;  // R / 2 representable in fp16 for every centroid
@@ -507,8 +528,11 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       if constexpr (DS == 4) {
         *reinterpret_cast<uint2*>(rv) = make_uint2(r[0] | ((uint32_t)r[1] << 16), r[2] | ((uint32_t)r[3] << 16));
       } else {
-        *reinterpret_cast<uint4*>(rv) = make_uint4(r[0] | ((uint32_t)r[1] << 16), r[2] | ((uint32_t)r[3] << 16),
-                                                   r[4] | ((uint32_t)r[5] << 16), r[6] | ((uint32_t)r[7] << 16));
+#pragma unroll
+        for (int h = 0; h < DS / 8; ++h)
+          reinterpret_cast<uint4*>(rv)[h] =
+              make_uint4(r[8 * h] | ((uint32_t)r[8 * h + 1] << 16), r[8 * h + 2] | ((uint32_t)r[8 * h + 3] << 16),
+                         r[8 * h + 4] | ((uint32_t)r[8 * h + 5] << 16), r[8 * h + 6] | ((uint32_t)r[8 * h + 7] << 16));
       }
     } else {
 #pragma unroll
@@ -1055,6 +1079,531 @@ __global__ void __launch_bounds__(kFeThreads, 1) warm_encode_fused_kernel(const 
   }
 }
 
+// ---------------------------------------------------------------- reference-mode RVQ on MFMA
+// ResidualVQMLX.encode (quantization.py:206-252) over the gated rows, for
+// head_dim D in {64, 128, 256} and 3 <= C <= 16384 centroids per stage.  One
+// launch runs every stage; a row's running residual stays in a float32
+// workspace [A][D] between stages (stage 0 reads the fp16 PQ residual).
+//
+// Screening: a block (4 waves) holds 4 * kRvqSets * 16 rows; each wave holds
+// kRvqSets B operands of 16 rows as -fp16(x) (v_mfma_f32_16x16x32_f16: lane l
+// has row l % 16, coordinates 32 ks + 8 (l / 16) + e).  The stage's codebook
+// streams through LDS in chunks of 64 centroid rows (16-byte groups XOR-
+// swizzled by the row, so the 16 rows of an A operand hit distinct banks),
+// double-buffered, with R_j / 2 beside them.  Each A operand feeds kRvqSets
+// MFMAs, whose accumulators start at R_j / 2: accumulator i of lane l holds
+//   z = R_j / 2 - x . c_j   (j = 16 T + 4 (l / 16) + i of tile T, row l % 16),
+// i.e. (dist_j - L) / 2 up to the screening error.  A key is z with its low
+// F = ceil(log2 C) bits replaced by the lane's local centroid order; keys
+// compare as floats (denormals are preserved), and each lane keeps its four
+// smallest (v_med3_f32 / v_min_f32), merged over the row's four lanes.
+//
+// Certificate (every j): |z_j - (dist_j - L) / 2| <= E with
+//   E = split + mfma + canon,
+//   split = |x - fp16(x)| Cn                  (x rounded to fp16 for the B
+//           operand; 0 at stage 0, where x is the fp16 residual itself),
+//   mfma  = (D + 2) 2^-24 (|x| Cn + Rmax / 2) (fp32 accumulation of exact
+//           fp16 products),
+//   canon = 2^-21 (L + Rmax)                  (the canonical chain's roundings),
+// Cn = sqrt(Rmax) bounding every |c_j|, plus the keys' truncation t.  With
+// v1 <= .. <= v4 the four smallest keys: v2 - v1 > 2E + t proves the first
+// key's centroid is the canonical first-min; v(k+1) - v1 > 2E + t (k = 2, 3)
+// proves it is one of the first k, which are rescored with the float64 chain
+// (ties to the lower index), the wave's rescoring sums spread over its lanes;
+// anything else, non-finite values or |x| beyond fp16 take the canonical
+// float64 scan over all C, spread over the wave.
+constexpr int kRvqWaves = 4;
+constexpr int kRvqThreads = kRvqWaves * 64;
+constexpr int kRvqChunk = 64;          // centroid rows per LDS chunk
+constexpr float kRvqPadHalfR = 1.0e38f;  // R / 2 of rows past the codebook: never a minimum
+
+template <int D>
+struct RvqShape {
+  static constexpr int KS = D / 32;               // 16x16x32 k-steps
+  static constexpr int G16 = D / 8;               // 16-byte groups of a row
+  static constexpr int RB = D * 2;                // row bytes
+  static constexpr int SETS = D <= 128 ? 4 : 2;   // B operands per wave
+  static constexpr int VECS = kRvqWaves * SETS * 16;
+};
+
+typedef _Float16 rh8 __attribute__((ext_vector_type(8)));
+typedef float rf4 __attribute__((ext_vector_type(4)));
+
+// canonical R_j = fl32(S c_j * c_j) per (stage, centroid) into r[L][Cp]
+// (rows past C: +inf): one thread per row, the row in 16-byte loads
+template <int D>
+__global__ void __launch_bounds__(256) rvq_norms_kernel(const uint16_t* __restrict__ cb, int C, int Cp,
+                                                        float* __restrict__ r) {
+  const int layer = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= Cp) return;
+  float R = __builtin_inff();
+  if (j < C) {
+    const uint4* row = reinterpret_cast<const uint4*>(cb + ((size_t)layer * C + j) * D);
+    uint4 w[D / 8];
+#pragma unroll
+    for (int q = 0; q < D / 8; ++q) w[q] = row[q];
+    double acc = 0.0;
+#pragma unroll
+    for (int q = 0; q < D / 8; ++q) {
+      const uint32_t pw[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double c = (double)h2f((uint16_t)(pw[e >> 1] >> (16 * (e & 1))));
+        acc = __builtin_fma(c, c, acc);
+      }
+    }
+    R = (float)acc;
+  }
+  r[(size_t)layer * Cp + j] = R;
+}
+
+// the stage's largest R over its C rows (+inf when some R is not finite): one block per stage
+__global__ void __launch_bounds__(256) rvq_rmax_kernel(const float* __restrict__ r, int C, int Cp,
+                                                       float* __restrict__ rmax) {
+  __shared__ float red[256];
+  const int layer = blockIdx.x;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < C; j += 256) {
+    const float R = r[(size_t)layer * Cp + j];
+    mx = R <= 3.0e38f ? fmaxf(mx, R) : __builtin_inff();  // NaN or inf: the stage is unsafe
+  }
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) rmax[layer] = red[0];
+}
+
+// insert float key k into the sorted m1 <= m2 <= m3 <= m4 (as floats): each new
+// entry is the median of its old value, the one below it and k
+__device__ __forceinline__ void fkey_insert4(float& m1, float& m2, float& m3, float& m4, float k) {
+  asm("v_med3_f32 %3, %2, %3, %4\n\t"
+      "v_med3_f32 %2, %1, %2, %4\n\t"
+      "v_med3_f32 %1, %0, %1, %4\n\t"
+      "v_min_f32_e32 %0, %0, %4"
+      : "+v"(m1), "+v"(m2), "+v"(m3), "+v"(m4)
+      : "v"(k));
+}
+
+template <int D>
+__global__ void __launch_bounds__(kRvqThreads) __attribute__((amdgpu_waves_per_eu(2)))
+rvq_mfma_kernel(const uint16_t* __restrict__ resid, int64_t ld, const int32_t* __restrict__ offsets,
+                int64_t active, const uint16_t* __restrict__ cb, int L, int C, int Cp, int F,
+                const float* __restrict__ rr, const float* __restrict__ rmax_all, float* __restrict__ run,
+                uint16_t* __restrict__ codes) {
+  using S = RvqShape<D>;
+  constexpr int KS = S::KS, G16 = S::G16, RB = S::RB, SETS = S::SETS;
+  __shared__ __align__(16) uint8_t tab[2][kRvqChunk * RB];
+  __shared__ __align__(16) float rs[2][kRvqChunk];
+  __shared__ float xsc[kRvqWaves][D];  // one row's coordinates for the wave's float64 scans
+  __shared__ int pitem[kRvqWaves][SETS * 16][3];     // rows to rescore: their candidates
+  __shared__ int pslot[kRvqWaves][SETS * 16];        // item -> row (16 s + vi)
+  __shared__ double pres[kRvqWaves][SETS * 16][4];   // L, then X of each candidate
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int vi = lane & 15, g = lane >> 4;
+  const int64_t v0 = (int64_t)blockIdx.x * S::VECS + wave * (SETS * 16);
+  int64_t vid[SETS];
+  bool live[SETS];
+#pragma unroll
+  for (int s = 0; s < SETS; ++s) {
+    vid[s] = v0 + 16 * s + vi;
+    live[s] = vid[s] < active;
+  }
+  const int fmask = (1 << F) - 1;
+  const int keep = ~fmask;  // key bits kept from z (in a VGPR: the key build's other operand is an SGPR)
+  int keepv;
+  asm("v_mov_b32 %0, %1" : "=v"(keepv) : "s"(keep));
+
+  // the row's coordinate u at the current stage: the fp16 PQ residual at stage 0, then the workspace
+  auto x_at = [&](int64_t v, int layer, int u) -> float {
+    return layer == 0 ? h2f(resid[(int64_t)offsets[v] * ld + u]) : run[v * D + u];
+  };
+  // coordinates 8 q .. 8 q + 7 of row v
+  auto load_row8 = [&](int64_t v, int layer, int q, float (&x)[8]) {
+    const int k0 = 8 * q;
+    if (layer == 0) {
+      const uint4 h = *reinterpret_cast<const uint4*>(resid + (int64_t)offsets[v] * ld + k0);
+      const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>(run + v * D + k0);
+      const float4 b = *reinterpret_cast<const float4*>(run + v * D + k0 + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+  };
+  // the lane's 8 coordinates 32 ks + 8 g .. + 7 of row v
+  auto load8 = [&](int64_t v, int layer, int ks, float (&x)[8]) {
+    const int k0 = 32 * ks + 8 * g;
+    if (layer == 0) {
+      const uint4 h = *reinterpret_cast<const uint4*>(resid + (int64_t)offsets[v] * ld + k0);
+      const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>(run + v * D + k0);
+      const float4 b = *reinterpret_cast<const float4*>(run + v * D + k0 + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+  };
+
+  rh8 b[SETS][KS];
+  float lsq[SETS], esq[SETS];  // |x|^2 and |x - fp16(x)|^2 (the lane's share, then the row's)
+  bool fin[SETS];
+  // the B operand -fp16(x) of 8 coordinates, with their shares of |x|^2 and of the rounding error
+  auto to_b = [](const float (&x)[8], rh8& bo, float& l2, float& e2, bool& ok) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 h = (_Float16)x[e];
+      bo[e] = -h;
+      const float d = x[e] - (float)h;  // exact in float32
+      l2 = __builtin_fmaf(x[e], x[e], l2);
+      e2 = __builtin_fmaf(d, d, e2);
+      ok = ok && fabsf(x[e]) <= 65504.0f;
+    }
+  };
+  // B operands and the screening L of each row at stage 0
+#pragma unroll
+  for (int s = 0; s < SETS; ++s) {
+    float l2 = 0.0f, e2 = 0.0f;
+    bool ok = true;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (live[s]) load8(vid[s], 0, ks, x);
+      to_b(x, b[s][ks], l2, e2, ok);
+    }
+    lsq[s] = l2;
+    esq[s] = e2;
+    fin[s] = ok;
+  }
+  auto quad_sum = [&](float v) {  // sum over the row's four lanes l, l ^ 16, l ^ 32, l ^ 48
+    v += __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(int, v)));
+    return v + __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(int, v), 4 * (lane ^ 32)));
+  };
+  auto quad_all = [&](bool p) {
+    int v = p ? 1 : 0;
+    v &= lane_xor16(v);
+    return (v & lane_xor32(v, 4 * (lane ^ 32))) != 0;
+  };
+
+  const int nchunks = Cp / kRvqChunk;
+  constexpr int kLoads = kRvqChunk * G16 / kRvqThreads;  // 16-byte staging loads per thread and chunk
+  static_assert(kRvqChunk * G16 % kRvqThreads == 0, "staging loads per thread");
+
+  for (int layer = 0; layer < L; ++layer) {
+    const uint16_t* cbl = cb + (size_t)layer * C * D;
+    const float* rl = rr + (size_t)layer * Cp;
+    const float rmax = rmax_all[layer];
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+      lsq[s] = quad_sum(lsq[s]);
+      esq[s] = quad_sum(esq[s]);
+      fin[s] = quad_all(fin[s]);
+    }
+    // ---- staging of chunk c into buffer c & 1: loads, then stores
+    uint4 stg[kLoads];
+    float rstg = 0.0f;
+    auto stage_load = [&](int c) {
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const int q = tid + kRvqThreads * it;
+        const int row = q / G16, grp = q % G16;
+        const int j = c * kRvqChunk + row;
+        stg[it] = j < C ? *reinterpret_cast<const uint4*>(cbl + (size_t)j * D + 8 * grp) : make_uint4(0u, 0u, 0u, 0u);
+      }
+      if (tid < kRvqChunk) {
+        const int j = c * kRvqChunk + tid;
+        rstg = j < C ? 0.5f * rl[j] : kRvqPadHalfR;
+      }
+    };
+    auto stage_store = [&](int c) {
+      uint8_t* tb = tab[c & 1];
+#pragma unroll
+      for (int it = 0; it < kLoads; ++it) {
+        const int q = tid + kRvqThreads * it;
+        const int row = q / G16, grp = q % G16;
+        *reinterpret_cast<uint4*>(tb + row * RB + 16 * (grp ^ (row & (G16 - 1)))) = stg[it];
+      }
+      if (tid < kRvqChunk) rs[c & 1][tid] = rstg;
+    };
+    __syncthreads();  // the previous stage's last chunk is no longer read
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+
+    float m1[SETS], m2[SETS], m3[SETS], m4[SETS];
+    const float nokey = __builtin_inff();
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) m1[s] = m2[s] = m3[s] = m4[s] = nokey;
+#pragma unroll 1
+    for (int c = 0; c < nchunks; ++c) {
+      if (c + 1 < nchunks) stage_load(c + 1);
+      const uint8_t* tb = tab[c & 1];
+#pragma unroll
+      for (int tile = 0; tile < kRvqChunk / 16; ++tile) {
+        const int row = tile * 16 + vi;
+        const uint8_t* trow = tb + row * RB;
+        rh8 a[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          a[ks] = *reinterpret_cast<const rh8*>(trow + 16 * ((4 * ks + g) ^ (row & (G16 - 1))));
+        const rf4 rinit = *reinterpret_cast<const rf4*>(&rs[c & 1][tile * 16 + 4 * g]);
+        const int base = 4 * (c * (kRvqChunk / 16) + tile);  // local order 4 T + i
+#pragma unroll
+        for (int s = 0; s < SETS; ++s) {
+          rf4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], b[s][0], rinit, 0, 0, 0);
+#pragma unroll
+          for (int ks = 1; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ks], b[s][ks], acc, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float z = acc[i];  // through a scalar: a bit_cast of the vector element reads element 0
+            // one v_and_or_b32 with the order in an SGPR (readfirstlane keeps the
+            // compiler from splitting it into an and plus an or3 of base | i);
+            // built in C++ so that the compiler sees, and pads, the read of the
+            // MFMA result
+            const int idx = __builtin_amdgcn_readfirstlane(base + i);
+            const float key = __builtin_bit_cast(float, (__builtin_bit_cast(int, z) & keepv) | idx);
+            fkey_insert4(m1[s], m2[s], m3[s], m4[s], key);
+          }
+        }
+      }
+      if (c + 1 < nchunks) stage_store(c + 1);
+      __syncthreads();
+    }
+
+    // ---- merge the row's four lanes: local order 4 T + i -> centroid 16 T + 4 g + i
+    const int gq = 4 * g;
+    auto widen = [&](float k) {
+      const int b = __builtin_bit_cast(int, k);
+      const int li = b & fmask;
+      return __builtin_bit_cast(float, (b & ~fmask) | ((li & ~3) << 2) | gq | (li & 3));
+    };
+    const float Cn = sqrtf(rmax) * 1.0001f;
+    int code[SETS];
+    int how[SETS];  // 0 unique, 1 rescore the first two, 2 full scan
+    int pa[SETS], pb[SETS], pc[SETS];  // the rescored candidates, ascending (pc = pb for two)
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+      float p[4] = {widen(m1[s]), widen(m2[s]), widen(m3[s]), widen(m4[s])};
+      auto merge_from = [&](auto&& other) {
+        float o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = __builtin_bit_cast(float, other(__builtin_bit_cast(int, p[k])));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) fkey_insert4(p[0], p[1], p[2], p[3], o[k]);
+      };
+      merge_from([](int v) { return lane_xor16(v); });
+      const int x32 = 4 * (lane ^ 32);
+      merge_from([&](int v) { return lane_xor32(v, x32); });
+      const float xn = sqrtf(lsq[s]) * 1.0001f;
+      const float split = sqrtf(esq[s]) * 1.0001f * Cn;  // |(x - fp16(x)) . c_j| <= |x - fp16(x)| Cn
+      const float mf = (float)(D + 2) * 0x1p-24f * (xn * Cn + 0.5f * rmax);
+      const float canon = 0x1p-21f * (lsq[s] + rmax);
+      const float E = 1.25f * (split + mf + canon) + 0x1p-100f;
+      const float tq = __builtin_bit_cast(float, (127 + F - 22) << 23);  // 2^(F - 22)
+      const bool safe = fin[s] && lsq[s] <= 1.0e30f && rmax <= 1.0e30f && C >= 3;
+      // candidates: the keys within 2E + t of the first; 1 -> settled, 2 or 3 ->
+      // rescored with the canonical chain, 4 (or unsafe values) -> the full scan
+      auto apart = [&](float a, float b) { return b - a > 2.0f * E + tq * (fabsf(a) + fabsf(b)); };
+      const int ncand = apart(p[0], p[1]) ? 1 : apart(p[0], p[2]) ? 2 : apart(p[0], p[3]) ? 3 : 4;
+      how[s] = !safe || ncand == 4 ? 2 : (ncand == 1 ? 0 : 1);
+      code[s] = __builtin_bit_cast(int, p[0]) & fmask;
+      // the rescored candidates in ascending index order (the third repeats the second for a pair)
+      int j0 = code[s], j1 = __builtin_bit_cast(int, p[1]) & fmask, j2 = __builtin_bit_cast(int, p[2]) & fmask;
+      if (ncand < 3) j2 = j1;
+      const int lo = min(j0, min(j1, j2)), hi = max(j0, max(j1, j2));
+      pa[s] = lo;
+      pb[s] = j0 + j1 + j2 - lo - hi;
+      pc[s] = hi;
+      if (!live[s]) how[s] = 0;
+    }
+    // ---- rows whose first two candidates need the canonical chain: three
+    // float64 sums in coordinate order each (L, X_a, X_b), spread over the
+    // wave's lanes as independent units, then each row picks its code
+    {
+      int nitems = 0;
+      int myitem[SETS];
+#pragma unroll
+      for (int s = 0; s < SETS; ++s) {
+        const uint64_t want = __builtin_amdgcn_ballot_w64(g == 0 && how[s] == 1);
+        // every lane of row vi takes the row's rank among the set's wanting rows
+        const int rank = __builtin_popcountll(want & ((1ull << vi) - 1));
+        myitem[s] = ((want >> vi) & 1) ? nitems + rank : -1;
+        if (g == 0 && myitem[s] >= 0) {
+          pitem[wave][myitem[s]][0] = pa[s];
+          pitem[wave][myitem[s]][1] = pb[s];
+          pitem[wave][myitem[s]][2] = pc[s];
+          pslot[wave][myitem[s]] = 16 * s + vi;
+        }
+        nitems += __builtin_popcountll(want);
+      }
+      if (nitems) {  // uniform
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int u = lane; u < 4 * nitems; u += 64) {
+          const int it = u >> 2, comp = u & 3;
+          const int slot = pslot[wave][it];
+          const int64_t v = v0 + slot;
+          const uint4* crow = reinterpret_cast<const uint4*>(cbl + (size_t)pitem[wave][it][comp == 0 ? 0 : comp - 1] * D);
+          double acc = 0.0;
+#pragma unroll 4
+          for (int q = 0; q < D / 8; ++q) {
+            float x8[8];
+            load_row8(v, layer, q, x8);
+            const uint4 w = crow[q];  // unused for L
+            const uint32_t pw[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const double xu = (double)x8[e];
+              const double y = comp == 0 ? xu : (double)h2f((uint16_t)(pw[e >> 1] >> (16 * (e & 1))));
+              acc = __builtin_fma(xu, y, acc);
+            }
+          }
+          pres[wave][it][comp] = acc;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int s = 0; s < SETS; ++s) {
+          if (myitem[s] >= 0) {
+            const int it = myitem[s];
+            const float Lc = (float)pres[wave][it][0];
+            const float da = __fadd_rn(__fsub_rn(Lc, 2.0f * (float)pres[wave][it][1]), rl[pa[s]]);
+            const float db = __fadd_rn(__fsub_rn(Lc, 2.0f * (float)pres[wave][it][2]), rl[pb[s]]);
+            const float dc = __fadd_rn(__fsub_rn(Lc, 2.0f * (float)pres[wave][it][3]), rl[pc[s]]);
+            // first min in ascending index order: ties keep the lower index
+            int best = pa[s];
+            float bd = da;
+            if (db < bd) { bd = db; best = pb[s]; }
+            if (dc < bd) best = pc[s];
+            code[s] = best;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // the item tables are rewritten at the next stage
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+    // ---- rows left uncertain: the canonical scan over all C, one row at a time
+    // across the wave (lane j scans centroids j, j + 64, ...)
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+      uint64_t todo = __builtin_amdgcn_ballot_w64(g == 0 && live[s] && how[s] == 2);
+      while (todo) {  // uniform
+        const int r0 = __builtin_ctzll(todo);
+        todo &= todo - 1;
+        const int64_t v = v0 + 16 * s + r0;
+        for (int u = lane; u < D; u += 64) xsc[wave][u] = x_at(v, layer, u);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        double lacc = 0.0;
+        for (int u = 0; u < D; ++u) {
+          const double xu = (double)xsc[wave][u];
+          lacc = __builtin_fma(xu, xu, lacc);
+        }
+        const float Lc = (float)lacc;
+        float best = __builtin_inff();
+        int bi = 0x7fffffff;
+        for (int j = lane; j < C; j += 64) {
+          const uint4* cj = reinterpret_cast<const uint4*>(cbl + (size_t)j * D);
+          double xacc = 0.0;
+#pragma unroll 4
+          for (int q = 0; q < D / 8; ++q) {  // the row's loads issued together
+            const uint4 w = cj[q];
+            const uint32_t pw[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              xacc = __builtin_fma((double)xsc[wave][8 * q + e], (double)h2f((uint16_t)(pw[e >> 1] >> (16 * (e & 1)))),
+                                   xacc);
+          }
+          const float dist = __fadd_rn(__fsub_rn(Lc, 2.0f * (float)xacc), rl[j]);
+          if (dist < best) {  // ascending j per lane: first min kept
+            best = dist;
+            bi = j;
+          }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float ob = __shfl_xor(best, o, 64);
+          const int oi = __shfl_xor(bi, o, 64);
+          if (ob < best || (ob == best && oi < bi)) {
+            best = ob;
+            bi = oi;
+          }
+        }
+        if (bi == 0x7fffffff) bi = 0;  // no finite distance: index 0, as the reference's merge leaves it
+        if (vi == r0) code[s] = bi;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // xsc is rewritten by the next row
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+    // ---- codes, then the next stage's running residual fl32(run - c) and B operands
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+      if (live[s] && g == 0) codes[vid[s] * L + layer] = (uint16_t)code[s];
+      if (layer + 1 == L) continue;
+      const uint16_t* crow = cbl + (size_t)code[s] * D;
+      float l2 = 0.0f, e2 = 0.0f;
+      bool ok = true;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int k0 = 32 * ks + 8 * g;
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live[s]) {
+          load8(vid[s], layer, ks, x);
+          const uint4 cw = *reinterpret_cast<const uint4*>(crow + k0);
+          const uint32_t w[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = __fsub_rn(x[e], h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1)))));
+          *reinterpret_cast<float4*>(run + vid[s] * D + k0) = make_float4(x[0], x[1], x[2], x[3]);
+          *reinterpret_cast<float4*>(run + vid[s] * D + k0 + 4) = make_float4(x[4], x[5], x[6], x[7]);
+        }
+        to_b(x, b[s][ks], l2, e2, ok);
+      }
+      lsq[s] = l2;
+      esq[s] = e2;
+      fin[s] = ok;
+    }
+  }
+}
+
+size_t rvq_mfma_ws_bytes(int64_t active, int D, int L, int C) {
+  const int64_t Cp = (C + kRvqChunk - 1) / kRvqChunk * kRvqChunk;
+  const auto up = [](int64_t n) { return (size_t)((n + 255) / 256 * 256); };
+  return up(4 * L * Cp) + up(4 * L) + up(4 * (active > 0 ? active : 1) * D);
+}
+
+bool rvq_mfma_ok(int D, int C) { return (D == 64 || D == 128 || D == 256) && C >= 3 && C <= 16384; }
+
+template <int D>
+int launch_rvq_mfma(const void* resid, int64_t ld, const int32_t* offsets, int64_t active, const void* cb, int L,
+                    int C, uint16_t* codes, void* ws, hipStream_t s) {
+  const int Cp = (C + kRvqChunk - 1) / kRvqChunk * kRvqChunk;
+  int F = 0;
+  while ((1 << F) < Cp) ++F;
+  const auto up = [](int64_t n) { return (size_t)((n + 255) / 256 * 256); };
+  float* r = (float*)ws;
+  float* rmax = (float*)((uint8_t*)ws + up(4 * L * (int64_t)Cp));
+  float* run = (float*)((uint8_t*)rmax + up(4 * L));
+  hipLaunchKernelGGL(rvq_norms_kernel<D>, dim3((unsigned)ceil_div(Cp, 256), (unsigned)L), dim3(256), 0, s,
+                     (const uint16_t*)cb, C, Cp, r);
+  hipLaunchKernelGGL(rvq_rmax_kernel, dim3(L), dim3(256), 0, s, (const float*)r, C, Cp, rmax);
+  const int64_t blocks = ceil_div(active, (int64_t)RvqShape<D>::VECS);
+  hipLaunchKernelGGL(rvq_mfma_kernel<D>, dim3((unsigned)blocks), dim3(kRvqThreads), 0, s, (const uint16_t*)resid, ld,
+                     offsets, active, (const uint16_t*)cb, L, C, Cp, F, (const float*)r, (const float*)rmax, run, codes);
+  return check_launch("rvq_encode_full");
+}
+
 // The fused encode serves head_dim 64, 4- or 8-dim subspaces, an RVQ stage of
 // the same split or none, k in {0, 4}, and aligned rows (16-byte x rows,
 // code and sparse rows at their natural alignment).
@@ -1122,7 +1671,7 @@ int pq_encode_impl(const void* x, int64_t n, int D, int64_t ldx, int64_t xg, con
   switch (d) {
     case 4: return launch_pq_mfma<4>(x, n, ldx, xg, cb, M, C, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
     case 8: return launch_pq_mfma<8>(x, n, ldx, xg, cb, M, C, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
-    case 16: return launch_pq<16>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
+    case 16: return launch_pq_mfma<16>(x, n, ldx, xg, cb, M, C, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
     default: return launch_pq<0>(x, n, ldx, xg, cb, M, C, d, cbg, codes, ldc, cg, resid, ldr, rg, groups, s);
   }
 }
@@ -1300,11 +1849,31 @@ extern "C" int rfsn_mask_compact(const uint8_t* mask, int64_t n, int32_t* offset
   return check_launch("mask_compact");
 }
 
+extern "C" size_t rfsn_rvq_encode_full_workspace_bytes(int64_t active, int32_t D, int32_t L, int32_t C) {
+  if (active < 0 || D <= 0 || L <= 0 || C <= 0) return 0;
+  return rvq_mfma_ok(D, C) ? rvq_mfma_ws_bytes(active, D, L, C) : 0;
+}
+
 extern "C" int rfsn_rvq_encode_full(const void* resid, int64_t ld, int32_t D, const int32_t* offsets, int64_t active,
-                                    const void* cb, int32_t L, int32_t C, uint16_t* codes, void* stream) {
+                                    const void* cb, int32_t L, int32_t C, uint16_t* codes, void* ws, size_t ws_bytes,
+                                    void* stream) {
   RFSN_REQUIRE(resid && offsets && cb && codes, "rvq_encode_full: null pointer");
   RFSN_REQUIRE(D > 0 && D <= 1024 && ld >= D && L >= 1 && C >= 1 && C <= 65535, "rvq_encode_full: bad shape");
+  RFSN_REQUIRE(active >= 0, "rvq_encode_full: negative row count");
   if (active == 0) return RFSN_OK;
+  if (rvq_mfma_ok(D, C)) {
+    RFSN_REQUIRE(ws != nullptr && ws_bytes >= rvq_mfma_ws_bytes(active, D, L, C),
+                 "rvq_encode_full: workspace too small (rfsn_rvq_encode_full_workspace_bytes)");
+    RFSN_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 16 == 0 && reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(cb) % 16 == 0 && ld % 8 == 0,
+                 "rvq_encode_full: residual rows, codebooks and workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    switch (D) {
+      case 64: return launch_rvq_mfma<64>(resid, ld, offsets, active, cb, L, C, codes, ws, s);
+      case 128: return launch_rvq_mfma<128>(resid, ld, offsets, active, cb, L, C, codes, ws, s);
+      default: return launch_rvq_mfma<256>(resid, ld, offsets, active, cb, L, C, codes, ws, s);
+    }
+  }
   const int waves = 4;
   const size_t lds = (size_t)waves * D * sizeof(double);
   hipLaunchKernelGGL(rvq_full_kernel, dim3((unsigned)ceil_div(active, waves)), dim3(64 * waves), lds,

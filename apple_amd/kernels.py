@@ -175,6 +175,8 @@ def rvq_encode_full(resid: torch.Tensor, codebooks: torch.Tensor, threshold: flo
     """Gated full-dimension RVQ (quantization.py:206-252) -> (codes u16 [A, L], mask [N], offsets [A])."""
     _dev(resid, "rvq_encode_full")
     resid = _contig(resid)
+    if resid.data_ptr() % 16:
+        resid = resid.clone()  # the MFMA search loads 16-byte groups of a row
     n, D = resid.shape
     Ls, Cn, Dc = codebooks.shape
     if D != Dc:
@@ -192,8 +194,13 @@ def rvq_encode_full(resid: torch.Tensor, codebooks: torch.Tensor, threshold: flo
     offsets = offsets_all[:a].clone()
     codes = torch.empty((a, Ls), dtype=torch.uint16, device=dev)
     if a:
-        L.call("rfsn_rvq_encode_full", resid.data_ptr(), D, D, offsets.data_ptr(), a, _contig(codebooks).data_ptr(),
-               Ls, Cn, codes.data_ptr(), s)
+        wsb = L.load().rfsn_rvq_encode_full_workspace_bytes(a, D, Ls, Cn)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        cb = _contig(codebooks)
+        if cb.data_ptr() % 16:
+            cb = cb.clone()
+        L.call("rfsn_rvq_encode_full", resid.data_ptr(), D, D, offsets.data_ptr(), a, cb.data_ptr(),
+               Ls, Cn, codes.data_ptr(), ws.data_ptr() if wsb else None, wsb, s)
     return codes, mask8.bool(), offsets
 
 

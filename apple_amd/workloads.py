@@ -144,4 +144,9 @@ REF_WORKLOADS: Dict[str, RefWorkload] = {
     # context, so 24,576 warm tokens
     "refdefault_32k": RefWorkload("refdefault_32k", heads=32, head_dim=128, context=32768, hot=8192,
                                   pq_subspaces=8, pq_centroids=256, rvq_layers=4, rvq_centroids=4096),
+    # encode in the same format: one 4,096-token chunk of 32 heads through
+    # HybridQuantizerMLX.encode (PQ, norm gate, 4 full-dimension stages of
+    # 4,096 centroids), codebooks drawn as the reference initialises them
+    "refencode_4k": RefWorkload("refencode_4k", heads=32, head_dim=128, context=4096, hot=0,
+                                pq_subspaces=8, pq_centroids=256, rvq_layers=4, rvq_centroids=4096),
 }

@@ -387,6 +387,104 @@ def bench_ref(w, args, dev) -> dict:
     return result
 
 
+def bench_refencode(w, args, dev) -> dict:
+    """Warm-tier encode in the reference's own format at its default
+    configuration: one chunk of ``w.context`` tokens x ``w.heads`` heads
+    through HybridQuantizerMLX.encode (quantization.py:305-308): PQ, the norm
+    gate and its compaction (one host sync for the active count, as the
+    reference's np.asarray(mask)), then the full-dimension RVQ stages.  The
+    roofline is the RVQ search kernel's (the dominant one): its algorithmic
+    flops 2 * C * D per active row and stage over its own HIP-event time."""
+    import torch
+    from apple_amd import _lib as L
+    from apple_amd import kernels as K
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    H, D, M, C, Ls, Cr = w.heads, w.head_dim, w.pq_subspaces, w.pq_centroids, w.rvq_layers, w.rvq_centroids
+    cfg = RFSNConfig(hidden_dim=H * D, num_heads=H, head_dim=D, num_subspaces=M, subspace_dim=D // M,
+                     pq_bits=(C - 1).bit_length(), num_rvq_layers=Ls, rvq_codebook_size=Cr)
+    g = torch.Generator("cpu").manual_seed(17)
+    qz = HybridQuantizerMLX(cfg, device=dev, generator=g)  # codebooks drawn as at quantization.py:110-115, 190-197
+    scale = torch.rand((H, D), generator=g) * 1.5 + 0.5
+    x = (torch.randn((w.context, H, D), generator=g) * scale).half().reshape(-1, D)
+    xd = x.to(dev)
+    n = x.shape[0]
+
+    def step():
+        return qz.encode(xd)
+
+    log(f"workload {w.name}: {n} vectors, head_dim {D}, PQ {M}x{C}, RVQ {Ls}x{Cr}, threshold "
+        f"{cfg.rvq_sparsity_threshold}")
+    warm = warm_up(step, args.warmup)
+    steps = max(args.steps // 10, 10)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        pq, rvq, mask, offs = step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+    a = int(offs.numel())
+    # the RVQ search kernel alone, on its stream, over the step's active rows
+    _, resid = K.pq_encode(xd, qz.pq.codebooks)
+    lib = L.load()
+    wsb = lib.rfsn_rvq_encode_full_workspace_bytes(a, D, Ls, Cr)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    codes = torch.empty((a, Ls), dtype=torch.uint16, device=dev)
+    cb = qz.rvq.codebooks.contiguous()
+    stream = torch.cuda.current_stream()
+
+    def rvq_only():
+        L.call("rfsn_rvq_encode_full", resid.data_ptr(), D, D, offs.data_ptr(), a, cb.data_ptr(), Ls, Cr,
+               codes.data_ptr(), ws.data_ptr() if wsb else None, wsb, stream.cuda_stream)
+
+    rvq_only()
+    torch.cuda.synchronize()
+    same = bool(torch.equal(codes, rvq))
+    _, rvq_ms = _timed(rvq_only, steps, stream)
+    pct = step_percentiles(rvq_only, steps)
+    flops = a * Ls * Cr * D * 2
+    tflops = flops / (rvq_ms * 1e-3) / 1e12
+    result = {
+        "metric": "reference-format encode vectors/s (PQ + gated full-dimension RVQ, MFMA search), 1 GPU",
+        "value": round(n / (ms_per_step * 1e-3), 1),
+        "unit": "vectors/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_run": warm,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) K with per-channel scale U(0.5,2); codebooks drawn as the reference "
+                "initialises them)",
+        "config": {"workload": w.name, "vectors_per_step": n, "heads": H, "head_dim": D,
+                   "format": f"PQ M{M}x{C} + gated RVQ {Ls}x{Cr}, threshold {cfg.rvq_sparsity_threshold}",
+                   "active_rows": a},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 5), "traffic": None, "kernel": "rvq_mfma_kernel<128>",
+                     "kernel_ms": round(rvq_ms, 5), "kernel_ms_percentiles": pct, "flops_per_launch": flops,
+                     "rows_per_s": round(a / (rvq_ms * 1e-3), 1), "codes_match_step": same},
+    }
+    if not args.no_cpu:
+        from oracle import cpu_baseline as cbl
+
+        log("CPU baseline")
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        sample = 2048
+        xs, pcb, rcb = x[:sample], qz.pq.codebooks.cpu(), qz.rvq.codebooks.cpu()
+        _, ccodes, _, _ = cbl.ref_encode(xs, pcb, rcb, cfg.rvq_sparsity_threshold)
+        agree = float((ccodes == rvq[:ccodes.shape[0]].cpu().long()).float().mean()) if a >= sample else None
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0 * args.cpu_budget or reps == 0:
+            cbl.ref_encode(xs, pcb, rcb, cfg.rvq_sparsity_threshold)
+            reps += 1
+        sec = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(sample * reps / sec, 1), "unit": "vectors/s", "cores": cores,
+                                  "kind": "port", "cpu_model": cpu_model(),
+                                  "sample": f"the chunk's first {sample} vectors, {reps} times: torch-CPU cdist^2 "
+                                            f"PQ, norm gate, {Ls} chunked (|x|^2 - 2xc) + |c|^2 stages",
+                                  "seconds": round(sec, 2), "codes_agree_with_gpu": agree}
+    return result
+
+
 def encode_cpu_baseline(w, xs, cbs, k: int, threads=None, budget_s: float = 10.0) -> dict:
     """The step's K and V chunks encoded by the torch-CPU restatement of the
     reference's PyTorch encode (fp32 cdist^2 + argmin per subspace, both
@@ -755,7 +853,9 @@ def main(argv=None) -> int:
 
     dev = torch.device("cuda", 0)
     if args.workload in REF_WORKLOADS:
-        print(json.dumps(bench_ref(REF_WORKLOADS[args.workload], args, dev)), flush=True)
+        w = REF_WORKLOADS[args.workload]
+        fn = bench_refencode if w.name.startswith("refencode") else bench_ref
+        print(json.dumps(fn(w, args, dev)), flush=True)
         return 0
     w = WORKLOADS[args.workload]
     if w.name == "encode_4k":
@@ -847,6 +947,8 @@ def main(argv=None) -> int:
         result["encode_4k"] = sub_record(bench_encode(WORKLOADS["encode_4k"], sub, dev))
         log("sub-record longctx_128k")
         result["longctx_128k"] = sub_record(bench_longctx(WORKLOADS["longctx_128k"], sub, dev))
+        log("sub-record refencode_4k")
+        result["refencode_4k"] = sub_record(bench_refencode(REF_WORKLOADS["refencode_4k"], sub, dev))
     print(json.dumps(result), flush=True)
     return 0
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 4
+#define RFSN_ABI_VERSION 5
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -111,15 +111,22 @@ int rfsn_warm_encode_batch(const rfsn_format* fmt, const rfsn_encode_job* jobs, 
  * (2) compaction: offsets[0..A) = ascending indices with mask set,
  *     count_dev[0] = A  (np.flatnonzero, quantization.py:218);
  * (3) L-stage full-dimension encode of the active rows (running residual in
- *     fp32, first-min argmin over C <= 65535 centroids), codes [A][L] u16. */
+ *     fp32, first-min argmin over C <= 65535 centroids, which equals the
+ *     reference's 512-centroid chunks merged with a strict <), codes [A][L]
+ *     u16.  For D in {64, 128, 256} and 3 <= C <= 16384 the search screens
+ *     on MFMA and needs a workspace of
+ *     rfsn_rvq_encode_full_workspace_bytes(A, D, L, C) bytes (16-byte
+ *     aligned; 0 = none needed), and the residual rows and codebooks must be
+ *     16-byte aligned (ld a multiple of 8). */
 int rfsn_rvq_gate(const void* resid_dev, int64_t n, int32_t D, int64_t ld, float threshold,
                   uint8_t* mask_dev, void* stream);
 size_t rfsn_mask_compact_workspace_bytes(int64_t n);
 int rfsn_mask_compact(const uint8_t* mask_dev, int64_t n, int32_t* offsets_dev, int32_t* count_dev,
                       void* workspace_dev, size_t workspace_bytes, void* stream);
+size_t rfsn_rvq_encode_full_workspace_bytes(int64_t active, int32_t D, int32_t L, int32_t C);
 int rfsn_rvq_encode_full(const void* resid_dev, int64_t ld, int32_t D, const int32_t* offsets_dev,
                          int64_t active, const void* codebooks_dev, int32_t L, int32_t C,
-                         uint16_t* codes_dev, void* stream);
+                         uint16_t* codes_dev, void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- decode
  * Warm-format decode to fp16 [N][ldo]: fp16(base + rvq) then sparse

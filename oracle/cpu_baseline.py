@@ -18,6 +18,9 @@ GQA: query head h reads KV head h // (Hq // Hkv).
 Decode (reference format): ``ref_decode`` / ``ref_decode_step``, the gated
 full-dimension correction of quantization.py:254-275 on the PQ base, then
 the same attention.
+
+Encode (reference format): ``ref_encode``, the PQ search above, the norm
+gate and the chunked full-dimension RVQ search of quantization.py:206-252.
 """
 
 from __future__ import annotations
@@ -144,6 +147,40 @@ def pq_encode_cdist(x: torch.Tensor, codebooks: torch.Tensor):
         codes[:, m] = idx.to(torch.uint8)
         resid[:, m * d:(m + 1) * d] = (sub - F.embedding(idx, cents)).half()
     return codes, resid
+
+
+def ref_encode(x: torch.Tensor, pq_cb: torch.Tensor, rvq_cb: torch.Tensor, threshold: float):
+    """Reference-format encode (HybridQuantizerMLX.encode, quantization.py:
+    305-308) in torch-CPU fp32: PQ by ``cdist ** 2`` + ``argmin`` per subspace
+    (launcher:358-373); the gate ``|fp32(r)| > threshold`` on the fp16 PQ
+    residual (quantization.py:216-218); then per stage the distance form of
+    ``_squared_l2_distance`` (quantization.py:92-96), ``(|x|^2 - 2 x c^T) +
+    |c|^2``, over the reference's 512-centroid chunks merged with a strict <
+    (quantization.py:233-246), and ``running -= c`` (249-250).  Returns
+    (pq codes [N, M] u8, rvq codes [A, L] int64, mask [N] bool, offsets [A] int32)."""
+    pq, r1 = pq_encode_cdist(x, pq_cb)
+    r = r1.float()
+    mask = torch.sqrt((r * r).sum(dim=1)) > threshold
+    offsets = torch.nonzero(mask).flatten().to(torch.int32)
+    run = r[offsets.long()]
+    L, C, _ = rvq_cb.shape
+    codes = torch.zeros((run.shape[0], L), dtype=torch.int64)
+    chunk = min(512, C)
+    for layer in range(L):
+        cb = rvq_cb[layer].float()
+        x2 = (run * run).sum(dim=1, keepdim=True)
+        best = torch.full((run.shape[0],), float("inf"))
+        idx = torch.zeros((run.shape[0],), dtype=torch.int64)
+        for s in range(0, C, chunk):
+            c = cb[s:s + chunk]
+            d = (x2 - 2.0 * run @ c.T) + (c * c).sum(dim=1)[None, :]
+            lb, li = d.min(dim=1)
+            upd = lb < best
+            best = torch.where(upd, lb, best)
+            idx = torch.where(upd, li + s, idx)
+        codes[:, layer] = idx
+        run = run - cb[idx]
+    return pq, codes, mask, offsets
 
 
 def warm_encode(x: torch.Tensor, pq_cb: torch.Tensor, rvq_cb: Optional[torch.Tensor], k: int) -> dict:

@@ -333,6 +333,63 @@ def test_rvq_full_bit_exact(device, thr):
     assert np.array_equal(H(dec).view(np.uint16), rdec.view(np.uint16))
 
 
+def _planted_rvq_case(g, n, D, L, C):
+    """Reference-default RVQ codebooks (row 0 zeroed) with ties planted
+    across the 512-centroid chunks that ResidualVQMLX.encode merges with a
+    strict < (quantization.py:233-246): exact duplicates at j and j + 512 m,
+    and sign-flipped copies whose distance to a vector equals the original's
+    (placed above and below it); the vectors hit those ties in stage 0, plus
+    random residuals at two scales."""
+    cb = rand_codebooks(g, L, C, D)
+    cb[:, 0] = 0
+    x = np.concatenate([randn16(g, (n - 48) // 2, D, scale=0.015), randn16(g, n - 48 - (n - 48) // 2, D)], 0)
+    picks = []
+    for layer in range(L):
+        for i, j in enumerate(range(3, 3 + 24)):
+            m = 1 + (i % ((C - 1 - j) // 512))
+            dup = j + 512 * m
+            cb[layer, dup] = cb[layer, j]                        # exact duplicate in a later chunk
+            flip = j + 512 * ((m + 1) % (C // 512)) + 100        # sign-flipped copy, later or earlier chunk
+            cb[layer, flip] = cb[layer, j]
+            cb[layer, flip, :8] = -cb[layer, j, :8]
+            if layer == 0:
+                picks.append(j)
+    rows = []
+    for j in picks:
+        rows.append(cb[0, j].copy())                            # ties with its duplicate: distance 0
+        r = cb[0, j].copy()
+        r[:8] = 0                                               # equidistant from c_j and its flipped copy
+        rows.append(r)
+    x = np.concatenate([x, np.stack(rows)], 0)
+    assert x.shape[0] == n
+    return x.astype(np.float16), cb
+
+
+@pytest.mark.parametrize("thr", [0.005, 0.25])
+def test_rvq_full_reference_default_shape(device, thr):
+    """ResidualVQMLX.encode at the reference's default shape (C = 4,096,
+    L = 4, D = 128; storage.py:25, 33-34) with ties planted across the
+    512-centroid chunks: mask, offsets and every stage's code bit-exact
+    against the oracle's global first-min, which equals the reference's
+    chunked strict-< merge."""
+    from apple_amd import kernels as K
+
+    g = rng(70 + int(thr * 1000))
+    n, D, L, C = 512, 128, 4, 4096
+    resid, cb = _planted_rvq_case(g, n, D, L, C)
+    codes, mask, offs = K.rvq_encode_full(T(resid, device), T(cb, device), thr)
+    rc, rm, ro = nx.rvq_encode_full(resid, cb, thr)
+    assert rm.sum() > n // 2
+    assert np.array_equal(H(mask), rm)
+    assert np.array_equal(H(offs), ro)
+    got = H(codes)
+    assert np.array_equal(got, rc), np.argwhere(got != rc)[:8]
+    # the planted tie rows took the lower index in stage 0
+    tied = [i for i in range(n - 48, n) if rm[i]]
+    pos = np.searchsorted(ro, tied)
+    assert (rc[pos, 0] < 512).all()
+
+
 def _qpos_cases(B, Hq, T_):
     g = rng(3)
     return [None, g.integers(-1, T_, (B, Hq)).astype(np.int32)]

@@ -769,3 +769,67 @@ def test_cpu_baseline_planted_mistakes():
         assert not check_decode_step(cb.decode_step, rng(33))
     finally:
         cb.blockwise_attention = real_attn
+
+
+def _ref_encode_le(x, pq_cb, rvq_cb, threshold):
+    """cpu_baseline.ref_encode with a planted mistake: the chunk merge written
+    with <= (a tie moves to the later chunk) instead of the reference's <."""
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    pqc, r1 = cb.pq_encode_cdist(x, pq_cb)
+    rr = r1.float()
+    m = torch.sqrt((rr * rr).sum(dim=1)) > threshold
+    o = torch.nonzero(m).flatten().to(torch.int32)
+    run = rr[o.long()]
+    Ln, Cn, _ = rvq_cb.shape
+    out = torch.zeros((run.shape[0], Ln), dtype=torch.int64)
+    for layer in range(Ln):
+        c_all = rvq_cb[layer].float()
+        x2 = (run * run).sum(dim=1, keepdim=True)
+        best = torch.full((run.shape[0],), float("inf"))
+        idx = torch.zeros((run.shape[0],), dtype=torch.int64)
+        for s0 in range(0, Cn, 512):
+            c = c_all[s0:s0 + 512]
+            d = (x2 - 2.0 * run @ c.T) + (c * c).sum(dim=1)[None, :]
+            lb, li = d.min(dim=1)
+            upd = lb <= best
+            best = torch.where(upd, lb, best)
+            idx = torch.where(upd, li + s0, idx)
+        out[:, layer] = idx
+        run = run - c_all[idx]
+    return pqc, out, m, o
+
+
+def test_cpu_baseline_ref_encode_matches_oracle():
+    """The timed torch-CPU reference-format encode (cdist^2 PQ, norm gate,
+    chunked (|x|^2 - 2xc) + |c|^2 stages) gives the oracle's PQ codes, mask,
+    offsets and every stage's code on data without near-ties, across three
+    512-centroid chunks; with a planted mistake (the chunk merge keeping the
+    later index on ties) it differs on a row that ties two chunks."""
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    g = np.random.default_rng(8)
+    x = (g.standard_normal((160, 64)) * np.linspace(0.5, 2.0, 64)).astype(np.float16)
+    p = (g.standard_normal((4, 256, 16)) * 0.5).astype(np.float16)
+    for i in range(20):  # rows that are PQ centroids exactly: zero residual, gated off
+        x[i] = p[np.arange(4), g.integers(0, 256, 4)].reshape(-1)
+    r = (g.standard_normal((3, 1536, 64)) * 0.25).astype(np.float16)
+    r[:, 0] = 0
+    r[:, 1100] = r[:, 77]  # a duplicate in a later chunk: the first index must win
+    # a row whose PQ residual is exactly centroid 77 of stage 0
+    x[20] = (p[np.arange(4), [3, 4, 5, 6]].reshape(-1).astype(np.float32)
+             + r[0, 77].astype(np.float32)).astype(np.float16)
+    args = (torch.from_numpy(x), torch.from_numpy(p), torch.from_numpy(r), 0.005)
+    pq, codes, mask, offs = cb.ref_encode(*args)
+    rp, rc, rm, ro = nx.hybrid_encode(x, p, r, 0.005)
+    assert np.array_equal(pq.numpy(), rp)
+    assert np.array_equal(mask.numpy(), rm) and not rm[:20].any()
+    assert np.array_equal(offs.numpy(), ro)
+    assert np.array_equal(codes.numpy(), rc.astype(np.int64))
+    assert 77 in rc[:, 0] and 1100 not in rc[:, 0]
+    _, bad, _, _ = _ref_encode_le(*args)
+    assert not np.array_equal(bad.numpy(), rc.astype(np.int64))
