@@ -219,6 +219,58 @@ def test_fused_error_envelope_peaked_queries(device):
     assert not fired[1] and fired[4] and fired[8], fired
 
 
+ENVELOPE_SCALES = tuple(1.0 + 0.5 * i for i in range(15))  # 1, 1.5, ..., 8
+
+
+def _excess(out: np.ndarray, ref: np.ndarray) -> tuple:
+    """(max |out - ref|, max of |out - ref| - max(TOL, ulp(ref))): outputs are
+    fp16, and from |ref| = 4 up one rounding step (3.9e-3 at [4, 8)) exceeds
+    2e-3 whatever the arithmetic before it, so the envelope allows the larger
+    of 2e-3 and one fp16 ulp of the reference output."""
+    o, r = out.astype(np.float32), ref.astype(np.float32)
+    d = np.abs(o - r)
+    ulp = np.spacing(np.abs(ref.astype(np.float16))).astype(np.float32)
+    return float(d.max()), float((d - np.maximum(TOL, ulp)).max())
+
+
+@pytest.mark.parametrize("seed,family", [(21, "outlier"), (22, "outlier"), (23, "plain")])
+def test_guard_envelope(device, seed, family):
+    """The default path (score tables with the drift guard) holds 2e-3 (or
+    one fp16 ulp of outputs at |x| >= 4) at every query scale from 1 to 8 in
+    steps of 0.5, with the guard's own split count and with one split per
+    (query, KV head).  "outlier": queries whose channels carry per-head
+    scales drawn from U(0.5, 4) (the shape RoPE'd decoder queries have: some
+    channels several times the rest); the guard fires on nearly every block
+    from scale 1.  "plain": N(0, 1) queries, where it is quiet at 1 and fires
+    on a growing share of blocks above.  Points where the guard stays quiet
+    are the tables' own error; points where it fires are the exact pass."""
+    from apple_amd.cache import RFSNv10KVCacheMLX
+
+    g, cfg, keys, values, cbs, kq, vq = _setup(seed, 32, 8, 16, 16, 4, 2000, 64)
+    cache = RFSNv10KVCacheMLX(cfg, device=device)
+    cache.update(T(keys, device), T(values, device), (kq, vq))
+    assert cache._k_layout == 1 and cache._guarded
+    wk, wv = _oracle_window(keys, values, cbs, 16, 4, 2000)
+    chan = (g.random((1, 32, 64), dtype=np.float32) * 3.5 + 0.5).astype(np.float32) if family == "outlier" else 1.0
+    q0 = g.standard_normal((4, 32, 64), dtype=np.float32) * chan
+    rows = []
+    for scale in ENVELOPE_SCALES:
+        q = (q0 * np.float32(scale)).astype(np.float16)
+        ref = nx.blockwise_attention(q, wk, wv, 64 ** -0.5, 256, False, None)
+        out = H(cache.attention_forward(T(q, device), causal=False))
+        one = torch.empty_like(T(q, device))
+        cache.prepare(T(q, device), causal=False, splits=1, out=one)()
+        drift = H(cache.last_drift)[:, :, 0]
+        e, x = _excess(out, ref)
+        e1, x1 = _excess(H(one), ref)
+        rows.append((scale, e, x, e1, x1, float(drift.max()), float((drift > cfg.score_table_tolerance).mean())))
+    print("\nscale  err        excess      err(1 split)  excess      max estimate  fired")
+    for r in rows:
+        print("%5.1f  %.3e  %+.3e  %.3e     %+.3e  %.3e     %.2f" % r)
+    bad = [r for r in rows if not (r[2] <= 0 and r[4] <= 0)]
+    assert not bad, bad
+
+
 def test_guard_follows_recalibrated_codebooks(device):
     """The drift guard's weights and the entry tables follow the K codebooks:
     after calibrate_quantizer replaces them, and after an in-place write, the
