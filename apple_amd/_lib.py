@@ -56,7 +56,8 @@ class FusedParams(C.Structure):
                 ("part_base", i32), ("part_slots", i32), ("merge", i32), ("k_layout", i32),
                 ("guard", vp), ("drift", vp), ("guard_tol", f32),
                 ("tile_map", vp), ("tile_map_count", vp), ("tile_map_stride", i64),
-                ("k_tab", vp), ("v_tab", vp), ("tab_stride", i64)]
+                ("k_tab", vp), ("v_tab", vp), ("tab_stride", i64),
+                ("app_k", vp), ("app_v", vp), ("app_ld", i64), ("app_vabs", vp), ("app_count", i32)]
 
 
 class RefStoreCodes(C.Structure):
@@ -111,6 +112,9 @@ SIGNATURES = {
     "rfsn_blockwise_attention": (i32, [vp, i32, i32, i32, vp, vp, i64, i32, i64, i64, f32, i32, vp, vp, vp, sz, vp]),
     "rfsn_pack_codes": (i32, [vp, i64, i64, i32, i32, vp, i64, i64, vp]),
     "rfsn_pack_score_codes": (i32, [vp, vp, vp, vp, i32, i64, i32, vp, vp, vp, vp, i64, i64, vp]),
+    "rfsn_warm_append_pair": (i32, [C.POINTER(Format), C.POINTER(Codes), C.POINTER(Codes), i64, i32, vp, vp, vp,
+                                    vp, C.POINTER(Codes), i32, vp, C.POINTER(Codes), i64, i64, C.POINTER(Codes),
+                                    vp, C.POINTER(Codes), vp, i64, vp]),
     "rfsn_fused_splits": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_k_scoring": (i32, [C.POINTER(FusedParams)]),
     "rfsn_fused_workspace_bytes": (sz, [C.POINTER(FusedParams)]),
@@ -148,7 +152,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 5:
+    if lib.rfsn_abi_version() != 6:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib
@@ -178,6 +182,8 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 def stream_handle(device: Optional[torch.device] = None) -> int:
     """The current torch stream of ``device`` as a hipStream_t."""
+    if isinstance(device, torch.device) and device.index is not None:
+        return torch._C._cuda_getCurrentRawStream(device.index)  # no Stream object built
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -218,6 +218,66 @@ class TiledCodes:
             self.t["sparse_val"][:, t_base:t_base + T] = sval
         self.len = need
 
+    @staticmethod
+    def append_pair(kt: "TiledCodes", vt: "TiledCodes", kc: tuple, vc: tuple, kq, vq,
+                    rings: Optional[tuple] = None) -> bool:
+        """``append`` of a K/V block to a (K, V) pair of stores in one launch
+        (``rfsn_warm_append_pair``) for the 16 + 16 subspace formats of
+        head_dim 64 with a sparse stage, when both stores take the block in
+        place at the same token; False, with nothing written, otherwise.
+        kc / vc: plain head-major (pq, rvq, sparse_idx, sparse_val) [H, T, *]
+        with residual sparse values.  ``rings`` (K, V ``_RingStore``): the same
+        launch also appends the codes to them, which must then take the block
+        in place as well."""
+        f = kt.fmt
+        if not (not vt.score_rows and vt.fmt == f and f.head_dim == 64 and f.pq_subspaces == 16
+                and f.rvq_subspaces == 16 and 0 < f.sparse_k <= 16):
+            return False
+        if (kt.cap, kt.head, kt.len) != (vt.cap, vt.head, vt.len) or kt.heads != vt.heads:
+            return False
+        H, T = kt.heads, int(kc[0].shape[1])
+        t_base = kt.head * K.TILE + kt.len
+        if t_base + T > kt.cap:
+            return False  # the stores grow or move: the per-store append handles it
+        for c in (kc, vc):
+            for t, last in zip(c, (16, 16, f.sparse_k, f.sparse_k)):
+                if t is None or tuple(t.shape) != (H, T, last) or not t.is_contiguous():
+                    return False
+        ring_args = [None, None, None, None, 0]
+        if rings is not None:
+            kr, vr = rings
+            if (kr.head, kr.n, kr._cap()) != (vr.head, vr.n, vr._cap()) or kr.head + kr.n + T > kr._cap():
+                return False
+            want = {"pq_codes": (16, torch.uint8), "rvq_codes": (16, torch.uint8), "rvq_mask": (None, torch.bool),
+                    "sparse_idx": (f.sparse_k, torch.uint8), "sparse_val": (f.sparse_k, torch.float16)}
+            for r in rings:
+                for key, (w, dt) in want.items():
+                    t = r.buf.get(key)
+                    shape = (r._cap(), H) if w is None else (r._cap(), H, w)
+                    if t is None or t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous():
+                        return False
+            rc = lambda r: L.Codes(*(r.buf[key].data_ptr() for key in ("pq_codes", "rvq_codes", "sparse_idx",
+                                                                        "sparse_val")))
+            ring_args = [C.byref(rc(kr)), kr.buf["rvq_mask"].data_ptr(), C.byref(rc(vr)), vr.buf["rvq_mask"].data_ptr(),
+                         kr.head + kr.n]
+        codes = lambda c: L.Codes(c[0].data_ptr(), c[1].data_ptr(), c[2].data_ptr(), c[3].data_ptr())
+        ks, vs = codes(kc), codes(vc)
+        kd = L.Codes(kt.t["pq"].data_ptr(), kt.t["rvq"].data_ptr(), kt.t["sparse_idx"].data_ptr(),
+                     kt.t["sparse_val"].data_ptr())
+        vd = L.Codes(vt.t["pq"].data_ptr(), vt.t["rvq"].data_ptr(), vt.t["sparse_idx"].data_ptr(),
+                     vt.t["sparse_val"].data_ptr())
+        cbs = [K._contig(x) for x in (kq.pq.codebooks, kq.rvq_codebooks, vq.pq.codebooks, vq.rvq_codebooks)]
+        fc = f.c()
+        L.call("rfsn_warm_append_pair", C.byref(fc), C.byref(ks), C.byref(vs), T, H, *(x.data_ptr() for x in cbs),
+               C.byref(kd), int(kt.score_rows), kt.t["sparse_cc"].data_ptr() if kt.exact_plane else None, C.byref(vd),
+               kt.cap, t_base, *ring_args, K._stream(kc[0]))
+        kt.len += T
+        vt.len += T
+        if rings is not None:
+            for r in rings:
+                r.n += T
+        return True
+
     def seg(self, tile_skip: int = 0):
         """(rfsn_codes addresses from live tile ``tile_skip``, the arrays to
         keep alive, tokens available from there): a segment without building
@@ -599,6 +659,12 @@ class RFSNv10KVCacheMLX:
             self._tables_key = key
         return self._tables
 
+    def _dev16(self, t: torch.Tensor) -> torch.Tensor:
+        """``t`` as fp16 on the cache's device (itself when it already is)."""
+        if t.dtype is torch.float16 and t.device == self.device:
+            return t
+        return t.to(self.device, torch.float16)
+
     def _hot_append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Append [T, H, D] tokens to the hot tier.  The buffers hold up to
         twice the hot capacity under the recency policy, so the live range
@@ -620,8 +686,18 @@ class RFSNv10KVCacheMLX:
                 nv[:, : self.num_hot] = self._hot_v[:, h:h + self.num_hot]
                 self._hot_k, self._hot_v = nk, nv
             self._hot_head = h = 0
-        self._hot_k[:, h + self.num_hot:h + need] = k.permute(1, 0, 2).to(self.device, torch.float16)
-        self._hot_v[:, h + self.num_hot:h + need] = v.permute(1, 0, 2).to(self.device, torch.float16)
+        k, v = self._dev16(k), self._dev16(v)
+        if T and k.is_contiguous() and v.is_contiguous() and not (k.data_ptr() % 16 or v.data_ptr() % 16) \
+                and self.D % 8 == 0:
+            # one launch for K and V, which also folds |v| into the drift guard's V bound
+            L.call("rfsn_hot_append", k.data_ptr(), v.data_ptr(), self.H * self.D, T, self.H, self.D,
+                   self._hot_k.data_ptr(), self._hot_v.data_ptr(), cap, h + self.num_hot,
+                   self._vabs.data_ptr() if self._guarded else None, K._stream(k))
+        else:
+            self._hot_k[:, h + self.num_hot:h + need] = k.permute(1, 0, 2)
+            self._hot_v[:, h + self.num_hot:h + need] = v.permute(1, 0, 2)
+            if T and self._guarded:
+                torch.maximum(self._vabs, v.abs().amax().float().view(1), out=self._vabs)
         self.num_hot = need
 
     def _hot_append_args(self, stream: Optional[int] = None) -> Tuple[Optional[int], int]:
@@ -630,6 +706,43 @@ class RFSNv10KVCacheMLX:
         per rebuild."""
         return (self._vabs.data_ptr() if self._guarded else None,
                 L.stream_handle(self.device) if stream is None else stream)
+
+    def _session_layout(self) -> Optional[tuple]:
+        """What a prepared fused launch's segments depend on, then the warm
+        length: the warm tiled arrays (addresses, head tile, capacity), the
+        cold tier's extent, the hot buffers and the codebooks.  Two layouts
+        equal but for the last entry describe launches that differ only in
+        the hot range and the length of the warm segment.  None when the
+        warm tier has no tiled store."""
+        if self._warm_tiled is None:
+            return None
+        warm = tuple((tuple(t.data_ptr() for t in w.t.values() if t is not None), w.head, w.cap)
+                     for w in self._warm_tiled)
+        return (warm, self.num_cold, len(self.cold_chunk_metadata), self._hot_k.data_ptr(),
+                self._hot_v.data_ptr(), int(self._hot_k.shape[1]), self._codebook_key(bool(self._fmt().rvq_subspaces)),
+                self.num_warm)
+
+    def _hot_rows(self, k: torch.Tensor, v: torch.Tensor) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        """New tokens [T, H, D] as device fp16 rows that a fused launch can
+        append itself (``rfsn_fused_params.app_*``): the hot tier holds them
+        without demoting (recency, num_hot + T <= hot_capacity, T <= 32), its
+        buffers hold them at the current head, and the rows are 16-byte
+        aligned.  None otherwise (the tokens then go through ``update``)."""
+        T = k.shape[0]
+        if not self._recency or not 0 < T <= K.TILE or self.num_hot + T > self.hot_capacity:
+            return None
+        if self._hot_head + self.num_hot + T > self._hot_k.shape[1]:
+            return None
+        f16 = torch.float16
+        if not (k.dtype is f16 and k.is_contiguous() and k.device == self.device):
+            k = k.to(self.device, f16).contiguous()
+        if not (v.dtype is f16 and v.is_contiguous() and v.device == self.device):
+            v = v.to(self.device, f16).contiguous()
+        if k.shape != (T, self.H, self.D) or v.shape != (T, self.H, self.D):
+            raise ValueError(f"new_keys and new_values must be [T, {self.H}, {self.D}]")
+        if k.data_ptr() % 16 or v.data_ptr() % 16:
+            return None
+        return k, v
 
     def _try_hot_append(self, k: torch.Tensor, v: torch.Tensor,
                         args: Optional[Tuple[Optional[int], int]] = None) -> bool:
@@ -701,10 +814,10 @@ class RFSNv10KVCacheMLX:
             raise ValueError(f"new_keys must be [T, {self.H}, {self.D}]")
         self.quantizer = quantizer
         self._kq, self._vq = _pair(quantizer)
-        keys = new_keys.to(self.device, torch.float16)
-        values = new_values.to(self.device, torch.float16)
+        keys, values = self._dev16(new_keys), self._dev16(new_values)
         num_tokens = int(keys.shape[0])
-        if num_tokens and self._guarded:
+        if num_tokens and self._guarded and not (self._recency and num_tokens <= self.hot_capacity):
+            # tokens that skip the hot tier (whose append folds its own |v|)
             torch.maximum(self._vabs, values.abs().amax().float().view(1), out=self._vabs)
         if self._recency:
             self._update_recency(keys, values, disk_dir)
@@ -777,6 +890,13 @@ class RFSNv10KVCacheMLX:
         encode serves, K and V share one launch whose head-major codes feed
         the tiled store as they are."""
         hm = _encode_pair_head_major(keys, values, self._kq, self._vq) if self._subspace else None
+        if hm is not None and isinstance(self._wk, _RingStore) and self._warm_tiled is not None \
+                and self._fmt().fused_ok:
+            # one launch: the tiled stores and the reference-layout rings
+            if TiledCodes.append_pair(*self._warm_tiled, hm[0], hm[1], self._kq, self._vq,
+                                      rings=(self._wk, self._wv)):
+                self.num_warm += int(keys.shape[0])
+                return
         if hm is None:
             ck = _compress_tensor_sequence(keys, self._kq)
             cv = _compress_tensor_sequence(values, self._vq)
@@ -794,8 +914,9 @@ class RFSNv10KVCacheMLX:
         elif self._fmt().fused_ok:
             if self._warm_tiled is None:
                 self._warm_tiled = self._tiled_pair()
-            for tiled, codes, qz in zip(self._warm_tiled, hm, (self._kq, self._vq)):
-                tiled.append(*codes, qz.pq.codebooks, qz.rvq_codebooks)
+            if not TiledCodes.append_pair(*self._warm_tiled, hm[0], hm[1], self._kq, self._vq):
+                for tiled, codes, qz in zip(self._warm_tiled, hm, (self._kq, self._vq)):
+                    tiled.append(*codes, qz.pq.codebooks, qz.rvq_codebooks)
         self.num_warm += int(keys.shape[0])
 
     def _warm_to_cold(self, n: int, disk_dir) -> None:
@@ -1520,7 +1641,10 @@ class RFSNv10KVCacheMLX:
         fetched = set(fetched)
         read_slots = [slots[c]["slot"] for c in cold_ids]
         self._order_after_copies()  # resident chunks may still be arriving from a prefetch
-        for kind, x in plan:
+        # the warm tier is segment 0 (the kernel keeps segment 0's bases in
+        # registers, and a decode session grows it in place by its length);
+        # the cold chunks follow in position order
+        for kind, x in sorted(plan, key=lambda e: e[0] != "warm"):
             if kind == "hot":
                 hot_off = self._hot_head + x[0] - spans["hot"][0]
                 hot_len = x[1] - x[0]
@@ -1630,11 +1754,16 @@ class DecodeSession:
     the query buffer ``q`` (read at launch time, so the caller refills it in
     place), writing ``out``.
 
-    While a step only adds hot tokens (``_try_hot_append``) and the router's
-    chunk set stays, the step re-issues one prepared fused launch with its hot
-    length grown in place: two launches and no host-side rebuilding.  Any
-    other step (a demotion into warm, a migration to cold, another chunk set)
-    goes through the cache's general ``update`` and rebuilds the launch.  The
+    While a step only adds hot tokens (``_hot_rows``) and the router's chunk
+    set stays, the step re-issues one prepared fused launch with its hot
+    length grown in place, which appends the new rows itself (attends them
+    from the caller's buffers and writes them to their hot slots): the
+    attention launch (and its split merge) and no host-side rebuilding.  Any
+    other step goes through the cache's general ``update``; when that kept
+    the launch's segments in place (a demotion that grows warm at its tail,
+    the hot buffers' live range moved to their front) the step patches the
+    prepared launch (``_regrow``), and otherwise (a migration to cold,
+    another chunk set, new codebooks) it rebuilds the launch.  The
     query is the newest token, so every window token is allowed and the launch
     carries no query positions (cache.py:395-428 with causal masking at the
     newest position).  The split count is pinned at each rebuild, so the
@@ -1660,15 +1789,36 @@ class DecodeSession:
         self._launch: Optional[K.FusedLaunch] = None
         self._ids: Optional[List[int]] = None
         self._hot_args: Optional[Tuple[Optional[int], int]] = None  # the fast step's hot-append arguments
+        self._layout: Optional[tuple] = None  # the cache's segment layout at the last rebuild
+        self._rows: Optional[tuple] = None  # the last fast step's new rows (read by its launch)
         self.rebuilds = 0
+        self.regrows = 0  # steps whose update kept the segments in place (launch patched, not rebuilt)
 
-    def _chunk_set(self) -> Optional[List[int]]:
-        """The router's nearest ``cold_attended`` chunks, or None (the cache's
-        own choice: every cold chunk of the window) without a router."""
+    def _chunk_set(self, total: Optional[int] = None) -> Optional[List[int]]:
+        """The router's nearest ``cold_attended`` chunks for a window of
+        ``total`` tokens (default: the cache's), or None (the cache's own
+        choice: every cold chunk of the window) without a router."""
         if self.router is None or not self.cold_attended:
             return None
-        total = self.cache.total_tokens
+        if total is None:
+            total = self.cache.total_tokens
         return self.router.rank(total - 1, total)[:self.cold_attended]
+
+    def _append_launch(self, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """The fast step: the prepared launch appends the new rows itself
+        (attends them from ``k`` / ``v`` and writes them to their hot slots)
+        with its hot length grown by them; one launch per step."""
+        c = self.cache
+        T = int(k.shape[0])
+        p = self._launch.params
+        p.app_k, p.app_v, p.app_ld, p.app_count = k.data_ptr(), v.data_ptr(), c.H * c.D, T
+        p.app_vabs = self._hot_args[0]
+        p.hot_len += T
+        p.max_tokens += T
+        c.num_hot += T
+        c.total_tokens += T
+        self._rows = (k, v)  # the caller's rows stay alive while the launch may read them
+        return self._launch()
 
     def step(self, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         c = self.cache
@@ -1676,15 +1826,18 @@ class DecodeSession:
         # the fast step appends and launches on the stream pinned at the last
         # rebuild; a caller that has switched streams since takes the rebuild
         # path, so its conversions and the launches stay on one stream
-        fast = (self._launch is not None and L.stream_handle(c.device) == self._hot_args[1]
-                and c._try_hot_append(k, v, self._hot_args))
-        if not fast:
-            c.update(k, v, self.quantizer)
+        same_stream = self._launch is not None and L.stream_handle(c.device) == self._hot_args[1]
+        if same_stream:
+            rows = c._hot_rows(k, v)  # None unless the hot tier takes the tokens in place
+            if rows is not None:
+                ids = self._chunk_set(c.total_tokens + T)
+                if ids == self._ids:
+                    return self._append_launch(*rows)
+        before = c._session_layout() if same_stream else None
+        c.update(k, v, self.quantizer)
         ids = self._chunk_set()
-        if fast and ids == self._ids:
-            p = self._launch.params
-            p.hot_len += T
-            p.max_tokens += T
+        if same_stream and ids == self._ids and c._fused_ok(int(self.q.shape[1])) and self._regrow(before, T):
+            self.regrows += 1
             return self._launch()
         if not c._fused_ok(int(self.q.shape[1])):
             # a format the tiled kernel does not serve: one decode-in-register
@@ -1709,9 +1862,39 @@ class DecodeSession:
             # fast steps append on the launch's stream, so the append and the
             # launch that reads it stay ordered
             self._hot_args = c._hot_append_args(step.stream)
+            self._layout = c._session_layout()
         else:  # chunks still copying in: no prepared launch to grow until they are resident
             self._launch, self._ids = None, None
         step()
+
+    def _regrow(self, before: tuple, tokens: int) -> bool:
+        """After a general ``update`` that kept the launch's segments in place
+        -- the same warm arrays, head and cold tier, the same hot buffers --
+        point the prepared launch at the new hot range and grow its warm
+        segment by the demoted tokens, instead of rebuilding it.  ``before``
+        is the cache's ``_session_layout`` before the update."""
+        c = self.cache
+        after = c._session_layout()
+        if after is None or before is None or after[:-1] != before[:-1] or before[:-1] != self._layout[:-1]:
+            return False
+        grown = after[-1] - before[-1]  # warm tokens added by the update
+        if grown and (before[-1] == 0 or self._launch.seg_table is None):
+            return False  # no warm segment 0 in the launch to grow
+        p = self._launch.params
+        D = c.D
+        p.app_count = 0  # the update wrote the new tokens to the hot buffers
+        p.hot_k = c._hot_k.data_ptr() + c._hot_head * D * 2
+        p.hot_v = c._hot_v.data_ptr() + c._hot_head * D * 2
+        p.hot_len = c.num_hot
+        p.hot_pos0 = c._tier_spans()["hot"][0]
+        p.max_tokens += tokens
+        if grown:
+            # segment 0 of sequence 0 is the warm tier: its length grows on
+            # the launch stream, after the launches that read the old one
+            off = L.Segment.len.offset
+            self._launch.seg_table[off:off + 4].view(torch.int32).add_(grown)
+        self._layout = after
+        return True
 
 
 def _to_host_store(s: CompressedTensorMLX) -> CompressedTensorMLX:

@@ -54,6 +54,32 @@ decode_ext_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C
 // leaves at coordinate idx (the indices of one vector are distinct).
 // DELTA = false: the corrected coordinate c = fp16(fp16(base + rvq) + val);
 // DELTA = true: the score delta fp16(c - (float(base) + float(rvq))).
+// Sparse entry (index byte sidx_e, residual sval_e) of the vector whose codes
+// are pq_v[M] and rvq_v[Mr]: writes the corrected coordinate to *cc and the
+// score delta to *delta (either may be NULL).
+__device__ __forceinline__ void fold_entry(int D, const uint8_t* __restrict__ pq_v, int M, int C,
+                                           const uint16_t* __restrict__ pq_cb, const uint8_t* __restrict__ rvq_v,
+                                           int Mr, int Cr, const uint16_t* __restrict__ rvq_cb, uint8_t sidx_e,
+                                           uint16_t sval_e, uint16_t* cc, uint16_t* delta) {
+  const int i = min((int)sidx_e, D - 1);
+  const int d = D / M;
+  const int m = i / d;
+  const uint16_t base = pq_cb[((size_t)m * C + min((int)pq_v[m], C - 1)) * d + (i - m * d)];
+  uint16_t corr = 0, val = base;
+  if (Mr > 0) {
+    const int dr = D / Mr;
+    const int mr = i / dr;
+    corr = rvq_cb[((size_t)mr * Cr + min((int)rvq_v[mr], Cr - 1)) * dr + (i - mr * dr)];
+    val = hadd_bits(base, corr);
+  }
+  const uint16_t c = hadd_bits(val, sval_e);
+  if (cc) *cc = c;
+  if (delta) {
+    const float exact = h2f(base) + (Mr > 0 ? h2f(corr) : 0.f);
+    *delta = f2h(h2f(c) - exact);
+  }
+}
+
 template <bool DELTA>
 __global__ void __launch_bounds__(256)
 sparse_fold_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int C, const uint16_t* __restrict__ pq_cb,
@@ -63,23 +89,105 @@ sparse_fold_kernel(int64_t n, int D, const uint8_t* __restrict__ pq, int M, int 
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= n * k) return;
   const int64_t v = gid / k;
-  const int i = min((int)sidx[gid], D - 1);
-  const int d = D / M;
-  const int m = i / d;
-  const uint16_t base = pq_cb[((size_t)m * C + min((int)pq[v * M + m], C - 1)) * d + (i - m * d)];
-  uint16_t corr = 0, val = base;
-  if (Mr > 0) {
-    const int dr = D / Mr;
-    const int mr = i / dr;
-    corr = rvq_cb[((size_t)mr * Cr + min((int)rvq[v * Mr + mr], Cr - 1)) * dr + (i - mr * dr)];
-    val = hadd_bits(base, corr);
+  fold_entry(D, pq + v * M, M, C, pq_cb, Mr > 0 ? rvq + v * Mr : nullptr, Mr, Cr, rvq_cb, sidx[gid], sval[gid],
+             DELTA ? nullptr : out + gid, DELTA ? out + gid : nullptr);
+}
+
+// The warm append of one K/V block in one launch (16 PQ + 16 RVQ subspaces,
+// k sparse entries): plain head-major codes [H][T][16] and sparse entries
+// [H][T][k] of K and V into tokens t_base .. of their tiled stores.  V, and K
+// without KSCORE, go to the tiled layout (rfsn_pack_codes) with the corrected
+// coordinates at the plain positions [H][dst_tokens][k]; K with KSCORE goes
+// to the score-table layout (rfsn_pack_score_codes) with the score deltas as
+// sparse values and, when kcc is given, the corrected coordinates in the
+// plane kcc at the same positions.  One thread per (head, token, row byte
+// j); the threads j < k also fold sparse entry j of K and of V.
+// Token-major rows [cap][H][*] of a reference-layout store (pq, rvq codes,
+// the all-ones RVQ mask of the subspace formats, sparse index / residual);
+// pq == NULL: none.
+struct RingRows {
+  uint8_t* pq;
+  uint8_t* rvq;
+  uint8_t* mask;
+  uint8_t* sidx;
+  uint16_t* sval;
+};
+
+// Copy one token's codes (row byte j, sparse entry j < k) into row rr of a ring.
+__device__ __forceinline__ void ring_put(const RingRows& rg, int64_t rr, int H, int h, int j, int k,
+                                         const uint8_t* __restrict__ pq, const uint8_t* __restrict__ rvq,
+                                         const uint8_t* __restrict__ si, const uint16_t* __restrict__ sv, int64_t row,
+                                         int64_t se) {
+  const int64_t o = rr * H + h;
+  rg.pq[o * 16 + j] = pq[row * 16 + j];
+  rg.rvq[o * 16 + j] = rvq[row * 16 + j];
+  if (j == 0) rg.mask[o] = 1;
+  if (j < k) {
+    rg.sidx[o * k + j] = si[se];
+    rg.sval[o * k + j] = sv[se];
   }
-  const uint16_t c = hadd_bits(val, sval[gid]);
-  if constexpr (DELTA) {
-    const float exact = h2f(base) + (Mr > 0 ? h2f(corr) : 0.f);
-    out[gid] = f2h(h2f(c) - exact);
+}
+
+template <bool KSCORE>
+__global__ void __launch_bounds__(256)
+warm_append_pair_kernel(int64_t T, int C, int Cr, int k, const uint8_t* __restrict__ kpq,
+                        const uint8_t* __restrict__ krvq, const uint8_t* __restrict__ ksi,
+                        const uint16_t* __restrict__ ksv, const uint8_t* __restrict__ vpq,
+                        const uint8_t* __restrict__ vrvq, const uint8_t* __restrict__ vsi,
+                        const uint16_t* __restrict__ vsv, const uint16_t* __restrict__ kpq_cb,
+                        const uint16_t* __restrict__ krvq_cb, const uint16_t* __restrict__ vpq_cb,
+                        const uint16_t* __restrict__ vrvq_cb, uint8_t* __restrict__ dkpq, uint8_t* __restrict__ dkrvq,
+                        uint8_t* __restrict__ dksi, uint16_t* __restrict__ dksv, uint16_t* __restrict__ dkcc,
+                        uint8_t* __restrict__ dvpq, uint8_t* __restrict__ dvrvq, uint8_t* __restrict__ dvsi,
+                        uint16_t* __restrict__ dvsv, int64_t dst_tokens, int64_t t_base, RingRows kring,
+                        RingRows vring, int64_t ring_row) {
+  constexpr int kM = 16, kDim = 64;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int h = blockIdx.y;
+  if (gid >= T * kM) return;
+  const int64_t tl = gid >> 4;
+  const int j = (int)(gid & 15);
+  const int64_t t = t_base + tl;
+  const int64_t row = (int64_t)h * T + tl;  // plain code row of (head, token)
+  const int64_t tau = t >> 5;
+  const int u = (int)((t >> 4) & 1), r = (int)(t & 15);
+  // tiled rows: subspace j of token t (TPI = 4 tokens per gather, IPT = 8)
+  const int64_t to = (int64_t)h * dst_tokens * kM + tau * 32 * kM + ((t % 4) * kM + j) * 8 + (t % 32) / 4;
+  const int64_t pe = (int64_t)h * dst_tokens * k + t * k + j;  // plain sparse position (j < k)
+  if constexpr (KSCORE) {
+    const int m = (j & 12) | ((j & 3) ^ ((r >> 2) & 3));
+    const uint8_t a = kpq[row * kM + m], c = krvq[row * kM + m];
+    const int64_t dst = (int64_t)h * dst_tokens * kM + tau * 512 + r * 32 + (j >> 2) * 8 + u * 4 + (j & 3);
+    const bool odd = (r & 1) != 0;
+    dkpq[dst] = odd ? c : a;
+    dkrvq[dst] = odd ? a : c;
   } else {
-    out[gid] = c;
+    dkpq[to] = kpq[row * kM + j];
+    dkrvq[to] = krvq[row * kM + j];
+  }
+  dvpq[to] = vpq[row * kM + j];
+  dvrvq[to] = vrvq[row * kM + j];
+  if (j < k) {
+    const int64_t se = row * k + j;
+    if constexpr (KSCORE) {
+      const int64_t de = (int64_t)h * dst_tokens * k + tau * 32 * k + r * 2 * k + 2 * j + u;
+      dksi[de] = ksi[se];
+      fold_entry(kDim, kpq + row * kM, kM, C, kpq_cb, krvq + row * kM, kM, Cr, krvq_cb, ksi[se], ksv[se],
+                 dkcc ? dkcc + de : nullptr, dksv + de);
+    } else {
+      dksi[pe] = ksi[se];
+      fold_entry(kDim, kpq + row * kM, kM, C, kpq_cb, krvq + row * kM, kM, Cr, krvq_cb, ksi[se], ksv[se], dksv + pe,
+                 nullptr);
+    }
+    dvsi[pe] = vsi[se];
+    fold_entry(kDim, vpq + row * kM, kM, C, vpq_cb, vrvq + row * kM, kM, Cr, vrvq_cb, vsi[se], vsv[se], dvsv + pe,
+               nullptr);
+  }
+  if (kring.pq) {
+    const int H = (int)gridDim.y;
+    const int64_t se = row * k + j;
+    ring_put(kring, ring_row + tl, H, h, j, k, kpq, krvq, ksi, ksv, row, se);
+    ring_put(vring, ring_row + tl, H, h, j, k, vpq, vrvq, vsi, vsv, row, se);
   }
 }
 
@@ -277,6 +385,48 @@ extern "C" int rfsn_sparse_fold(const rfsn_format* f, const rfsn_codes* codes, i
 extern "C" int rfsn_sparse_delta(const rfsn_format* f, const rfsn_codes* codes, int64_t n, const void* pq_cb,
                                  const void* rvq_cb, void* out, void* stream) {
   return sparse_fold_launch(true, "sparse_delta", f, codes, n, pq_cb, rvq_cb, out, stream);
+}
+
+extern "C" int rfsn_warm_append_pair(const rfsn_format* f, const rfsn_codes* k_src, const rfsn_codes* v_src, int64_t T,
+                                     int32_t heads, const void* k_pq_cb, const void* k_rvq_cb, const void* v_pq_cb,
+                                     const void* v_rvq_cb, const rfsn_codes* k_dst, int32_t k_score_rows, void* k_cc,
+                                     const rfsn_codes* v_dst, int64_t dst_tokens, int64_t t_base,
+                                     const rfsn_codes* k_ring, uint8_t* k_ring_mask, const rfsn_codes* v_ring,
+                                     uint8_t* v_ring_mask, int64_t ring_row, void* stream) {
+  RFSN_REQUIRE(k_score_rows == 0 || k_score_rows == 1, "warm_append_pair: k_score_rows must be 0 or 1");
+  RFSN_REQUIRE(k_cc == nullptr || k_score_rows, "warm_append_pair: a corrected-coordinate plane needs score rows");
+  RFSN_REQUIRE(f && k_src && v_src && k_dst && v_dst, "warm_append_pair: null pointer");
+  RFSN_REQUIRE(f->head_dim == 64 && f->pq_subspaces == 16 && f->rvq_subspaces == 16 && f->sparse_k > 0 &&
+                   f->sparse_k <= 16,
+               "warm_append_pair: needs head_dim 64, 16 PQ and 16 RVQ subspaces and 1..16 sparse entries");
+  RFSN_REQUIRE(f->pq_centroids >= 1 && f->pq_centroids <= 256 && f->rvq_centroids >= 1 && f->rvq_centroids <= 256,
+               "warm_append_pair: codebook sizes must be in [1, 256]");
+  RFSN_REQUIRE(heads > 0 && T >= 0 && t_base >= 0, "warm_append_pair: bad arguments");
+  RFSN_REQUIRE(dst_tokens % 32 == 0 && dst_tokens >= ceil_div(t_base + T, 32) * 32,
+               "warm_append_pair: destination too small (whole 32-token tiles)");
+  const rfsn_codes* all[4] = {k_src, v_src, k_dst, v_dst};
+  for (const rfsn_codes* c : all)
+    RFSN_REQUIRE(c->pq && c->rvq && c->sparse_idx && c->sparse_val, "warm_append_pair: missing code arrays");
+  RFSN_REQUIRE(k_pq_cb && k_rvq_cb && v_pq_cb && v_rvq_cb, "warm_append_pair: missing codebooks");
+  RFSN_REQUIRE((k_ring == nullptr) == (v_ring == nullptr) && ring_row >= 0, "warm_append_pair: rings come as a pair");
+  RingRows kr = {}, vr = {};
+  if (k_ring) {
+    RFSN_REQUIRE(k_ring->pq && k_ring->rvq && k_ring->sparse_idx && k_ring->sparse_val && k_ring_mask && v_ring->pq &&
+                     v_ring->rvq && v_ring->sparse_idx && v_ring->sparse_val && v_ring_mask,
+                 "warm_append_pair: missing ring arrays");
+    kr = {k_ring->pq, k_ring->rvq, k_ring_mask, k_ring->sparse_idx, (uint16_t*)k_ring->sparse_val};
+    vr = {v_ring->pq, v_ring->rvq, v_ring_mask, v_ring->sparse_idx, (uint16_t*)v_ring->sparse_val};
+  }
+  if (T == 0) return RFSN_OK;
+  auto kern = k_score_rows ? warm_append_pair_kernel<true> : warm_append_pair_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)ceil_div(T * 16, 256), (unsigned)heads), dim3(256), 0,
+                     (hipStream_t)stream, T, f->pq_centroids, f->rvq_centroids, f->sparse_k, k_src->pq, k_src->rvq,
+                     k_src->sparse_idx, (const uint16_t*)k_src->sparse_val, v_src->pq, v_src->rvq, v_src->sparse_idx,
+                     (const uint16_t*)v_src->sparse_val, (const uint16_t*)k_pq_cb, (const uint16_t*)k_rvq_cb,
+                     (const uint16_t*)v_pq_cb, (const uint16_t*)v_rvq_cb, k_dst->pq, k_dst->rvq, k_dst->sparse_idx,
+                     (uint16_t*)k_dst->sparse_val, (uint16_t*)k_cc, v_dst->pq, v_dst->rvq, v_dst->sparse_idx,
+                     (uint16_t*)v_dst->sparse_val, dst_tokens, t_base, kr, vr, ring_row);
+  return check_launch("warm_append_pair");
 }
 
 extern "C" int rfsn_decode_ref(const uint8_t* pq, int64_t n, int32_t D, int32_t M, int32_t C, const void* pq_cb,

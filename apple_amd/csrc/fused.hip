@@ -316,15 +316,19 @@ __device__ __forceinline__ void load_tile(TileRegs<M, RVQ, KS>& r, const WarmBas
 
 // Rows [16u, 16u+16) of one exact (hot) tile, this lane's two 16-byte units:
 // rows [off, off+count) of hot[...][D] (rows past count re-read the last valid
-// row and are zeroed when stored).  A tile's four halves (K and V) are loaded
-// together, so that it waits for one memory round trip.
+// row and are zeroed when stored).  Hot tokens from app_first on are the
+// launch's appended tokens, read from the caller's rows app + j*app_ld (j =
+// token - app_first) instead of the hot buffers.  A tile's four halves (K and
+// V) are loaded together, so that it waits for one memory round trip.
 __device__ __forceinline__ void load_hot_half(uint4 (&v)[2], const TileSrc& src, const uint16_t* __restrict__ hot,
-                                              int lane, int u) {
+                                              int lane, int u, const uint16_t* __restrict__ app, int app_first,
+                                              int64_t app_ld) {
   const int u16 = lane & 7;  // 16-byte unit of the row
 #pragma unroll
   for (int k2 = 0; k2 < 2; ++k2) {
-    const int row = min(16 * u + (lane >> 3) + 8 * k2, src.count - 1);
-    v[k2] = *reinterpret_cast<const uint4*>(hot + (int64_t)(src.off + row) * kD + u16 * 8);
+    const int row = src.off + min(16 * u + (lane >> 3) + 8 * k2, src.count - 1);
+    const uint16_t* a = row >= app_first ? app + (int64_t)(row - app_first) * app_ld : hot + (int64_t)row * kD;
+    v[k2] = *reinterpret_cast<const uint4*>(a + u16 * 8);
   }
 }
 // Store a loaded half into the wave's half-tile buffer (rows past count -> 0).
@@ -725,6 +729,10 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
   const int t_end = min(total_tiles, t_begin + tiles_per_split);
   const uint16_t* hotk = (const uint16_t*)p.hot_k + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
   const uint16_t* hotv = (const uint16_t*)p.hot_v + (int64_t)b * p.hot_seq_stride + (int64_t)h * p.hot_cap * kD;
+  // the launch's appended tokens: hot tokens app_first .. hot_len - 1
+  const int app_first = p.hot_len - p.app_count;
+  const uint16_t* appk = p.app_count ? (const uint16_t*)p.app_k + (int64_t)h * kD : hotk;
+  const uint16_t* appv = p.app_count ? (const uint16_t*)p.app_v + (int64_t)h * kD : hotv;
 
 
   using Regs = TileRegs<M, RVQ, KS>;
@@ -1135,8 +1143,8 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
     uint4 hk[2][2], hv[2][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      load_hot_half(hk[u], src, hotk, lane, u);
-      load_hot_half(hv[u], src, hotv, lane, u);
+      load_hot_half(hk[u], src, hotk, lane, u, appk, app_first, p.app_ld);
+      load_hot_half(hv[u], src, hotv, lane, u, appv, app_first, p.app_ld);
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -1309,6 +1317,16 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
         float s2 = qv * qv * gw[lane];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) s2 += __shfl_xor(s2, o, 64);
+        // vmax also covers the launch's appended V rows (their fold into
+        // the guard row may land after this read)
+        uint32_t vb = __builtin_bit_cast(uint32_t, gw[64]);
+        for (int i = lane; i < p.app_count * p.kv_heads * kD; i += 64) {
+          const int j = i / (p.kv_heads * kD), r = i - j * (p.kv_heads * kD);
+          vb = max(vb, __builtin_bit_cast(uint32_t, fabsf(h2f(((const uint16_t*)p.app_v)[(int64_t)j * p.app_ld + r]))));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) vb = max(vb, (uint32_t)__shfl_xor((int)vb, o, 64));
+        const float vmax = __builtin_bit_cast(float, vb);
         if (lane == 0) {
           float Mx = -__builtin_inff();
           for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, red_m[w * 8 + wave]);
@@ -1320,7 +1338,7 @@ __device__ __forceinline__ bool attn_body(const rfsn_fused_params& p, int splits
             Q += red_q[w * 8 + wave] * f * f;
           }
           const float sigma = p.scale * sqrtf(kDriftVar * s2);
-          const float e = Ls > 0.f ? sigma * sqrtf(Q) / Ls * 2.f * gw[64] : 0.f;
+          const float e = Ls > 0.f ? sigma * sqrtf(Q) / Ls * 2.f * vmax : 0.f;
           est[wave] = e;
           if (p.drift) p.drift[((int64_t)b * p.q_heads + h * G + wave) * slots + p.part_base + split] = e;
         }
@@ -1368,12 +1386,47 @@ __device__ __noinline__ void exact_rows_pass(const rfsn_fused_params p, int spli
   attn_body<M, RVQ, KS, NHG, kExactRows>(p, splits, tiles_per_split, blocks_total, lds);
 }
 
+// The launch's appended tokens (app_count of them, rows in the caller's
+// buffers) into their hot slots hot_len - app_count .. for KV head h, and
+// max |v| over them into *app_vabs.  Run by the first split of sequence 0 of
+// each KV head; the launch itself reads these tokens from the caller's rows,
+// so no block waits for the copy.
+__device__ __forceinline__ void append_hot_tokens(const rfsn_fused_params& p, int h) {
+  constexpr int kUnits = kD / 8;  // 16-byte units of a row
+  const int per = p.app_count * kUnits;
+  const int i = threadIdx.x;
+  if (i >= 2 * per) return;
+  const bool is_v = i >= per;
+  const int j = (is_v ? i - per : i) / kUnits, u = i % kUnits;
+  const uint16_t* src = (const uint16_t*)(is_v ? p.app_v : p.app_k) + (int64_t)j * p.app_ld + h * kD + u * 8;
+  uint16_t* dst = (uint16_t*)(is_v ? p.hot_v : p.hot_k) +
+                  ((int64_t)h * p.hot_cap + (p.hot_len - p.app_count) + j) * kD + u * 8;
+  const uint4 w = *reinterpret_cast<const uint4*>(src);
+  *reinterpret_cast<uint4*>(dst) = w;
+  if (is_v && p.app_vabs) {
+    // float bits compared as integers: |v| >= 0, NaN bits order above +inf
+    uint32_t m = 0;
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m = max(m, __builtin_bit_cast(uint32_t, fabsf(h2f((uint16_t)(ww[e] & 0xFFFFu)))));
+      m = max(m, __builtin_bit_cast(uint32_t, fabsf(h2f((uint16_t)(ww[e] >> 16)))));
+    }
+    atomicMax(p.app_vabs, m);
+  }
+}
+
 template <int M, bool RVQ, int KS, int NHG, int KM>
 __global__ void __launch_bounds__(BlockShape<NHG>::T, 1)
 fused_decode_attn_kernel(const rfsn_fused_params p, int splits, int tiles_per_split, int blocks_total) {
   // static allocation: its base address is known at compile time, so LDS
   // addresses built in registers need no base add
   __shared__ __align__(16) uint8_t lds[BlockShape<NHG>::L];
+  if (p.app_count > 0) {  // uniform
+    int b, h, split;
+    block_unit(blocks_total, splits, p.kv_heads, b, h, split);
+    if (b == 0 && split == 0) append_hot_tokens(p, h);
+  }
   const bool redo = attn_body<M, RVQ, KS, NHG, KM>(p, splits, tiles_per_split, blocks_total, lds);
   if constexpr (KM == kTables) {
     if (redo) {  // uniform
@@ -1548,6 +1601,18 @@ extern "C" int rfsn_fused_decode_attention(const rfsn_fused_params* p, void* str
                "fused: entry tables come as a 16-byte aligned K and V pair of 64 KB per sequence (stride 0 or >= 65536)");
   const size_t wsb = rfsn_fused_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "fused: workspace too small");
+  RFSN_REQUIRE(p->app_count >= 0 && p->app_count <= kTile && p->app_count <= p->hot_len,
+               "fused: app_count must be in [0, 32] and within hot_len");
+  RFSN_REQUIRE(p->app_count == 0 ||
+                   (p->app_k && p->app_v && p->app_ld >= (int64_t)p->kv_heads * kD && p->app_ld % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(p->app_k) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(p->app_v) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(p->hot_k) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(p->hot_v) % 16 == 0 && p->hot_cap % 8 == 0),
+               "fused: appended rows need K and V pointers, a token stride of at least kv_heads * 64 (a multiple "
+               "of 8) and 16-byte alignment of them and of the hot buffers");
+  RFSN_REQUIRE(p->app_count == 0 || p->hot_seq_stride == 0 || p->batch == 1,
+               "fused: appending in the launch needs one hot tier shared by the sequences (hot_seq_stride 0)");
   hipStream_t s = (hipStream_t)stream;
   const bool rvq = f.rvq_subspaces > 0;
   if (f.pq_subspaces == 16) return rvq ? dispatch_ks<16, true>(p, s) : dispatch_ks<16, false>(p, s);

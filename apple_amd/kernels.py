@@ -679,6 +679,7 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
     fl = FusedLaunch(p, [q, out, qp, seg_t, nseg_t, *tmap[:2], workspace, segments, *cbs, guard, drift,
                          *(tables or ())], out, _stream(q))
     fl.drift = drift
+    fl.seg_table = seg_t
     if not launch:
         return fl
     fl()
@@ -860,6 +861,7 @@ class FusedLaunch:
         self.out = out
         self.stream = stream
         self.drift: Optional[torch.Tensor] = None  # [B, Hq, slots] drift estimates of the guard, if any
+        self.seg_table: Optional[torch.Tensor] = None  # the device rfsn_segment table the launch reads
         self._fn = L.load().rfsn_fused_decode_attention
         self._ref = C.byref(self.params)
 

@@ -256,8 +256,8 @@ def _encode_pair_head_major(keys: torch.Tensor, values: torch.Tensor, kq: Hybrid
     T, H, D = keys.shape
     if T == 0:
         return None
-    hm = [t.to(device=kq.device, dtype=torch.float16).permute(1, 0, 2).contiguous().view(H * T, D)
-          for t in (keys, values)]
+    hm = [(t if t.dtype is torch.float16 and t.device == kq.device else t.to(device=kq.device, dtype=torch.float16))
+          .permute(1, 0, 2).contiguous().view(H * T, D) for t in (keys, values)]
     outs = K.warm_encode_batch([(hm[0], kq.pq.codebooks, kq.rvq_codebooks),
                                 (hm[1], vq.pq.codebooks, vq.rvq_codebooks)], fmt)
     shape = lambda t: None if t is None else t.view(H, T, -1)

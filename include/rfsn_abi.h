@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 5
+#define RFSN_ABI_VERSION 6
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -154,6 +154,29 @@ int rfsn_sparse_fold(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
  * rfsn_sparse_fold). */
 int rfsn_sparse_delta(const rfsn_format* fmt, const rfsn_codes* codes, int64_t n,
                       const void* pq_cb_dev, const void* rvq_cb_dev, void* out_dev, void* stream);
+
+/* The warm append of one block of K and V in one launch, for the 16 + 16
+ * subspace formats of head_dim 64 with 1..16 sparse entries: plain
+ * head-major codes k_src / v_src ([heads][T][16] codes, [heads][T][k] sparse
+ * index bytes and fp16 residuals, contiguous) into tokens t_base ..
+ * t_base+T-1 of blocks of dst_tokens tokens (a multiple of 32) per head.  V,
+ * and K with k_score_rows = 0, go to the rfsn_pack_codes layout with the
+ * corrected coordinates of rfsn_sparse_fold at [heads][dst_tokens][k]; K
+ * with k_score_rows = 1 goes to the rfsn_pack_score_codes layout with the
+ * score deltas of rfsn_sparse_delta as its sparse values and, when k_cc is
+ * not NULL, the corrected coordinates in the array k_cc at the same
+ * positions.  With k_ring / v_ring (NULL: none) the plain codes also go to
+ * rows ring_row .. ring_row+T-1 of token-major stores in the reference
+ * layout (CompressedTensorMLX: pq and rvq codes [cap][heads][16], the RVQ
+ * mask [cap][heads] set to 1, sparse index and residual [cap][heads][k]).
+ * The same bytes as those calls and copies, in one launch instead of up to
+ * twelve.  Replaces the warm append of cache.py:122-132. */
+int rfsn_warm_append_pair(const rfsn_format* fmt, const rfsn_codes* k_src, const rfsn_codes* v_src, int64_t T,
+                          int32_t heads, const void* k_pq_cb_dev, const void* k_rvq_cb_dev, const void* v_pq_cb_dev,
+                          const void* v_rvq_cb_dev, const rfsn_codes* k_dst, int32_t k_score_rows, void* k_cc_dev,
+                          const rfsn_codes* v_dst, int64_t dst_tokens, int64_t t_base,
+                          const rfsn_codes* k_ring, uint8_t* k_ring_mask_dev, const rfsn_codes* v_ring,
+                          uint8_t* v_ring_mask_dev, int64_t ring_row, void* stream);
 
 /* Reference-format hybrid decode (quantization.py:310-319): base =
  * C_pq[pq_codes]; corr = fp16(sum_l C_l[rvq_codes[a][l]]) scattered to rows
@@ -336,6 +359,23 @@ typedef struct rfsn_fused_params {
   const void* k_tab;
   const void* v_tab;
   int64_t tab_stride;
+  /* Append in the launch (optional; app_count = 0: none).  The hot range
+   * [0, hot_len) ends with app_count (<= 32) new tokens whose K and V rows
+   * are still in the caller's buffers, token j of KV head h at
+   * app_k + j*app_ld + h*D (fp16 elements, 16-byte aligned rows), not in the
+   * hot buffers yet: the launch attends them from there, writes them to hot
+   * tokens hot_len - app_count .. hot_len - 1 (blocks of sequence 0, so the
+   * next launch finds them in place), and folds max |v| over them into
+   * *app_vabs (float bits as an unsigned maximum; may be NULL), which the
+   * drift guard's vmax also takes.  Needs hot_seq_stride = 0 (the sequences
+   * share one hot tier).  The reference appends in cache.py:89-120 and
+   * attends in cache.py:395-428; this fuses the two for a decode loop's
+   * one-token step (rfsn_v10_mlx_ane_complete.py:138-158). */
+  const void* app_k;
+  const void* app_v;
+  int64_t app_ld;
+  uint32_t* app_vabs;
+  int32_t app_count;
 } rfsn_fused_params;
 
 /* Token splits the call would use (p->splits, or the automatic choice when 0);

@@ -154,3 +154,59 @@ def test_csv_byte_known_answers(device, tmp_path, T_, mode, cache_bytes):
     mem = c.memory_usage_bytes()
     assert mem["hot_bytes"] + mem["warm_pq_bytes"] + mem["warm_rvq_bytes"] == cache_bytes
     assert mem == o.memory_usage_bytes()
+
+
+def test_warm_append_pair_matches_per_store_appends(device):
+    """rfsn_warm_append_pair (one launch for a K/V block) writes the same
+    bytes as the per-store appends (sparse fold and delta, score-row and
+    tiled packing): every array of both stores, K's corrected-coordinate
+    plane included, bit for bit, for a block that starts inside a tile, with
+    K as score-table rows and as tiled rows."""
+    from types import SimpleNamespace
+
+    from apple_amd import kernels as K
+
+    fmt = K.WarmFormat(64, 16, 256, 16, 256, 4)
+    g = rng(77)
+    Hh = 4
+    qz = [SimpleNamespace(pq=SimpleNamespace(codebooks=T(rand_codebooks(g, 16, 256, 4), device)),
+                          rvq_codebooks=T(rand_codebooks(g, 16, 256, 4) * np.float16(0.35), device)) for _ in range(2)]
+
+    def block(n):
+        out = []
+        for _ in range(2):
+            pq = T(g.integers(0, 256, (Hh, n, 16), dtype=np.uint8), device)
+            rvq = T(g.integers(0, 256, (Hh, n, 16), dtype=np.uint8), device)
+            si = T(np.stack([np.stack([g.choice(64, 4, replace=False) for _ in range(n)]) for _ in range(Hh)])
+                   .astype(np.uint8), device)
+            sv = T(randn16(g, Hh, n, 4, scale=0.2), device)
+            out.append((pq, rvq, si, sv))
+        return out
+
+    for score in (True, False):
+        _pair_case(device, fmt, Hh, qz, block, score)
+
+
+def _pair_case(device, fmt, Hh, qz, block, score):
+    from apple_amd.cache import TiledCodes
+
+    stores = []
+    for _ in range(2):
+        stores.append((TiledCodes(fmt, Hh, device, cap=128, score_rows=score, exact_plane=score),
+                       TiledCodes(fmt, Hh, device, cap=128)))
+    first, second = block(40), block(29)
+    for kt, vt in stores:
+        for t, c, q in ((kt, first[0], qz[0]), (vt, first[1], qz[1])):
+            t.append(*c, q.pq.codebooks, q.rvq_codebooks)
+    a, b = stores
+    for t, c, q in ((a[0], second[0], qz[0]), (a[1], second[1], qz[1])):
+        t.append(*c, q.pq.codebooks, q.rvq_codebooks)
+    assert TiledCodes.append_pair(b[0], b[1], second[0], second[1], qz[0], qz[1])
+    assert (a[0].len, a[1].len) == (b[0].len, b[1].len) == (69, 69)
+    for x, y in zip(a, b):
+        assert set(x.t) == set(y.t)
+        for key in x.t:
+            if x.t[key] is not None:
+                assert torch.equal(x.t[key].view(torch.uint8), y.t[key].view(torch.uint8)), key
+    # a block past the capacity is refused (the per-store append grows the stores)
+    assert not TiledCodes.append_pair(b[0], b[1], *block(60)[:2], qz[0], qz[1])

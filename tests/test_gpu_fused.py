@@ -698,8 +698,9 @@ def test_decode_session_streaming(device):
     every 32 steps, and warm overflow migrates whole 64-token chunks), the
     router's 4 nearest chunks attended.  Every step is within 2e-3 of the
     oracle over the step's window; the hot tier holds the newest tokens bit
-    for bit; the launch is rebuilt only when a step demotes, migrates or
-    changes the chunk set."""
+    for bit; the launch is rebuilt only when a step migrates chunks or
+    changes the chunk set, and a demotion that leaves the segments in place
+    (warm grows at its tail) patches the prepared launch instead."""
     from apple_amd.quantization import HybridQuantizerMLX
     from apple_amd.storage import AsyncHierarchicalRouterMLX, RFSNConfig
     from apple_amd.cache import RFSNv10KVCacheMLX
@@ -744,6 +745,7 @@ def test_decode_session_streaming(device):
     for tier, src in ((cache.hot_keys, keys), (cache.hot_values, values)):  # [T_hot, H, D], oldest first
         assert np.array_equal(H(tier.contiguous()).view(np.uint16), src[total - cache.num_hot:total].view(np.uint16))
     assert sess.rebuilds <= changes + 1 and sess.rebuilds < steps // 4, (sess.rebuilds, changes)
+    assert sess.regrows >= 1, (sess.rebuilds, sess.regrows, changes)
 
 
 def test_cold_chunks_npz_roundtrip(device, tmp_path):
