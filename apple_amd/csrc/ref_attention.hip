@@ -262,6 +262,33 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
   }
 }
 
+// Splits balance the work, not the tokens: an exact (hot) token costs
+// kExactCost and a coded one kCodedCost (at the reference's default config
+// one block's coded tokens took 2.6x its exact ones: 214 us for 24,576 coded
+// tokens per head against 28 us for 8,192 exact ones).  Split s covers the
+// tokens t with bound(s) <= t < bound(s + 1), bound(s) = the first token
+// whose cost prefix reaches s / splits of the total: a partition of the
+// window whatever the segments (uniform scalar arithmetic).
+constexpr int kExactCost = 2, kCodedCost = 5;
+
+__device__ __forceinline__ int split_bound(cref segs, int nseg, int64_t total_cost, int splits, int s) {
+  if (s <= 0) return 0;
+  const int64_t target = (int64_t)s * total_cost;  // prefix * splits >= target
+  int64_t prefix = 0;
+  int base = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const int len = segs[i].len;
+    const int64_t c = segs[i].k.pq != nullptr ? kCodedCost : kExactCost;
+    const int64_t need = target - prefix * splits;
+    if (need <= 0) return base;
+    const int64_t k = (need + c * splits - 1) / (c * splits);  // tokens of this segment before the bound
+    if (k < len) return base + (int)k;
+    prefix += (int64_t)len * c;
+    base += len;
+  }
+  return base;
+}
+
 // Lane geometry: a wave holds P token groups of 64 / P lanes, and lane ll of
 // a group owns coordinates c0 = DPL * ll .. c0 + DPL - 1 (DPL = D * P / 64),
 // so one instruction serves P tokens.  A wave takes U * P consecutive tokens
@@ -334,7 +361,12 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
   rs.dr = p.rvq_subspaces > 0 ? D / p.rvq_subspaces : 0;
   rs.k = p.sparse_k;
   const cref segs = (cref)p.segments;
-  const int begin = split * tps, end = min(p.total_tokens, begin + tps);
+  int64_t total_cost = 0;
+  for (int s = 0; s < p.num_segments; ++s)
+    total_cost += (int64_t)segs[s].len * (segs[s].k.pq != nullptr ? kCodedCost : kExactCost);
+  const int begin = split_bound(segs, p.num_segments, total_cost, splits, split);
+  const int end = min(p.total_tokens, split_bound(segs, p.num_segments, total_cost, splits, split + 1));
+  (void)tps;
   int seg_base = 0;
   for (int s = 0; s < p.num_segments; ++s) {
     const int len = segs[s].len;
