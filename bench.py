@@ -375,7 +375,7 @@ def bench_ref(w, args, dev) -> dict:
         ref = cb.ref_decode_step(q[:, :hs], hk_c, hv_c, warm_c[0], warm_c[1], cbs, scale, 128)
         cpu_err = float((out[:, :hs].float().cpu() - ref.float()).abs().max())
         reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < 10.0 or reps == 0:
+        while time.perf_counter() - t0 < 10.0 * args.cpu_budget or reps == 0:
             cb.ref_decode_step(q[:, :hs], hk_c, hv_c, warm_c[0], warm_c[1], cbs, scale, 128)
             reps += 1
         sec = (time.perf_counter() - t0) / reps * (H / hs)
@@ -949,6 +949,8 @@ def main(argv=None) -> int:
         result["longctx_128k"] = sub_record(bench_longctx(WORKLOADS["longctx_128k"], sub, dev))
         log("sub-record refencode_4k")
         result["refencode_4k"] = sub_record(bench_refencode(REF_WORKLOADS["refencode_4k"], sub, dev))
+        log("sub-record refdefault_32k")
+        result["refdefault_32k"] = sub_record(bench_ref(REF_WORKLOADS["refdefault_32k"], sub, dev))
     print(json.dumps(result), flush=True)
     return 0
 
