@@ -740,6 +740,14 @@ def test_decode_session_streaming(device):
         ref = nx.blockwise_attention(q, wk, wv, 0.125, 256, False, None)
         err = np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max()
         assert err <= TOL, (i, err)
+        # a launch prepared afresh over the cache after the step, with the
+        # session's split count, gives the same bits: the launch that appended
+        # the token itself, or was patched after a demotion, attended the same
+        # window as one built from the cache's state
+        if sess._launch is not None:
+            fresh = torch.empty_like(qd)
+            cache.prepare(qd, causal=False, cold_chunks=ids, splits=int(sess._launch.params.splits), out=fresh)()
+            assert torch.equal(fresh, out), (i, sess.rebuilds, sess.regrows)
     total = total0 + steps
     assert cache.total_tokens == total and cache.num_hot + cache.num_warm + cache.num_cold == total
     for tier, src in ((cache.hot_keys, keys), (cache.hot_values, values)):  # [T_hot, H, D], oldest first
