@@ -76,7 +76,8 @@ class RefParams(C.Structure):
                 ("q", vp), ("out", vp), ("scale", f32), ("causal", i32), ("qpos", vp),
                 ("segments", vp), ("num_segments", i32), ("total_tokens", i32),
                 ("k_pq_cb", vp), ("v_pq_cb", vp), ("k_rvq_cb", vp), ("v_rvq_cb", vp),
-                ("splits", i32), ("workspace", vp), ("workspace_bytes", sz)]
+                ("splits", i32), ("workspace", vp), ("workspace_bytes", sz),
+                ("score_tables", i32), ("table_tol", f32), ("table_stats", vp), ("drift", vp)]
 
 
 class EncodeJob(C.Structure):
@@ -98,6 +99,8 @@ SIGNATURES = {
     "rfsn_hot_append": (i32, [vp, vp, i64, i32, i32, i32, vp, vp, i64, i64, vp, vp]),
     "rfsn_ref_attention_workspace_bytes": (sz, [C.POINTER(RefParams)]),
     "rfsn_ref_attention": (i32, [C.POINTER(RefParams), vp]),
+    "rfsn_ref_tables_ok": (i32, [C.POINTER(RefParams)]),
+    "rfsn_ref_table_stats": (i32, [C.POINTER(RefParams), vp, vp]),
     "rfsn_read_stream": (i32, [vp, i64, vp, i32, vp]),
     "rfsn_rvq_gate": (i32, [vp, i64, i32, i64, f32, vp, vp]),
     "rfsn_mask_compact_workspace_bytes": (sz, [i64]),
@@ -152,7 +155,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 6:
+    if lib.rfsn_abi_version() != 7:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

@@ -26,6 +26,9 @@ from . import kernels as K
 from .quantization import HybridQuantizerMLX, _decode_compressed_tensor
 from .storage import MASK_FILL_VALUE, CompressedTensorMLX, RFSNConfig
 
+# query heads (queries x heads) up to which the fused path uses score tables
+REF_TABLES_MAX_QUERY_HEADS = 256
+
 logger = logging.getLogger("RFSN_ATTENTION")
 
 Positions = Optional[Union[Sequence[int], torch.Tensor]]
@@ -111,12 +114,30 @@ class RFSNHybridAttentionMLX:
         pos = _normalize_query_positions(query_positions, B, Hq, T - 1, dev) if causal else None
         cb, rcb = quantizer.pq.codebooks, quantizer.rvq_codebooks
         f = quantizer.warm_format()
+        # score tables with their drift guard (config.score_table_tolerance)
+        # for decode-sized calls of the reference format
+        tol = quantizer.config.score_table_tolerance
+        tables = {}
+        if tol is not None and not quantizer.subspace and B * Hq <= REF_TABLES_MAX_QUERY_HEADS:
+            tables = dict(score_tables=float(tol), table_stats=self._table_stats(quantizer))
         out = K.ref_attention(q.to(device=dev, dtype=torch.float16), kv_heads=key_store.num_heads,
                               scale=self.scale, causal=causal, qpos=pos,
                               segments=[K.ref_store_segment(kst, vst, 0, T, 0)], k_pq_cb=cb, v_pq_cb=cb,
                               k_rvq_cb=rcb, v_rvq_cb=rcb, rvq_subspaces=f.rvq_subspaces if quantizer.subspace else 0,
-                              sparse_k=f.sparse_k if quantizer.subspace else 0)
+                              sparse_k=f.sparse_k if quantizer.subspace else 0, **tables)
         return out.to(q.dtype)
+
+    def _table_stats(self, quantizer: HybridQuantizerMLX) -> torch.Tensor:
+        """The score tables' guard statistics of the quantizer's codebooks,
+        rebuilt when the quantizer or a codebook changes."""
+        cbs = (quantizer.pq.codebooks, quantizer.rvq_codebooks)
+        key = (quantizer,) + cbs + tuple(None if t is None else t._version for t in cbs)
+        memo = getattr(self, "_stats_memo", None)
+        if memo is None or len(memo[0]) != len(key) or not all(
+                (a is b) if not isinstance(a, int) else a == b for a, b in zip(memo[0], key)):
+            memo = (key, K.ref_table_stats(cbs[0], cbs[0], cbs[1], cbs[1]))
+            self._stats_memo = memo
+        return memo[1]
 
 
 def _on(store: CompressedTensorMLX, device) -> CompressedTensorMLX:

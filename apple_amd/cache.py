@@ -451,6 +451,11 @@ def _plain_head_major(store: CompressedTensorMLX):
     return pm(store.pq_codes), pm(store.rvq_codes), pm(store.sparse_idx), pm(store.sparse_val)
 
 
+# query heads (queries x heads) up to which the reference-format path uses
+# score tables: each query head builds its own table and histograms
+REF_TABLES_MAX_QUERY_HEADS = 256
+
+
 class _CodebookKey:
     """Memo key of tables built from a quantizer pair's codebooks.  It holds
     the objects themselves (compared by identity, so a freed tensor's address
@@ -536,6 +541,12 @@ class RFSNv10KVCacheMLX:
         self._tables_key: Optional[_CodebookKey] = None
         self._tables: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self.last_drift: Optional[torch.Tensor] = None
+        # score tables of the reference-format path: codebook statistics of
+        # their drift guard, whether the last call used them, its estimates
+        self._ref_stats_key: Optional[_CodebookKey] = None
+        self._ref_stats: Optional[torch.Tensor] = None
+        self.last_ref_tables = False
+        self.last_ref_drift: Optional[torch.Tensor] = None
         self.last_access_stats = self._empty_access_stats()
 
     # ------------------------------------------------------------------ stats
@@ -646,6 +657,17 @@ class RFSNv10KVCacheMLX:
             torch.maximum(self._vabs, vcb.view(1), out=self._vabs)
             self._guard_key = key
         return self._guard
+
+    def _ref_table_stats(self) -> torch.Tensor:
+        """The reference-format score tables' guard statistics
+        (``kernels.ref_table_stats``), rebuilt when a codebook changes."""
+        kq, vq = self._kq, self._vq
+        cbs = (kq.pq.codebooks, vq.pq.codebooks, kq.rvq_codebooks, vq.rvq_codebooks)
+        key = _CodebookKey((kq, vq) + cbs, tuple(None if t is None else t._version for t in cbs))
+        if self._ref_stats_key != key:
+            self._ref_stats = K.ref_table_stats(*cbs)
+            self._ref_stats_key = key
+        return self._ref_stats
 
     def _entry_tables(self, rvq: bool) -> Tuple[torch.Tensor, torch.Tensor]:
         """The fused kernel's entry-major K and V tables (``kernels.entry_tables``),
@@ -1590,10 +1612,23 @@ class RFSNv10KVCacheMLX:
         qpos = _normalize_query_positions(adjusted, B, Hq, pos - 1, self.device) if causal else None
         kq, vq = self._kq, self._vq
         sub = self._fmt() if self._subspace else None
+        # decode steps of the reference format: score tables with their drift
+        # guard (config.score_table_tolerance), as the tiled path uses them
+        tol = self.config.score_table_tolerance
+        tables = {}
+        self.last_ref_drift = None
+        if tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS:
+            self.last_ref_drift = torch.empty((B, Hq), dtype=torch.float32, device=self.device)
+            tables = dict(score_tables=float(tol), table_stats=self._ref_table_stats(), drift=self.last_ref_drift)
+        info = {}
         out = K.ref_attention(q.to(torch.float16), kv_heads=self.H, scale=self.D ** -0.5, causal=causal, qpos=qpos,
                               segments=segs, k_pq_cb=kq.pq.codebooks, v_pq_cb=vq.pq.codebooks,
                               k_rvq_cb=kq.rvq_codebooks, v_rvq_cb=vq.rvq_codebooks,
-                              rvq_subspaces=sub.rvq_subspaces if sub else 0, sparse_k=sub.sparse_k if sub else 0)
+                              rvq_subspaces=sub.rvq_subspaces if sub else 0, sparse_k=sub.sparse_k if sub else 0,
+                              info=info, **tables)
+        self.last_ref_tables = bool(info.get("score_tables"))
+        if not self.last_ref_tables:
+            self.last_ref_drift = None
         return out.to(q.dtype)
 
     def prepare(self, q: torch.Tensor, causal: bool = True, query_positions=None,

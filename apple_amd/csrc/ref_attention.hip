@@ -269,16 +269,23 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
 // tokens t with bound(s) <= t < bound(s + 1), bound(s) = the first token
 // whose cost prefix reaches s / splits of the total: a partition of the
 // window whatever the segments (uniform scalar arithmetic).
+// With score tables, the coded tokens of a group that keeps the tables'
+// result cost 0: the splits partition its exact tokens.
 constexpr int kExactCost = 2, kCodedCost = 5;
 
-__device__ __forceinline__ int split_bound(cref segs, int nseg, int64_t total_cost, int splits, int s) {
+__device__ __forceinline__ int split_bound(cref segs, int nseg, int64_t total_cost, int splits, int s,
+                                           int coded_cost) {
   if (s <= 0) return 0;
   const int64_t target = (int64_t)s * total_cost;  // prefix * splits >= target
   int64_t prefix = 0;
   int base = 0;
   for (int i = 0; i < nseg; ++i) {
     const int len = segs[i].len;
-    const int64_t c = segs[i].k.pq != nullptr ? kCodedCost : kExactCost;
+    const int64_t c = segs[i].k.pq != nullptr ? coded_cost : kExactCost;
+    if (c == 0) {
+      base += len;
+      continue;
+    }
     const int64_t need = target - prefix * splits;
     if (need <= 0) return base;
     const int64_t k = (need + c * splits - 1) / (c * splits);  // tokens of this segment before the bound
@@ -295,8 +302,8 @@ __device__ __forceinline__ int split_bound(cref segs, int nseg, int64_t total_co
 // per step.  EXT: the long-context format (subspace RVQ stage, sparse
 // residuals); otherwise the reference format (gated RVQ) or PQ only.
 template <int D, int P, int U, int GMAX, bool EXT>
-__global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_eu(GMAX == 1 ? 4 : 1))) ref_attn_kernel(const rfsn_ref_params p, int splits, int tps,
-                                                               int kv_tab_shared) {
+__global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_eu(GMAX == 1 ? 4 : 1))) ref_attn_kernel(const rfsn_ref_params p, int splits, int slots,
+                                                               int kv_tab_shared, const float* __restrict__ tab_est) {
   extern __shared__ __align__(16) uint16_t tabs[];
   constexpr int DPL = D * P / 64;
   constexpr int LG = 64 / P;  // lanes per token group
@@ -361,17 +368,25 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
   rs.dr = p.rvq_subspaces > 0 ? D / p.rvq_subspaces : 0;
   rs.k = p.sparse_k;
   const cref segs = (cref)p.segments;
+  // score tables: the group's coded tokens are the tables' unless the drift
+  // estimate of one of its heads exceeds the tolerance (uniform)
+  bool skip_coded = false;
+  if (tab_est != nullptr) {
+    bool redo = false;
+    for (int g = 0; g < G; ++g) redo = redo || !(tab_est[(int64_t)b * p.q_heads + h * G + g] <= p.table_tol);
+    skip_coded = !redo;
+  }
+  const int coded_cost = skip_coded ? 0 : kCodedCost;
   int64_t total_cost = 0;
   for (int s = 0; s < p.num_segments; ++s)
-    total_cost += (int64_t)segs[s].len * (segs[s].k.pq != nullptr ? kCodedCost : kExactCost);
-  const int begin = split_bound(segs, p.num_segments, total_cost, splits, split);
-  const int end = min(p.total_tokens, split_bound(segs, p.num_segments, total_cost, splits, split + 1));
-  (void)tps;
+    total_cost += (int64_t)segs[s].len * (segs[s].k.pq != nullptr ? coded_cost : kExactCost);
+  const int begin = split_bound(segs, p.num_segments, total_cost, splits, split, coded_cost);
+  const int end = min(p.total_tokens, split_bound(segs, p.num_segments, total_cost, splits, split + 1, coded_cost));
   int seg_base = 0;
   for (int s = 0; s < p.num_segments; ++s) {
     const int len = segs[s].len;
     const int lo = max(begin, seg_base), hi = min(end, seg_base + len);
-    if (lo < hi) {
+    if (lo < hi && !(skip_coded && segs[s].k.pq != nullptr)) {
       rfsn_ref_store_codes kc{}, vc{};  // field by field: the table lives in the constant address space
       kc.pq = segs[s].k.pq;
       kc.rvq = segs[s].k.rvq;
@@ -501,12 +516,12 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
       A += red_a[(w * kRefMaxG + g) * D + c] * f;
     }
     const int hq = h * G + g;
-    if (splits == 1) {
+    if (slots == 1) {
       // a query with no allowed key returns zeros (attention.py:104-105)
       ((uint16_t*)p.out)[((int64_t)b * p.q_heads + hq) * D + c] = f2h(Ls > 0.f ? A / Ls : 0.f);
       continue;
     }
-    float* o = reinterpret_cast<float*>(p.workspace) + (((int64_t)b * p.q_heads + hq) * splits + split) * (D + 2);
+    float* o = reinterpret_cast<float*>(p.workspace) + (((int64_t)b * p.q_heads + hq) * slots + split) * (D + 2);
     if (c == 0) {
       // the merge works in base 2
       o[0] = Mx * 1.4426950408889634f;
@@ -537,7 +552,18 @@ size_t ref_lds_bytes(const rfsn_ref_params* p, bool shared) {
 template <int D, int P>
 int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
   const int splits = ref_splits(p);
-  const int tps = (p->total_tokens + splits - 1) / splits;
+  const bool tables = p->score_tables != 0;
+  // score tables: their launches first (the last partial slot of every query
+  // head and the drift estimates the exact pass reads), then the exact pass
+  // over the exact segments (and the coded ones of groups the guard sends
+  // back), then the merge of splits + 1 slots
+  const int slots = tables ? splits + 1 : splits;
+  RefTabLayout tw{};
+  if (tables) {
+    ref_tab_bytes(p, slots, &tw, p->workspace);
+    const int st = launch_ref_tables(p, tw, s);
+    if (st) return st;
+  }
   const bool shared = p->k_pq_cb == p->v_pq_cb;
   const size_t lds = ref_lds_bytes(p, shared);
   const int blocks = p->batch * p->kv_heads * splits;
@@ -555,10 +581,11 @@ int launch_ref(const rfsn_ref_params* p, hipStream_t s) {
                   : pick_g(ref_attn_kernel<D, P, UG, 1, false>, ref_attn_kernel<D, P, UG, 2, false>,
                            ref_attn_kernel<D, P, UG, 4, false>, ref_attn_kernel<D, P, UG, 8, false>);
   if (lds > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, tps, (int)shared);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kRefThreads), lds, s, *p, splits, slots, (int)shared,
+                     tables ? (const float*)tw.est : nullptr);
   int st = check_launch("ref_attention");
-  if (st || splits == 1) return st;
-  return launch_merge(reinterpret_cast<const float*>(p->workspace), (int64_t)p->batch * p->q_heads, splits,
+  if (st || slots == 1) return st;
+  return launch_merge(reinterpret_cast<const float*>(p->workspace), (int64_t)p->batch * p->q_heads, slots,
                       p->head_dim, p->out, s);
 }
 
@@ -570,6 +597,7 @@ using namespace rfsn;
 extern "C" size_t rfsn_ref_attention_workspace_bytes(const rfsn_ref_params* p) {
   if (p == nullptr || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->total_tokens <= 0) return 0;
   const int splits = ref_splits(p);
+  if (p->score_tables) return ref_tables_shape_ok(p) ? ref_tab_bytes(p, splits + 1, nullptr, nullptr) : 0;
   if (splits == 1) return 0;
   return (size_t)p->batch * p->q_heads * splits * (p->head_dim + 2) * sizeof(float);
 }
@@ -606,6 +634,12 @@ extern "C" int rfsn_ref_attention(const rfsn_ref_params* p, void* stream) {
   RFSN_REQUIRE(shared_lds <= 160 * 1024, "ref_attention: the PQ codebooks do not fit the LDS (head_dim x centroids too large)");
   RFSN_REQUIRE(p->total_tokens > 0, "ref_attention: empty window (the caller returns zeros, attention.py:104-105)");
   RFSN_REQUIRE(p->splits >= 0 && p->splits <= 8192, "ref_attention: splits must be in [0, 8192]");
+  RFSN_REQUIRE(p->score_tables == 0 || p->score_tables == 1, "ref_attention: score_tables must be 0 or 1");
+  RFSN_REQUIRE(!p->score_tables || ref_tables_shape_ok(p),
+               "ref_attention: score tables need the gated reference format (or PQ only), (2 E + 64) * 4 bytes "
+               "of LDS for E = M C + L C_r entries and a window within the tables' token limit");
+  RFSN_REQUIRE(!p->score_tables || (p->table_tol >= 0.f && p->table_stats != nullptr),
+               "ref_attention: score tables need table_tol >= 0 and table_stats");
   hipStream_t s = (hipStream_t)stream;
   const size_t wsb = rfsn_ref_attention_workspace_bytes(p);
   RFSN_REQUIRE(wsb == 0 || (p->workspace && p->workspace_bytes >= wsb), "ref_attention: workspace too small");

@@ -779,22 +779,76 @@ def ref_attention_ok(head_dim: int, M: int, C: int, q_heads: int, kv_heads: int,
             and sub_ok and 0 <= sparse_k <= 8)
 
 
-def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, qpos: Optional[torch.Tensor],
-                  segments: Sequence[dict], k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor,
-                  k_rvq_cb: Optional[torch.Tensor], v_rvq_cb: Optional[torch.Tensor],
-                  rvq_subspaces: int = 0, sparse_k: int = 0,
-                  out: Optional[torch.Tensor] = None, splits: int = 0) -> torch.Tensor:
-    """Attention of q [B, Hq, D] over the window of ``segments`` (window
-    order; ``ref_store_segment`` / ``ref_exact_segment``), decoding the coded
-    ones on the fly (``rfsn_ref_attention``).  RVQ codebooks are [L, C_r, D]
-    (gated full-dimension layers) or, with ``rvq_subspaces``, [M_r, C_r, D/M_r]."""
+REF_TABLES_MIN_TOKENS = 4096  # coded tokens below which the score tables do not pay off
+
+
+def _ref_format_params(k_pq_cb: torch.Tensor, k_rvq_cb: Optional[torch.Tensor], rvq_subspaces: int,
+                       sparse_k: int) -> "L.RefParams":
+    M, Cn, d = k_pq_cb.shape
+    p = L.RefParams()
+    p.head_dim, p.pq_subspaces, p.pq_centroids = M * d, M, Cn
+    if k_rvq_cb is not None and rvq_subspaces:
+        p.rvq_subspaces, p.rvq_centroids = int(rvq_subspaces), int(k_rvq_cb.shape[1])
+    elif k_rvq_cb is not None:
+        p.rvq_layers, p.rvq_centroids = int(k_rvq_cb.shape[0]), int(k_rvq_cb.shape[1])
+    p.sparse_k = int(sparse_k)
+    return p
+
+
+def ref_table_stats(k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor, k_rvq_cb: Optional[torch.Tensor],
+                    v_rvq_cb: Optional[torch.Tensor]) -> torch.Tensor:
+    """The score tables' drift-guard statistics of a codebook set, float32
+    [3, D] (``rfsn_ref_table_stats``): per coordinate i, the second moments
+    mean_c PQ(c, i)^2 + 2 sum_l mean_c RVQ(l, c, i)^2 of K and of V, then
+    max_c |PQ_V(c, i)| + sum_l max_c |RVQ_V(l, c, i)|."""
+    _dev(k_pq_cb, "ref_table_stats")
+    cbs = [_contig(t) if t is not None else None for t in (k_pq_cb, v_pq_cb, k_rvq_cb, v_rvq_cb)]
+    p = _ref_format_params(cbs[0], cbs[2], 0, 0)
+    p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
+    out = torch.empty((3, p.head_dim), dtype=torch.float32, device=k_pq_cb.device)
+    L.call("rfsn_ref_table_stats", C.byref(p), out.data_ptr(), _stream(k_pq_cb))
+    return out
+
+
+class RefLaunch:
+    """A prepared ``rfsn_ref_attention`` call: its parameter block, segment
+    table and workspace, with the tensors they point to kept alive;
+    ``__call__`` re-issues it on the stream it was prepared on (q is read at
+    launch time, so a decode loop refills it in place)."""
+
+    def __init__(self, params: "L.RefParams", keep: list, out: torch.Tensor, stream: int, tables: bool):
+        self.params = params
+        self._keep = keep
+        self.out = out
+        self.stream = stream
+        self.score_tables = tables  # whether the launch attends the coded segments through score tables
+        self._fn = L.load().rfsn_ref_attention
+        self._ref = C.byref(self.params)
+
+    def __call__(self) -> torch.Tensor:
+        st = self._fn(self._ref, self.stream)
+        if st:
+            L.check(st, "rfsn_ref_attention")
+        return self.out
+
+
+def ref_prepare(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, qpos: Optional[torch.Tensor],
+                segments: Sequence[dict], k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor,
+                k_rvq_cb: Optional[torch.Tensor], v_rvq_cb: Optional[torch.Tensor],
+                rvq_subspaces: int = 0, sparse_k: int = 0,
+                out: Optional[torch.Tensor] = None, splits: int = 0,
+                score_tables: Optional[float] = None, table_stats: Optional[torch.Tensor] = None,
+                drift: Optional[torch.Tensor] = None) -> Optional[RefLaunch]:
+    """The launch of ``ref_attention`` for these arguments, or None for an
+    empty window (``out`` is then zeroed)."""
     _dev(q, "ref_attention")
     q = _contig(q)
     B, Hq, D = q.shape
     out = torch.empty_like(q) if out is None else out
     total = sum(s["len"] for s in segments)
     if total == 0:
-        return out.zero_()
+        out.zero_()
+        return None
     keep = [q, out]
     arr = (L.RefSegment * len(segments))()
     for i, sd in enumerate(segments):
@@ -816,14 +870,8 @@ def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool,
                 codes.rvq_sub, codes.sparse_idx, codes.sparse_val = L.ptr(rsub), L.ptr(sidx), L.ptr(sval)
                 keep += [pq, rvq, act, rsub, sidx, sval]
     dev_segs = _ref_table(C.string_at(C.addressof(arr), C.sizeof(arr)), q.device)
-    M, Cn, _ = k_pq_cb.shape
-    p = L.RefParams()
-    p.head_dim, p.pq_subspaces, p.pq_centroids = D, M, Cn
-    if k_rvq_cb is not None and rvq_subspaces:
-        p.rvq_subspaces, p.rvq_centroids = int(rvq_subspaces), int(k_rvq_cb.shape[1])
-    elif k_rvq_cb is not None:
-        p.rvq_layers, p.rvq_centroids = int(k_rvq_cb.shape[0]), int(k_rvq_cb.shape[1])
-    p.sparse_k = int(sparse_k)
+    p = _ref_format_params(k_pq_cb, k_rvq_cb, rvq_subspaces, sparse_k)
+    p.head_dim = D
     p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
     p.q, p.out, p.scale, p.causal = q.data_ptr(), out.data_ptr(), float(scale), int(causal)
     qp = None if qpos is None else _qpos(qpos, B, Hq, q.device)
@@ -832,12 +880,57 @@ def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool,
     cbs = [_contig(t) if t is not None else None for t in (k_pq_cb, v_pq_cb, k_rvq_cb, v_rvq_cb)]
     p.k_pq_cb, p.v_pq_cb, p.k_rvq_cb, p.v_rvq_cb = (L.ptr(t) for t in cbs)
     p.splits = splits
+    coded = sum(sd["len"] for sd in segments if sd["exact"] is None)
+    use_tables = (score_tables is not None and coded >= REF_TABLES_MIN_TOKENS
+                  and bool(L.load().rfsn_ref_tables_ok(C.byref(p))))
+    if use_tables:
+        if table_stats is None:
+            table_stats = ref_table_stats(*cbs)
+        if (table_stats.dtype != torch.float32 or tuple(table_stats.shape) != (3, D) or not table_stats.is_contiguous()
+                or table_stats.device != q.device):
+            raise ValueError("ref_attention: table_stats must be a contiguous float32 [3, head_dim] device tensor")
+        if drift is not None and (drift.dtype != torch.float32 or drift.numel() != B * Hq or not drift.is_contiguous()
+                                  or drift.device != q.device):
+            raise ValueError("ref_attention: drift must be a contiguous float32 [B, Hq] device tensor")
+        p.score_tables, p.table_tol = 1, float(score_tables)
+        p.table_stats, p.drift = table_stats.data_ptr(), L.ptr(drift)
+        keep += [table_stats, drift]
     wsb = L.load().rfsn_ref_attention_workspace_bytes(C.byref(p))
     ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=q.device)
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
-    L.call("rfsn_ref_attention", C.byref(p), _stream(q))
-    keep += [dev_segs, qp, ws, *cbs]  # alive until the launch is queued (the stream orders the reads)
-    return out
+    keep += [dev_segs, qp, ws, *cbs]
+    return RefLaunch(p, keep, out, _stream(q), use_tables)
+
+
+def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, qpos: Optional[torch.Tensor],
+                  segments: Sequence[dict], k_pq_cb: torch.Tensor, v_pq_cb: torch.Tensor,
+                  k_rvq_cb: Optional[torch.Tensor], v_rvq_cb: Optional[torch.Tensor],
+                  rvq_subspaces: int = 0, sparse_k: int = 0,
+                  out: Optional[torch.Tensor] = None, splits: int = 0,
+                  score_tables: Optional[float] = None, table_stats: Optional[torch.Tensor] = None,
+                  drift: Optional[torch.Tensor] = None, info: Optional[dict] = None) -> torch.Tensor:
+    """Attention of q [B, Hq, D] over the window of ``segments`` (window
+    order; ``ref_store_segment`` / ``ref_exact_segment``), decoding the coded
+    ones on the fly (``rfsn_ref_attention``).  RVQ codebooks are [L, C_r, D]
+    (gated full-dimension layers) or, with ``rvq_subspaces``, [M_r, C_r, D/M_r].
+
+    ``score_tables`` (a tolerance) attends the coded segments through q .
+    codeword tables and per-codeword sums of the weights where the format and
+    shape allow it (``rfsn_ref_tables_ok``) and the window holds at least
+    ``REF_TABLES_MIN_TOKENS`` coded tokens, with the drift guard sending a
+    group whose estimate exceeds the tolerance back to the exact decode;
+    ``table_stats`` (``ref_table_stats`` of the codebooks, computed here when
+    None), ``drift`` [B, Hq] float32 receives the estimates.  ``info`` (a
+    dict) receives ``score_tables``: whether the launch used them."""
+    launch = ref_prepare(q, kv_heads=kv_heads, scale=scale, causal=causal, qpos=qpos, segments=segments,
+                         k_pq_cb=k_pq_cb, v_pq_cb=v_pq_cb, k_rvq_cb=k_rvq_cb, v_rvq_cb=v_rvq_cb,
+                         rvq_subspaces=rvq_subspaces, sparse_k=sparse_k, out=out, splits=splits,
+                         score_tables=score_tables, table_stats=table_stats, drift=drift)
+    if info is not None:
+        info["score_tables"] = launch is not None and launch.score_tables
+    if launch is None:
+        return out if out is not None else torch.zeros_like(q)
+    return launch()
 
 
 def fused_splits(batch: int, q_heads: int, kv_heads: int, hot_len: int, max_tokens: int, max_segments: int,

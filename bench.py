@@ -284,10 +284,12 @@ def bench_ref(w, args, dev) -> dict:
     registers by rfsn_ref_attention.  Beside it: the decode-then-attend path
     it replaces (decode_ref of the warm K and V into HBM, concatenation,
     blockwise attention)."""
+    import dataclasses
+
     import numpy as np
     import torch
     from apple_amd import kernels as K
-    from apple_amd.storage import CompressedTensorMLX
+    from apple_amd.storage import CompressedTensorMLX, RFSNConfig
 
     H, D, M, C, L, Cr = w.heads, w.head_dim, w.pq_subspaces, w.pq_centroids, w.rvq_layers, w.rvq_centroids
     d = D // M
@@ -316,10 +318,18 @@ def bench_ref(w, args, dev) -> dict:
             K.ref_store_segment(dstores[0], dstores[1], 0, w.warm, w.hot)]
     out = torch.empty_like(qd)
     scale = D ** -0.5
-
-    def fused():
-        K.ref_attention(qd, kv_heads=H, scale=scale, causal=False, qpos=None, segments=segs, k_pq_cb=cbd,
-                        v_pq_cb=cbd, k_rvq_cb=rcbd, v_rvq_cb=rcbd, out=out)
+    # the decode step as the cache issues it: score tables for the coded
+    # tokens under the drift guard at the config's default tolerance (a group
+    # whose estimate exceeds it decodes them instead); the exact decode of
+    # every coded vector beside it
+    tol = next(f.default for f in dataclasses.fields(RFSNConfig) if f.name == "score_table_tolerance")
+    stats = K.ref_table_stats(cbd, cbd, rcbd, rcbd)
+    drift = torch.empty((1, H), dtype=torch.float32, device=dev)
+    common = dict(kv_heads=H, scale=scale, causal=False, qpos=None, segments=segs, k_pq_cb=cbd, v_pq_cb=cbd,
+                  k_rvq_cb=rcbd, v_rvq_cb=rcbd)
+    fused = K.ref_prepare(qd, out=out, score_tables=tol, table_stats=stats, drift=drift, **common)
+    xout = torch.empty_like(qd)
+    exact = K.ref_prepare(qd, out=xout, **common)
 
     def materialized():
         dk = K.decode_ref(dstores[0].pq_codes.reshape(n, M), cbd, dstores[0].rvq_codes, dstores[0].rvq_offsets, rcbd)
@@ -335,10 +345,13 @@ def bench_ref(w, args, dev) -> dict:
     stream = torch.cuda.current_stream()
     ms_per_step, kernel_ms = _timed(fused, steps, stream)
     pct = step_percentiles(fused, min(steps, 100))
+    warm_up(exact, 20)
+    x_ms, x_kernel_ms = _timed(exact, steps, stream)
     mat_out = materialized()
     warm_up(materialized, 20, floor_ms=50.0, batch=4)
     mat_ms, mat_kernel_ms = _timed(materialized, max(steps // 4, 10), stream)
     err = float((out.float() - mat_out.float()).abs().max())
+    x_err = float((xout.float() - mat_out.float()).abs().max())
     algo = w.bytes_per_step()
     gbs = algo / (kernel_ms * 1e-3) / 1e9
     result = {
@@ -357,6 +370,12 @@ def bench_ref(w, args, dev) -> dict:
                      "rvq_codeword_bytes_per_step": 2 * w.warm * H * L * D * 2},
         "materialized_path": {"kernel_ms": round(mat_kernel_ms, 5), "ms_per_step": round(mat_ms, 5),
                               "speedup": round(mat_kernel_ms / kernel_ms, 2), "max_abs_vs_fused": err},
+        "score_tables": {"used": fused.score_tables, "tolerance": tol,
+                         "max_estimate": float(drift.max()) if fused.score_tables else None,
+                         "heads_decoded_exactly": int((drift > tol).sum()) if fused.score_tables else None},
+        "exact_decode_path": {"kernel_ms": round(x_kernel_ms, 5), "ms_per_step": round(x_ms, 5),
+                              "speedup_of_tables": round(x_kernel_ms / kernel_ms, 2),
+                              "max_abs_vs_materialized": x_err},
     }
     if not args.no_cpu:
         from oracle import cpu_baseline as cb

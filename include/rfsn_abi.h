@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 6
+#define RFSN_ABI_VERSION 7
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -474,10 +474,38 @@ typedef struct rfsn_ref_params {
   int32_t splits;         /* token splits per (query, KV head); 0 = auto */
   void* workspace;        /* split partials: rfsn_ref_attention_workspace_bytes */
   size_t workspace_bytes;
+  /* Score tables for the coded segments (0 = decode every coded vector).
+   * With 1, each query head gets a table of scale log2(e) q . c over every
+   * PQ entry c (on its subspace) and every gated RVQ codeword: a coded
+   * token's score is the sum of its entries; its weight p = 2^(score - the
+   * block's largest) goes, in fixed point of 2^-19, into a sum per V
+   * codeword, and the output is those sums times the V codebooks over the
+   * sum of p.  This skips the fp16 rounding of the decoded K and V
+   * (quantization.py:310-319); a drift guard estimates the output change
+   * per query head from it and from the fixed-point steps, and a (query,
+   * KV head) group whose estimate exceeds table_tol for one of its heads
+   * decodes its coded tokens instead (exact segments are always exact).
+   * Needs the reference format without the long-context stages (gated RVQ,
+   * or PQ only), E = M C + L C_r entries with (2 E + 64) * 4 <= 160 KB of
+   * LDS, and at most 1,048,576 window tokens (rfsn_ref_tables_ok). */
+  int32_t score_tables;
+  float table_tol;           /* >= 0 */
+  const float* table_stats;  /* [3][head_dim] fp32 from rfsn_ref_table_stats */
+  float* drift;              /* [B][Hq] the guard's estimates, or NULL */
 } rfsn_ref_params;
 
 size_t rfsn_ref_attention_workspace_bytes(const rfsn_ref_params* p);
 int rfsn_ref_attention(const rfsn_ref_params* p, void* stream);
+/* 1 when the params' format and shape allow score_tables (ignoring the
+ * flag itself), else 0. */
+int rfsn_ref_tables_ok(const rfsn_ref_params* p);
+/* The drift guard's codebook statistics, [3][head_dim] fp32 into stats_dev:
+ * row 0 = mean_c PQ_K(c, i)^2 + 2 sum_l mean_c RVQ_K(l, c, i)^2 (the second
+ * moment of the decoded K coordinate and of its correction, whose fp16
+ * roundings the tables skip), row 1 the same for V, row 2 = max_c
+ * |PQ_V(c, i)| + sum_l max_c |RVQ_V(l, c, i)| (a bound on |V_i|).  Reads
+ * the params' format and codebooks only; depends on nothing else. */
+int rfsn_ref_table_stats(const rfsn_ref_params* p, float* stats_dev, void* stream);
 
 /* ---------------------------------------------------------------- k-means
  * One Lloyd update of PQ codebooks (rfsn_v10_mlx_ane_complete.py:197-207):
