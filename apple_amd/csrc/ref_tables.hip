@@ -394,14 +394,20 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
   const bool pq = sec < g.M;
   const int lo = pq ? sec * g.dsub : 0;
 
-  // gated rows: 8-byte units (the codebook is 8-byte aligned)
+  // V rows in units of 4 coordinates (8 bytes): gated rows (8-byte aligned
+  // codebook), PQ rows on their subspace when it holds whole units (dsub a
+  // multiple of 4; 16-byte aligned codebook), zeros elsewhere
+  const bool pq4 = pq && g.dsub % 4 == 0;
   uint2 rw[RU];
-  if (!pq) {
+  if (!pq || pq4) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int idx = threadIdx.x + u * NT, j = idx / (D / 4), c4 = idx - j * (D / 4);
-      rw[u] = j < n ? *reinterpret_cast<const uint2*>(rvq_cb + (int64_t)(e0 + j - g.M * g.C) * D + 4 * c4)
-                    : make_uint2(0u, 0u);
+      const int dd = 4 * c4;
+      const uint16_t* src = !pq ? rvq_cb + (int64_t)(e0 + j - g.M * g.C) * D + dd
+                                : pq_cb + (int64_t)(e0 + j) * g.dsub + (dd - lo);
+      rw[u] = j < n && (!pq || (dd >= lo && dd < lo + g.dsub)) ? *reinterpret_cast<const uint2*>(src)
+                                                                : make_uint2(0u, 0u);
     }
   }
   // split weights of head row r = threadIdx.x < 32
@@ -416,7 +422,7 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
       wk[r * S + k] = m > -__builtin_inff() ? exp2f(m - mx) : 0.f;
     }
   }
-  if (!pq) {
+  if (!pq || pq4) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int idx = threadIdx.x + u * NT, j = idx / (D / 4), c4 = idx - j * (D / 4);
@@ -425,7 +431,7 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
                       h2f((uint16_t)(rw[u].y >> 16)));
     }
   } else {
-    // PQ rows: the subspace's coordinates, zero elsewhere
+    // 2-wide PQ subspaces: the subspace's coordinates, zero elsewhere
     for (int i = threadIdx.x; i < kChunk * D; i += NT) {
       const int j = i / D, dd = i - j * D;
       rows[i] = (j < n && dd >= lo && dd < lo + g.dsub) ? h2f(pq_cb[(int64_t)(e0 + j) * g.dsub + (dd - lo)]) : 0.f;
