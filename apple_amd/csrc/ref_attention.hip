@@ -169,10 +169,12 @@ __device__ __forceinline__ void rebuild(float (&out)[U][DPL], const rfsn_ref_sto
         }
       }
     }
-  } else if (!EXT && sc.active != nullptr) {
+  } else if (!EXT && (sc.active != nullptr || sc.rvq != nullptr)) {
+    // a row's index into the gated codes: the active map, or the row itself
+    // when every row is active (no map)
     int a[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = sc.active[row[u]];
+    for (int u = 0; u < U; ++u) a[u] = sc.active != nullptr ? sc.active[row[u]] : (int)row[u];
     int64_t base[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) base[u] = (int64_t)(a[u] < 0 ? 0 : a[u]) * r.L;  // the store holds >= 1 active row

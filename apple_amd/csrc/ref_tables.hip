@@ -235,10 +235,11 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
         vc[u][w] = vp[w];
       }
       if (LQ > 0) {
+        // the active map, or every row active (dense codes, no map), or none
         const int32_t* kact = segs[s].k.active;
         const int32_t* vact = segs[s].v.active;
-        ka[u] = kact ? kact[row] : -1;
-        va[u] = vact ? vact[row] : -1;
+        ka[u] = kact ? kact[row] : segs[s].k.rvq ? (int)row : -1;
+        va[u] = vact ? vact[row] : segs[s].v.rvq ? (int)row : -1;
       }
     }
   }

@@ -728,9 +728,11 @@ def ref_store_segment(key_store, value_store, token0: int, length: int, pos0: in
             sval = _contig(st.sparse_val) if k else None
             seg[name] = (pq, None, None, rsub, sidx, sval)
         else:
+            # every row active (the offsets, sorted and distinct, are then 0 .. rows-1): the
+            # gated codes of row r are row r, and the kernels take no active map
             a = int(st.rvq_codes.shape[0])
-            seg[name] = (pq, _contig(st.rvq_codes) if a else None, active_map(st.rvq_offsets, rows) if a else None,
-                         None, None, None)
+            act = active_map(st.rvq_offsets, rows) if 0 < a < rows else None
+            seg[name] = (pq, _contig(st.rvq_codes) if a else None, act, None, None, None)
     return seg
 
 

@@ -430,7 +430,9 @@ int rfsn_fused_decode_attention_noalloc(const rfsn_fused_params* p, void* stream
 typedef struct rfsn_ref_store_codes {
   const uint8_t* pq;          /* [T][heads][M] u8 (4-byte aligned); NULL: an exact segment  */
   const uint16_t* rvq;        /* gated format: [A][L] u16 codes of the active rows          */
-  const int32_t* active;      /* gated format: [T][heads] index into rvq, or -1; NULL: none */
+  const int32_t* active;      /* gated format: [T][heads] index into rvq, or -1.  NULL with rvq
+                                 non-NULL: every row active, row r's codes at rvq + r L (dense);
+                                 NULL with rvq NULL: no gated stage */
   const uint8_t* rvq_sub;     /* long-context format: [T][heads][M_r] u8, or NULL            */
   const uint8_t* sparse_idx;  /* long-context format: [T][heads][k] u8, or NULL              */
   const uint16_t* sparse_val; /* long-context format: [T][heads][k] fp16 residuals           */

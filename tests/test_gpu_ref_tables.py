@@ -281,3 +281,37 @@ def test_cache_decode_takes_the_tables(device, tmp_path):
             assert dr.shape == (1, 4) and np.isfinite(dr).all()
     err, excess = _excess(outs[cfg.score_table_tolerance], outs[None])
     assert excess <= 0, err
+
+
+@pytest.mark.parametrize("tables", [False, True])
+def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
+    """A store whose rows are all active is attended without its active map
+    (the gated codes of row r are row r): bit-identical to the same segment
+    given the identity map, on the exact path and with score tables."""
+    from apple_amd import kernels as K
+
+    monkeypatch.setattr(K, "REF_TABLES_MIN_TOKENS", 0)
+    g = rng(3400 + int(tables))
+    D, M, C, L, Cr, B, Hq, Hkv = 128, 8, 256, 4, 4096, 1, 8, 4
+    d = D // M
+    pq_cb = rand_codebooks(g, M, C, d)
+    rv_cb = rand_codebooks(g, L, Cr, D)
+    sk, sv = _store(g, 3000, Hkv, M, C, L, Cr, 1.0), _store(g, 3000, Hkv, M, C, L, Cr, 1.0)
+    assert sk["rvq_offsets"].size == 3000 * Hkv
+    dk, dv = _dev_store(sk, device), _dev_store(sv, device)
+    dense = K.ref_store_segment(dk, dv, 0, 3000, 0)
+    assert dense["k"][2] is None and dense["v"][2] is None and dense["k"][1] is not None
+    mapped = dict(dense)
+    for name, st in (("k", dk), ("v", dv)):
+        pq, rvq, _, rsub, sidx, sval = dense[name]
+        mapped[name] = (pq, rvq, K.active_map(st.rvq_offsets, 3000 * Hkv), rsub, sidx, sval)
+    q = T(randn16(g, B, Hq, D), device)
+    kw = dict(kv_heads=Hkv, scale=D ** -0.5, causal=False, qpos=None, k_pq_cb=T(pq_cb, device),
+              v_pq_cb=T(pq_cb, device), k_rvq_cb=T(rv_cb, device), v_rvq_cb=T(rv_cb, device),
+              score_tables=TOL if tables else None)
+    a = K.ref_attention(q, segments=[dense], **kw)
+    b = K.ref_attention(q, segments=[mapped], **kw)
+    assert torch.equal(a, b)
+    ref = nx.blockwise_attention(H(q), nx.decode_compressed(sk, pq_cb, rv_cb), nx.decode_compressed(sv, pq_cb, rv_cb),
+                                 D ** -0.5, 16, False, None)
+    assert _excess(H(a), ref)[1] <= 0
