@@ -151,9 +151,13 @@ exact_attn_kernel(const uint16_t* __restrict__ q, int Hq, const uint16_t* __rest
 // threads per (sequence, query head).  The split weights exp2(m_s - max) go
 // to LDS once; then 256/D groups of D threads each sum a share of the splits
 // with independent loads, and the groups are added in LDS.  A split with
-// m_s = -inf (no allowed key) has weight 0.
+// m_s = -inf (no allowed key) has weight 0.  Every thread issues its first
+// split header and its first kMergePre partial sums together at the start,
+// so a merge of up to 256 splits (kMergePre per group) waits for one memory
+// round trip; the sums are formed in the same order either way.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxSplits = 8192;
+constexpr int kMergePre = 16;
 
 __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
 #pragma unroll
@@ -179,22 +183,42 @@ __global__ void __launch_bounds__(kMergeThreads) merge_partials_kernel(const flo
   const int64_t bh = blockIdx.x;
   const int t = threadIdx.x;
   const float* p = partial + bh * splits * (D + 2);
-  float mx = -__builtin_inff();
-  for (int s = t; s < splits; s += kMergeThreads) mx = fmaxf(mx, p[s * (D + 2)]);
+  const int groups = kMergeThreads / D, g = t / D, c = t % D;
+  // the loads of one round trip: header t, sums g, g + groups, ...
+  const bool h0 = t < splits;
+  const float m0 = h0 ? p[t * (D + 2)] : -__builtin_inff();
+  const float l0 = h0 ? p[t * (D + 2) + 1] : 0.f;
+  float av[kMergePre];
+#pragma unroll
+  for (int u = 0; u < kMergePre; ++u) {
+    const int s = g + u * groups;
+    av[u] = g < groups && s < splits ? p[s * (D + 2) + 2 + c] : 0.f;
+  }
+  float mx = m0;
+  for (int s = t + kMergeThreads; s < splits; s += kMergeThreads) mx = fmaxf(mx, p[s * (D + 2)]);
   mx = block_reduce(mx, red, true);
   float l = 0.f;
-  for (int s = t; s < splits; s += kMergeThreads) {
+  if (h0) {
+    const float w = m0 > -__builtin_inff() ? exp2f(m0 - mx) : 0.f;
+    weight[t] = w;
+    l += l0 * w;
+  }
+  for (int s = t + kMergeThreads; s < splits; s += kMergeThreads) {
     const float m = p[s * (D + 2)];
     const float w = m > -__builtin_inff() ? exp2f(m - mx) : 0.f;
     weight[s] = w;
     l += p[s * (D + 2) + 1] * w;
   }
   l = block_reduce(l, red, false);  // its barriers also publish weight[]
-  const int groups = kMergeThreads / D, g = t / D, c = t % D;
   float a = 0.f;
   if (g < groups) {
+#pragma unroll
+    for (int u = 0; u < kMergePre; ++u) {
+      const int s = g + u * groups;
+      if (s < splits) a += weight[s] * av[u];
+    }
 #pragma unroll 8
-    for (int s = g; s < splits; s += groups) a += weight[s] * p[s * (D + 2) + 2 + c];
+    for (int s = g + kMergePre * groups; s < splits; s += groups) a += weight[s] * p[s * (D + 2) + 2 + c];
   }
   part[t] = a;
   __syncthreads();
