@@ -180,3 +180,46 @@ def test_ref_attention_validation(lib):
     assert lib.rfsn_ref_attention_workspace_bytes(ctypes.byref(p)) > 0  # 4 units: split
     assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
     assert b"workspace" in lib.rfsn_last_error()
+
+
+def test_ref_tables_shape_checks(lib):
+    """rfsn_ref_tables_ok and score_tables' host checks: the gated reference
+    format (or PQ only) with its tables and histograms in LDS and a window
+    within the histogram blocks' token limit; anything else is refused before
+    a launch (and rfsn_ref_attention_workspace_bytes reports 0)."""
+    from apple_amd import _lib
+
+    assert lib.rfsn_ref_tables_ok(None) == 0
+    p = _lib.RefParams()
+    p.head_dim, p.pq_subspaces, p.pq_centroids, p.rvq_layers, p.rvq_centroids = 128, 8, 256, 4, 4096
+    p.batch, p.q_heads, p.kv_heads, p.total_tokens = 1, 32, 32, 32768
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 1          # the reference default: 18,432 entries
+    p.rvq_centroids = 8192                                        # 34,816 entries: no room in LDS
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 0
+    p.rvq_centroids, p.rvq_layers = 4096, 0                       # PQ only
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 1
+    p.rvq_layers, p.total_tokens = 4, 1 << 20                     # 256 blocks x 4,096 tokens per query head
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 1
+    p.total_tokens = (1 << 20) + 1
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 0
+    p.total_tokens, p.pq_subspaces = 1 << 19, 32                  # M = 32: 1,024 tokens per block
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 0
+    p.pq_subspaces, p.rvq_layers, p.rvq_subspaces, p.rvq_centroids = 8, 0, 8, 256   # long-context format
+    assert lib.rfsn_ref_tables_ok(ctypes.byref(p)) == 0
+    p.rvq_subspaces, p.rvq_layers, p.rvq_centroids, p.total_tokens = 0, 4, 4096, 32768
+    p.q = p.out = p.k_pq_cb = p.v_pq_cb = p.k_rvq_cb = p.v_rvq_cb = 16
+    p.num_segments, p.segments = 1, 64
+    p.score_tables, p.table_tol = 1, 2e-3
+    assert lib.rfsn_ref_attention_workspace_bytes(ctypes.byref(p)) > 0
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"table_stats" in lib.rfsn_last_error()
+    p.table_stats, p.table_tol = 16, -1.0
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"table_tol" in lib.rfsn_last_error()
+    p.table_tol, p.rvq_centroids = 2e-3, 8192
+    assert lib.rfsn_ref_attention_workspace_bytes(ctypes.byref(p)) == 0
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"score tables need" in lib.rfsn_last_error()
+    p.rvq_centroids, p.score_tables = 4096, 2
+    assert lib.rfsn_ref_attention(ctypes.byref(p), None) == -1
+    assert b"score_tables must be 0 or 1" in lib.rfsn_last_error()
