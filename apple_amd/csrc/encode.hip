@@ -82,16 +82,37 @@ pq_encode_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, int64_t
   }
 }
 
-// Reference-mode RVQ gate: fl32(sqrt(fl32(S r^2))) > thr.
+// Reference-mode RVQ gate: fl32(sqrt(fl32(S r^2))) > thr, S summed in
+// float64 in coordinate order.  Rows of 16-byte aligned fp16 load 8
+// coordinates per instruction (a lane's row is two 128-byte lines, read
+// whole), others one at a time.
 __global__ void rvq_gate_kernel(const uint16_t* __restrict__ r, int64_t n, int D, int64_t ld, float thr,
                                 uint8_t* __restrict__ mask) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint16_t* row = r + i * ld;
   double acc = 0.0;
-  for (int u = 0; u < D; ++u) {
-    const double v = (double)h2f(row[u]);
-    acc = __builtin_fma(v, v, acc);
+  if (D % 8 == 0 && ld % 8 == 0 && reinterpret_cast<uintptr_t>(r) % 16 == 0) {  // uniform
+    for (int u0 = 0; u0 < D; u0 += 32) {
+      uint4 w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = u0 + 8 * k < D ? reinterpret_cast<const uint4*>(row + u0)[k] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (u0 + 8 * k >= D) break;
+        const uint32_t ww[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const double v = (double)h2f((uint16_t)(ww[e >> 1] >> (16 * (e & 1))));
+          acc = __builtin_fma(v, v, acc);
+        }
+      }
+    }
+  } else {
+    for (int u = 0; u < D; ++u) {
+      const double v = (double)h2f(row[u]);
+      acc = __builtin_fma(v, v, acc);
+    }
   }
   const float s = (float)acc;
   // correctly rounded float sqrt: the f64 square root of an f32 input rounded
@@ -121,15 +142,24 @@ __global__ void mask_count_kernel(const uint8_t* __restrict__ mask, int64_t n, i
 }
 
 __global__ void tile_prefix_kernel(int32_t* __restrict__ tile_counts, int64_t tiles, int32_t* __restrict__ count) {
-  // single thread: tiles is small (n / 1024)
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
-  for (int64_t t = 0; t < tiles; ++t) {
-    const int32_t c = tile_counts[t];
-    tile_counts[t] = acc;
-    acc += c;
+  // one wave: exclusive prefix over 64 tiles at a time (shuffle scan), the
+  // running total carried from chunk to chunk
+  if (blockIdx.x != 0 || threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  int32_t carry = 0;
+  for (int64_t t0 = 0; t0 < tiles; t0 += 64) {
+    const int64_t t = t0 + lane;
+    const int32_t c = t < tiles ? tile_counts[t] : 0;
+    int32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += y;
+    }
+    if (t < tiles) tile_counts[t] = carry + inc - c;
+    carry += __shfl(inc, 63, 64);
   }
-  count[0] = acc;
+  if (lane == 0) count[0] = carry;
 }
 
 __global__ void mask_scatter_kernel(const uint8_t* __restrict__ mask, int64_t n, const int32_t* __restrict__ tile_base,
