@@ -19,7 +19,7 @@
 //                          head's table in LDS, per token one LDS read per
 //                          entry, then p into an integer histogram of the V
 //                          entries (LDS u32 atomics, p in steps of 2^-19;
-//                          fp32 LDS atomics run at a quarter of their rate)
+//                          fp32 LDS atomics run at a quarter of the u32 rate)
 //   ref_tab_values_kernel  per 64-entry chunk: H over the splits (rescaled
 //                          to a common maximum) times the chunk's V rows
 //   ref_tab_out_kernel     per (query, KV head) group: the chunk sums, the
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   float* red = tsm + 2 * g.Ep;                              // [64]
   const int bh = blockIdx.x / S, split = blockIdx.x % S;
   const int G = p.q_heads / p.kv_heads;
-  const int hq = bh % p.q_heads, bq = bh / p.q_heads, h = hq / G;
+  const int hq = bh % p.q_heads, h = hq / G;
   const int qp = (p.causal && p.qpos) ? p.qpos[bh] : 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // chunk-space indices: section s starts at chunk boundary (PQ sections of
@@ -367,7 +367,6 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
     reinterpret_cast<float4*>(hbuf + ((c * BH + bh) * S + split) * kChunk)[j4] =
         make_float4((float)hv.x * f, (float)hv.y * f, (float)hv.z * f, (float)hv.w * f);
   }
-  (void)bq;
 }
 
 // part2[c][bh][d] = sum over chunk c's entries e of H_bh[e] V_e[d], H_bh =
