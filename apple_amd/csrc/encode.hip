@@ -327,6 +327,7 @@ sparse_topk_kernel(const uint16_t* __restrict__ x, int64_t n, int D, int64_t ldx
 // are identical to it (and to the oracle) by construction.
 constexpr int kMfmaVecsPerWave = 32;
 constexpr int kMfmaThreads = 256;
+constexpr int kMfmaVecsPerBlock = (kMfmaThreads / 64) * kMfmaVecsPerWave;
 
 typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
 typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
@@ -364,13 +365,17 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
   const int nch = (C + 31) / 32;  // 32-centroid chunks
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, hi = lane >> 5;
-  const int64_t v = ((int64_t)blockIdx.x * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
-  const bool live = v < n;
-  // the lane's vector slice, loaded ahead of the codebook staging
+  // the block's first tile of vectors: its slices load ahead of the codebook staging
+  const int64_t ntiles = (n + kMfmaVecsPerBlock - 1) / kMfmaVecsPerBlock;
   uint16_t xr[DS];
-  const uint16_t* xv = x + (size_t)g * x_gstride + (live ? v : 0) * ldx + (size_t)m * DS;
+  auto load_slice = [&](int64_t tile) {
+    const int64_t v = (tile * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
+    const bool live = v < n;
+    const uint16_t* xv = x + (size_t)g * x_gstride + (live ? v : 0) * ldx + (size_t)m * DS;
 #pragma unroll
-  for (int u = 0; u < DS; ++u) xr[u] = live ? xv[u] : (uint16_t)0;
+    for (int u = 0; u < DS; ++u) xr[u] = live ? xv[u] : (uint16_t)0;
+  };
+  load_slice(blockIdx.x);
 
   uint32_t rmax_t = 0;  // this thread's largest R_j, as bits (R >= 0; NaN above +inf)
   for (int j = threadIdx.x; j < 32 * nch; j += kMfmaThreads) {
@@ -415,6 +420,15 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
   for (int w = 1; w < kMfmaThreads / 64; ++w) rmax_b = max(rmax_b, rmax_s[w]);
   const float rmax = __builtin_bit_cast(float, rmax_b);
 
+  // residual rows take one DS*2-byte store when the output is aligned for it
+  const bool vec_ok = resid != nullptr && ldr % DS == 0 && (reinterpret_cast<uintptr_t>(resid) % (2 * DS)) == 0 &&
+                      (resid_gstride % DS) == 0;
+  // the block's tiles of vectors: blockIdx.x, + gridDim.x, ... (the staged
+  // codebook serves them all)
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  if (tile != blockIdx.x) load_slice(tile);
+  const int64_t v = (tile * (kMfmaThreads / 64) + wave) * kMfmaVecsPerWave + col;
+  const bool live = v < n;
   // the lane's vector: canonical L and the B operand
   double xs[DS];
   double lacc = 0.0;
@@ -435,7 +449,14 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
     for (int u = 0; u < KH; ++u) bop[st][u] = (_Float16)0.0f;
   if constexpr (DS == 16) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) bop[0][u] = (_Float16)(-(float)xs[8 * hi + u]);
+    for (int u = 0; u < 8; ++u) {
+      // -fp16(x) of coordinate 8 hi + u: the half's sign flipped, chosen by a
+      // bit mask (a select between xs[u] and xs[8 + u] became an indexed
+      // access that kept xs in scratch memory)
+      const uint32_t msk = 0u - (uint32_t)hi;
+      const uint32_t w = ((uint32_t)xr[u] ^ (((uint32_t)xr[u] ^ (uint32_t)xr[8 + u]) & msk)) ^ 0x8000u;
+      bop[0][u] = __builtin_bit_cast(_Float16, (uint16_t)w);
+    }
     if (hi == 0) {
       bop[1][0] = (_Float16)1.0f;
       bop[1][1] = (_Float16)1.0f;
@@ -451,10 +472,6 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
     bop[0][2] = lh;
     bop[0][3] = ll;
   }
-
-  // residual rows take one DS*2-byte store when the output is aligned for it
-  const bool vec_ok = resid != nullptr && ldr % DS == 0 && (reinterpret_cast<uintptr_t>(resid) % (2 * DS)) == 0 &&
-                      (resid_gstride % DS) == 0;
 
   // screen: the three smallest keys of the lane's rows 8(r/4) + 4 hi + r%4
   // two independent lists (even / odd accumulator registers) for more ILP
@@ -547,7 +564,7 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       }
     }
   }
-  if (!live || hi != 0) return;
+  if (!live || hi != 0) continue;
   codes[(size_t)g * codes_gstride + v * ldc + m] = (uint8_t)code;
   if (resid != nullptr) {
     uint16_t* rv = resid + (size_t)g * resid_gstride + v * ldr + (size_t)m * DS;
@@ -569,14 +586,18 @@ pq_encode_mfma_kernel(const uint16_t* __restrict__ x, int64_t n, int64_t ldx, in
       for (int u = 0; u < DS; ++u) rv[u] = r[u];
     }
   }
+  }  // tiles
 }
 
 template <int DS>
 int launch_pq_mfma(const void* x, int64_t n, int64_t ldx, int64_t xg, const void* cb, int M, int C, int64_t cbg,
                    uint8_t* codes, int64_t ldc, int64_t cg, void* resid, int64_t ldr, int64_t rg, int groups,
                    hipStream_t s) {
-  constexpr int per_block = (kMfmaThreads / 64) * kMfmaVecsPerWave;
-  dim3 grid((unsigned)ceil_div(n, per_block), (unsigned)M, (unsigned)groups);
+  // about 16 blocks per CU in all: each block stages its subspace's codebook
+  // once and takes every gridDim.x-th tile of 128 vectors
+  const int64_t tiles = ceil_div(n, kMfmaVecsPerBlock);
+  const int64_t want = ceil_div(4096, (int64_t)M * groups);
+  dim3 grid((unsigned)std::max<int64_t>(1, std::min(tiles, want)), (unsigned)M, (unsigned)groups);
   hipLaunchKernelGGL(pq_encode_mfma_kernel<DS>, grid, dim3(kMfmaThreads), 0, s, (const uint16_t*)x, n, ldx, xg,
                      (const uint16_t*)cb, M, C, cbg, codes, ldc, cg, (uint16_t*)resid, ldr, rg);
   return check_launch("pq_encode");
