@@ -64,13 +64,18 @@ __device__ __forceinline__ void group_sums(float v, float (&s)[P]) {
   }
 }
 
-// The value of x for this lane's token group (tg < P), from uniform x[0..P).
+// The value of x for this lane's token group (tg < P), from uniform x[0..P),
+// blended with bit masks: a chain of selects on tg becomes an indexed load
+// through scratch memory at P = 4.
 template <int P>
 __device__ __forceinline__ float pick(const float (&x)[P], int tg) {
-  float r = x[0];
+  uint32_t r = __builtin_bit_cast(uint32_t, x[0]);
 #pragma unroll
-  for (int p = 1; p < P; ++p) r = tg == p ? x[p] : r;
-  return r;
+  for (int p = 1; p < P; ++p) {
+    const uint32_t m = 0u - (uint32_t)(tg == p);
+    r = (r & ~m) | (__builtin_bit_cast(uint32_t, x[p]) & m);
+  }
+  return __builtin_bit_cast(float, r);
 }
 
 // Sum of v over the lanes that hold the same coordinates in the P token
