@@ -315,3 +315,49 @@ def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
     ref = nx.blockwise_attention(H(q), nx.decode_compressed(sk, pq_cb, rv_cb), nx.decode_compressed(sv, pq_cb, rv_cb),
                                  D ** -0.5, 16, False, None)
     assert _excess(H(a), ref)[1] <= 0
+
+
+def test_hybrid_attention_takes_the_tables(device, tmp_path):
+    """RFSNHybridAttentionMLX over two stores of 5,000 tokens (more than
+    REF_TABLES_MIN_TOKENS): the decode step goes through the score tables
+    (once per codebook set the guard's statistics, kept between calls) and
+    agrees with the same call at score_table_tolerance None; with the
+    codebooks written in place the statistics are rebuilt."""
+    import dataclasses
+
+    from apple_amd import kernels as K
+    from apple_amd.attention import RFSNHybridAttentionMLX
+    from apple_amd.quantization import HybridQuantizerMLX, _compress_tensor_sequence
+    from apple_amd.storage import RFSNConfig
+
+    g = rng(3500)
+    cfg = RFSNConfig(hidden_dim=512, num_heads=4, head_dim=128, num_layers=2, num_subspaces=8, subspace_dim=16,
+                     num_rvq_layers=3, rvq_codebook_size=256, rvq_sparsity_threshold=0.25, hot_capacity=16,
+                     warm_capacity=24, cold_capacity=128, block_size_seq=16, disk_cache_dir=str(tmp_path))
+    pq, rv = rand_codebooks(g, 8, 256, 16), rand_codebooks(g, 3, 256, 128)
+    rv[:, 0] = 0
+    qz = HybridQuantizerMLX(cfg, device=device, pq_codebooks=T(pq, device), rvq_codebooks=T(rv, device))
+    k, v = randn16(g, 5000, 4, 128), randn16(g, 5000, 4, 128)
+    ks, vs = _compress_tensor_sequence(T(k, device), qz), _compress_tensor_sequence(T(v, device), qz)
+    q = T(randn16(g, 1, 4, 128), device)
+    calls = []
+    orig = K.ref_table_stats
+
+    def counted(*a, **kw):
+        calls.append(1)
+        return orig(*a, **kw)
+
+    K.ref_table_stats = counted
+    try:
+        att = RFSNHybridAttentionMLX(cfg)
+        a = H(att(q, ks, vs, qz, causal=False))
+        b = H(att(q, ks, vs, qz, causal=False))
+        assert len(calls) == 1 and np.array_equal(a, b)
+        qz.pq.codebooks.mul_(1.0)  # an in-place write bumps the version
+        att(q, ks, vs, qz, causal=False)
+        assert len(calls) == 2
+    finally:
+        K.ref_table_stats = orig
+    qz.config = dataclasses.replace(cfg, score_table_tolerance=None)
+    exact = H(RFSNHybridAttentionMLX(qz.config)(q, ks, vs, qz, causal=False))
+    assert _excess(a, exact)[1] <= 0
