@@ -99,7 +99,12 @@ __global__ void __launch_bounds__(128) ref_tab_scores_kernel(const uint16_t* __r
   for (int st = st0; st < st1; ++st) {
     const int d0 = 16 * st + 8 * hi;
     th8 a, b;
-    if (qa < BH) {
+    if (qa < BH && reinterpret_cast<uintptr_t>(q) % 16 == 0) {  // uniform alignment: one 16-byte load
+      const uint4 w = *reinterpret_cast<const uint4*>(q + (int64_t)qa * D + d0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a[u] = hbits((uint16_t)(ww[u >> 1] >> (16 * (u & 1))));
+    } else if (qa < BH) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) a[u] = hbits(q[(int64_t)qa * D + d0 + u]);
     } else {
@@ -523,12 +528,13 @@ __global__ void __launch_bounds__(1024) ref_tab_out_kernel(const rfsn_ref_params
     float v = 0.f;
     if (oo) {
       const float* src = part2 + (int64_t)bhb * D + o;
-      for (int k = wave; k < nch; k += 16 * 8) {
-        float x[8];
+      // 24 chunks' loads in flight per thread: one round trip for up to 384 chunks
+      for (int k = wave; k < nch; k += 16 * 24) {
+        float x[24];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = k + 16 * u < nch ? src[(int64_t)(k + 16 * u) * BH * D] : 0.f;
+        for (int u = 0; u < 24; ++u) x[u] = k + 16 * u < nch ? src[(int64_t)(k + 16 * u) * BH * D] : 0.f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v += x[u];
+        for (int u = 0; u < 24; ++u) v += x[u];
       }
     }
     red[t] = v;
