@@ -67,7 +67,7 @@ class RefStoreCodes(C.Structure):
 class RefSegment(C.Structure):
     _fields_ = [("k", RefStoreCodes), ("v", RefStoreCodes), ("exact_k", vp), ("exact_v", vp),
                 ("exact_token_stride", i64), ("exact_head_stride", i64), ("token0", i64), ("len", i32),
-                ("pos0", i32)]
+                ("pos0", i32), ("code_token_stride", i64), ("code_head_stride", i64)]
 
 
 class RefParams(C.Structure):
@@ -155,7 +155,7 @@ def load(path: Optional[os.PathLike] = None) -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.rfsn_abi_version() != 7:
+    if lib.rfsn_abi_version() != 8:
         raise RuntimeError("librfsn_hip.so ABI version mismatch")
     if path is None:
         _lib = lib

@@ -120,9 +120,13 @@ class RFSNHybridAttentionMLX:
         tables = {}
         if tol is not None and not quantizer.subspace and B * Hq <= REF_TABLES_MAX_QUERY_HEADS:
             tables = dict(score_tables=float(tol), table_stats=self._table_stats(quantizer))
+        # the tables read a head's codes in whole lines from a head-major
+        # copy, kept per store (only for stores already on the device, which
+        # outlive the call)
+        hm = bool(tables) and kst is key_store and vst is value_store
         out = K.ref_attention(q.to(device=dev, dtype=torch.float16), kv_heads=key_store.num_heads,
                               scale=self.scale, causal=causal, qpos=pos,
-                              segments=[K.ref_store_segment(kst, vst, 0, T, 0)], k_pq_cb=cb, v_pq_cb=cb,
+                              segments=[K.ref_store_segment(kst, vst, 0, T, 0, head_major=hm)], k_pq_cb=cb, v_pq_cb=cb,
                               k_rvq_cb=rcb, v_rvq_cb=rcb, rvq_subspaces=f.rvq_subspaces if quantizer.subspace else 0,
                               sparse_k=f.sparse_k if quantizer.subspace else 0, **tables)
         return out.to(q.dtype)

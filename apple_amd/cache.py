@@ -1584,6 +1584,14 @@ class RFSNv10KVCacheMLX:
         stats["used_router"] = int(router is not None)
         plan = self._plan(start, end, stats, router, current_position, context_window, cold_chunks)
         spans = self._tier_spans()
+        B, Hq = int(q.shape[0]), int(q.shape[1])
+        sub = self._fmt() if self._subspace else None
+        # decode steps of the reference format: score tables with their drift
+        # guard (config.score_table_tolerance), as the tiled path uses them;
+        # they read the warm tier's codes from a head-major copy of its stores
+        # (kept until a demotion or eviction replaces them)
+        tol = self.config.score_table_tolerance
+        use_tables = tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
         segs, pos = [], 0
         for kind, x in plan:
             if kind == "hot":
@@ -1592,7 +1600,8 @@ class RFSNv10KVCacheMLX:
                 segs.append(K.ref_exact_segment(hk, hv, hk.stride(1), hk.stride(0), self._hot_head + a, b - a, pos))
             elif kind == "warm":
                 a, b = x[0] - spans["warm"][0], x[1] - spans["warm"][0]
-                segs.append(K.ref_store_segment(self.warm_keys, self.warm_values, a, b - a, pos))
+                segs.append(K.ref_store_segment(self.warm_keys, self.warm_values, a, b - a, pos,
+                                                head_major=use_tables))
             else:
                 meta, ov, got = x
                 if got is None or self.config.cold_medium == "pinned":
@@ -1608,16 +1617,11 @@ class RFSNv10KVCacheMLX:
         self.last_access_stats = dict(stats)
         if pos == 0:
             return torch.zeros_like(q)
-        B, Hq = int(q.shape[0]), int(q.shape[1])
         qpos = _normalize_query_positions(adjusted, B, Hq, pos - 1, self.device) if causal else None
         kq, vq = self._kq, self._vq
-        sub = self._fmt() if self._subspace else None
-        # decode steps of the reference format: score tables with their drift
-        # guard (config.score_table_tolerance), as the tiled path uses them
-        tol = self.config.score_table_tolerance
         tables = {}
         self.last_ref_drift = None
-        if tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS:
+        if use_tables:
             self.last_ref_drift = torch.empty((B, Hq), dtype=torch.float32, device=self.device)
             tables = dict(score_tables=float(tol), table_stats=self._ref_table_stats(), drift=self.last_ref_drift)
         info = {}

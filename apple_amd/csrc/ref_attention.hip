@@ -409,6 +409,10 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
       vc.sparse_val = segs[s].v.sparse_val;
       const int64_t tok0 = segs[s].token0;
       const int pos0 = segs[s].pos0;
+      // code rows: the segment's strides, or the stores' [T][heads] order
+      const int64_t cts = segs[s].code_token_stride, chs = segs[s].code_head_stride;
+      const bool own = (cts | chs) == 0;
+      const int64_t rts = own ? (int64_t)p.kv_heads : cts, rhs = own ? 1 : chs;
       const uint16_t* ek = (const uint16_t*)segs[s].exact_k;
       const uint16_t* ev = (const uint16_t*)segs[s].exact_v;
       const int64_t ets = segs[s].exact_token_stride, ehs = segs[s].exact_head_stride;
@@ -423,7 +427,7 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
           const int tl = g0 + u * P + tg;
           const int t = (tl < hi ? tl : g0) - seg_base;  // past the end: re-read the step's first token
           tk[u] = tok0 + t;
-          row[u] = tk[u] * p.kv_heads + h;
+          row[u] = tk[u] * rts + h * rhs;
         }
         float kk[U][DPL], vv[U][DPL];
         if (kc.pq == nullptr) {

@@ -37,6 +37,8 @@
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
 
+#include <type_traits>
+
 namespace rfsn {
 namespace {
 
@@ -148,6 +150,24 @@ __global__ void __launch_bounds__(128) ref_tab_scores_kernel(const uint16_t* __r
   }
 }
 
+// The gated stage of a segment's K or V codes, as the histogram kernel
+// loads them: none, dense rows (row r's codes are row r), an active map, or
+// anything else (codes not in 8-byte aligned groups of 4 layers; blocks over
+// segments of different kinds), which takes the per-token loads.
+constexpr int kGNone = 0, kGDense = 1, kGMapped = 2, kGMixed = 3;
+__device__ __forceinline__ int gated_kind(const int32_t* act, const uint16_t* rvq, int L) {
+  if (rvq == nullptr) return act ? kGMixed : kGNone;
+  if (L % 4 != 0 || reinterpret_cast<uintptr_t>(rvq) % 8 != 0) return kGMixed;
+  return act ? kGMapped : kGDense;
+}
+__device__ __forceinline__ int merge_kind(int a, int b) { return a < 0 || a == b ? b : kGMixed; }
+
+// row of (store token t, KV head h) in a coded segment's arrays: its code
+// strides, or (both 0) the stores' [T][heads] order
+__device__ __forceinline__ int64_t code_row(int64_t cts, int64_t chs, int64_t t, int h, int kv_heads) {
+  return (cts | chs) == 0 ? t * kv_heads + h : t * cts + h * chs;
+}
+
 // The window's coded tokens, in window order, split S ways per query head.
 // Block b: split b % S, query head row bh = b / S (with S a multiple of 8,
 // the blocks of one split share an XCD and its L2 copy of the split's codes).
@@ -206,83 +226,188 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   const int tps = (coded + S - 1) / S;
   const int ci0 = min(coded, split * tps), ci1 = min(coded, ci0 + tps);
 
-  // codes of the thread's tokens ci0 + threadIdx.x + 512 u
+  // codes of the thread's tokens ci0 + threadIdx.x + 512 u.  A wave-uniform
+  // walk over the segments (scalar loads of their fields) finds each token's
+  // segment; the code loads follow in straight-line code, reading segment
+  // fields as scalars where the wave's tokens share one segment, so a thread
+  // issues the loads of all its tokens before its first wait.  (A per-token
+  // walk read the fields with vector loads and waited on them: one memory
+  // round trip per token.)
   uint32_t kc[KT][MW], vc[KT][MW];
-  int ka[KT], va[KT], sg[KT];
+  int ka[KT], va[KT], sg[KT], tt[KT];
   bool live[KT];
+  // the gated codes of the active rows: LQ groups of 4 layers (u16 each),
+  // read only where ka / va >= 0 (so they need no initial value: a zero
+  // merged across the map / dense branches made the compiler wait on loads)
+  constexpr int LQ1 = LQ > 0 ? LQ : 1;
+  uint2 kr[KT][LQ1], vr[KT][LQ1];
+  int kam[KT], vam[KT];  // active-map entries of the fast tokens
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    live[u] = false;
+    ka[u] = va[u] = -1;
+    sg[u] = tt[u] = 0;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) kc[u][w] = vc[u][w] = 0u;
+  }
+  // the gated stage of the block's segments, K and V (uniform): kGNone,
+  // kGDense, kGMapped, or kGMixed (mixed kinds, or codes not in 8-byte
+  // aligned groups of 4 layers)
+  int kkind = LQ > 0 ? -1 : kGNone, vkind = LQ > 0 ? -1 : kGNone;
   {
-    int s = 0, cpre = 0;  // cursor: segment s, coded tokens before it
+    int cpre = 0;  // coded tokens before segment s
+    for (int s = 0; s < p.num_segments && cpre < ci1; ++s) {
+      if (segs[s].k.pq == nullptr) continue;
+      const int lo = cpre;
+      cpre += segs[s].len;
+      if (cpre <= ci0) continue;  // before the block's tokens
+      if constexpr (LQ > 0) {
+        kkind = merge_kind(kkind, gated_kind(segs[s].k.active, segs[s].k.rvq, L));
+        vkind = merge_kind(vkind, gated_kind(segs[s].v.active, segs[s].v.rvq, L));
+      }
+      const int pos0 = segs[s].pos0;
+#pragma unroll
+      for (int u = 0; u < KT; ++u) {
+        const int ci = ci0 + (int)threadIdx.x + u * kHistThreads;
+        const int t = ci - lo, pos = pos0 + t;
+        if (ci >= lo && ci < cpre && ci < ci1 && pos >= 0 && pos <= qp) {  // else outside or masked
+          live[u] = true;
+          sg[u] = s;
+          tt[u] = t;
+        }
+      }
+    }
+  }
+  // Fast issue, straight-line and specialized on the block's gated kinds:
+  // token u of every lane of the wave, where the wave's live tokens u share
+  // one segment s0 (scalar fields).  The rest goes per token below.
+  bool done[KT];
+  int s0u[KT];  // uniform: the fast segment of token u, or -1
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    done[u] = !live[u];
+    s0u[u] = -1;
+  }
+  auto fast = [&](auto kk, auto vk) __attribute__((always_inline)) {
+    constexpr int KK = decltype(kk)::value, VK = decltype(vk)::value;
 #pragma unroll
     for (int u = 0; u < KT; ++u) {
-      const int ci = ci0 + (int)threadIdx.x + u * kHistThreads;
-      live[u] = ci < ci1;
-      ka[u] = va[u] = -1;
-      sg[u] = 0;
-#pragma unroll
-      for (int w = 0; w < MW; ++w) kc[u][w] = vc[u][w] = 0u;
+      const uint64_t lm = __ballot(live[u]);
+      if (lm == 0) continue;
+      const int s0 = __builtin_amdgcn_readlane(sg[u], __builtin_ctzll(lm));
+      if (__ballot(live[u] && sg[u] != s0) != 0) continue;
+      s0u[u] = s0;
+      done[u] = true;
       if (!live[u]) continue;
-      for (;;) {
-        const bool cs = segs[s].k.pq != nullptr;
-        if (cs && ci < cpre + segs[s].len) break;
-        if (cs) cpre += segs[s].len;
-        ++s;
-      }
-      const int t = ci - cpre;
-      const int pos = segs[s].pos0 + t;
-      if (pos < 0 || pos > qp) live[u] = false;  // masked
-      sg[u] = s;
-      const int64_t row = (segs[s].token0 + t) * p.kv_heads + h;
-      const uint32_t* kp = reinterpret_cast<const uint32_t*>(segs[s].k.pq + row * M);
-      const uint32_t* vp = reinterpret_cast<const uint32_t*>(segs[s].v.pq + row * M);
+      const int64_t row = code_row(segs[s0].code_token_stride, segs[s0].code_head_stride, segs[s0].token0 + tt[u], h, p.kv_heads);
+      const uint32_t* kp = reinterpret_cast<const uint32_t*>(segs[s0].k.pq + row * M);
+      const uint32_t* vp = reinterpret_cast<const uint32_t*>(segs[s0].v.pq + row * M);
 #pragma unroll
       for (int w = 0; w < MW; ++w) {
         kc[u][w] = kp[w];
         vc[u][w] = vp[w];
       }
-      if (LQ > 0) {
-        // the active map, or every row active (dense codes, no map), or none
-        const int32_t* kact = segs[s].k.active;
-        const int32_t* vact = segs[s].v.active;
-        ka[u] = kact ? kact[row] : segs[s].k.rvq ? (int)row : -1;
-        va[u] = vact ? vact[row] : segs[s].v.rvq ? (int)row : -1;
+      // dense rows: row r's gated codes are row r; an active map: read here,
+      // its rows' codes load below
+      if constexpr (KK == kGDense) {
+        ka[u] = (int)row;
+#pragma unroll
+        for (int k = 0; k < LQ1; ++k) kr[u][k] = *reinterpret_cast<const uint2*>(segs[s0].k.rvq + row * L + 4 * k);
+      } else if constexpr (KK == kGMapped) {
+        kam[u] = segs[s0].k.active[row];
+      }
+      if constexpr (VK == kGDense) {
+        va[u] = (int)row;
+#pragma unroll
+        for (int k = 0; k < LQ1; ++k) vr[u][k] = *reinterpret_cast<const uint2*>(segs[s0].v.rvq + row * L + 4 * k);
+      } else if constexpr (VK == kGMapped) {
+        vam[u] = segs[s0].v.active[row];
       }
     }
-  }
-  // the gated codes of the active rows: LQ groups of 4 layers (u16 each)
-  uint2 kr[KT][LQ > 0 ? LQ : 1], vr[KT][LQ > 0 ? LQ : 1];
+    if constexpr (KK == kGMapped || VK == kGMapped) {  // one round trip after the maps
 #pragma unroll
-  for (int u = 0; u < KT; ++u)
+      for (int u = 0; u < KT; ++u) {
+        const int s0 = s0u[u];
+        if (s0 < 0 || !live[u]) continue;
+        if constexpr (KK == kGMapped) {
+          ka[u] = kam[u];
+          if (ka[u] >= 0) {
 #pragma unroll
-    for (int k = 0; k < (LQ > 0 ? LQ : 1); ++k) kr[u][k] = vr[u][k] = make_uint2(0u, 0u);
-  if constexpr (LQ > 0) {
-#pragma unroll
-    for (int u = 0; u < KT; ++u) {
-      if (!live[u]) continue;
-#pragma unroll
-      for (int pass = 0; pass < 2; ++pass) {
-        const int a = pass ? va[u] : ka[u];
-        if (a < 0) continue;
-        const uint16_t* rc = (pass ? segs[sg[u]].v.rvq : segs[sg[u]].k.rvq) + (int64_t)a * L;
-        uint2 w[LQ];
-        if (L % 4 == 0 && reinterpret_cast<uintptr_t>(rc) % 8 == 0) {
-#pragma unroll
-          for (int k = 0; k < LQ; ++k) w[k] = 4 * k < L ? *reinterpret_cast<const uint2*>(rc + 4 * k) : make_uint2(0u, 0u);
-        } else {
-#pragma unroll
-          for (int k = 0; k < LQ; ++k) {
-            uint32_t x[2] = {0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (4 * k + j < L) x[j >> 1] |= (uint32_t)rc[4 * k + j] << (16 * (j & 1));
-            w[k] = make_uint2(x[0], x[1]);
+            for (int k = 0; k < LQ1; ++k)
+              kr[u][k] = *reinterpret_cast<const uint2*>(segs[s0].k.rvq + (int64_t)ka[u] * L + 4 * k);
           }
         }
+        if constexpr (VK == kGMapped) {
+          va[u] = vam[u];
+          if (va[u] >= 0) {
 #pragma unroll
-        for (int k = 0; k < LQ; ++k) {
-          if (pass)
-            vr[u][k] = w[k];
-          else
-            kr[u][k] = w[k];
+            for (int k = 0; k < LQ1; ++k)
+              vr[u][k] = *reinterpret_cast<const uint2*>(segs[s0].v.rvq + (int64_t)va[u] * L + 4 * k);
+          }
+        }
+      }
+    }
+  };
+  using G0 = std::integral_constant<int, kGNone>;
+  using G1 = std::integral_constant<int, kGDense>;
+  using G2 = std::integral_constant<int, kGMapped>;
+  auto fast_v = [&](auto kk) __attribute__((always_inline)) {
+    if (vkind == kGNone) fast(kk, G0{});
+    else if (vkind == kGDense) fast(kk, G1{});
+    else if (vkind == kGMapped) fast(kk, G2{});
+  };
+  if (LQ == 0 || kkind == kGNone) fast_v(G0{});
+  else if (kkind == kGDense) fast_v(G1{});
+  else if (kkind == kGMapped) fast_v(G2{});
+  // The rest, per token (a wave whose tokens u span segments; gated codes
+  // not in aligned groups of 4), after every fast load is issued.
+  bool rest = false;
+#pragma unroll
+  for (int u = 0; u < KT; ++u) rest |= !done[u];
+  if (__ballot(rest) != 0) {
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+      if (done[u]) continue;
+      const int sx = sg[u];
+      const int64_t row = code_row(segs[sx].code_token_stride, segs[sx].code_head_stride, segs[sx].token0 + tt[u], h, p.kv_heads);
+      const uint32_t* kp = reinterpret_cast<const uint32_t*>(segs[sx].k.pq + row * M);
+      const uint32_t* vp = reinterpret_cast<const uint32_t*>(segs[sx].v.pq + row * M);
+#pragma unroll
+      for (int w = 0; w < MW; ++w) {
+        kc[u][w] = kp[w];
+        vc[u][w] = vp[w];
+      }
+      if constexpr (LQ > 0) {
+        const int32_t* kact = segs[sx].k.active;
+        const int32_t* vact = segs[sx].v.active;
+        ka[u] = kact ? kact[row] : segs[sx].k.rvq ? (int)row : -1;
+        va[u] = vact ? vact[row] : segs[sx].v.rvq ? (int)row : -1;
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+          const int a = pass ? va[u] : ka[u];
+          if (a < 0) continue;
+          const uint16_t* rc = (pass ? segs[sx].v.rvq : segs[sx].k.rvq) + (int64_t)a * L;
+          uint2 w[LQ];
+          if (L % 4 == 0 && reinterpret_cast<uintptr_t>(rc) % 8 == 0) {
+#pragma unroll
+            for (int k = 0; k < LQ; ++k) w[k] = *reinterpret_cast<const uint2*>(rc + 4 * k);
+          } else {
+#pragma unroll
+            for (int k = 0; k < LQ; ++k) {
+              uint32_t x[2] = {0u, 0u};
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (4 * k + j < L) x[j >> 1] |= (uint32_t)rc[4 * k + j] << (16 * (j & 1));
+              w[k] = make_uint2(x[0], x[1]);
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < LQ; ++k) {
+            if (pass)
+              vr[u][k] = w[k];
+            else
+              kr[u][k] = w[k];
+          }
         }
       }
     }

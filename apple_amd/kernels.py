@@ -709,30 +709,88 @@ def active_map(offsets: torch.Tensor, rows: int) -> torch.Tensor:
     return out
 
 
-def ref_store_segment(key_store, value_store, token0: int, length: int, pos0: int) -> dict:
+_HEAD_MAJOR: Dict[int, tuple] = {}  # id(pq_codes) -> (weakref, signature, codes)
+
+
+def _store_rows(st) -> tuple:
+    """A store's per-row code arrays in its own [T][heads] row order: (pq,
+    rvq, active, rvq_sub, sparse_idx, sparse_val) as the segment table takes
+    them (rvq with active None: dense rows, row r's codes are row r)."""
+    pq = _contig(st.pq_codes)
+    rows = int(pq.shape[0]) * int(pq.shape[1])
+    if st.rvq_codes.dim() == 3:
+        rsub = _contig(st.rvq_codes) if st.rvq_codes.shape[-1] else None
+        k = 0 if st.sparse_idx is None else int(st.sparse_idx.shape[-1])
+        return (pq, None, None, rsub, _contig(st.sparse_idx) if k else None, _contig(st.sparse_val) if k else None)
+    # every row active (the offsets, sorted and distinct, are then 0 .. rows-1): the
+    # gated codes of row r are row r, and the kernels take no active map
+    a = int(st.rvq_codes.shape[0])
+    act = active_map(st.rvq_offsets, rows) if 0 < a < rows else None
+    return (pq, _contig(st.rvq_codes) if a else None, act, None, None, None)
+
+
+def _store_rows_head_major(st) -> tuple:
+    """``_store_rows`` with every per-row array in [heads][T] order (row h * T
+    + t; active entries still index the store's rvq codes), memoized per store
+    until its code tensors change (data pointer, version or shape).  A head's
+    consecutive tokens then have consecutive codes, which the decode kernels
+    read in whole lines instead of a few bytes of each."""
+    pq = st.pq_codes
+    sig = tuple(None if t is None else (t.data_ptr(), t._version, tuple(t.shape))
+                for t in (pq, st.rvq_codes, st.rvq_offsets, st.sparse_idx, st.sparse_val))
+    key = id(pq)
+    hit = _HEAD_MAJOR.get(key)
+    if hit is not None and hit[0]() is pq and hit[1] == sig:
+        return hit[2]
+    codes = copy_head_major(st)
+    _HEAD_MAJOR[key] = (weakref.ref(pq, lambda _r, k=key: _HEAD_MAJOR.pop(k, None)), sig, codes)
+    return codes
+
+
+def copy_head_major(st) -> tuple:
+    """A new [heads][T] copy of a store's per-row code arrays (what
+    ``ref_store_segment(..., head_major=True)`` keeps per store version)."""
+    pq = st.pq_codes
+    T, H = int(pq.shape[0]), int(pq.shape[1])
+    base = _store_rows(st)
+    gated = st.rvq_codes.dim() != 3
+
+    def hm(t, width):  # [T * H, width] or [T, H, width] rows -> [H, T, width]
+        return None if t is None else t.reshape(T, H, width).transpose(0, 1).contiguous()
+
+    pqb, rvq, act, rsub, sidx, sval = base
+    if gated:
+        dense = rvq is not None and act is None
+        codes = (hm(pqb, pqb.shape[-1]), hm(rvq, rvq.shape[-1]) if dense else rvq,
+                 None if act is None else act.view(T, H).t().contiguous().view(-1), None, None, None)
+    else:
+        codes = (hm(pqb, pqb.shape[-1]), None, None, None if rsub is None else hm(rsub, rsub.shape[-1]),
+                 None if sidx is None else hm(sidx, sidx.shape[-1]), None if sval is None else hm(sval, sval.shape[-1]))
+    return codes
+
+
+def ref_store_segment(key_store, value_store, token0: int, length: int, pos0: int,
+                      head_major: bool = False) -> dict:
     """A coded segment of tokens token0 .. token0+length-1 of two stores in
     CompressedTensorMLX's layout: reference format (pq_codes [T, H, M] u8,
     rvq_codes [A, L] u16 placed by rvq_offsets [A] over the T*H rows) or the
     long-context format (rvq_codes [T, H, M_r] u8, sparse_idx / sparse_val
-    [T, H, k])."""
+    [T, H, k]).
+
+    ``head_major`` attends a copy of the codes in [heads][T] order instead,
+    kept per store until its code tensors change (so for stores that outlive
+    the call: a decode loop's warm tier); stores of unequal lengths keep their
+    own order."""
     seg = {"len": int(length), "pos0": int(pos0), "token0": int(token0), "exact": None}
     if token0 < 0 or length < 0 or token0 + length > min(key_store.num_tokens, value_store.num_tokens):
         raise ValueError("segment tokens outside the stores")
+    if head_major and key_store.num_tokens == value_store.num_tokens:
+        seg["k"] = _store_rows_head_major(key_store)
+        seg["v"] = _store_rows_head_major(value_store)
+        seg["rows"] = (1, int(key_store.num_tokens))  # row of (t, h) = t * 1 + h * T
+        return seg
     for name, st in (("k", key_store), ("v", value_store)):
-        pq = _contig(st.pq_codes)
-        rows = int(pq.shape[0]) * int(pq.shape[1])
-        if st.rvq_codes.dim() == 3:
-            rsub = _contig(st.rvq_codes) if st.rvq_codes.shape[-1] else None
-            k = 0 if st.sparse_idx is None else int(st.sparse_idx.shape[-1])
-            sidx = _contig(st.sparse_idx) if k else None
-            sval = _contig(st.sparse_val) if k else None
-            seg[name] = (pq, None, None, rsub, sidx, sval)
-        else:
-            # every row active (the offsets, sorted and distinct, are then 0 .. rows-1): the
-            # gated codes of row r are row r, and the kernels take no active map
-            a = int(st.rvq_codes.shape[0])
-            act = active_map(st.rvq_offsets, rows) if 0 < a < rows else None
-            seg[name] = (pq, _contig(st.rvq_codes) if a else None, act, None, None, None)
+        seg[name] = _store_rows(st)
     return seg
 
 
@@ -856,6 +914,7 @@ def ref_prepare(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, q
     for i, sd in enumerate(segments):
         seg = arr[i]
         seg.token0, seg.len, seg.pos0 = sd["token0"], sd["len"], sd["pos0"]
+        seg.code_token_stride, seg.code_head_stride = sd.get("rows", (0, 0))
         if sd["exact"] is not None:
             ek, ev, ts, hs = sd["exact"]
             seg.exact_k, seg.exact_v = ek.data_ptr(), ev.data_ptr()

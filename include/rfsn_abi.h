@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define RFSN_ABI_VERSION 7
+#define RFSN_ABI_VERSION 8
 
 #define RFSN_OK 0
 #define RFSN_ERR_INVALID (-1)     /* shape / contract violation -> ValueError   */
@@ -448,6 +448,14 @@ typedef struct rfsn_ref_segment {
   int64_t token0;              /* the segment's first window token is token token0 of its store */
   int32_t len;                 /* tokens */
   int32_t pos0;                /* window position of the segment's first token */
+  /* Coded segments: the codes of (token t, KV head h) are row
+   * t * code_token_stride + h * code_head_stride of every per-row array (pq,
+   * active, dense rvq, rvq_sub, sparse_idx, sparse_val; active entries still
+   * index rvq).  0 and 0: the stores' own [T][heads] order, row t * kv_heads + h.
+   * A head-major copy ([heads][T]: strides 1 and T) gives a head's consecutive
+   * tokens consecutive codes, which the decode kernels read in whole lines. */
+  int64_t code_token_stride;
+  int64_t code_head_stride;
 } rfsn_ref_segment;
 
 typedef struct rfsn_ref_params {

@@ -104,6 +104,15 @@ def test_segments_match_oracle(device, D, M, C, L, Cr, B, Hq, Hkv, causal, split
     assert np.abs(got - ref.astype(np.float32)).max() <= TOL
     if causal:
         assert not got[-1, -1].any()  # position -1 sees no key: zeros (attention.py:104-105)
+    # the same window over head-major copies of the stores' codes (code
+    # strides 1 and T): the same tokens in the same order, bit-identical
+    hm = [K.ref_store_segment(ds1, ds1v, 5, 37, 0, head_major=True), segs[1],
+          K.ref_store_segment(ds2, ds2v, 17, 1, 66, head_major=True),
+          K.ref_store_segment(ds2, ds2v, 0, 71, 67, head_major=True)]
+    assert hm[0]["rows"] == (1, 50) and hm[3]["rows"] == (1, 71)
+    out_hm = K.ref_attention(T(q, device), kv_heads=Hkv, scale=D ** -0.5, causal=causal,
+                             qpos=T(qp, device) if causal else None, segments=hm, splits=splits, **cbs)
+    assert torch.equal(out_hm, out)
 
 
 def _ext_store(g, n_tok, heads, M, C, Mr, Cr, k, D):
@@ -171,6 +180,13 @@ def test_long_context_format_matches_oracle(device, D, M, C, Mr, Cr, k, B, Hq, H
                           sparse_k=k)
     ref = nx.blockwise_attention(q, keys, vals, D ** -0.5, 16, True, qp)
     assert np.abs(H(out).astype(np.float32) - ref.astype(np.float32)).max() <= TOL
+    # head-major copies of the long-context arrays (rvq_sub, sparse_idx, sparse_val)
+    dsk, dsv = _ext_dev_store(sk, device), _ext_dev_store(sv, device)
+    hm = [K.ref_store_segment(dsk, dsv, 3, 77, 0, head_major=True), segs[1]]
+    out_hm = K.ref_attention(T(q, device), kv_heads=Hkv, scale=D ** -0.5, causal=True, qpos=T(qp, device),
+                             segments=hm, k_pq_cb=cb, v_pq_cb=cb, k_rvq_cb=rcb, v_rvq_cb=rcb, rvq_subspaces=Mr,
+                             sparse_k=k)
+    assert torch.equal(out_hm, out)
 
 
 def test_long_window_split_merge(device):

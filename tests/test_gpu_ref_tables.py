@@ -149,6 +149,35 @@ def test_tolerance_zero_is_the_exact_path(device, monkeypatch, splits):
     assert torch.equal(tab, exact)
 
 
+@pytest.mark.parametrize("case", [0, 1, 7])
+@pytest.mark.parametrize("tables", [False, True])
+def test_head_major_codes_match(device, monkeypatch, case, tables):
+    """The window over head-major copies of its stores' codes (code strides 1
+    and T; the stores keep 40-90 % of their rows active, so the gated codes go
+    through active maps) attends bit-identically to the stores' own order, on
+    the exact path and with score tables, for 4, 3 and 5 gated layers (3 and
+    5: the tables' per-token loads)."""
+    from apple_amd import kernels as K
+
+    monkeypatch.setattr(K, "REF_TABLES_MIN_TOKENS", 0)
+    D, M, C, L, Cr, B, Hq, Hkv, causal = CASES[case]
+    g = rng(3600 + 2 * case + int(tables))
+    n1, n2, hot = 900, 1500, 64
+    segs, keys, vals, cbs, keep, _ = _window(g, device, D, M, C, L, Cr, Hkv, n1, n2, hot)
+    ds1, ds1v, ds2, ds2v = keep[:4]
+    hm = [K.ref_store_segment(ds1, ds1v, 3, n1, 0, head_major=True), segs[1],
+          K.ref_store_segment(ds2, ds2v, 0, n2, n1 + hot, head_major=True)]
+    q = T(randn16(g, B, Hq, D), device)
+    W = n1 + hot + n2
+    qp = T(g.integers(W // 2, W, (B, Hq)).astype(np.int32), device) if causal else None
+    kw = dict(kv_heads=Hkv, scale=D ** -0.5, causal=causal, qpos=qp, score_tables=TOL if tables else None, **cbs)
+    info = {}
+    a = K.ref_attention(q, segments=segs, info=info, **kw)
+    assert info["score_tables"] == tables
+    b = K.ref_attention(q, segments=hm, **kw)
+    assert torch.equal(a, b)
+
+
 def _estimate(q, s, stats, scale, blocks):
     """The guard's estimate restated for one query head over its coded
     tokens' scores s (base 2): p = 2^(s - max), L = sum p, Q = sum p^2, and
@@ -312,6 +341,10 @@ def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
     a = K.ref_attention(q, segments=[dense], **kw)
     b = K.ref_attention(q, segments=[mapped], **kw)
     assert torch.equal(a, b)
+    # dense rows over the head-major copy ([heads][T][L] gated codes)
+    hm = K.ref_store_segment(dk, dv, 0, 3000, 0, head_major=True)
+    assert hm["k"][2] is None and hm["rows"] == (1, 3000)
+    assert torch.equal(K.ref_attention(q, segments=[hm], **kw), a)
     ref = nx.blockwise_attention(H(q), nx.decode_compressed(sk, pq_cb, rv_cb), nx.decode_compressed(sv, pq_cb, rv_cb),
                                  D ** -0.5, 16, False, None)
     assert _excess(H(a), ref)[1] <= 0

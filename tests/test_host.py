@@ -475,6 +475,8 @@ def test_reference_active_map_and_segments():
     K.ref_exact_segment(ring, ring, ring.stride(1), ring.stride(0), 2, 6, 0)
     with pytest.raises(ValueError):
         K.ref_exact_segment(ring, ring, ring.stride(1), ring.stride(0), 3, 6, 0)
+    hm = K.ref_store_segment(st, st, 2, 4, 10, head_major=True)
+    assert hm["rows"] == (1, T) and hm["k"][1] is not None and hm["k"][2] is not None
     assert K.ref_attention_ok(128, 8, 256, 4, 4, True) and not K.ref_attention_ok(96, 8, 256, 4, 4, True)
     assert not K.ref_attention_ok(256, 16, 256, 8, 1, False)  # 2 x 128 KB of tables
     assert K.ref_attention_ok(256, 16, 256, 8, 1, True, 16, 256, 4)
@@ -517,3 +519,57 @@ def test_guard_refuses_k_segments_without_exact_plane():
         else:
             with pytest.raises(ValueError, match="plane"):
                 t.check_exact_planes(H, k)
+
+
+def test_ref_store_segment_head_major():
+    """head_major segments carry [heads][T] copies of every per-row code array
+    (row h * T + t; active entries still index the store's RVQ codes) for
+    mapped, dense and long-context stores; a copy is reused while its store is
+    unchanged and remade after an in-place write; stores of unequal lengths
+    keep their own order."""
+    from apple_amd import kernels as K
+    from apple_amd.storage import CompressedTensorMLX
+
+    g = torch.Generator().manual_seed(5)
+    T, H, M, L, Mr, k = 6, 3, 8, 3, 4, 2
+    rows = T * H
+    pq = torch.randint(0, 256, (T, H, M), generator=g).to(torch.uint8)
+    offs = torch.tensor([1, 4, 5, 9, 16], dtype=torch.int32)
+    rvq = torch.randint(0, 500, (5, L), generator=g).to(torch.uint16)
+    st = CompressedTensorMLX(pq_codes=pq, rvq_codes=rvq, rvq_mask=torch.zeros((T, H), dtype=torch.bool),
+                             rvq_offsets=offs, num_heads=H)
+    amap = K.active_map(offs, rows)
+    seg = K.ref_store_segment(st, st, 1, 5, 0, head_major=True)
+    assert seg["rows"] == (1, T)
+    hpq, hrvq, hact = seg["k"][:3]
+    assert torch.equal(hrvq, rvq)  # mapped: the codes stay, the map moves
+    for t in range(T):
+        for h in range(H):
+            assert torch.equal(hpq.view(-1, M)[h * T + t], pq[t, h]) and int(hact[h * T + t]) == int(amap[t * H + h])
+    assert K.ref_store_segment(st, st, 0, T, 0, head_major=True)["k"][0] is hpq  # reused
+    pq[2, 1, 3] ^= 7
+    again = K.ref_store_segment(st, st, 0, T, 0, head_major=True)["k"][0]
+    assert again is not hpq and int(again.view(-1, M)[1 * T + 2, 3]) == int(pq[2, 1, 3])
+    # every row active: dense gated codes, [heads][T][L]
+    rv_d = torch.randint(0, 500, (rows, L), generator=g).to(torch.uint16)
+    sd = CompressedTensorMLX(pq_codes=pq, rvq_codes=rv_d, rvq_mask=torch.ones((T, H), dtype=torch.bool),
+                             rvq_offsets=torch.arange(rows, dtype=torch.int32), num_heads=H)
+    dseg = K.ref_store_segment(sd, sd, 0, T, 0, head_major=True)
+    assert dseg["k"][2] is None
+    for t in range(T):
+        for h in range(H):
+            assert torch.equal(dseg["k"][1].view(-1, L)[h * T + t], rv_d[t * H + h])
+    # long-context arrays
+    rsub = torch.randint(0, 64, (T, H, Mr), generator=g).to(torch.uint8)
+    sidx = torch.randint(0, 64, (T, H, k), generator=g).to(torch.uint8)
+    sval = torch.randn((T, H, k), generator=g).half()
+    se = CompressedTensorMLX(pq_codes=pq, rvq_codes=rsub, rvq_mask=torch.ones((T, H), dtype=torch.bool),
+                             rvq_offsets=torch.zeros((0,), dtype=torch.int32), num_heads=H, sparse_idx=sidx,
+                             sparse_val=sval)
+    eseg = K.ref_store_segment(se, se, 0, T, 0, head_major=True)
+    for arr, src in ((eseg["k"][3], rsub), (eseg["k"][4], sidx), (eseg["k"][5], sval)):
+        assert torch.equal(arr, src.transpose(0, 1).contiguous())
+    # unequal lengths: the stores' own order
+    short = CompressedTensorMLX(pq_codes=pq[:5].contiguous(), rvq_codes=rvq, rvq_mask=torch.zeros((5, H), dtype=torch.bool),
+                                rvq_offsets=offs[:4], num_heads=H)
+    assert "rows" not in K.ref_store_segment(st, short, 0, 5, 0, head_major=True)
