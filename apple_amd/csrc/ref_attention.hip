@@ -324,11 +324,37 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
   const int tg = lane / LG;        // the lane's token group
   const int c0 = DPL * (lane % LG);  // its first coordinate
 
+  const cref segs = (cref)p.segments;
+  // score tables: the group's coded tokens are the tables' unless the drift
+  // estimate of one of its heads exceeds the tolerance (uniform)
+  bool skip_coded = false;
+  if (tab_est != nullptr) {
+    bool redo = false;
+    for (int g = 0; g < G; ++g) redo = redo || !(tab_est[(int64_t)b * p.q_heads + h * G + g] <= p.table_tol);
+    skip_coded = !redo;
+  }
+  const int coded_cost = skip_coded ? 0 : kCodedCost;
+  int64_t total_cost = 0;
+  for (int s = 0; s < p.num_segments; ++s)
+    total_cost += (int64_t)segs[s].len * (segs[s].k.pq != nullptr ? coded_cost : kExactCost);
+  const int begin = split_bound(segs, p.num_segments, total_cost, splits, split, coded_cost);
+  const int end = min(p.total_tokens, split_bound(segs, p.num_segments, total_cost, splits, split + 1, coded_cost));
+  // whether the split decodes coded tokens (uniform): else the tables stay unstaged
+  bool coded_here = false;
+  if (!skip_coded) {
+    int base = 0;
+    for (int s = 0; s < p.num_segments && base < end; ++s) {
+      const int len = segs[s].len;
+      if (segs[s].k.pq != nullptr && max(begin, base) < min(end, base + len)) coded_here = true;
+      base += len;
+    }
+  }
+
   // PQ tables: [M][C][dsub] for K, then V (unless they share one), copied in
   // 16-byte units (C * D * 2 bytes, a multiple of 16), up to 8 loads per
   // thread in flight before their stores
   const int tab_elems = M * C * dsub;
-  {
+  if (coded_here) {
     const int units = tab_elems / 8;
     uint4* dst = reinterpret_cast<uint4*>(tabs);
     for (int t = 0; t < (kv_tab_shared ? 1 : 2); ++t) {
@@ -374,21 +400,6 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
   rs.Mr = p.rvq_subspaces;
   rs.dr = p.rvq_subspaces > 0 ? D / p.rvq_subspaces : 0;
   rs.k = p.sparse_k;
-  const cref segs = (cref)p.segments;
-  // score tables: the group's coded tokens are the tables' unless the drift
-  // estimate of one of its heads exceeds the tolerance (uniform)
-  bool skip_coded = false;
-  if (tab_est != nullptr) {
-    bool redo = false;
-    for (int g = 0; g < G; ++g) redo = redo || !(tab_est[(int64_t)b * p.q_heads + h * G + g] <= p.table_tol);
-    skip_coded = !redo;
-  }
-  const int coded_cost = skip_coded ? 0 : kCodedCost;
-  int64_t total_cost = 0;
-  for (int s = 0; s < p.num_segments; ++s)
-    total_cost += (int64_t)segs[s].len * (segs[s].k.pq != nullptr ? coded_cost : kExactCost);
-  const int begin = split_bound(segs, p.num_segments, total_cost, splits, split, coded_cost);
-  const int end = min(p.total_tokens, split_bound(segs, p.num_segments, total_cost, splits, split + 1, coded_cost));
   int seg_base = 0;
   for (int s = 0; s < p.num_segments; ++s) {
     const int len = segs[s].len;

@@ -47,14 +47,15 @@ typedef float tf16 __attribute__((ext_vector_type(16)));
 typedef const rfsn_ref_segment __attribute__((address_space(4)))* tcref;
 
 constexpr int kChunk = 64;           // codebook entries per chunk (within one section)
-constexpr int kHistThreads = 512;
+constexpr int kHistThreads = 1024;
+constexpr int kHistWaves = kHistThreads / 64;  // red[] holds 4 values per wave: 64 floats
 constexpr int kHistF = 19;           // fraction bits of the fixed-point weights
 constexpr int kMaxHistSplits = 256;  // token splits per query head
 constexpr float kTabDriftVar = 1.0f / (12.0f * 1048576.0f);
 
 // tokens per thread of a histogram block (its codes stay in registers from
 // the score pass to the histogram pass)
-constexpr int hist_tokens(int M) { return M <= 8 ? 8 : (M == 16 ? 4 : 2); }
+constexpr int hist_tokens(int M) { return M <= 8 ? 4 : (M == 16 ? 2 : 1); }
 
 __device__ __forceinline__ _Float16 hbits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
@@ -226,7 +227,7 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   const int tps = (coded + S - 1) / S;
   const int ci0 = min(coded, split * tps), ci1 = min(coded, ci0 + tps);
 
-  // codes of the thread's tokens ci0 + threadIdx.x + 512 u.  A wave-uniform
+  // codes of the thread's tokens ci0 + threadIdx.x + kHistThreads u.  A wave-uniform
   // walk over the segments (scalar loads of their fields) finds each token's
   // segment; the code loads follow in straight-line code, reading segment
   // fields as scalars where the wave's tokens share one segment, so a thread
@@ -440,7 +441,7 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   __syncthreads();
   mx = red[0];
 #pragma unroll
-  for (int w = 1; w < kHistThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+  for (int w = 1; w < kHistWaves; ++w) mx = fmaxf(mx, red[w]);
 
   float ls = 0.f, q2 = 0.f, qe = 0.f;
   if (mx > -__builtin_inff()) {  // uniform
@@ -473,17 +474,17 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   qe = wave_sum(qe);
   __syncthreads();  // every histogram add is done; red is read
   if (lane == 0) {
-    red[8 + wave] = ls;
-    red[16 + wave] = q2;
-    red[24 + wave] = qe;
+    red[kHistWaves + wave] = ls;
+    red[2 * kHistWaves + wave] = q2;
+    red[3 * kHistWaves + wave] = qe;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     float a = 0.f, b2 = 0.f, c2 = 0.f;
-    for (int w = 0; w < kHistThreads / 64; ++w) {
-      a += red[8 + w];
-      b2 += red[16 + w];
-      c2 += red[24 + w];
+    for (int w = 0; w < kHistWaves; ++w) {
+      a += red[kHistWaves + w];
+      b2 += red[2 * kHistWaves + w];
+      c2 += red[3 * kHistWaves + w];
     }
     *reinterpret_cast<float4*>(pst + ((int64_t)bh * S + split) * 4) = make_float4(mx, a, b2, c2);
   }
@@ -501,10 +502,10 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
 
 // part2[c][bh][d] = sum over chunk c's entries e of H_bh[e] V_e[d], H_bh =
 // sum over splits k of 2^(m_k - max m) H_k.  Block: chunk x 32 query heads,
-// 2 D threads owning 4 heads x 4 coordinates each.  The chunk's V rows and
-// the split maxima load together; the first 32 threads turn the maxima into
-// weights; the chunk's sums (one contiguous run of [32][S][64]) load as
-// 16-byte units, 8 splits at a time.
+// 2 D threads owning 4 heads x 4 coordinates each.  The chunk's V rows, its
+// first 8 splits' sums (one contiguous run of [32][S][64], 16-byte units)
+// and the split maxima load together; the first 32 threads turn the maxima
+// into weights; further splits load 8 at a time.
 template <int D>
 __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __restrict__ pst,
                                                                const float* __restrict__ hbuf, int S, int BH,
@@ -540,6 +541,20 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
                                                                 : make_uint2(0u, 0u);
     }
   }
+  // the first 8 splits' sums: unit (r, j4) = entries 4 j4 .. 4 j4 + 3 of head row r
+  const float4* hsrc = reinterpret_cast<const float4*>(hbuf + ((int64_t)blockIdx.x * BH + bh0) * S * kChunk);
+  float4 x[HU][8];
+  auto load_h = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < HU; ++a) {
+      const int i = threadIdx.x + a * NT, r = i / (kChunk / 4), j4 = i - r * (kChunk / 4);
+      const bool ok = bh0 + r < BH && 4 * j4 < n;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        x[a][u] = ok && k0 + u < S ? hsrc[((int64_t)r * S + k0 + u) * (kChunk / 4) + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  load_h(0);
   // split weights of head row r = threadIdx.x < 32
   if (threadIdx.x < 32) {
     const int r = threadIdx.x;
@@ -573,17 +588,8 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
     float4 v[HU];
 #pragma unroll
     for (int a = 0; a < HU; ++a) v[a] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* src = reinterpret_cast<const float4*>(hbuf + ((int64_t)blockIdx.x * BH + bh0) * S * kChunk);
     for (int k0 = 0; k0 < S; k0 += 8) {
-      float4 x[HU][8];
-#pragma unroll
-      for (int a = 0; a < HU; ++a) {
-        const int i = threadIdx.x + a * NT, r = i / (kChunk / 4), j4 = i - r * (kChunk / 4);
-        const bool ok = bh0 + r < BH && 4 * j4 < n;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          x[a][u] = ok && k0 + u < S ? src[((int64_t)r * S + k0 + u) * (kChunk / 4) + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      if (k0 > 0) load_h(k0);
 #pragma unroll
       for (int a = 0; a < HU; ++a) {
         const int r = (threadIdx.x + a * NT) / (kChunk / 4);
