@@ -27,12 +27,17 @@
 #include "rfsn_common.h"
 #include "rfsn_internal.h"
 
+#include <type_traits>
+
 namespace rfsn {
 namespace {
 
 constexpr int kRefWaves = 8;
 constexpr int kRefThreads = kRefWaves * 64;
 constexpr int kRefMaxG = 8;  // query heads per KV head
+// exact rows: token slots per lane in units of U (2: 0.0693 -> 0.0684 ms at
+// the reference default's table step; 4: 0.0698 ms)
+constexpr int kExactSlots = 2;
 constexpr int kRefMaxL = 8;  // gated RVQ layers
 
 typedef const rfsn_ref_segment __attribute__((address_space(4)))* cref;
@@ -429,45 +434,20 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
       const int64_t ets = segs[s].exact_token_stride, ehs = segs[s].exact_head_stride;
       // exact rows: DPL-wide loads when the rows and strides allow them (uniform)
       const bool evec = (((uintptr_t)ek | (uintptr_t)ev) % (2 * DPL) == 0) && ets % DPL == 0 && ehs % DPL == 0;
-      // wave w takes steps of U * P consecutive tokens, every kRefWaves-th step;
-      // token g0 + u * P + tg is slot u of the lane's group
-      for (int g0 = lo + wave * (U * P); g0 < hi; g0 += kRefWaves * U * P) {
-        int64_t row[U], tk[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int tl = g0 + u * P + tg;
-          const int t = (tl < hi ? tl : g0) - seg_base;  // past the end: re-read the step's first token
-          tk[u] = tok0 + t;
-          row[u] = tk[u] * rts + h * rhs;
-        }
-        float kk[U][DPL], vv[U][DPL];
-        if (kc.pq == nullptr) {
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const int64_t e = tk[u] * ets + (int64_t)h * ehs + c0;
-            uint16_t wk[DPL], wv[DPL];
-            load_h<DPL>(ek + e, wk, evec);
-            load_h<DPL>(ev + e, wv, evec);
-#pragma unroll
-            for (int v = 0; v < DPL; ++v) {
-              kk[u][v] = h2f(wk[v]);
-              vv[u][v] = h2f(wv[v]);
-            }
-          }
-        } else {
-          rebuild<D, DPL, U, EXT>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, c0);
-          rebuild<D, DPL, U, EXT>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, c0);
-        }
+      // one step of UU * P consecutive tokens from g0 (token g0 + u * P + tg
+      // is slot u of the lane's group): scores, online softmax, P.V
+      auto attend = [&](auto uu, int g0, const auto& kk, const auto& vv) __attribute__((always_inline)) {
+        constexpr int UU = decltype(uu)::value;
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
           if (g >= G) continue;  // uniform
-          float sc[U][P];
+          float sc[UU][P];
           float mx = -__builtin_inff();
 #pragma unroll
-          for (int u = 0; u < U; ++u) {
+          for (int u = 0; u < UU; ++u) {
             float part = 0.0f;
 #pragma unroll
-            for (int v = 0; v < DPL; ++v) part = __builtin_fmaf(qv[g][v], kk[u][v], part);
+            for (int v = 0; v < DPL; ++v) part = __builtin_fmaf(qv[g][v], (float)kk[u][v], part);
             group_sums<P>(part, sc[u]);  // q was scaled on load
 #pragma unroll
             for (int q = 0; q < P; ++q) {
@@ -484,7 +464,7 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
 #pragma unroll
           for (int v = 0; v < DPL; ++v) acc[g][v] *= corr;
 #pragma unroll
-          for (int u = 0; u < U; ++u) {
+          for (int u = 0; u < UU; ++u) {
             float pr[P];
 #pragma unroll
             for (int q = 0; q < P; ++q) {
@@ -493,10 +473,49 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
             }
             const float pl = pick<P>(pr, tg);
 #pragma unroll
-            for (int v = 0; v < DPL; ++v) acc[g][v] = __builtin_fmaf(pl, vv[u][v], acc[g][v]);
+            for (int v = 0; v < DPL; ++v) acc[g][v] = __builtin_fmaf(pl, (float)vv[u][v], acc[g][v]);
           }
           l_run[g] = l;
           m_run[g] = mn;
+        }
+      };
+      // wave w takes steps of U * P consecutive tokens, every kRefWaves-th
+      // step; exact rows take steps of UE * P (no decode registers are live
+      // there: more loads in flight per lane, the rows kept in fp16, which
+      // the FMAs convert exactly)
+      if (kc.pq == nullptr) {
+        constexpr int UE = kExactSlots * U;
+        for (int g0 = lo + wave * (UE * P); g0 < hi; g0 += kRefWaves * UE * P) {
+          _Float16 kk[UE][DPL], vv[UE][DPL];
+#pragma unroll
+          for (int u = 0; u < UE; ++u) {
+            const int tl = g0 + u * P + tg;
+            const int t = (tl < hi ? tl : g0) - seg_base;  // past the end: re-read the step's first token
+            const int64_t e = (tok0 + t) * ets + (int64_t)h * ehs + c0;
+            uint16_t wk[DPL], wv[DPL];
+            load_h<DPL>(ek + e, wk, evec);
+            load_h<DPL>(ev + e, wv, evec);
+#pragma unroll
+            for (int v = 0; v < DPL; ++v) {
+              kk[u][v] = __builtin_bit_cast(_Float16, wk[v]);
+              vv[u][v] = __builtin_bit_cast(_Float16, wv[v]);
+            }
+          }
+          attend(std::integral_constant<int, UE>{}, g0, kk, vv);
+        }
+      } else {
+        for (int g0 = lo + wave * (U * P); g0 < hi; g0 += kRefWaves * U * P) {
+          int64_t row[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int tl = g0 + u * P + tg;
+            const int t = (tl < hi ? tl : g0) - seg_base;  // past the end: re-read the step's first token
+            row[u] = (tok0 + t) * rts + h * rhs;
+          }
+          float kk[U][DPL], vv[U][DPL];
+          rebuild<D, DPL, U, EXT>(kk, kc, row, ktab, M, C, dsub, (const uint16_t*)p.k_rvq_cb, rs, c0);
+          rebuild<D, DPL, U, EXT>(vv, vc, row, vtab, M, C, dsub, (const uint16_t*)p.v_rvq_cb, rs, c0);
+          attend(std::integral_constant<int, U>{}, g0, kk, vv);
         }
       }
     }
