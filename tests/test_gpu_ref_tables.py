@@ -312,6 +312,55 @@ def test_cache_decode_takes_the_tables(device, tmp_path):
     assert excess <= 0, err
 
 
+def test_cache_tables_follow_the_warm_tier(device, tmp_path):
+    """A decode loop over a reference-format cache with score tables: every
+    update demotes blocks into warm (new warm stores), and each step's
+    attention reads a head-major copy of the current stores, remade when they
+    change and reused while they stay; every step within 2e-3 of the same
+    cache decoded exactly (tolerance None)."""
+    import dataclasses
+
+    from apple_amd import kernels as K
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    g = rng(3310)
+    cfg = RFSNConfig(hidden_dim=512, num_heads=4, head_dim=128, num_layers=2, num_subspaces=8, subspace_dim=16,
+                     num_rvq_layers=4, rvq_codebook_size=512, rvq_sparsity_threshold=0.25, hot_capacity=64,
+                     warm_capacity=8192, cold_capacity=128, block_size_seq=64, disk_cache_dir=str(tmp_path),
+                     prefetch_throttle_s=0.0)
+    pq, rv = rand_codebooks(g, 8, 256, 16), rand_codebooks(g, 4, 512, 128)
+    rv[:, 0] = 0
+    qz = HybridQuantizerMLX(cfg, device=device, pq_codebooks=T(pq, device), rvq_codebooks=T(rv, device))
+    caches = {tol: RFSNv10KVCacheMLX(dataclasses.replace(cfg, score_table_tolerance=tol), layer_idx=0, device=device)
+              for tol in (cfg.score_table_tolerance, None)}
+    k0, v0 = randn16(g, 4500, 4, 128), randn16(g, 4500, 4, 128)
+    for c in caches.values():
+        c.update(T(k0, device), T(v0, device), qz, disk_dir=tmp_path)
+    tab = caches[cfg.score_table_tolerance]
+    copies, stores = [], []
+    for step in range(5):
+        q = T(randn16(g, 1, 4, 128), device)
+        outs = {tol: H(c.attention_forward(q, causal=True)) for tol, c in caches.items()}
+        assert tab.last_ref_tables
+        hm = K._HEAD_MAJOR.get(id(tab.warm_keys.pq_codes))
+        assert hm is not None and hm[0]() is tab.warm_keys.pq_codes
+        copies.append(hm[2][0])
+        stores.append(tab.warm_keys.pq_codes)
+        err, excess = _excess(outs[cfg.score_table_tolerance], outs[None])
+        assert excess <= 0, (step, err)
+        if step == 2:  # a second call over unchanged stores reuses the copy
+            tab.attention_forward(q, causal=True)
+            assert K._HEAD_MAJOR[id(tab.warm_keys.pq_codes)][2][0] is hm[2][0]
+        k1, v1 = randn16(g, 96, 4, 128), randn16(g, 96, 4, 128)  # 96 tokens: at least one block demoted
+        for c in caches.values():
+            c.update(T(k1, device), T(v1, device), qz, disk_dir=tmp_path)
+    # every update replaced the warm stores, and each version got its own copy
+    assert all(a is not b for a, b in zip(stores, stores[1:]))
+    assert all(a is not b for a, b in zip(copies, copies[1:]))
+
+
 @pytest.mark.parametrize("tables", [False, True])
 def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
     """A store whose rows are all active is attended without its active map
