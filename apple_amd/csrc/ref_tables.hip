@@ -506,22 +506,22 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
 // first 8 splits' sums (one contiguous run of [32][S][64], 16-byte units)
 // and the split maxima load together; the first 32 threads turn the maxima
 // into weights; further splits load 8 at a time.
-template <int D>
-__global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __restrict__ pst,
+template <int D, int HB>
+__global__ void __launch_bounds__(D * HB / 16) ref_tab_values_kernel(const float* __restrict__ pst,
                                                                const float* __restrict__ hbuf, int S, int BH,
                                                                const uint16_t* __restrict__ pq_cb,
                                                                const uint16_t* __restrict__ rvq_cb, RefTabGeom g,
                                                                float* __restrict__ part2) {
-  constexpr int NT = 2 * D;
+  constexpr int NT = D * HB / 16;  // D / 4 coordinate groups x HB / 4 head groups
   constexpr int RU = kChunk * (D / 4) / NT;  // 4-coordinate units of the rows per thread (8)
-  constexpr int HU = 32 * (kChunk / 4) / NT;  // (head, 4 entries) units per thread: 256 / D
+  constexpr int HU = HB * (kChunk / 4) / NT;  // (head, 4 entries) units per thread: 256 / D
   extern __shared__ __align__(16) float vsm[];
   float* rows = vsm;             // [64][D]
-  float* hs = vsm + kChunk * D;  // [64][32]
-  float* wk = hs + kChunk * 32;  // [32][S]
+  float* hs = vsm + kChunk * D;  // [64][HB]
+  float* wk = hs + kChunk * HB;  // [HB][S]
   int sec, e0, n;
   chunk_of(g, blockIdx.x, sec, e0, n);
-  const int bh0 = blockIdx.y * 32;
+  const int bh0 = blockIdx.y * HB;
   const bool pq = sec < g.M;
   const int lo = pq ? sec * g.dsub : 0;
 
@@ -555,8 +555,8 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
     }
   };
   load_h(0);
-  // split weights of head row r = threadIdx.x < 32
-  if (threadIdx.x < 32) {
+  // split weights of head row r = threadIdx.x < HB
+  if (threadIdx.x < HB) {
     const int r = threadIdx.x;
     const float* src = pst + (int64_t)(bh0 + r) * S * 4;
     float mx = -__builtin_inff();
@@ -608,10 +608,10 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
     for (int a = 0; a < HU; ++a) {
       const int i = threadIdx.x + a * NT, r = i / (kChunk / 4), j4 = i - r * (kChunk / 4);
       // entries past the chunk's n hold stale values: zero them
-      hs[(4 * j4 + 0) * 32 + r] = 4 * j4 + 0 < n ? v[a].x : 0.f;
-      hs[(4 * j4 + 1) * 32 + r] = 4 * j4 + 1 < n ? v[a].y : 0.f;
-      hs[(4 * j4 + 2) * 32 + r] = 4 * j4 + 2 < n ? v[a].z : 0.f;
-      hs[(4 * j4 + 3) * 32 + r] = 4 * j4 + 3 < n ? v[a].w : 0.f;
+      hs[(4 * j4 + 0) * HB + r] = 4 * j4 + 0 < n ? v[a].x : 0.f;
+      hs[(4 * j4 + 1) * HB + r] = 4 * j4 + 1 < n ? v[a].y : 0.f;
+      hs[(4 * j4 + 2) * HB + r] = 4 * j4 + 2 < n ? v[a].z : 0.f;
+      hs[(4 * j4 + 3) * HB + r] = 4 * j4 + 3 < n ? v[a].w : 0.f;
     }
   }
   __syncthreads();
@@ -620,7 +620,7 @@ __global__ void __launch_bounds__(2 * D) ref_tab_values_kernel(const float* __re
 #pragma unroll 4
   for (int j = 0; j < n; ++j) {
     const float4 rv = *reinterpret_cast<const float4*>(rows + j * D + d0);
-    const float4 hv = *reinterpret_cast<const float4*>(hs + j * 32 + b0);
+    const float4 hv = *reinterpret_cast<const float4*>(hs + j * HB + b0);
     const float hb[4] = {hv.x, hv.y, hv.z, hv.w}, rd[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -818,10 +818,12 @@ int launch_tables_d(const rfsn_ref_params* p, const RefTabGeom& g, const RefTabL
     default: st = launch_hist<32>(p, g, S, w.tab, w.pst, w.part, s); break;
   }
   if (st) return st;
-  const size_t vlds = ((size_t)kChunk * D + kChunk * 32 + 32 * S) * sizeof(float);
-  (void)hipFuncSetAttribute((const void*)ref_tab_values_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+  constexpr int HB = 32;  // query heads per values block (16 measured the same, 8 slower)
+  const dim3 vg((unsigned)g.nch, (unsigned)((BH + HB - 1) / HB));
+  const size_t vlds = ((size_t)kChunk * D + kChunk * HB + HB * S) * sizeof(float);
+  (void)hipFuncSetAttribute((const void*)ref_tab_values_kernel<D, HB>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)vlds);
-  hipLaunchKernelGGL(ref_tab_values_kernel<D>, cg, dim3(2 * D), vlds, s, w.pst, w.part, S, BH,
+  hipLaunchKernelGGL((ref_tab_values_kernel<D, HB>), vg, dim3(D * HB / 16), vlds, s, w.pst, w.part, S, BH,
                      (const uint16_t*)p->v_pq_cb, (const uint16_t*)p->v_rvq_cb, g, w.part2);
   st = check_launch("ref_tables values");
   if (st) return st;
