@@ -502,23 +502,36 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
 
 // part2[c][bh][d] = sum over chunk c's entries e of H_bh[e] V_e[d], H_bh =
 // sum over splits k of 2^(m_k - max m) H_k.  Block: chunk x 32 query heads,
-// 2 D threads owning 4 heads x 4 coordinates each.  The chunk's V rows, its
-// first 8 splits' sums (one contiguous run of [32][S][64], 16-byte units)
-// and the split maxima load together; the first 32 threads turn the maxima
-// into weights; further splits load 8 at a time.
+// 2 D threads (D / 32 waves).  The chunk's V rows, its first 8 splits' sums
+// (one contiguous run of [32][S][64], 16-byte units) and the split maxima
+// load together; the first 32 threads turn the maxima into weights; further
+// splits load 8 at a time.  The product runs on v_mfma_f32_32x32x16_f16, wave
+// w taking coordinates 32 w .. 32 w + 31: A = H of the 32 heads, 16 entries
+// per step, as fp16 hi + lo of s_bh H (s_bh a power of 2 that puts the head's
+// largest sum of the chunk in [2^14, 2^15); hi + lo holds 22 bits of it), B =
+// the V rows (fp16, exact), and the fp32 result is divided by s_bh.
+constexpr int kValHs = kChunk + 4;  // LDS row of a head's sums (floats; +4: rows start 4 banks apart)
+constexpr int kValRt = kChunk + 8;  // LDS row of a coordinate's V entries (halves; +8: 4 banks apart)
+template <int D>
+constexpr size_t values_lds_bytes(int S) {
+  return ((size_t)32 * kValHs + 32 + 32 * S) * sizeof(float) + (size_t)D * kValRt * sizeof(uint16_t);
+}
+
 template <int D, int HB>
 __global__ void __launch_bounds__(D * HB / 16) ref_tab_values_kernel(const float* __restrict__ pst,
                                                                const float* __restrict__ hbuf, int S, int BH,
                                                                const uint16_t* __restrict__ pq_cb,
                                                                const uint16_t* __restrict__ rvq_cb, RefTabGeom g,
                                                                float* __restrict__ part2) {
-  constexpr int NT = D * HB / 16;  // D / 4 coordinate groups x HB / 4 head groups
+  static_assert(HB == 32, "the query heads are the 32 rows of one MFMA tile");
+  constexpr int NT = D * HB / 16;  // 2 D: D / 32 waves of 32 coordinates
   constexpr int RU = kChunk * (D / 4) / NT;  // 4-coordinate units of the rows per thread (8)
   constexpr int HU = HB * (kChunk / 4) / NT;  // (head, 4 entries) units per thread: 256 / D
   extern __shared__ __align__(16) float vsm[];
-  float* rows = vsm;             // [64][D]
-  float* hs = vsm + kChunk * D;  // [64][HB]
-  float* wk = hs + kChunk * HB;  // [HB][S]
+  float* hs = vsm;                     // [HB][kValHs] scaled sums
+  float* hinv = hs + HB * kValHs;      // [HB] 1 / s_bh
+  float* wk = hinv + HB;               // [HB][S]
+  uint16_t* rt = reinterpret_cast<uint16_t*>(wk + HB * S);  // [D][kValRt] fp16 V rows, transposed
   int sec, e0, n;
   chunk_of(g, blockIdx.x, sec, e0, n);
   const int bh0 = blockIdx.y * HB;
@@ -571,19 +584,23 @@ __global__ void __launch_bounds__(D * HB / 16) ref_tab_values_kernel(const float
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int idx = threadIdx.x + u * NT, j = idx / (D / 4), c4 = idx - j * (D / 4);
-      *reinterpret_cast<float4*>(rows + j * D + 4 * c4) =
-          make_float4(h2f((uint16_t)rw[u].x), h2f((uint16_t)(rw[u].x >> 16)), h2f((uint16_t)rw[u].y),
-                      h2f((uint16_t)(rw[u].y >> 16)));
+      uint16_t* col = rt + (4 * c4) * kValRt + j;
+      col[0] = (uint16_t)rw[u].x;
+      col[kValRt] = (uint16_t)(rw[u].x >> 16);
+      col[2 * kValRt] = (uint16_t)rw[u].y;
+      col[3 * kValRt] = (uint16_t)(rw[u].y >> 16);
     }
   } else {
     // 2-wide PQ subspaces: the subspace's coordinates, zero elsewhere
     for (int i = threadIdx.x; i < kChunk * D; i += NT) {
       const int j = i / D, dd = i - j * D;
-      rows[i] = (j < n && dd >= lo && dd < lo + g.dsub) ? h2f(pq_cb[(int64_t)(e0 + j) * g.dsub + (dd - lo)]) : 0.f;
+      rt[dd * kValRt + j] = (j < n && dd >= lo && dd < lo + g.dsub) ? pq_cb[(int64_t)(e0 + j) * g.dsub + (dd - lo)]
+                                                                     : (uint16_t)0;
     }
   }
   __syncthreads();
-  // H over the splits: unit (r, j4) = entries 4 j4 .. 4 j4 + 3 of head row r
+  // H over the splits: unit (r, j4) = entries 4 j4 .. 4 j4 + 3 of head row r,
+  // r's 16 units in 16 consecutive lanes
   {
     float4 v[HU];
 #pragma unroll
@@ -608,31 +625,52 @@ __global__ void __launch_bounds__(D * HB / 16) ref_tab_values_kernel(const float
     for (int a = 0; a < HU; ++a) {
       const int i = threadIdx.x + a * NT, r = i / (kChunk / 4), j4 = i - r * (kChunk / 4);
       // entries past the chunk's n hold stale values: zero them
-      hs[(4 * j4 + 0) * HB + r] = 4 * j4 + 0 < n ? v[a].x : 0.f;
-      hs[(4 * j4 + 1) * HB + r] = 4 * j4 + 1 < n ? v[a].y : 0.f;
-      hs[(4 * j4 + 2) * HB + r] = 4 * j4 + 2 < n ? v[a].z : 0.f;
-      hs[(4 * j4 + 3) * HB + r] = 4 * j4 + 3 < n ? v[a].w : 0.f;
+      float4 h = v[a];
+      h.x = 4 * j4 + 0 < n ? h.x : 0.f;
+      h.y = 4 * j4 + 1 < n ? h.y : 0.f;
+      h.z = 4 * j4 + 2 < n ? h.z : 0.f;
+      h.w = 4 * j4 + 3 < n ? h.w : 0.f;
+      // the head's largest sum (sums are >= 0) and its scale 2^(15 - e), with
+      // largest = f 2^e, f in [0.5, 1): s H < 2^15, clamped to normal scales
+      float mx = fmaxf(fmaxf(h.x, h.y), fmaxf(h.z, h.w));
+#pragma unroll
+      for (int o = 1; o < kChunk / 4; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      int e = 0;
+      (void)frexpf(mx, &e);
+      const int k = mx > 0.f ? min(126, max(-126, 15 - e)) : 0;
+      const float sc = ldexpf(1.0f, k);
+      *reinterpret_cast<float4*>(hs + r * kValHs + 4 * j4) = make_float4(h.x * sc, h.y * sc, h.z * sc, h.w * sc);
+      if (j4 == 0) hinv[r] = ldexpf(1.0f, -k);
     }
   }
   __syncthreads();
-  const int d0 = 4 * (threadIdx.x % (D / 4)), b0 = 4 * (threadIdx.x / (D / 4));
-  float acc[4][4] = {};
-#pragma unroll 4
-  for (int j = 0; j < n; ++j) {
-    const float4 rv = *reinterpret_cast<const float4*>(rows + j * D + d0);
-    const float4 hv = *reinterpret_cast<const float4*>(hs + j * HB + b0);
-    const float hb[4] = {hv.x, hv.y, hv.z, hv.w}, rd[4] = {rv.x, rv.y, rv.z, rv.w};
+  {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, hi = lane >> 5;
+    const int d = 32 * wave + col;
+    tf16 acc = {};
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int st = 0; st < kChunk / 16; ++st) {
+      const int e = 16 * st + 8 * hi;
+      const float4 h0 = *reinterpret_cast<const float4*>(hs + col * kValHs + e);
+      const float4 h1 = *reinterpret_cast<const float4*>(hs + col * kValHs + e + 4);
+      const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+      th8 ah, al;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[a][c] = __builtin_fmaf(hb[a], rd[c], acc[a][c]);
-  }
+      for (int u = 0; u < 8; ++u) {
+        ah[u] = (_Float16)hv[u];
+        al[u] = (_Float16)(hv[u] - (float)ah[u]);
+      }
+      const th8 bv = __builtin_bit_cast(th8, *reinterpret_cast<const uint4*>(rt + d * kValRt + e));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bv, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bv, acc, 0, 0, 0);
+    }
+    // D[i][j]: lane (j, hi), register r holds head i = 8 (r / 4) + 4 hi + r % 4, coordinate j
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int bh = bh0 + b0 + a;
-    if (bh < BH)
-      *reinterpret_cast<float4*>(part2 + ((int64_t)blockIdx.x * BH + bh) * D + d0) =
-          make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+    for (int r = 0; r < 16; ++r) {
+      const int i = 8 * (r >> 2) + 4 * hi + (r & 3);
+      if (bh0 + i < BH) part2[((int64_t)blockIdx.x * BH + bh0 + i) * D + d] = acc[r] * hinv[i];
+    }
   }
 }
 
@@ -820,7 +858,7 @@ int launch_tables_d(const rfsn_ref_params* p, const RefTabGeom& g, const RefTabL
   if (st) return st;
   constexpr int HB = 32;  // query heads per values block (16 measured the same, 8 slower)
   const dim3 vg((unsigned)g.nch, (unsigned)((BH + HB - 1) / HB));
-  const size_t vlds = ((size_t)kChunk * D + kChunk * HB + HB * S) * sizeof(float);
+  const size_t vlds = values_lds_bytes<D>(S);
   (void)hipFuncSetAttribute((const void*)ref_tab_values_kernel<D, HB>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)vlds);
   hipLaunchKernelGGL((ref_tab_values_kernel<D, HB>), vg, dim3(D * HB / 16), vlds, s, w.pst, w.part, S, BH,
