@@ -169,9 +169,8 @@ __device__ __forceinline__ int64_t code_row(int64_t cts, int64_t chs, int64_t t,
   return (cts | chs) == 0 ? t * kv_heads + h : t * cts + h * chs;
 }
 
-// The window's coded tokens, in window order, split S ways per query head.
-// Block b: split b % S, query head row bh = b / S (with S a multiple of 8,
-// the blocks of one split share an XCD and its L2 copy of the split's codes).
+// The window's coded tokens, in window order, split S ways per query head
+// (S a multiple of 8); BH * S blocks, each one (query head row bh, split).
 // A thread holds KT tokens: their codes, then their scores.
 // pst[bh][split] = {m, L, Q, QE}: m the block's largest score (base 2), L =
 // sum p, Q = sum p^2, QE = sum (p~ - p)^2 (p~ = p rounded to 2^-19); hbuf
@@ -189,7 +188,23 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   float* tl = tsm;                                          // [Ep] the head's table
   uint32_t* hist = reinterpret_cast<uint32_t*>(tsm + g.Ep);  // [Ep]
   float* red = tsm + 2 * g.Ep;                              // [64]
-  const int bh = blockIdx.x / S, split = blockIdx.x % S;
+  const tcref segs = (tcref)p.segments;
+  // Blocks run on XCD blockIdx.x % 8.  Over head-major codes (every coded
+  // segment with code strides) the S blocks of a query head share an XCD, so
+  // its L2 holds the head's table once for all of them (blockIdx.x = split *
+  // BH + bh); over the stores' own [T][heads] codes the blocks of a split
+  // share one, and with them the 128-byte lines of the split's codes
+  // (blockIdx.x = bh * S + split).
+  int coded = 0;
+  bool head_rows = true;
+  for (int s = 0; s < p.num_segments; ++s)
+    if (segs[s].k.pq != nullptr) {
+      coded += segs[s].len;
+      head_rows = head_rows && (segs[s].code_token_stride | segs[s].code_head_stride) != 0;
+    }
+  const int BHn = p.batch * p.q_heads;
+  const int bh = head_rows ? (int)blockIdx.x % BHn : (int)blockIdx.x / S;
+  const int split = head_rows ? (int)blockIdx.x / BHn : (int)blockIdx.x % S;
   const int G = p.q_heads / p.kv_heads;
   const int hq = bh % p.q_heads, h = hq / G;
   const int qp = (p.causal && p.qpos) ? p.qpos[bh] : 0x7fffffff;
@@ -197,7 +212,6 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   // chunk-space indices: section s starts at chunk boundary (PQ sections of
   // Cp = 64 ceil(C / 64) slots, then gated layers of Crp = 64 ceil(Cr / 64))
   const int C = g.C, Cr = g.Cr, L = g.L, Cp = g.cpq * kChunk, Crp = g.crv * kChunk, MC = g.M * Cp;
-  const tcref segs = (tcref)p.segments;
 
   // stage the table, zero the histogram (Ep is a multiple of 4)
   {
@@ -221,9 +235,6 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
     }
   }
 
-  int coded = 0;
-  for (int s = 0; s < p.num_segments; ++s)
-    if (segs[s].k.pq != nullptr) coded += segs[s].len;
   const int tps = (coded + S - 1) / S;
   const int ci0 = min(coded, split * tps), ci1 = min(coded, ci0 + tps);
 
