@@ -190,11 +190,13 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
   float* red = tsm + 2 * g.Ep;                              // [64]
   const tcref segs = (tcref)p.segments;
   // Blocks run on XCD blockIdx.x % 8.  Over head-major codes (every coded
-  // segment with code strides) the S blocks of a query head share an XCD, so
-  // its L2 holds the head's table once for all of them (blockIdx.x = split *
-  // BH + bh); over the stores' own [T][heads] codes the blocks of a split
-  // share one, and with them the 128-byte lines of the split's codes
-  // (blockIdx.x = bh * S + split).
+  // segment with code strides) the blocks of a (query, KV head) unit share an
+  // XCD when there are a multiple of 8 units -- its L2 then holds the unit's
+  // codes once for its G query heads and each head's table once for its S
+  // splits (blockIdx.x = (split G + g) NKV + unit) -- else those of a query
+  // head (blockIdx.x = split BH + bh).  Over the stores' own [T][heads] codes
+  // the blocks of a split share one, and with them the 128-byte lines of the
+  // split's codes (blockIdx.x = bh S + split).
   int coded = 0;
   bool head_rows = true;
   for (int s = 0; s < p.num_segments; ++s)
@@ -202,10 +204,20 @@ __global__ void __launch_bounds__(kHistThreads) ref_tab_hist_kernel(const rfsn_r
       coded += segs[s].len;
       head_rows = head_rows && (segs[s].code_token_stride | segs[s].code_head_stride) != 0;
     }
-  const int BHn = p.batch * p.q_heads;
-  const int bh = head_rows ? (int)blockIdx.x % BHn : (int)blockIdx.x / S;
-  const int split = head_rows ? (int)blockIdx.x / BHn : (int)blockIdx.x % S;
   const int G = p.q_heads / p.kv_heads;
+  const int NKV = p.batch * p.kv_heads, BHn = p.batch * p.q_heads;
+  int bh, split;
+  if (head_rows && NKV % 8 == 0) {
+    const int t = (int)blockIdx.x / NKV;
+    bh = ((int)blockIdx.x % NKV) * G + t % G;
+    split = t / G;
+  } else if (head_rows) {
+    bh = (int)blockIdx.x % BHn;
+    split = (int)blockIdx.x / BHn;
+  } else {
+    bh = (int)blockIdx.x / S;
+    split = (int)blockIdx.x % S;
+  }
   const int hq = bh % p.q_heads, h = hq / G;
   const int qp = (p.causal && p.qpos) ? p.qpos[bh] : 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
