@@ -399,6 +399,38 @@ def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
     assert _excess(H(a), ref)[1] <= 0
 
 
+@pytest.mark.parametrize("k_active,v_active", [(1.0, 0.6), (0.6, 1.0)])
+def test_mixed_gated_kinds(device, monkeypatch, k_active, v_active):
+    """K codes with every row active (no map) beside V codes through an active
+    map, and the reverse: the histogram blocks' loads specialized on each
+    side's kind agree with the oracle on the tables path, and the head-major
+    copies attend bit-identically to the stores' own order."""
+    from apple_amd import kernels as K
+
+    monkeypatch.setattr(K, "REF_TABLES_MIN_TOKENS", 0)
+    g = rng(3700 + int(10 * k_active))
+    D, M, C, L, Cr, B, Hq, Hkv = 128, 8, 256, 4, 1024, 1, 8, 8
+    pq_cb = rand_codebooks(g, M, C, D // M)
+    rv_cb = rand_codebooks(g, L, Cr, D)
+    rv_cb[:, 0] = 0
+    n = 2600
+    sk, sv = _store(g, n, Hkv, M, C, L, Cr, k_active), _store(g, n, Hkv, M, C, L, Cr, v_active)
+    dk, dv = _dev_store(sk, device), _dev_store(sv, device)
+    own = K.ref_store_segment(dk, dv, 0, n, 0)
+    hm = K.ref_store_segment(dk, dv, 0, n, 0, head_major=True)
+    assert (own["k"][2] is None) == (k_active == 1.0) and (own["v"][2] is None) == (v_active == 1.0)
+    q = T(randn16(g, B, Hq, D), device)
+    kw = dict(kv_heads=Hkv, scale=D ** -0.5, causal=False, qpos=None, k_pq_cb=T(pq_cb, device),
+              v_pq_cb=T(pq_cb, device), k_rvq_cb=T(rv_cb, device), v_rvq_cb=T(rv_cb, device), score_tables=TOL)
+    info = {}
+    a = K.ref_attention(q, segments=[own], info=info, **kw)
+    assert info["score_tables"]
+    assert torch.equal(K.ref_attention(q, segments=[hm], **kw), a)
+    ref = nx.blockwise_attention(H(q), nx.decode_compressed(sk, pq_cb, rv_cb), nx.decode_compressed(sv, pq_cb, rv_cb),
+                                 D ** -0.5, 16, False, None)
+    assert _excess(H(a), ref)[1] <= 0
+
+
 def test_hybrid_attention_takes_the_tables(device, tmp_path):
     """RFSNHybridAttentionMLX over two stores of 5,000 tokens (more than
     REF_TABLES_MIN_TOKENS): the decode step goes through the score tables
