@@ -453,7 +453,10 @@ typedef struct rfsn_ref_segment {
    * active, dense rvq, rvq_sub, sparse_idx, sparse_val; active entries still
    * index rvq).  0 and 0: the stores' own [T][heads] order, row t * kv_heads + h.
    * A head-major copy ([heads][T]: strides 1 and T) gives a head's consecutive
-   * tokens consecutive codes, which the decode kernels read in whole lines. */
+   * tokens consecutive codes, which the decode kernels read in whole lines.
+   * The segment table lives in device memory, so the library cannot check
+   * these rows: the caller keeps every row of tokens token0 .. token0 + len - 1
+   * and heads 0 .. kv_heads - 1 inside the arrays. */
   int64_t code_token_stride;
   int64_t code_head_stride;
 } rfsn_ref_segment;
