@@ -377,7 +377,9 @@ def bench_ref(w, args, dev) -> dict:
         "config": {"workload": w.name, "heads": H, "head_dim": D, "context": w.context, "hot": w.hot,
                    "warm": w.warm, "format": f"PQ M{M}x{C} + gated RVQ {L}x{Cr} (reference format)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None, "kernel_ms": round(kernel_ms, 5),
+                     "frac": round(gbs / HBM_PEAK_GBS, 5),
+                     "traffic": traffic_from_profiles(w.name, "ref_attn_{}_kernel_trace.md", "traffic_bytes_per_step"),
+                     "kernel_ms": round(kernel_ms, 5),
                      "kernel_ms_percentiles": pct, "bytes_per_step": algo,
                      "rvq_codeword_bytes_per_step": 2 * w.warm * H * L * D * 2},
         "materialized_path": {"kernel_ms": round(mat_kernel_ms, 5), "ms_per_step": round(mat_ms, 5),
@@ -861,12 +863,13 @@ def cpu_baseline_longctx(w, cache, ids, q, gpu_out, repeats, budget_s=20.0):
             "seconds": round(sec, 2)}, err
 
 
-def traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs, if committed."""
-    p = ROOT / "profiles" / f"fused_decode_attn_{workload}_traffic.md"
+def traffic_from_profiles(workload: str, name: str = "fused_decode_attn_{}_traffic.md",
+                          key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch (or step) measured by rocprofv3 PMC runs, if committed."""
+    p = ROOT / "profiles" / name.format(workload)
     if not p.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    m = re.search(key + r":\s*([0-9.eE+]+)", p.read_text())
     return float(m.group(1)) if m else None
 
 
