@@ -149,18 +149,22 @@ def test_tolerance_zero_is_the_exact_path(device, monkeypatch, splits):
     assert torch.equal(tab, exact)
 
 
-@pytest.mark.parametrize("case", [0, 1, 7])
+HM_CASES = CASES[:2] + [CASES[7], (128, 8, 256, 4, 1024, 1, 32, 8, True)]  # + 8 KV units of 4 query heads
+
+
+@pytest.mark.parametrize("case", range(len(HM_CASES)))
 @pytest.mark.parametrize("tables", [False, True])
 def test_head_major_codes_match(device, monkeypatch, case, tables):
     """The window over head-major copies of its stores' codes (code strides 1
     and T; the stores keep 40-90 % of their rows active, so the gated codes go
     through active maps) attends bit-identically to the stores' own order, on
     the exact path and with score tables, for 4, 3 and 5 gated layers (3 and
-    5: the tables' per-token loads)."""
+    5: the tables' per-token loads) and for 8 (query, KV head) units of 4
+    query heads (the histogram blocks grouped per unit on an XCD)."""
     from apple_amd import kernels as K
 
     monkeypatch.setattr(K, "REF_TABLES_MIN_TOKENS", 0)
-    D, M, C, L, Cr, B, Hq, Hkv, causal = CASES[case]
+    D, M, C, L, Cr, B, Hq, Hkv, causal = HM_CASES[case]
     g = rng(3600 + 2 * case + int(tables))
     n1, n2, hot = 900, 1500, 64
     segs, keys, vals, cbs, keep, _ = _window(g, device, D, M, C, L, Cr, Hkv, n1, n2, hot)
