@@ -690,22 +690,22 @@ def fused_attention(q: torch.Tensor, fmt: WarmFormat, *, kv_heads: int, scale: f
 # reference-format attention (PQ + gated full-dimension RVQ, decoded on the fly)
 # --------------------------------------------------------------------------
 
-_ACTIVE_MAPS: Dict[int, tuple] = {}  # id(offsets) -> (weakref, rows, map)
+_ACTIVE_MAPS: Dict[int, tuple] = {}  # id(offsets) -> (weakref, (rows, version), map)
 
 
 def active_map(offsets: torch.Tensor, rows: int) -> torch.Tensor:
     """int32 [rows]: row r's index into the store's RVQ codes, or -1 -- the
     scatter of the reference's decode (quantization.py:273-274: correction row
-    offsets[a] = codes row a); memoized per offsets tensor."""
+    offsets[a] = codes row a); memoized per offsets tensor and version."""
     key = id(offsets)
     hit = _ACTIVE_MAPS.get(key)
-    if hit is not None and hit[0]() is offsets and hit[1] == rows:
+    if hit is not None and hit[0]() is offsets and hit[1] == (rows, offsets._version):
         return hit[2]
     out = torch.full((rows,), -1, dtype=torch.int32, device=offsets.device)
     a = int(offsets.shape[0])
     if a:
         out[offsets.long()] = torch.arange(a, dtype=torch.int32, device=offsets.device)
-    _ACTIVE_MAPS[key] = (weakref.ref(offsets, lambda _r, k=key: _ACTIVE_MAPS.pop(k, None)), rows, out)
+    _ACTIVE_MAPS[key] = (weakref.ref(offsets, lambda _r, k=key: _ACTIVE_MAPS.pop(k, None)), (rows, offsets._version), out)
     return out
 
 

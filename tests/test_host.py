@@ -462,6 +462,10 @@ def test_reference_active_map_and_segments():
     m = K.active_map(offs, 12)
     assert m.tolist() == [-1, 0, -1, -1, 1, 2, -1, -1, -1, 3, -1, -1]
     assert K.active_map(offs, 12) is m  # memoized per offsets tensor
+    offs2 = offs.clone()
+    m2 = K.active_map(offs2, 12)
+    offs2[3] = 11  # an in-place write: the map is made again
+    assert K.active_map(offs2, 12) is not m2 and int(K.active_map(offs2, 12)[11]) == 3
     assert K.active_map(offs, 16).shape == (16,)
     T, H, M, L = 6, 2, 8, 3
     st = CompressedTensorMLX(pq_codes=torch.zeros((T, H, M), dtype=torch.uint8),
