@@ -574,8 +574,16 @@ __global__ void __launch_bounds__(kRefThreads) __attribute__((amdgpu_waves_per_e
 
 int ref_splits(const rfsn_ref_params* p) {
   if (p->splits > 0) return p->splits;
+  // blocks to aim for: two per CU, or one where a block's fixed cost (its
+  // heads' q, combine and partials) outweighs its tokens -- groups of query
+  // heads, and the exact pass of the score tables, which holds the hot
+  // tokens only.  Measured on the default format (32 query heads, D 128,
+  // 10k-33k tokens), 256 blocks against 512: 8 or 4 KV heads 4-14% faster
+  // (exact decode) and 11-23% (score tables); one query head per KV head
+  // flat or slower in the exact decode (8 heads, 9k tokens: 15% slower).
   const int units = p->batch * p->kv_heads;
-  int s = (512 + units - 1) / units;
+  const int target = (p->score_tables != 0 || p->q_heads > p->kv_heads) ? 256 : 512;
+  int s = (target + units - 1) / units;
   const int max_s = (p->total_tokens + 63) / 64;  // at least 64 tokens per split
   if (s > max_s) s = max_s;
   return s < 1 ? 1 : s;

@@ -847,10 +847,10 @@ def ref_tables_min_tokens(group: int) -> int:
     ``group`` query heads per KV head.  The tables' histograms cost grows
     with the query heads while the exact decode of a token is shared by its
     group, so the break-even moves out with the group: measured near 3.3k,
-    4.7k, 8.3k and 13.6k coded tokens for groups of 1, 2, 4 and 8 (32 query
+    4.7k, 8.2k and 10.3k coded tokens for groups of 1, 2, 4 and 8 (32 query
     heads, D 128, 4 gated layers of 4,096), which ``(group + 2) / 3`` times
-    ``REF_TABLES_MIN_TOKENS`` follows."""
-    return REF_TABLES_MIN_TOKENS * (max(group, 1) + 2) // 3
+    ``REF_TABLES_MIN_TOKENS``, at most 2.5 times, follows."""
+    return min(REF_TABLES_MIN_TOKENS * (max(group, 1) + 2) // 3, REF_TABLES_MIN_TOKENS * 5 // 2)
 
 
 def _ref_format_params(k_pq_cb: torch.Tensor, k_rvq_cb: Optional[torch.Tensor], rvq_subspaces: int,
