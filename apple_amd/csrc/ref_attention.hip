@@ -36,7 +36,8 @@ constexpr int kRefWaves = 8;
 constexpr int kRefThreads = kRefWaves * 64;
 constexpr int kRefMaxG = 8;  // query heads per KV head
 // exact rows: token slots per lane in units of U (2: 0.0693 -> 0.0684 ms at
-// the reference default's table step; 4: 0.0698 ms)
+// the reference default's table step; 4: 0.0698 ms; at one block per CU 3 and
+// 4 tie there and lose 2-7% with 8 or 4 KV heads)
 constexpr int kExactSlots = 2;
 constexpr int kRefMaxL = 8;  // gated RVQ layers
 
