@@ -115,10 +115,12 @@ class RFSNHybridAttentionMLX:
         cb, rcb = quantizer.pq.codebooks, quantizer.rvq_codebooks
         f = quantizer.warm_format()
         # score tables with their drift guard (config.score_table_tolerance)
-        # for decode-sized calls of the reference format
+        # for decode-sized calls of the reference format over enough coded
+        # tokens for the tables to beat the exact decode
         tol = quantizer.config.score_table_tolerance
         tables = {}
-        if tol is not None and not quantizer.subspace and B * Hq <= REF_TABLES_MAX_QUERY_HEADS:
+        if (tol is not None and not quantizer.subspace and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
+                and T >= K.ref_tables_min_tokens(Hq // key_store.num_heads)):
             tables = dict(score_tables=float(tol), table_stats=self._table_stats(quantizer))
         # the tables read a head's codes in whole lines from a head-major
         # copy, kept per store (only for stores already on the device, which

@@ -1589,9 +1589,12 @@ class RFSNv10KVCacheMLX:
         # decode steps of the reference format: score tables with their drift
         # guard (config.score_table_tolerance), as the tiled path uses them;
         # they read the warm tier's codes from a head-major copy of its stores
-        # (kept until a demotion or eviction replaces them)
+        # (kept until a demotion or eviction replaces them), for windows with
+        # enough coded tokens for the tables to beat the exact decode
         tol = self.config.score_table_tolerance
-        use_tables = tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
+        coded = sum(x[1] - x[0] if kind == "warm" else x[1][1] - x[1][0] for kind, x in plan if kind != "hot")
+        use_tables = (tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
+                      and coded >= K.ref_tables_min_tokens(Hq // self.H))
         segs, pos = [], 0
         for kind, x in plan:
             if kind == "hot":

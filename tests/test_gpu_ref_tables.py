@@ -386,6 +386,43 @@ def test_cache_tables_follow_the_warm_tier(device, tmp_path):
     assert all(a is not b for a, b in zip(copies, copies[1:]))
 
 
+def test_cache_tables_wait_for_the_group_break_even(device, tmp_path):
+    """A cache of 8 query heads over 2 KV heads (groups of 4: the tables pay
+    off from 8,192 coded tokens): with about 6,000 warm tokens the decode step
+    is the exact one and makes no head-major copy; after 3,000 more it takes
+    the tables over a copy.  Both within 2e-3 of the same cache decoded
+    exactly (tolerance None)."""
+    import dataclasses
+
+    from apple_amd import kernels as K
+    from apple_amd.cache import RFSNv10KVCacheMLX
+    from apple_amd.quantization import HybridQuantizerMLX
+    from apple_amd.storage import RFSNConfig
+
+    g = rng(3320)
+    cfg = RFSNConfig(hidden_dim=1024, num_heads=8, num_kv_heads=2, head_dim=128, num_layers=2, num_subspaces=8,
+                     subspace_dim=16, num_rvq_layers=4, rvq_codebook_size=512, rvq_sparsity_threshold=0.25,
+                     hot_capacity=64, warm_capacity=16384, cold_capacity=128, block_size_seq=64,
+                     disk_cache_dir=str(tmp_path), prefetch_throttle_s=0.0)
+    assert K.ref_tables_min_tokens(4) == 8192
+    pq, rv = rand_codebooks(g, 8, 256, 16), rand_codebooks(g, 4, 512, 128)
+    rv[:, 0] = 0
+    qz = HybridQuantizerMLX(cfg, device=device, pq_codebooks=T(pq, device), rvq_codebooks=T(rv, device))
+    caches = {tol: RFSNv10KVCacheMLX(dataclasses.replace(cfg, score_table_tolerance=tol), layer_idx=0, device=device)
+              for tol in (cfg.score_table_tolerance, None)}
+    tab = caches[cfg.score_table_tolerance]
+    for n, tables in ((6000, False), (3000, True)):
+        k, v = randn16(g, n, 2, 128), randn16(g, n, 2, 128)
+        for c in caches.values():
+            c.update(T(k, device), T(v, device), qz, disk_dir=tmp_path)
+        q = T(randn16(g, 1, 8, 128), device)
+        outs = {tol: H(c.attention_forward(q, causal=True)) for tol, c in caches.items()}
+        assert tab.last_ref_tables == tables, n
+        assert (id(tab.warm_keys.pq_codes) in K._HEAD_MAJOR) == tables, n
+        err, excess = _excess(outs[cfg.score_table_tolerance], outs[None])
+        assert excess <= 0, (n, err)
+
+
 @pytest.mark.parametrize("tables", [False, True])
 def test_dense_rows_match_the_active_map(device, monkeypatch, tables):
     """A store whose rows are all active is attended without its active map
