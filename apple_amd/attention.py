@@ -120,7 +120,7 @@ class RFSNHybridAttentionMLX:
         tol = quantizer.config.score_table_tolerance
         tables = {}
         if (tol is not None and not quantizer.subspace and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
-                and T >= K.ref_tables_min_tokens(Hq // key_store.num_heads)):
+                and T >= K.ref_tables_min_tokens(Hq // key_store.num_heads, B)):
             tables = dict(score_tables=float(tol), table_stats=self._table_stats(quantizer))
         # the tables read a head's codes in whole lines from a head-major
         # copy, kept per store (only for stores already on the device, which

@@ -1594,7 +1594,7 @@ class RFSNv10KVCacheMLX:
         tol = self.config.score_table_tolerance
         coded = sum(x[1] - x[0] if kind == "warm" else x[1][1] - x[1][0] for kind, x in plan if kind != "hot")
         use_tables = (tol is not None and sub is None and B * Hq <= REF_TABLES_MAX_QUERY_HEADS
-                      and coded >= K.ref_tables_min_tokens(Hq // self.H))
+                      and coded >= K.ref_tables_min_tokens(Hq // self.H, B))
         segs, pos = [], 0
         for kind, x in plan:
             if kind == "hot":

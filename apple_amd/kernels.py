@@ -842,15 +842,22 @@ def ref_attention_ok(head_dim: int, M: int, C: int, q_heads: int, kv_heads: int,
 REF_TABLES_MIN_TOKENS = 4096  # coded tokens below which the score tables do not pay off (one q head per KV head)
 
 
-def ref_tables_min_tokens(group: int) -> int:
+def ref_tables_min_tokens(group: int, queries: int = 1) -> int:
     """Coded tokens from which the score tables beat the exact decode for
-    ``group`` query heads per KV head.  The tables' histograms cost grows
-    with the query heads while the exact decode of a token is shared by its
-    group, so the break-even moves out with the group: measured near 3.3k,
-    4.7k, 8.2k and 10.3k coded tokens for groups of 1, 2, 4 and 8 (32 query
-    heads, D 128, 4 gated layers of 4,096), which ``(group + 2) / 3`` times
-    ``REF_TABLES_MIN_TOKENS``, at most 2.5 times, follows."""
-    return min(REF_TABLES_MIN_TOKENS * (max(group, 1) + 2) // 3, REF_TABLES_MIN_TOKENS * 5 // 2)
+    ``group`` query heads per KV head and ``queries`` query tokens.  The
+    tables' histograms cost grows with the query heads while the exact
+    decode of a token is shared by its group, so the break-even moves out
+    with the group: measured near 3.3k, 4.7k, 8.2k and 10.3k coded tokens for
+    groups of 1, 2, 4 and 8 at one query (32 query heads, D 128, 4 gated
+    layers of 4,096), which ``(group + 2) / 3`` times
+    ``REF_TABLES_MIN_TOKENS``, at most 2.5 times, follows.  The exact decode
+    repeats per query token while the tables' launches are shared, so it
+    moves in with the queries: at 2, 4 and 8 the measured break-evens were
+    0.73, 0.60 and 0.57 times those of one query (groups of 1 and 4), which
+    ``(queries + 1) / (2 queries)`` follows."""
+    q = max(queries, 1)
+    base = min(REF_TABLES_MIN_TOKENS * (max(group, 1) + 2) // 3, REF_TABLES_MIN_TOKENS * 5 // 2)
+    return base * (q + 1) // (2 * q)
 
 
 def _ref_format_params(k_pq_cb: torch.Tensor, k_rvq_cb: Optional[torch.Tensor], rvq_subspaces: int,
@@ -954,7 +961,7 @@ def ref_prepare(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool, q
     p.splits = splits
     coded = sum(sd["len"] for sd in segments if sd["exact"] is None)
     group = Hq // kv_heads if kv_heads > 0 else 1
-    use_tables = (score_tables is not None and coded >= ref_tables_min_tokens(group)
+    use_tables = (score_tables is not None and coded >= ref_tables_min_tokens(group, B)
                   and bool(L.load().rfsn_ref_tables_ok(C.byref(p))))
     if use_tables:
         if table_stats is None:
@@ -990,7 +997,7 @@ def ref_attention(q: torch.Tensor, *, kv_heads: int, scale: float, causal: bool,
     ``score_tables`` (a tolerance) attends the coded segments through q .
     codeword tables and per-codeword sums of the weights where the format and
     shape allow it (``rfsn_ref_tables_ok``) and the window holds at least
-    ``ref_tables_min_tokens(Hq // kv_heads)`` coded tokens, with the drift guard sending a
+    ``ref_tables_min_tokens(Hq // kv_heads, B)`` coded tokens, with the drift guard sending a
     group whose estimate exceeds the tolerance back to the exact decode;
     ``table_stats`` (``ref_table_stats`` of the codebooks, computed here when
     None), ``drift`` [B, Hq] float32 receives the estimates.  ``info`` (a

@@ -129,24 +129,26 @@ def test_tables_match_oracle(device, monkeypatch, D, M, C, L, Cr, B, Hq, Hkv, ca
 
 
 def test_group_moves_the_break_even(device):
-    """The same window of 6,000 coded tokens over 2 KV heads: queries of 2
-    heads (one per KV head, at least 4,096 coded tokens) go through the score
-    tables, queries of 8 heads (groups of 4, below 8,192) through the exact
-    decode; both agree with the oracle."""
+    """The same window of 6,000 coded tokens over 2 KV heads: one query of 2
+    heads (one per KV head, at least 4,096 coded tokens) goes through the
+    score tables, one of 8 heads (groups of 4, below 8,192) through the exact
+    decode, and 4 queries of 8 heads (at least 5,120) through the tables
+    again; all agree with the oracle."""
     from apple_amd import kernels as K
 
     assert K.ref_tables_min_tokens(1) == K.REF_TABLES_MIN_TOKENS <= 6000 < K.ref_tables_min_tokens(4)
+    assert K.ref_tables_min_tokens(4, 4) <= 6000
     g = rng(3050)
     D = 128
     segs, keys, vals, cbs, keep, _ = _window(g, device, D, 8, 256, 4, 4096, 2, 3000, 3000, 64)
-    for Hq, tables in ((2, True), (8, False)):
-        q = randn16(g, 1, Hq, D)
+    for B, Hq, tables in ((1, 2, True), (1, 8, False), (4, 8, True)):
+        q = randn16(g, B, Hq, D)
         info = {}
         out = K.ref_attention(T(q, device), kv_heads=2, scale=D ** -0.5, causal=False, qpos=None,
                               segments=segs, score_tables=TOL, info=info, **cbs)
-        assert info["score_tables"] == tables, Hq
+        assert info["score_tables"] == tables, (B, Hq)
         ref = nx.blockwise_attention(q, keys, vals, D ** -0.5, 16, False, None)
-        assert _excess(H(out), ref)[1] <= 0, Hq
+        assert _excess(H(out), ref)[1] <= 0, (B, Hq)
 
 
 @pytest.mark.parametrize("splits", [0, 1, 3])
